@@ -1,0 +1,268 @@
+/*
+ * gdn_amd.h -- C ABI of the MI355X batch-1 GatedDeltaNet-1.3B decode engine
+ * (libgdn_amd.so).
+ *
+ * The declarations mirror the reference's c_impl/gdn_model.h (YAMWD/
+ * GatedDeltaNet) so that a caller written against gdn_model.cpp -- its own
+ * gdn_eval.cpp, or host.cpp's runner -- links against this library instead.
+ * Each entry point cites the reference interface it replaces.  Plain C types
+ * and pointers only; no HIP or torch type appears here.
+ *
+ * Errors: every int-returning entry point returns 0 on success and -1 on
+ * failure after printing one line to stderr, as the reference's
+ * gdn_print_error does (gdn_model.cpp:487-493).  Nothing throws across this
+ * boundary.  Not reentrant per run state, like the reference.
+ */
+#ifndef GDN_AMD_H
+#define GDN_AMD_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- .gdnw header: byte-identical to GDNWeightHeader, gdn_model.h:30-45
+ *      (60 bytes, little-endian; written by export_gdn_c.py:27-30). ---- */
+typedef struct {
+    char magic[8];              /* "GDNWv1\0\0" */
+    uint32_t version;           /* 1 */
+    uint32_t vocab_size;
+    uint32_t hidden_size;
+    uint32_t num_layers;
+    uint32_t num_heads;
+    uint32_t num_v_heads;
+    uint32_t head_dim;
+    uint32_t intermediate_size;
+    uint32_t conv_size;
+    uint32_t max_seq_len;
+    int32_t bos_token_id;
+    int32_t eos_token_id;
+    float norm_eps;
+} GDNWeightHeader;
+
+/* ---- workspace layout in FLOATS: identical values to gdn_model.h:54-75.
+ *      The engine keeps this layout in device memory. ---- */
+#define GDN_WSF_HID     2048u
+#define GDN_WSF_HEAD    16u
+#define GDN_WSF_MLP     5632u
+#define GDN_WSF_STATE   12582912u
+#define GDN_WSF_HEADBUF 442368u
+#define GDN_WSF_LOGITS  32000u
+#define GDN_WS_OFF_X          ((size_t)0)
+#define GDN_WS_OFF_X_NORM     (GDN_WS_OFF_X         + GDN_WSF_HID)
+#define GDN_WS_OFF_Q          (GDN_WS_OFF_X_NORM    + GDN_WSF_HID)
+#define GDN_WS_OFF_K          (GDN_WS_OFF_Q         + GDN_WSF_HID)
+#define GDN_WS_OFF_V          (GDN_WS_OFF_K         + GDN_WSF_HID)
+#define GDN_WS_OFF_A          (GDN_WS_OFF_V         + GDN_WSF_HID)
+#define GDN_WS_OFF_B          (GDN_WS_OFF_A         + GDN_WSF_HEAD)
+#define GDN_WS_OFF_GATE       (GDN_WS_OFF_B         + GDN_WSF_HEAD)
+#define GDN_WS_OFF_ATTN       (GDN_WS_OFF_GATE      + GDN_WSF_HID)
+#define GDN_WS_OFF_TMP_HIDDEN (GDN_WS_OFF_ATTN      + GDN_WSF_HID)
+#define GDN_WS_OFF_MLP_GATE   (GDN_WS_OFF_TMP_HIDDEN + GDN_WSF_HID)
+#define GDN_WS_OFF_MLP_UP     (GDN_WS_OFF_MLP_GATE  + GDN_WSF_MLP)
+#define GDN_WS_OFF_REC_STATE  (GDN_WS_OFF_MLP_UP    + GDN_WSF_MLP)
+#define GDN_WS_OFF_HEAD_BUF   (GDN_WS_OFF_REC_STATE + GDN_WSF_STATE)
+#define GDN_WS_OFF_LOGITS     (GDN_WS_OFF_HEAD_BUF  + GDN_WSF_HEADBUF)
+#define GDN_WS_FLOATS         (GDN_WS_OFF_LOGITS    + GDN_WSF_LOGITS)
+
+/* ---- arithmetic contracts (the reference implements GDN_CONTRACT_REF) ----
+ * GDN_CONTRACT_REF          gdn_model.cpp: BF16 weights, native BF16-product
+ *                           GEMVs, BF16 operator boundaries, BF16 state.
+ * GDN_CONTRACT_BF16W_FP32S  as REF but the recurrent state stays FP32.
+ * GDN_CONTRACT_FP32         FP32 weights/activations/state, FP32 products,
+ *                           no rounding points; same reduction orders. */
+#define GDN_CONTRACT_REF          0
+#define GDN_CONTRACT_BF16W_FP32S  1
+#define GDN_CONTRACT_FP32         2
+
+/* Host-side weight views into the .gdnw payload (gdn_model.h:123-142). */
+typedef struct {
+    const float *attn_norm;
+    const float *a_log;
+    const float *dt_bias;
+    const float *q_proj;
+    const float *k_proj;
+    const float *v_proj;
+    const float *a_proj;
+    const float *b_proj;
+    const float *q_conv;
+    const float *k_conv;
+    const float *v_conv;
+    const float *g_proj;
+    const float *o_norm;
+    const float *o_proj;
+    const float *mlp_norm;
+    const float *mlp_gate_proj;
+    const float *mlp_up_proj;
+    const float *mlp_down_proj;
+} GDNLayerWeights;
+
+/* Host model: gdn_model.h:144-151, unchanged. */
+typedef struct {
+    GDNWeightHeader config;
+    float *weight_data;
+    GDNLayerWeights *layers;
+    const float *embeddings;
+    const float *final_norm;
+    const float *lm_head;
+} GDNModel;
+
+struct GDNEngine;
+
+/* Run state (gdn_model.h:153-160).  The reference's 32 FPGA weight shards
+ * and aux image are replaced by `engine` (device weights, activations,
+ * stream, captured step graph).  workspace, x, recurrent_state and
+ * head_buffer keep their meaning and GDN_WS_OFF_* offsets but point to
+ * DEVICE memory. */
+typedef struct {
+    void *workspace;            /* device, GDN_WS_FLOATS floats */
+    float *x;                   /* device view at GDN_WS_OFF_X */
+    float *recurrent_state;     /* device view at GDN_WS_OFF_REC_STATE */
+    float *head_buffer;         /* device view at GDN_WS_OFF_HEAD_BUF */
+    struct GDNEngine *engine;
+} GDNRunState;
+
+/* ===== model (host) ===== */
+
+/* gdn_model.h:213 -- read a .gdnw file: 60-byte header, FP32 payload in
+ * gdn_assign_weight_views order; rejects bad magic/version,
+ * num_heads != num_v_heads, hidden != heads*head_dim and (unless the file
+ * is loaded for the FP32 contract) non-BF16-exact values. */
+int gdn_model_load(GDNModel *model, const char *path);
+/* gdn_model.h:214 */
+void gdn_model_free(GDNModel *model);
+/* Like gdn_model_load but keeps non-BF16-exact payloads (FP32 contract).
+ * No reference counterpart: the reference rejects such files. */
+int gdn_model_load_fp32(GDNModel *model, const char *path);
+/* Write a .gdnw (export_gdn_c.py:169-210 byte layout). */
+int gdn_model_save(const GDNModel *model, const char *path);
+/* Seeded synthetic model in .gdnw order: every tensor N(0, std) from
+ * gdn_synth_normal with stream = its .gdnw ordinal, norm weights = 1;
+ * BF16-rounded when bf16 != 0.  Replaces loading a checkpoint. */
+int gdn_model_synth(GDNModel *model, const GDNWeightHeader *config,
+                    uint64_t seed, float std, int bf16);
+/* gdn_model.h:174-175 */
+int gdn_validate_bf16_exact_weights(const float *weight_data,
+                                    const GDNWeightHeader *config);
+size_t gdn_total_weight_floats(const GDNWeightHeader *config);
+/* The GDN-1.3B header (vocab 32000, hidden 2048, 24 layers, 8x256 heads,
+ * intermediate 5632, conv 4, max_seq_len 2048, eps 1e-6f). */
+void gdn_default_config(GDNWeightHeader *config, uint32_t num_layers);
+
+/* ===== run state (device) ===== */
+
+/* gdn_model.h:216 -- allocate the device workspace, upload the weights in
+ * the engine's layout and zero the recurrent/conv state, for the REF
+ * contract.  Fails on max_tokens == 0 or > max_seq_len. */
+int gdn_run_state_init(GDNRunState *state, const GDNModel *model,
+                       uint32_t max_tokens);
+/* Same with an explicit contract (GDN_CONTRACT_*). */
+int gdn_run_state_init_contract(GDNRunState *state, const GDNModel *model,
+                                uint32_t max_tokens, int contract);
+/* gdn_model.h:217 */
+void gdn_run_state_free(GDNRunState *state);
+
+/* gdn_model.h:264 -- one teacher-forced decode step: embedding row of
+ * *token into workspace X, 24 layers against the persistent state, LM head
+ * into workspace LOGITS, argmax (as a float) into lane 0 of workspace
+ * X_NORM.  Returns -1 for a token outside [0, vocab). */
+int gdn_decode_step_host(const GDNModel *model, GDNRunState *state,
+                         const int32_t *token);
+/* Device results of the last step, copied to host memory. */
+int gdn_read_token(const GDNRunState *state, int32_t *token);
+int gdn_read_logits(const GDNRunState *state, float *logits, size_t count);
+int gdn_read_final_hidden(const GDNRunState *state, float *hidden,
+                          size_t count);
+
+/* Recurrent/conv state in the .gdnstate section layouts
+ * (gdn_eval.cpp:202-257): recurrent [L][H][K][V] FP32, conv tails
+ * [L][q,k,v][W-1 oldest..newest][hidden] FP32.  Loading replaces
+ * gdn_scatter_recurrent_state / gdn_pack_conv_tails_bf16 (gdn_model.h:
+ * 190-195); for the REF contract values must be BF16-exact. */
+int gdn_load_recurrent_state(GDNRunState *state, const float *recurrent,
+                             size_t floats);
+int gdn_load_conv_tails(GDNRunState *state, const float *conv_tails,
+                        size_t floats);
+int gdn_save_recurrent_state(const GDNRunState *state, float *recurrent,
+                             size_t floats);
+int gdn_save_conv_tails(const GDNRunState *state, float *conv_tails,
+                        size_t floats);
+/* load_gdnstate, gdn_eval.cpp:202-267: read a .gdnstate file into the run
+ * state; returns the header fields via the optional out pointers. */
+int gdn_load_gdnstate(GDNRunState *state, const GDNModel *model,
+                      const char *path, uint32_t *prompt_len,
+                      int32_t *seed_token);
+/* Write the current state as a .gdnstate file (export_gdn_state.py:
+ * 340-362 layout). */
+int gdn_save_gdnstate(const GDNRunState *state, const GDNModel *model,
+                      const char *path, const int32_t *prompt,
+                      uint32_t prompt_len, int32_t seed_token);
+
+/* Steady teacher-forced benchmark, host.cpp:2150-2256: tokens[i % n_tokens]
+ * is fed at step i for n_steps steps.  Per step: outer = host token in ->
+ * host token out (H2D of 4 bytes, graph launch, D2H of 4 bytes); inner =
+ * HIP events around the graph on the engine stream.  Any output pointer
+ * may be NULL. */
+int gdn_run_teacher_forced(GDNRunState *state, const int32_t *tokens,
+                           uint32_t n_tokens, uint32_t n_steps,
+                           int32_t *argmax_out, float *inner_ms,
+                           float *outer_ms);
+/* 0: launch kernels one by one; 1 (default): one captured hipGraph/step. */
+int gdn_set_graph_mode(GDNRunState *state, int use_graph);
+int gdn_get_contract(const GDNRunState *state);
+
+/* ===== reference host helpers ===== */
+
+/* gdn_model.h:267 -- the independent scalar LM head (host, CPU). */
+void gdn_compute_logits(const GDNModel *model, const float *hidden,
+                        float *logits_out);
+/* gdn_model.h:200 -- native BF16 product (host model of the contract). */
+float gdn_native_bf16_mul_to_fp32(uint16_t weight, uint16_t activation);
+/* gdn_model.h:205-206 */
+uint16_t gdn_test_fp32_to_bf16_rne_bits(uint32_t bits);
+uint32_t gdn_test_bf16_to_fp32_bits(uint16_t bits);
+
+/* ===== seeded synthetic inputs ===== */
+
+/* Counter-based N(mean, std) draws: element i of (seed, stream) is the
+ * Box-Muller pair (2*(i/2), +1) of SplitMix64 outputs; deterministic for
+ * any thread count.  round_bf16 RNE-rounds every value to BF16. */
+void gdn_synth_normal(float *out, size_t n, uint64_t seed, uint64_t stream,
+                      float mean, float std, int round_bf16);
+/* U[lo, hi) draws on the same counter scheme. */
+void gdn_synth_uniform(float *out, size_t n, uint64_t seed, uint64_t stream,
+                       float lo, float hi);
+/* Uniform token ids in [0, vocab). */
+void gdn_synth_tokens(int32_t *out, size_t n, uint64_t seed, uint64_t stream,
+                      uint32_t vocab);
+
+/* ===== isolated kernels on host buffers (test hooks, like the reference's
+ *       gdn_test_* family; each copies in, runs the engine's kernel, copies
+ *       out) ===== */
+
+/* Dense GEMV row results before any rounding point: y[M] (FP32) of W[M][K]
+ * and x[K] under the contract's product rule.  K in {2048, 5632}. */
+int gdn_test_gemv(int contract, const float *W, const float *x, uint32_t M,
+                  uint32_t K, float *y);
+/* n_steps of the gated delta-rule kernel on n_heads independent heads.
+ * q,k,v [steps][heads][256] (pre-L2-norm conv outputs), a,b,a_log,dt_bias
+ * [steps][heads]; S [heads][256][256] FP32 words in/out (BF16-exact for
+ * REF); o [steps][heads][256]. */
+int gdn_test_recurrence(int contract, uint32_t n_heads, uint32_t n_steps,
+                        const float *q, const float *k, const float *v,
+                        const float *a, const float *b, const float *a_log,
+                        const float *dt_bias, float *S, float *o);
+/* Layer `layer` of the run state's model for n_steps teacher-forced residual
+ * inputs x_in[step][H] (BF16-exact for the BF16 contracts): the same kernels
+ * a decode step runs for that layer, against the run state's persistent
+ * recurrent/conv state.  x_out[step][H] receives the layer's residual
+ * output. */
+int gdn_test_layer(GDNRunState *state, uint32_t layer, uint32_t n_steps,
+                   const float *x_in, float *x_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
