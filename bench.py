@@ -1,0 +1,207 @@
+#!/usr/bin/env python3
+"""Batch-1 GatedDeltaNet-1.3B decode on one MI355X.
+
+Workload: the 24-layer GDN-1.3B (hidden 2048, 8 heads x 256, MLP 5632,
+vocab 32000, untied LM head), random-init BF16 weights N(0, 0.02) with norm
+weights = 1 (seed 0), in the bf16 arm (BF16 weights and operator boundaries,
+FP32 recurrent state).  A uniform-random prompt of --warmup tokens builds the
+state step by step (untimed); then --steps teacher-forced steps run over a
+fixed uniform-random 4096-token stream consumed cyclically.
+
+One step = token id in on the host -> one captured hipGraph of 122 kernels
+-> argmax token id back on the host (the reference's "outer" boundary,
+host.cpp:945-1047).  `value` is the mean outer ms/token over the timed steps
+(wall clock of the whole loop / steps); `inner_ms_median` is HIP events
+around the graph.  Achieved GB/s uses the algorithmic bytes per token
+(weights + aux + state read/write + conv tails + embedding row + logits).
+
+`roofline` is the dominant kernel kind (largest share of per-token kernel
+time): its algorithmic bytes per launch over its average launch duration,
+measured here with HIP events on the engine stream over every layer's
+weights.  `cpu_baseline` times the CPU oracle (a port of the reference's
+native decode arithmetic, glibc transcendentals) on this host's cores for a
+few tokens of the same workload, starting from the GPU's post-prompt state.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "ms/token batch-1 GDN-1.3B decode (outer); achieved HBM GB/s vs peak"
+PEAK_HBM_GBPS = 8000.0
+FPGA_OUTER_MS = 8.233  # U55C FPGA outer ms/token (architecture.md:1215)
+
+H, I, V, L = 2048, 5632, 32000, 24
+# Algorithmic bytes per token (the figures of the hot-path scope table):
+DENSE = 2_798_649_344        # 1,399,324,672 BF16 GEMV weights (24 layers + LM head)
+AUX = 2_967_040              # norms, a/b rows, conv taps (BF16), a_log/dt_bias (FP32)
+STATE_F32 = 100_663_296      # 24 x 8 x 256 x 256 FP32 state, read + write
+CONV_BF16 = 1_769_472        # 24 x 3 x 3 x 2048 BF16 conv tails, read + write
+EMB_ROW = 4_096              # one BF16 embedding row
+LOGITS = 128_000             # FP32 logits written
+BYTES_PER_TOKEN = {
+    "bf16w_fp32s": DENSE + AUX + STATE_F32 + CONV_BF16 + EMB_ROW + LOGITS,   # 2,904,181,248
+    "ref": DENSE + AUX + STATE_F32 // 2 + CONV_BF16 + EMB_ROW + LOGITS,      # 2,853,853,696
+    "fp32": 5_707_569_664,   # FP32 weights, state, tails and row
+}
+# Algorithmic bytes per launch of each kernel kind (bf16 arm): weights at
+# BF16 plus the state / conv-tail traffic the kernel must move.
+KERNEL_BYTES = {
+    "qkvg": 4 * H * H * 2 + 2 * 8 * H * 2 + 3 * H * 4 * 2 + 3 * 3 * H * 2 * 2 + 2 * H * 2,
+    "recur": 8 * 256 * 256 * 4 * 2,
+    "o_proj": H * H * 2 + 256 * 2,
+    "gate_up": 2 * I * H * 2 + H * 2,
+    "down": H * I * 2,
+    "lm_head": V * H * 2 + H * 2 + V * 4,
+    "argmax": (V // 8) * 8,
+}
+LAUNCHES_PER_TOKEN = {"qkvg": L, "recur": L, "o_proj": L, "gate_up": L, "down": L, "lm_head": 1, "argmax": 1}
+
+
+def sync():
+    try:
+        import torch
+        if torch.cuda.is_available():
+            torch.cuda.synchronize()
+    except Exception:
+        pass
+
+
+def cpu_baseline(model, contract_id, state, conv, tokens, threads, single_tokens):
+    from oracle import oracle as O
+    hdr = O.header_from(model.config)
+    blob = model.blob
+    st = state.copy()
+    cv = conv.copy()
+    O.set_threads(threads)
+    O.decode_step(contract_id, hdr, blob, st, cv, int(tokens[0]), O.LIBM)  # warm caches
+    t0 = time.perf_counter()
+    n = 0
+    for tok in tokens[1:]:
+        O.decode_step(contract_id, hdr, blob, st, cv, int(tok), O.LIBM)
+        n += 1
+    ms = (time.perf_counter() - t0) * 1000.0 / max(n, 1)
+    single = None
+    if single_tokens > 0:
+        O.set_threads(1)
+        t0 = time.perf_counter()
+        for tok in tokens[:single_tokens]:
+            O.decode_step(contract_id, hdr, blob, st, cv, int(tok), O.LIBM)
+        single = (time.perf_counter() - t0) * 1000.0 / single_tokens
+        O.set_threads(threads)
+    return ms, n, single
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=4096, help="timed teacher-forced tokens")
+    ap.add_argument("--warmup", type=int, default=4096, help="untimed prompt tokens")
+    ap.add_argument("--contract", default="bf16w_fp32s", choices=sorted(BYTES_PER_TOKEN))
+    ap.add_argument("--profile-rounds", type=int, default=4)
+    ap.add_argument("--cpu-tokens", type=int, default=6, help="oracle tokens timed on all cores (0: skip)")
+    ap.add_argument("--cpu-single-tokens", type=int, default=1, help="oracle tokens timed on one core")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build is a single-GPU decode engine; run with --gpus 1 "
+              "(no multi-GPU figure is produced)", file=sys.stderr)
+        sys.exit(2)
+
+    import gateddeltanet_amd as g
+    contract = {"ref": g.CONTRACT_REF, "bf16w_fp32s": g.CONTRACT_BF16W_FP32S, "fp32": g.CONTRACT_FP32}[args.contract]
+    t_setup = time.perf_counter()
+    model = g.Model.synth(num_layers=L, seed=0, std=0.02, bf16=(contract != g.CONTRACT_FP32))
+    rs = g.RunState(model, contract)
+    prompt = g.synth_tokens(max(args.warmup, 1), 0, 1, V)
+    stream = g.synth_tokens(4096, 0, 2, V)
+    if args.warmup > 0:
+        rs.teacher_forced(prompt, args.warmup, timing=False)
+    post_prompt = rs.save_state()
+    setup_s = time.perf_counter() - t_setup
+
+    sync()
+    t0 = time.perf_counter()
+    argmax, inner, outer = rs.teacher_forced(stream, args.steps)
+    sync()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1000.0 / args.steps
+
+    prof = rs.profile_kernels(args.profile_rounds)
+    per_token = {k: prof[k] * LAUNCHES_PER_TOKEN[k] for k in prof}
+    dom = max(per_token, key=per_token.get)
+    kb = KERNEL_BYTES[dom] * (2 if contract == g.CONTRACT_FP32 and dom not in ("recur", "argmax") else 1)
+    achieved_k = kb / (prof[dom] * 1e-6) / 1e9
+    inner_med = float(np.median(inner))
+    bytes_tok = BYTES_PER_TOKEN[args.contract]
+    achieved = bytes_tok / (inner_med * 1e-3) / 1e9
+    achieved_outer = bytes_tok / (ms_per_step * 1e-3) / 1e9
+
+    cpu = None
+    if args.cpu_tokens > 0:
+        threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+        ms_cpu, n_cpu, single = cpu_baseline(model, contract, post_prompt[0], post_prompt[1],
+                                             stream[:args.cpu_tokens + 1], threads, args.cpu_single_tokens)
+        cpu = {"value": round(ms_cpu, 3), "unit": "ms/token", "cores": threads, "kind": "port",
+               "sample": f"{n_cpu} teacher-forced tokens of the same 24-layer model from the GPU's post-prompt "
+                         f"state, CPU oracle (gdn_model.cpp arithmetic, glibc expf/log1pf, OpenMP rows), "
+                         f"{threads} threads",
+               "single_thread_ms_per_token": None if single is None else round(single, 3)}
+
+    out = {
+        "metric": METRIC,
+        "value": round(ms_per_step, 5),
+        "unit": "ms/token",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": round(ms_per_step / FPGA_OUTER_MS, 5),
+        "dtype": "bf16" if contract != g.CONTRACT_FP32 else "fp32",
+        "data": "synthetic (seeded random-init weights, uniform random token streams)",
+        "config": {
+            "workload": "BASELINE config 3: GatedDeltaNet-1.3B decode, 24 layers, batch 1, "
+                        f"{args.warmup}-token uniform prompt then {args.steps} teacher-forced steps over a "
+                        "fixed 4096-token uniform stream (cyclic), greedy argmax",
+            "contract": args.contract,
+            "state_dtype": "bf16" if contract == g.CONTRACT_REF else "fp32",
+            "launch": "one hipGraph per token (122 kernels)",
+        },
+        "outer_ms_median": round(float(np.median(outer)), 5),
+        "inner_ms_median": round(inner_med, 5),
+        "inner_ms_p90": round(float(np.percentile(inner, 90)), 5),
+        "bytes_per_token": bytes_tok,
+        "achieved_GBps_inner": round(achieved, 1),
+        "achieved_GBps_outer": round(achieved_outer, 1),
+        "hbm_frac_inner": round(achieved / PEAK_HBM_GBPS, 4),
+        "kernel_us_per_launch": {k: round(v, 3) for k, v in prof.items()},
+        "kernel_us_per_token": {k: round(v, 2) for k, v in per_token.items()},
+        "roofline": {
+            "kernel": dom,
+            "bound": "hbm",
+            "achieved": round(achieved_k, 1),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved_k / PEAK_HBM_GBPS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_launch": kb,
+            "avg_launch_us": round(prof[dom], 3),
+        },
+        "cpu_baseline": cpu,
+        "setup_s": round(setup_s, 1),
+        "vs_baseline_note": "value / 8.233 ms (U55C FPGA outer ms/token, real checkpoint, same arithmetic volume)",
+    }
+    rs.free()
+    model.free()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

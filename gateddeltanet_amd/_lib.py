@@ -121,6 +121,7 @@ SIGNATURES = {
                                   c_uint32, c_int32]),
     "gdn_run_teacher_forced": (c_int, [POINTER(GDNRunState), IP, c_uint32, c_uint32, IP, FP, FP]),
     "gdn_set_graph_mode": (c_int, [POINTER(GDNRunState), c_int]),
+    "gdn_profile_kernels": (c_int, [POINTER(GDNRunState), c_uint32, FP, c_uint32]),
     "gdn_get_contract": (c_int, [POINTER(GDNRunState)]),
     "gdn_compute_logits": (None, [POINTER(GDNModel), FP, FP]),
     "gdn_native_bf16_mul_to_fp32": (c_float, [c_uint16, c_uint16]),

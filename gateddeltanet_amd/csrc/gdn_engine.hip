@@ -198,21 +198,23 @@ __device__ __forceinline__ void lds_load16(const float *src, float *v) {
     }
 }
 
-__device__ __forceinline__ float coherent_load(const float *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // ------------------------------------------------------------------ GEMV core
 //
-// A workgroup owns RB consecutive rows of the device matrix (stored
-// row-major, so the block is one contiguous stream).  Work item f is one
-// 16-column half-beat of one row: row f / (K/16), half-beat f % (K/16), at
-// element offset 16 f of the block -- consecutive threads read consecutive
-// 32-byte (BF16) or 64-byte (FP32) pieces.  Each item's 16 products are
-// reduced in-lane with tree16 into LDS; then lanes 0..4RB-1 of wave 0 each
-// run one of the reference's four bank chains (lower/upper half x even/odd
-// beat, beat order, from +0.0f) and two XOR shuffles form
+// A workgroup owns RB consecutive rows of the device matrix (row-major, so
+// the block is one contiguous stream).  Work item f is one 16-column
+// half-beat of one row: row f / (K/16), half-beat f % (K/16), at element
+// offset 16 f of the block -- consecutive threads read consecutive 32-byte
+// (BF16) or 64-byte (FP32) pieces.  Each item's 16 products are reduced
+// in-lane with tree16 into LDS; then lanes 0..4RB-1 of wave 0 each run one
+// of the reference's four bank chains (lower/upper half x even/odd beat, in
+// beat order from +0.0f) and two XOR shuffles form
 // (even_lo + even_hi) + (odd_lo + odd_hi).
+//
+// Every kernel issues its weight loads before any activation-dependent
+// work: the activation prologue (residual add, RMSNorm, output norm * gate)
+// runs while the weight stream is in flight, and s_barrier does not wait
+// on outstanding global loads.
 
 template <int K>
 struct Hb {
@@ -221,117 +223,64 @@ struct Hb {
     static constexpr int NB = K / 32;     // 32-column beats per row
 };
 
-// Copy x into LDS and decide whether the fast product path is exact for
-// this call: BF16 contracts only; all activations finite and normal (or
-// zero), weights finite, and min|x| * min|w| >= 2^-125.
-template <int C>
-__device__ bool stage_x(const float *__restrict__ x, int K, float *xs, WInfo wi, float *red,
-                        int *redi) {
-    int bad = 0;
-    float mn = INFINITY;
-    for (int i = threadIdx.x; i < K; i += kT) {
-        const float v = x[i];
-        xs[i] = v;
-        if constexpr (C != kFp32) {
-            const uint32_t m = f2u(v) & 0x7fffffffu;
-            if (m >= 0x7f800000u || (m != 0u && m < 0x00800000u)) bad = 1;
-            else if (m != 0u) mn = fminf(mn, u2f(m));
-        }
-    }
-    if constexpr (C == kFp32) {
-        __syncthreads();
-        return false;
-    } else {
-#pragma unroll
-        for (int m = 1; m < 64; m <<= 1) mn = fminf(mn, __shfl_xor(mn, m));
-        const int wbad = __any(bad) ? 1 : 0;
-        const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-        if (lane == 0) {
-            red[w] = mn;
-            redi[w] = wbad;
-        }
-        __syncthreads();
-        const float gm = fminf(fminf(red[0], red[1]), fminf(red[2], red[3]));
-        const int gb = redi[0] | redi[1] | redi[2] | redi[3];
-        if (gb || wi.nonfinite) return false;
-        if (gm == INFINITY || wi.min_abs == INFINITY) return true;
-        return (double)gm * (double)wi.min_abs >= 0x1p-125;
-    }
-}
+template <int K, int RB, int C>
+struct WRegs {
+    static constexpr int HB = Hb<K>::HB, HBP = Hb<K>::HBP;
+    static constexpr int ITEMS = RB * HB;
+    static constexpr int NIT = (ITEMS + kT - 1) / kT;
+    static constexpr bool kFull = (ITEMS % kT) == 0;
+    static constexpr int WPI = (C == kFp32) ? 4 : 2;  // 16-byte loads per item
+    u32x4 v[NIT][WPI];
 
-template <int K, int RB, int C, bool FAST>
-__device__ __forceinline__ void gemv_partials(const void *__restrict__ wblk, const float *xs,
-                                              float *part) {
-    constexpr int HB = Hb<K>::HB, HBP = Hb<K>::HBP;
-    constexpr int ITEMS = RB * HB;
-    constexpr int NIT = (ITEMS + kT - 1) / kT;
-    constexpr bool kFull = (ITEMS % kT) == 0;
-    const int t = threadIdx.x;
-    const u32x4 *W = reinterpret_cast<const u32x4 *>(wblk);
-    if constexpr (C != kFp32) {
-        u32x4 wv[NIT][2];
+    __device__ __forceinline__ void load(const void *__restrict__ W, int rb) {
+        constexpr size_t esz = (C == kFp32) ? 4 : 2;
+        const u32x4 *wb = reinterpret_cast<const u32x4 *>(reinterpret_cast<const char *>(W) +
+                                                           (size_t)rb * RB * K * esz);
 #pragma unroll
         for (int i = 0; i < NIT; ++i) {
-            const int f = t + kT * i;
+            const int f = threadIdx.x + kT * i;
             if (kFull || f < ITEMS) {
-                wv[i][0] = __builtin_nontemporal_load(W + 2 * f);
-                wv[i][1] = __builtin_nontemporal_load(W + 2 * f + 1);
+#pragma unroll
+                for (int q = 0; q < WPI; ++q) v[i][q] = __builtin_nontemporal_load(wb + WPI * f + q);
             }
         }
+    }
+
+    template <bool FAST>
+    __device__ __forceinline__ void compute(const float *xs, float *part) const {
 #pragma unroll
         for (int i = 0; i < NIT; ++i) {
-            const int f = t + kT * i;
+            const int f = threadIdx.x + kT * i;
             if (kFull || f < ITEMS) {
                 const int row = f / HB, hb = f - row * HB;
                 float xv[16], p[16];
                 lds_load16(xs + hb * 16, xv);
-                const uint32_t w8[8] = {wv[i][0].x, wv[i][0].y, wv[i][0].z, wv[i][0].w,
-                                        wv[i][1].x, wv[i][1].y, wv[i][1].z, wv[i][1].w};
+                if constexpr (C == kFp32) {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    if constexpr (FAST) {
-                        native_pair_fast(w8[e], xv[2 * e], xv[2 * e + 1], p[2 * e], p[2 * e + 1]);
-                    } else {
-                        p[2 * e] = native_exact(w8[e] & 0xffffu, xv[2 * e]);
-                        p[2 * e + 1] = native_exact(w8[e] >> 16, xv[2 * e + 1]);
+                    for (int q = 0; q < 4; ++q) {
+                        p[4 * q + 0] = u2f(v[i][q].x) * xv[4 * q + 0];
+                        p[4 * q + 1] = u2f(v[i][q].y) * xv[4 * q + 1];
+                        p[4 * q + 2] = u2f(v[i][q].z) * xv[4 * q + 2];
+                        p[4 * q + 3] = u2f(v[i][q].w) * xv[4 * q + 3];
+                    }
+                } else {
+                    const uint32_t w8[8] = {v[i][0].x, v[i][0].y, v[i][0].z, v[i][0].w,
+                                            v[i][1].x, v[i][1].y, v[i][1].z, v[i][1].w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        if constexpr (FAST) {
+                            native_pair_fast(w8[e], xv[2 * e], xv[2 * e + 1], p[2 * e], p[2 * e + 1]);
+                        } else {
+                            p[2 * e] = native_exact(w8[e] & 0xffffu, xv[2 * e]);
+                            p[2 * e + 1] = native_exact(w8[e] >> 16, xv[2 * e + 1]);
+                        }
                     }
                 }
                 part[row * HBP + hb] = tree16(p);
             }
         }
-    } else {
-        constexpr int BATCH = 4;
-#pragma unroll
-        for (int i0 = 0; i0 < NIT; i0 += BATCH) {
-            u32x4 wv[BATCH][4];
-#pragma unroll
-            for (int b = 0; b < BATCH; ++b) {
-                const int i = i0 + b, f = t + kT * i;
-                if (i < NIT && (kFull || f < ITEMS)) {
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) wv[b][q] = __builtin_nontemporal_load(W + 4 * f + q);
-                }
-            }
-#pragma unroll
-            for (int b = 0; b < BATCH; ++b) {
-                const int i = i0 + b, f = t + kT * i;
-                if (i < NIT && (kFull || f < ITEMS)) {
-                    const int row = f / HB, hb = f - row * HB;
-                    float xv[16], p[16];
-                    lds_load16(xs + hb * 16, xv);
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        p[4 * q + 0] = u2f(wv[b][q].x) * xv[4 * q + 0];
-                        p[4 * q + 1] = u2f(wv[b][q].y) * xv[4 * q + 1];
-                        p[4 * q + 2] = u2f(wv[b][q].z) * xv[4 * q + 2];
-                        p[4 * q + 3] = u2f(wv[b][q].w) * xv[4 * q + 3];
-                    }
-                    part[row * HBP + hb] = tree16(p);
-                }
-            }
-        }
     }
-}
+};
 
 // Wave 0 only.  Lane 4r ends with row r's result.
 template <int K, int RB>
@@ -350,104 +299,123 @@ __device__ __forceinline__ float gemv_chain(const float *part) {
     return s + __shfl_xor(s, 2);
 }
 
-template <int K, int RB, int C>
-__device__ __forceinline__ float gemv_block(const void *__restrict__ W, const float *__restrict__ x,
-                                            WInfo wi, float *xs, float *part, float *red,
-                                            int *redi) {
-    const bool fast = stage_x<C>(x, K, xs, wi, red, redi);
-    constexpr size_t esz = (C == kFp32) ? 4 : 2;
-    const char *wblk = reinterpret_cast<const char *>(W) + (size_t)blockIdx.x * RB * K * esz;
-    if (fast) gemv_partials<K, RB, C, true>(wblk, xs, part);
-    else gemv_partials<K, RB, C, false>(wblk, xs, part);
-    __syncthreads();
-    float y = 0.0f;
-    if (threadIdx.x < 64) y = gemv_chain<K, RB>(part);
-    return y;
+// ---------------------------------------------------------------- prologues
+
+enum { PRO_PLAIN = 0, PRO_RESNORM = 1, PRO_EMBED = 2, PRO_ONORM = 3 };
+
+// Where a GEMV's input vector comes from.
+//   PRO_PLAIN    x = a[0..K)
+//   PRO_RESNORM  r = b ? R(a + b) : a (the residual add, gdn_bf16_add_half),
+//                x = RMSNorm(r) * w (gdn_rmsnorm_rows_bf16 order)
+//   PRO_EMBED    r = R(row tok[0] of emb), x = RMSNorm(r) * w
+//   PRO_ONORM    x = per-head RMSNorm(a) * w * b * c with b the gate and c
+//                its sigmoid (gdn_output_norm_and_gate)
+// Block 0 also stores r in res_out and, for PRO_RESNORM, x in aux_out (the
+// final hidden vector before the LM head); for PRO_EMBED aux_out receives
+// the FP32 embedding row (workspace X).
+struct XSrc {
+    const float *a, *b, *c;
+    const void *emb;
+    const int *tok;
+    const float *w;
+    float *res_out;
+    float *aux_out;
+    int vocab;
+    float eps;
+};
+
+// Fast-path decision for one thread's final inputs: finite, normal or zero.
+struct XFlags {
+    int bad = 0;
+    float mn = INFINITY;
+    __device__ __forceinline__ void add(float v) {
+        const uint32_t m = f2u(v) & 0x7fffffffu;
+        if (m >= 0x7f800000u || (m != 0u && m < 0x00800000u)) bad = 1;
+        else if (m != 0u) mn = fminf(mn, u2f(m));
+    }
+};
+
+// Block-wide fast-path verdict (BF16 contracts): every input finite and
+// normal or zero, every weight finite, and min|x| * min|w| >= 2^-125 so no
+// product can reach the flush threshold.  Ends with a barrier.
+template <int C>
+__device__ __forceinline__ bool fast_verdict(XFlags fl, WInfo wi, float *red, int *redi) {
+    if constexpr (C == kFp32) {
+        __syncthreads();
+        return false;
+    } else {
+        float mn = fl.mn;
+#pragma unroll
+        for (int m = 1; m < 64; m <<= 1) mn = fminf(mn, __shfl_xor(mn, m));
+        const int wbad = __any(fl.bad) ? 1 : 0;
+        const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+        if (lane == 0) {
+            red[w] = mn;
+            redi[w] = wbad;
+        }
+        __syncthreads();
+        const float gm = fminf(fminf(red[0], red[1]), fminf(red[2], red[3]));
+        const int gb = redi[0] | redi[1] | redi[2] | redi[3];
+        if (gb || wi.nonfinite) return false;
+        if (gm == INFINITY || wi.min_abs == INFINITY) return true;
+        return (double)gm * (double)wi.min_abs >= 0x1p-125;
+    }
 }
 
-// Sum of squares of 2048 LDS values in the norm order (16-value chunks summed
-// sequentially, chunk sums added sequentially), then
-// out = R((x * scale) * w) with scale = 1/sqrtf(sum/2048 + eps)
-// (gdn_rmsnorm_rows_bf16 / gdn_residual_rmsnorm_bf16).
-template <int C>
-__device__ void block_rmsnorm_h(const float *xl, const float *__restrict__ w, float *__restrict__ out,
-                                float eps, float *scratch) {
+// Sum of squares of the hidden vector in LDS in the norm order: 16-value
+// chunks summed sequentially, chunk sums added sequentially.
+__device__ __forceinline__ float hidden_sumsq(const float *xs, float *scratch) {
     const int t = threadIdx.x;
     if (t < kH / 16) {
         float s = 0.0f;
 #pragma unroll
         for (int kk = 0; kk < 16; ++kk) {
-            const float v = xl[16 * t + kk];
+            const float v = xs[16 * t + kk];
             s += v * v;
         }
         scratch[t] = s;
     }
     __syncthreads();
     float sum = 0.0f;
+#pragma unroll 16
     for (int i = 0; i < kH / 16; ++i) sum += scratch[i];
-    const float scale = 1.0f / __builtin_sqrtf(sum / (float)kH + eps);
-    for (int i = t; i < kH; i += kT) out[i] = R<C>(xl[i] * scale * w[i]);
+    return sum;
 }
 
-// Arrival counter for "last workgroup finishes the step".  Call after the
-// block's global results are stored.  Returns true in exactly one block.
-__device__ __forceinline__ bool last_block_arrives(unsigned *cnt, unsigned total, int *flag) {
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const unsigned ticket = atomicAdd(cnt, 1u);
-        *flag = (ticket == total - 1u) ? 1 : 0;
-        if (*flag) *cnt = 0u;  // ready for the next launch
-    }
-    __syncthreads();
-    if (*flag) __threadfence();
-    return *flag != 0;
+// ---------------------------------------------------------------- epilogues
+
+enum { EPI_RAW = 0, EPI_STORE = 1, EPI_QKVG = 2, EPI_SWIGLU = 3, EPI_LM = 4 };
+
+struct Epi {
+    float *y;          // RAW/STORE/SWIGLU/LM: results; QKVG: conv outputs q,k,v
+    float *y2;         // QKVG: gate
+    float *y3;         // QKVG: sigmoid(gate)
+    const float *aux;  // QKVG: the layer's small weights
+    float *tails;      // QKVG: the layer's conv tails (3 stripes)
+    float *ab;         // QKVG: a[8], b[8]
+    float *bd;         // QKVG: (beta, decay) per head
+    float *part_val;   // LM: per-block argmax
+    int *part_idx;
+};
+
+// beta = sigmoid(b); decay = expf(-expf(a_log) * softplus(a + dt_bias))
+// (gdn_island_prep, gdn_model.cpp:2461-2465).
+__device__ __forceinline__ void head_scalars(float a, float b, float a_log, float dt_bias,
+                                             float &beta, float &decay) {
+    beta = sigmoid_ref(b);
+    const float decay_in = a + dt_bias;
+    const float decay_val = -exp_cr(a_log) * softplus_ref(decay_in);
+    decay = exp_cr(decay_val);
 }
 
-// -------------------------------------------------------------------- kernels
-
-// Embedding row (or a given residual row) -> residual stream -> RMSNorm.
+// The tiny a/b projections (16 rows: a 0..7, b 8..15) with FP32 products
+// and acc = (acc + tree16(lo)) + tree16(hi) per beat (gdn_gemv_tiny_ab),
+// then the per-head scalars.
 template <int C>
-__global__ __launch_bounds__(kT) void k_embed(const int *__restrict__ tok_in, int vocab,
-                                              const void *__restrict__ emb,
-                                              const float *__restrict__ resid_in,
-                                              float *__restrict__ ws_x, float *__restrict__ resid,
-                                              const float *__restrict__ norm_w,
-                                              float *__restrict__ xn, float eps) {
-    __shared__ __attribute__((aligned(16))) float xl[kH];
-    __shared__ float scratch[kH / 16];
-    if (resid_in == nullptr) {
-        int tok = tok_in[0];
-        if (tok < 0 || tok >= vocab) tok = 0;  // the host rejects these first
-        for (int i = threadIdx.x; i < kH; i += kT) {
-            float e;
-            if constexpr (C == kFp32) {
-                e = reinterpret_cast<const float *>(emb)[(size_t)tok * kH + i];
-            } else {
-                e = bf16_bits_to_f32(reinterpret_cast<const uint16_t *>(emb)[(size_t)tok * kH + i]);
-            }
-            ws_x[i] = e;
-            const float r = R<C>(e);
-            resid[i] = r;
-            xl[i] = r;
-        }
-    } else {
-        for (int i = threadIdx.x; i < kH; i += kT) {
-            const float r = resid_in[i];
-            resid[i] = r;
-            xl[i] = r;
-        }
-    }
-    __syncthreads();
-    block_rmsnorm_h<C>(xl, norm_w, xn, eps, scratch);
-}
-
-// The tiny a/b projections: 16 rows (a 0..7, b 8..15) of FP32 products,
-// acc = (acc + tree16(lo)) + tree16(hi) per beat (gdn_gemv_tiny_ab).
-template <int C>
-__device__ void ab_block(const float *__restrict__ abw, const float *xs, float *part,
-                         float *__restrict__ ab) {
+__device__ void ab_block(const float *__restrict__ aux, const float *xs, float *part, float *lds16,
+                         float *__restrict__ ab, float *__restrict__ bd) {
     constexpr int HB = Hb<kH>::HB, HBP = Hb<kH>::HBP;
+    const float *abw = aux + kAuxAB;
 #pragma unroll
     for (int i = 0; i < (16 * HB) / kT; ++i) {
         const int f = threadIdx.x + kT * i;
@@ -469,37 +437,174 @@ __device__ void ab_block(const float *__restrict__ abw, const float *xs, float *
         const float *pr = part + threadIdx.x * HBP;
         float acc = 0.0f;
         for (int j = 0; j < HB / 2; ++j) acc = (acc + pr[2 * j]) + pr[2 * j + 1];
-        ab[threadIdx.x] = R<C>(acc);
+        const float r = R<C>(acc);
+        ab[threadIdx.x] = r;
+        lds16[threadIdx.x] = r;
+    }
+    __syncthreads();
+    if (threadIdx.x < kNH) {
+        const int hh = threadIdx.x;
+        float beta, decay;
+        head_scalars(lds16[hh], lds16[kNH + hh], aux[kAuxALog + hh], aux[kAuxDtBias + hh], beta,
+                     decay);
+        bd[2 * hh] = beta;
+        bd[2 * hh + 1] = decay;
     }
 }
 
-// q/k/v/g projection + conv/SiLU + conv-tail shift; last block: a/b.
-template <int C, int RB>
-__global__ __launch_bounds__(kT) void k_qkvg(const void *__restrict__ W, const float *__restrict__ x,
-                                             WInfo wi, const float *__restrict__ aux,
-                                             float *__restrict__ tails, float *__restrict__ qkv,
-                                             float *__restrict__ gate, float *__restrict__ ab) {
-    __shared__ __attribute__((aligned(16))) float xs[kH];
-    __shared__ __attribute__((aligned(16))) float part[16 * Hb<kH>::HBP];
+// ------------------------------------------------------------ the GEMV kernel
+
+template <int C, int K, int RB, int PRO, int EPI>
+__global__ __launch_bounds__(kT) void k_gemv(const void *__restrict__ W, WInfo wi, XSrc src,
+                                             Epi ep) {
+    constexpr int HBP = Hb<K>::HBP;
+    constexpr int PART = (EPI == EPI_QKVG ? 16 : RB) * HBP;
+    constexpr int PER = K / kT;  // input values per thread
+    static_assert(K % kT == 0, "K splits evenly over the workgroup");
+    static_assert(PRO == PRO_PLAIN || K == kH, "normalised inputs are hidden-sized");
+    __shared__ __attribute__((aligned(16))) float xs[K];
+    __shared__ __attribute__((aligned(16))) float part[PART];
+    __shared__ float scratch[kH / 16];
     __shared__ float red[4];
     __shared__ int redi[4];
-    constexpr int nmain = 4 * kH / RB;
-    if (blockIdx.x == nmain) {
-        (void)stage_x<C>(x, kH, xs, wi, red, redi);
-        ab_block<C>(aux + kAuxAB, xs, part, ab);
-        return;
+    const int t = threadIdx.x;
+    // QKVG: block 0 is the a/b block (dispatched first: its serial tail is
+    // the longest), blocks 1.. own the projection rows.
+    const bool ab_blk = (EPI == EPI_QKVG) && blockIdx.x == 0;
+    const int rb = (EPI == EPI_QKVG) ? (int)blockIdx.x - 1 : (int)blockIdx.x;
+
+    // 1. activation loads (issued before the weight stream)
+    float va[PER], vb[PER], vc[PER], vw[PER];
+    int tok = 0;
+    if constexpr (PRO == PRO_PLAIN) {
+#pragma unroll
+        for (int m = 0; m < PER; ++m) va[m] = src.a[t + kT * m];
+    } else if constexpr (PRO == PRO_RESNORM) {
+#pragma unroll
+        for (int m = 0; m < PER; ++m) {
+            va[m] = src.a[t + kT * m];
+            vb[m] = src.b ? src.b[t + kT * m] : 0.0f;
+            vw[m] = src.w[t + kT * m];
+        }
+    } else if constexpr (PRO == PRO_EMBED) {
+        tok = src.tok[0];
+        if (tok < 0 || tok >= src.vocab) tok = 0;  // the host rejects these first
+#pragma unroll
+        for (int m = 0; m < PER; ++m) {
+            const size_t ix = (size_t)tok * kH + t + kT * m;
+            if constexpr (C == kFp32) va[m] = reinterpret_cast<const float *>(src.emb)[ix];
+            else va[m] = bf16_bits_to_f32(reinterpret_cast<const uint16_t *>(src.emb)[ix]);
+            vw[m] = src.w[t + kT * m];
+        }
+    } else {
+#pragma unroll
+        for (int m = 0; m < PER; ++m) {
+            va[m] = src.a[t + kT * m];
+            vb[m] = src.b[t + kT * m];
+            vc[m] = src.c[t + kT * m];
+        }
+        vw[0] = src.w[t];
     }
-    const float y = gemv_block<kH, RB, C>(W, x, wi, xs, part, red, redi);
-    const int lane = threadIdx.x;
-    if (lane < 64 && (lane & 3) == 0 && (lane >> 2) < RB) {
-        const int r = blockIdx.x * RB + (lane >> 2);
+
+    // 2. the weight stream
+    WRegs<K, RB, C> w;
+    if (!ab_blk) w.load(W, rb);
+
+    // 3. the prologue proper: the GEMV input lands in LDS
+    XFlags fl;
+    if constexpr (PRO == PRO_PLAIN) {
+#pragma unroll
+        for (int m = 0; m < PER; ++m) {
+            xs[t + kT * m] = va[m];
+            fl.add(va[m]);
+        }
+    } else if constexpr (PRO == PRO_RESNORM || PRO == PRO_EMBED) {
+        const bool blk0 = blockIdx.x == 0;
+#pragma unroll
+        for (int m = 0; m < PER; ++m) {
+            float r;
+            if constexpr (PRO == PRO_EMBED) {
+                r = R<C>(va[m]);
+                if (blk0 && src.aux_out) src.aux_out[t + kT * m] = va[m];
+            } else {
+                r = src.b ? R<C>(va[m] + vb[m]) : va[m];
+            }
+            va[m] = r;
+            xs[t + kT * m] = r;
+            if (blk0 && src.res_out) src.res_out[t + kT * m] = r;
+        }
+        __syncthreads();
+        const float sum = hidden_sumsq(xs, scratch);
+        const float scale = 1.0f / __builtin_sqrtf(sum / (float)kH + src.eps);
+#pragma unroll
+        for (int m = 0; m < PER; ++m) {
+            const float xn = R<C>(va[m] * scale * vw[m]);
+            xs[t + kT * m] = xn;
+            fl.add(xn);
+            if constexpr (PRO == PRO_RESNORM) {
+                if (blk0 && src.aux_out) src.aux_out[t + kT * m] = xn;
+            }
+        }
+    } else {
+        // per-head sums of squares of the attention output
+#pragma unroll
+        for (int m = 0; m < PER; ++m) xs[t + kT * m] = va[m];
+        __syncthreads();
+        if (t < kNH * (kHD / 16)) {
+            float s = 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < 16; ++kk) {
+                const float v = xs[16 * t + kk];
+                s += v * v;
+            }
+            scratch[t] = s;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < PER; ++m) {  // element t + 256 m belongs to head m
+            float sum = 0.0f;
+#pragma unroll
+            for (int ch = 0; ch < kHD / 16; ++ch) sum += scratch[m * (kHD / 16) + ch];
+            const float scale = 1.0f / __builtin_sqrtf(sum / (float)kHD + src.eps);
+            const float normalized = va[m] * scale * vw[0];
+            const float x = R<C>(normalized * vb[m] * vc[m]);
+            xs[t + kT * m] = x;
+            fl.add(x);
+        }
+    }
+    const bool fast = fast_verdict<C>(fl, wi, red, redi);
+
+    // 4. products and reduction
+    if constexpr (EPI == EPI_QKVG) {
+        if (ab_blk) {
+            ab_block<C>(ep.aux, xs, part, scratch, ep.ab, ep.bd);
+            return;
+        }
+    }
+    if (fast) w.template compute<true>(xs, part);
+    else w.template compute<false>(xs, part);
+    __syncthreads();
+    if (t >= 64) return;
+    const float y = gemv_chain<K, RB>(part);
+
+    // 5. epilogue (wave 0; lane 4r holds row r)
+    const int lane = t;
+    const bool owner = (lane & 3) == 0 && (lane >> 2) < RB;
+    const int r = rb * RB + (lane >> 2);
+    if constexpr (EPI == EPI_RAW) {
+        if (owner) ep.y[r] = y;
+    } else if constexpr (EPI == EPI_STORE) {
+        if (owner) ep.y[r] = R<C>(y);
+    } else if constexpr (EPI == EPI_QKVG) {
+        if (!owner) return;
         const float yv = R<C>(y);
         if (r < 3 * kH) {
+            // causal conv over [t0, t1, t2, x] + SiLU; tails shift to [t1, t2, x]
             const int kind = r / kH, c = r - kind * kH;
-            const float *cw = aux + kAuxConv + ((size_t)kind * kH + c) * 4;
+            const float *cw = ep.aux + kAuxConv + ((size_t)kind * kH + c) * 4;
             float t0, t1, t2;
             if constexpr (C == kFp32) {
-                float *tl = tails + (size_t)kind * kTailStripe;
+                float *tl = ep.tails + (size_t)kind * kTailStripe;
                 t0 = tl[c];
                 t1 = tl[kH + c];
                 t2 = tl[2 * kH + c];
@@ -507,7 +612,7 @@ __global__ __launch_bounds__(kT) void k_qkvg(const void *__restrict__ W, const f
                 tl[kH + c] = t2;
                 tl[2 * kH + c] = yv;
             } else {
-                uint16_t *tl = reinterpret_cast<uint16_t *>(tails + (size_t)kind * kTailStripe);
+                uint16_t *tl = reinterpret_cast<uint16_t *>(ep.tails + (size_t)kind * kTailStripe);
                 const uint16_t b0 = tl[c], b1 = tl[kH + c], b2 = tl[2 * kH + c];
                 t0 = bf16_bits_to_f32(b0);
                 t1 = bf16_bits_to_f32(b1);
@@ -517,258 +622,54 @@ __global__ __launch_bounds__(kT) void k_qkvg(const void *__restrict__ W, const f
                 tl[2 * kH + c] = (uint16_t)(f2u(yv) >> 16);
             }
             const float s = t0 * cw[0] + t1 * cw[1] + t2 * cw[2] + yv * cw[3];
-            qkv[r] = R<C>(silu_ref(s));
+            ep.y[r] = R<C>(silu_ref(s));
         } else {
-            gate[r - 3 * kH] = yv;
+            ep.y2[r - 3 * kH] = yv;
+            ep.y3[r - 3 * kH] = sigmoid_ref(yv);
         }
-    }
-}
-
-// Gated delta rule for one head and CB state columns.
-template <int C, int CB>
-__global__ __launch_bounds__(kT) void k_recur(
-    const float *__restrict__ qp, const float *__restrict__ kp, const float *__restrict__ vp,
-    const float *__restrict__ a, const float *__restrict__ b, const float *__restrict__ a_log,
-    const float *__restrict__ dt_bias, void *__restrict__ state, float *__restrict__ attn,
-    const float *__restrict__ gate, const float *__restrict__ onorm_w, float *__restrict__ og,
-    unsigned *__restrict__ cnt, float eps, int do_onorm) {
-    static_assert(CB <= 64 && (CB % 8) == 0, "one wave owns the column chains");
-    __shared__ float qn[kHD], kn[kHD];
-    __shared__ __attribute__((aligned(16))) float tile[kHD * CB];
-    __shared__ float dl[CB];
-    __shared__ float red[8], red2[4], sc[2];
-    __shared__ int flag;
-    const int h = blockIdx.y, c0 = blockIdx.x * CB, t = threadIdx.x;
-    const int lane = t & 63, w = t >> 6;
-
-    // q/k L2 norms (gdn_tree_reduce_256 order: four wave butterflies, then
-    // (w0 + w1) + (w2 + w3)).
-    const float q = qp[h * kHD + t], k = kp[h * kHD + t];
-    const float qs = wave_tree64(q * q), ks = wave_tree64(k * k);
-    if (lane == 0) {
-        red[w] = qs;
-        red[4 + w] = ks;
-    }
-    __syncthreads();
-    const float q_sq = (red[0] + red[1]) + (red[2] + red[3]);
-    const float k_sq = (red[4] + red[5]) + (red[6] + red[7]);
-    const float q_inv = 1.0f / __builtin_sqrtf(q_sq + 1e-6f);
-    const float k_inv = 1.0f / __builtin_sqrtf(k_sq + 1e-6f);
-    const float qv = q * q_inv, kv = k * k_inv;
-    qn[t] = qv;
-    kn[t] = kv;
-    const float ap = wave_tree64(qv * kv);
-    if (lane == 0) red2[w] = ap;
-    if (t == 0) {
-        sc[0] = sigmoid_ref(b[h]);
-        const float decay_in = a[h] + dt_bias[h];
-        const float decay_val = -exp_cr(a_log[h]) * softplus_ref(decay_in);
-        sc[1] = exp_cr(decay_val);
-    }
-
-    // Stage the 256 x CB state tile.
-    const size_t sbase = (size_t)h * kHD * kHD + c0;
-    if constexpr (C == kRef) {
-        constexpr int PER_ROW = CB / 8;  // 8 BF16 per 16-byte load
-        const uint16_t *S = reinterpret_cast<const uint16_t *>(state);
-#pragma unroll
-        for (int i = 0; i < (kHD * PER_ROW) / kT; ++i) {
-            const int u = t + kT * i, row = u / PER_ROW, c8 = u - row * PER_ROW;
-            const u32x4 v = *reinterpret_cast<const u32x4 *>(S + sbase + (size_t)row * kHD + c8 * 8);
-            f32x4 lo, hi;
-            lo.x = u2f(v.x << 16); lo.y = u2f(v.x & 0xffff0000u);
-            lo.z = u2f(v.y << 16); lo.w = u2f(v.y & 0xffff0000u);
-            hi.x = u2f(v.z << 16); hi.y = u2f(v.z & 0xffff0000u);
-            hi.z = u2f(v.w << 16); hi.w = u2f(v.w & 0xffff0000u);
-            f32x4 *dst = reinterpret_cast<f32x4 *>(tile + row * CB + c8 * 8);
-            dst[0] = lo;
-            dst[1] = hi;
-        }
-    } else {
-        constexpr int PER_ROW = CB / 4;
-        const float *S = reinterpret_cast<const float *>(state);
-#pragma unroll
-        for (int i = 0; i < (kHD * PER_ROW) / kT; ++i) {
-            const int u = t + kT * i, row = u / PER_ROW, c4 = u - row * PER_ROW;
-            *reinterpret_cast<f32x4 *>(tile + row * CB + c4 * 4) =
-                *reinterpret_cast<const f32x4 *>(S + sbase + (size_t)row * kHD + c4 * 4);
-        }
-    }
-    __syncthreads();
-    const float alpha = (red2[0] + red2[1]) + (red2[2] + red2[3]);
-    const float beta = sc[0], decay = sc[1];
-
-    // Read pass: column chains in row order (one lane per column).
-    if (t < CB) {
-        float r = 0.0f, p = 0.0f;
-#pragma unroll 16
-        for (int j = 0; j < kHD; ++j) {
-            const float s = tile[j * CB + t];
-            r = r + s * kn[j];
-            p = p + s * qn[j];
-        }
-        const float vi = vp[h * kHD + c0 + t];
-        const float delta = beta * (vi - decay * r);
-        const float o = 0.0625f * (decay * p + alpha * delta);
-        dl[t] = delta;
-        attn[h * kHD + c0 + t] = R<C>(o);
-    }
-    __syncthreads();
-
-    // Update pass: S' = decay * S + k (x) delta.
-    if constexpr (C == kRef) {
-        constexpr int PER_ROW = CB / 8;
-        uint16_t *S = reinterpret_cast<uint16_t *>(state);
-#pragma unroll
-        for (int i = 0; i < (kHD * PER_ROW) / kT; ++i) {
-            const int u = t + kT * i, row = u / PER_ROW, c8 = u - row * PER_ROW;
-            const float kj = kn[row];
-            uint32_t packed[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int col = c8 * 8 + 2 * e;
-                const float n0 = decay * tile[row * CB + col] + kj * dl[col];
-                const float n1 = decay * tile[row * CB + col + 1] + kj * dl[col + 1];
-                packed[e] = (f2u(rne_bf16(n0)) >> 16) | (f2u(rne_bf16(n1)) & 0xffff0000u);
-            }
-            u32x4 v;
-            v.x = packed[0]; v.y = packed[1]; v.z = packed[2]; v.w = packed[3];
-            *reinterpret_cast<u32x4 *>(S + sbase + (size_t)row * kHD + c8 * 8) = v;
-        }
-    } else {
-        constexpr int PER_ROW = CB / 4;
-        float *S = reinterpret_cast<float *>(state);
-#pragma unroll
-        for (int i = 0; i < (kHD * PER_ROW) / kT; ++i) {
-            const int u = t + kT * i, row = u / PER_ROW, c4 = u - row * PER_ROW;
-            const float kj = kn[row];
-            const f32x4 old = *reinterpret_cast<const f32x4 *>(tile + row * CB + c4 * 4);
-            f32x4 nv;
-            nv.x = decay * old.x + kj * dl[c4 * 4 + 0];
-            nv.y = decay * old.y + kj * dl[c4 * 4 + 1];
-            nv.z = decay * old.z + kj * dl[c4 * 4 + 2];
-            nv.w = decay * old.w + kj * dl[c4 * 4 + 3];
-            *reinterpret_cast<f32x4 *>(S + sbase + (size_t)row * kHD + c4 * 4) = nv;
-        }
-    }
-
-    if (!do_onorm) return;
-    // Output RMSNorm * gate for the head, by its last column block.
-    if (!last_block_arrives(cnt + h, gridDim.x, &flag)) return;
-    const float av = coherent_load(attn + h * kHD + t);
-    if (t < kHD / 16) {
-        float s = 0.0f;
-#pragma unroll
-        for (int kk = 0; kk < 16; ++kk) {
-            const float v = coherent_load(attn + h * kHD + 16 * t + kk);
-            s += v * v;
-        }
-        tile[t] = s;
-    }
-    __syncthreads();
-    float sum = 0.0f;
-    for (int i = 0; i < kHD / 16; ++i) sum += tile[i];
-    const float scale = 1.0f / __builtin_sqrtf(sum / (float)kHD + eps);
-    const float gv = gate[h * kHD + t];
-    const float normalized = av * scale * onorm_w[t];
-    og[h * kHD + t] = R<C>(normalized * gv * sigmoid_ref(gv));
-}
-
-// GEMV into a residual add + RMSNorm (o_proj, down).
-template <int C, int K, int RB>
-__global__ __launch_bounds__(kT) void k_gemv_res(const void *__restrict__ W,
-                                                 const float *__restrict__ x, WInfo wi,
-                                                 float *__restrict__ ybuf,
-                                                 const float *__restrict__ res_in,
-                                                 float *__restrict__ res_out,
-                                                 const float *__restrict__ norm_w,
-                                                 float *__restrict__ xn_out,
-                                                 unsigned *__restrict__ cnt, float eps) {
-    __shared__ __attribute__((aligned(16))) float xs[K];
-    __shared__ __attribute__((aligned(16))) float part[RB * Hb<K>::HBP > kH / 16 ? RB * Hb<K>::HBP : kH / 16];
-    __shared__ float red[4];
-    __shared__ int redi[4];
-    __shared__ int flag;
-    static_assert(K >= kH, "the LDS x copy is reused for the residual");
-    const float y = gemv_block<K, RB, C>(W, x, wi, xs, part, red, redi);
-    const int lane = threadIdx.x;
-    if (lane < 64 && (lane & 3) == 0 && (lane >> 2) < RB)
-        ybuf[blockIdx.x * RB + (lane >> 2)] = R<C>(y);
-    if (!last_block_arrives(cnt, gridDim.x, &flag)) return;
-    for (int i = threadIdx.x; i < kH; i += kT) {
-        const float xr = R<C>(res_in[i] + coherent_load(ybuf + i));
-        res_out[i] = xr;
-        xs[i] = xr;
-    }
-    __syncthreads();
-    block_rmsnorm_h<C>(xs, norm_w, xn_out, eps, part);
-}
-
-// gate/up GEMV with rows interleaved in blocks of 4 + 4, SwiGLU epilogue.
-template <int C>
-__global__ __launch_bounds__(kT) void k_gu(const void *__restrict__ W, const float *__restrict__ x,
-                                           WInfo wi, float *__restrict__ hout) {
-    constexpr int RB = kRbGu;
-    __shared__ __attribute__((aligned(16))) float xs[kH];
-    __shared__ __attribute__((aligned(16))) float part[RB * Hb<kH>::HBP];
-    __shared__ float red[4];
-    __shared__ int redi[4];
-    const float y = gemv_block<kH, RB, C>(W, x, wi, xs, part, red, redi);
-    if (threadIdx.x < 64) {
+    } else if constexpr (EPI == EPI_SWIGLU) {
+        // rows 0..RB/2-1 are gate rows, RB/2..RB-1 the matching up rows
         const float yu = __shfl_down(y, 4 * (RB / 2));
-        const int lane = threadIdx.x;
         if ((lane & 3) == 0 && (lane >> 2) < RB / 2) {
             const float g = R<C>(y), u = R<C>(yu);
-            hout[blockIdx.x * (RB / 2) + (lane >> 2)] = R<C>(silu_ref(g) * u);
+            ep.y[rb * (RB / 2) + (lane >> 2)] = R<C>(silu_ref(g) * u);
         }
-    }
-}
-
-// LM head: FP32 logits (not rounded) and the argmax (strict '>', lowest
-// index on ties, running best from -FLT_MAX at index 0).
-template <int C>
-__global__ __launch_bounds__(kT) void k_lm(const void *__restrict__ W, const float *__restrict__ x,
-                                           WInfo wi, float *__restrict__ logits,
-                                           float *__restrict__ part_val, int *__restrict__ part_idx,
-                                           unsigned *__restrict__ cnt, int *__restrict__ tok_out,
-                                           float *__restrict__ ws_token) {
-    constexpr int RB = kRbLm;
-    __shared__ __attribute__((aligned(16))) float xs[kH];
-    __shared__ __attribute__((aligned(16))) float part[RB * Hb<kH>::HBP];
-    __shared__ float red[4];
-    __shared__ int redi[4];
-    __shared__ int flag;
-    __shared__ float bv[4];
-    __shared__ int bi[4];
-    const float y = gemv_block<kH, RB, C>(W, x, wi, xs, part, red, redi);
-    if (threadIdx.x < 64) {
-        const int lane = threadIdx.x;
-        const int row0 = blockIdx.x * RB;
-        if ((lane & 3) == 0 && (lane >> 2) < RB) logits[row0 + (lane >> 2)] = y;
+    } else {
+        // LM head: FP32 logits (no rounding point) and the block's argmax
+        if (owner) ep.y[r] = y;
         float best = -3.402823466e38f;
         int idx = 0;
 #pragma unroll
-        for (int r = 0; r < RB; ++r) {
-            const float v = __shfl(y, 4 * r);
+        for (int rr = 0; rr < RB; ++rr) {
+            const float v = __shfl(y, 4 * rr);
             if (v > best) {
                 best = v;
-                idx = row0 + r;
+                idx = rb * RB + rr;
             }
         }
         if (lane == 0) {
-            part_val[blockIdx.x] = best;
-            part_idx[blockIdx.x] = idx;
+            ep.part_val[blockIdx.x] = best;
+            ep.part_idx[blockIdx.x] = idx;
         }
     }
-    if (!last_block_arrives(cnt, gridDim.x, &flag)) return;
+}
+
+// Second argmax stage over the LM head's per-block results, which are in
+// index order: strict '>' within a thread's increasing indices, then a
+// merge that keeps the larger value and, on ties, the lower index.
+__global__ __launch_bounds__(kT) void k_argmax(const float *__restrict__ part_val,
+                                               const int *__restrict__ part_idx, int n,
+                                               int *__restrict__ tok_out,
+                                               float *__restrict__ ws_token) {
+    __shared__ float bv[4];
+    __shared__ int bi[4];
     float best = -3.402823466e38f;
     int idx = 0;
-    for (int i = threadIdx.x; i < (int)gridDim.x; i += kT) {
-        const float v = coherent_load(part_val + i);
-        const int id = __hip_atomic_load(part_idx + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = threadIdx.x; i < n; i += kT) {
+        const float v = part_val[i];
         if (v > best) {
             best = v;
-            idx = id;
+            idx = part_idx[i];
         }
     }
 #pragma unroll
@@ -798,18 +699,145 @@ __global__ __launch_bounds__(kT) void k_lm(const void *__restrict__ W, const flo
     }
 }
 
-// Plain GEMV: FP32 row results before any rounding point (test hook).
-template <int C, int K, int RB>
-__global__ __launch_bounds__(kT) void k_gemv_plain(const void *__restrict__ W,
-                                                   const float *__restrict__ x, WInfo wi,
-                                                   float *__restrict__ y_out) {
-    __shared__ __attribute__((aligned(16))) float xs[K];
-    __shared__ __attribute__((aligned(16))) float part[RB * Hb<K>::HBP];
-    __shared__ float red[4];
-    __shared__ int redi[4];
-    const float y = gemv_block<K, RB, C>(W, x, wi, xs, part, red, redi);
-    const int lane = threadIdx.x;
-    if (lane < 64 && (lane & 3) == 0 && (lane >> 2) < RB) y_out[blockIdx.x * RB + (lane >> 2)] = y;
+// Gated delta rule for one head and CB state columns.
+//   q/k L2 norms in gdn_tree_reduce_256 order (four wave butterflies, then
+//   (w0 + w1) + (w2 + w3)), alpha = tree256(qn * kn);
+//   read pass: r_i, p_i column chains over the 256 rows in order, one lane
+//   per column; delta and o; update pass S' = decay * S + k (x) delta.
+template <int C, int CB>
+__global__ __launch_bounds__(kT) void k_recur(const float *__restrict__ qp,
+                                              const float *__restrict__ kp,
+                                              const float *__restrict__ vp,
+                                              const float *__restrict__ bd,
+                                              void *__restrict__ state, float *__restrict__ attn) {
+    static_assert(CB <= 64 && (CB % 8) == 0, "one wave owns the column chains");
+    constexpr int PER_ROW = (C == kRef) ? CB / 8 : CB / 4;  // 16-byte loads per tile row
+    constexpr int NLD = (kHD * PER_ROW) / kT;
+    static_assert((kHD * PER_ROW) % kT == 0, "tile loads split evenly");
+    __shared__ float qn[kHD], kn[kHD];
+    __shared__ __attribute__((aligned(16))) float tile[kHD * CB];
+    __shared__ float dl[CB];
+    __shared__ float red[8], red2[4];
+    const int h = blockIdx.y, c0 = blockIdx.x * CB, t = threadIdx.x;
+    const int lane = t & 63, w = t >> 6;
+    const size_t sbase = (size_t)h * kHD * kHD + c0;
+
+    const float q = qp[h * kHD + t], k = kp[h * kHD + t];
+    const float vi = (t < CB) ? vp[h * kHD + c0 + t] : 0.0f;
+    const float beta = bd[2 * h], decay = bd[2 * h + 1];
+    u32x4 tr[NLD];
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+        const int u = t + kT * i, row = u / PER_ROW, cq = u - row * PER_ROW;
+        if constexpr (C == kRef) {
+            tr[i] = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const uint16_t *>(state) + sbase +
+                                                     (size_t)row * kHD + cq * 8);
+        } else {
+            tr[i] = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const float *>(state) + sbase +
+                                                     (size_t)row * kHD + cq * 4);
+        }
+    }
+
+    const float qs = wave_tree64(q * q), ks = wave_tree64(k * k);
+    if (lane == 0) {
+        red[w] = qs;
+        red[4 + w] = ks;
+    }
+    __syncthreads();
+    const float q_sq = (red[0] + red[1]) + (red[2] + red[3]);
+    const float k_sq = (red[4] + red[5]) + (red[6] + red[7]);
+    const float q_inv = 1.0f / __builtin_sqrtf(q_sq + 1e-6f);
+    const float k_inv = 1.0f / __builtin_sqrtf(k_sq + 1e-6f);
+    const float qv = q * q_inv, kv = k * k_inv;
+    qn[t] = qv;
+    kn[t] = kv;
+    const float ap = wave_tree64(qv * kv);
+    if (lane == 0) red2[w] = ap;
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+        const int u = t + kT * i, row = u / PER_ROW, cq = u - row * PER_ROW;
+        if constexpr (C == kRef) {
+            const u32x4 v = tr[i];
+            f32x4 lo, hi;
+            lo.x = u2f(v.x << 16); lo.y = u2f(v.x & 0xffff0000u);
+            lo.z = u2f(v.y << 16); lo.w = u2f(v.y & 0xffff0000u);
+            hi.x = u2f(v.z << 16); hi.y = u2f(v.z & 0xffff0000u);
+            hi.z = u2f(v.w << 16); hi.w = u2f(v.w & 0xffff0000u);
+            f32x4 *dst = reinterpret_cast<f32x4 *>(tile + row * CB + cq * 8);
+            dst[0] = lo;
+            dst[1] = hi;
+        } else {
+            *reinterpret_cast<u32x4 *>(tile + row * CB + cq * 4) = tr[i];
+        }
+    }
+    __syncthreads();
+    const float alpha = (red2[0] + red2[1]) + (red2[2] + red2[3]);
+
+    if (t < CB) {
+        float r = 0.0f, p = 0.0f;
+#pragma unroll 16
+        for (int j = 0; j < kHD; ++j) {
+            const float s = tile[j * CB + t];
+            r = r + s * kn[j];
+            p = p + s * qn[j];
+        }
+        const float delta = beta * (vi - decay * r);
+        const float o = 0.0625f * (decay * p + alpha * delta);
+        dl[t] = delta;
+        attn[h * kHD + c0 + t] = R<C>(o);
+    }
+    __syncthreads();
+
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+        const int u = t + kT * i, row = u / PER_ROW, cq = u - row * PER_ROW;
+        const float kj = kn[row];
+        if constexpr (C == kRef) {
+            uint32_t packed[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int col = cq * 8 + 2 * e;
+                const float n0 = decay * tile[row * CB + col] + kj * dl[col];
+                const float n1 = decay * tile[row * CB + col + 1] + kj * dl[col + 1];
+                packed[e] = (f2u(rne_bf16(n0)) >> 16) | (f2u(rne_bf16(n1)) & 0xffff0000u);
+            }
+            u32x4 v;
+            v.x = packed[0]; v.y = packed[1]; v.z = packed[2]; v.w = packed[3];
+            *reinterpret_cast<u32x4 *>(reinterpret_cast<uint16_t *>(state) + sbase + (size_t)row * kHD +
+                                       cq * 8) = v;
+        } else {
+            const f32x4 old = *reinterpret_cast<const f32x4 *>(tile + row * CB + cq * 4);
+            f32x4 nv;
+            nv.x = decay * old.x + kj * dl[cq * 4 + 0];
+            nv.y = decay * old.y + kj * dl[cq * 4 + 1];
+            nv.z = decay * old.z + kj * dl[cq * 4 + 2];
+            nv.w = decay * old.w + kj * dl[cq * 4 + 3];
+            *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(state) + sbase + (size_t)row * kHD +
+                                       cq * 4) = nv;
+        }
+    }
+}
+
+// beta/decay for n heads from raw (a, b, a_log, dt_bias) (isolated-kernel hook).
+__global__ __launch_bounds__(kT) void k_head_scalars(const float *__restrict__ a,
+                                                     const float *__restrict__ b,
+                                                     const float *__restrict__ a_log,
+                                                     const float *__restrict__ dt_bias, int n,
+                                                     float *__restrict__ bd) {
+    const int i = blockIdx.x * kT + threadIdx.x;
+    if (i >= n) return;
+    float beta, decay;
+    head_scalars(a[i], b[i], a_log[i], dt_bias[i], beta, decay);
+    bd[2 * i] = beta;
+    bd[2 * i + 1] = decay;
+}
+
+// out = R(a + b) over the hidden vector (layer output for the layer hook).
+template <int C>
+__global__ __launch_bounds__(kT) void k_resadd(const float *__restrict__ a,
+                                               const float *__restrict__ b,
+                                               float *__restrict__ out) {
+    for (int i = threadIdx.x; i < kH; i += kT) out[i] = R<C>(a[i] + b[i]);
 }
 
 }  // namespace gdn
@@ -836,11 +864,10 @@ struct GDNEngine {
     // workspace (GDN_WS_OFF_* layout) and activations
     float *ws = nullptr;
     float *act = nullptr;
-    float *resid = nullptr, *resid_alt = nullptr, *xn = nullptr, *qkv = nullptr,
-          *gate = nullptr, *ab = nullptr, *attn = nullptr, *og = nullptr, *ybuf = nullptr,
-          *hbuf = nullptr, *lm_val = nullptr;
+    float *resid = nullptr, *resid_alt = nullptr, *fhid = nullptr, *qkv = nullptr,
+          *gate = nullptr, *sgate = nullptr, *ab = nullptr, *bd = nullptr, *attn = nullptr,
+          *ybuf_o = nullptr, *dbuf = nullptr, *hbuf = nullptr, *lm_val = nullptr;
     int *lm_idx = nullptr;
-    unsigned *counters = nullptr;
     int *tok_dev = nullptr;   // [0] in, [1] out
     int *tok_host = nullptr;  // pinned [0] in, [1] out
     hipGraph_t graph = nullptr;
@@ -854,10 +881,6 @@ size_t welem(int contract) { return contract == kFp32 ? 4 : 2; }
 
 float *layer_aux(GDNEngine *e, int l) { return e->aux + (size_t)l * kAuxLayer; }
 float *final_norm(GDNEngine *e) { return e->aux + (size_t)e->layers * kAuxLayer; }
-unsigned *cnt_recur(GDNEngine *e, int l) { return e->counters + (size_t)l * 16; }
-unsigned *cnt_o(GDNEngine *e, int l) { return e->counters + (size_t)l * 16 + 8; }
-unsigned *cnt_down(GDNEngine *e, int l) { return e->counters + (size_t)l * 16 + 9; }
-unsigned *cnt_lm(GDNEngine *e) { return e->counters + (size_t)e->layers * 16; }
 float *layer_tails(GDNEngine *e, int l) {
     return e->ws + GDN_WS_OFF_HEAD_BUF + (size_t)l * 3 * kTailStripe;
 }
@@ -1017,25 +1040,24 @@ int alloc_buffers(GDNEngine *e) {
     GDN_HIP(hipMalloc(&e->ws, (size_t)GDN_WS_FLOATS * 4));
     GDN_HIP(hipMemset(e->ws, 0, (size_t)GDN_WS_FLOATS * 4));
     const size_t nblk_lm = (size_t)e->vocab / kRbLm;
-    const size_t act_floats = 2 * kH + kI + 3 * kH + kH + 16 + kH + kH + kH + kI + nblk_lm;
+    const size_t act_floats = 3 * kH + 3 * kH + 2 * kH + 16 + 2 * kNH + 3 * kH + kI + nblk_lm;
     GDN_HIP(hipMalloc(&e->act, act_floats * 4));
     GDN_HIP(hipMemset(e->act, 0, act_floats * 4));
     float *p = e->act;
     e->resid = p; p += kH;
     e->resid_alt = p; p += kH;
-    e->xn = p; p += kI;
+    e->fhid = p; p += kH;
     e->qkv = p; p += 3 * kH;
     e->gate = p; p += kH;
+    e->sgate = p; p += kH;
     e->ab = p; p += 16;
+    e->bd = p; p += 2 * kNH;
     e->attn = p; p += kH;
-    e->og = p; p += kH;
-    e->ybuf = p; p += kH;
+    e->ybuf_o = p; p += kH;
+    e->dbuf = p; p += kH;
     e->hbuf = p; p += kI;
     e->lm_val = p; p += nblk_lm;
     GDN_HIP(hipMalloc(&e->lm_idx, nblk_lm * sizeof(int)));
-    const size_t ncnt = (size_t)(e->layers + 1) * 16;
-    GDN_HIP(hipMalloc(&e->counters, ncnt * sizeof(unsigned)));
-    GDN_HIP(hipMemset(e->counters, 0, ncnt * sizeof(unsigned)));
     GDN_HIP(hipMalloc(&e->tok_dev, 2 * sizeof(int)));
     GDN_HIP(hipMemset(e->tok_dev, 0, 2 * sizeof(int)));
     GDN_HIP(hipHostMalloc(&e->tok_host, 2 * sizeof(int), hipHostMallocDefault));
@@ -1046,36 +1068,151 @@ int alloc_buffers(GDNEngine *e) {
     return 0;
 }
 
-template <int C>
-void enqueue_layer(GDNEngine *e, int l, hipStream_t s) {
+XSrc xsrc(const float *a, const float *b, const float *c, const float *w, float *res_out,
+          float *aux_out, float eps) {
+    XSrc x{};
+    x.a = a;
+    x.b = b;
+    x.c = c;
+    x.w = w;
+    x.res_out = res_out;
+    x.aux_out = aux_out;
+    x.eps = eps;
+    return x;
+}
+
+// Per-kernel launches.  The QKVG prologue (PRO0) takes the embedding row
+// (first layer of a step), the previous layer's residual (res_b = its down
+// output), or a caller-given residual (res_b = nullptr).
+template <int C, int PRO0>
+void launch_qkvg(GDNEngine *e, int l, const float *res_a, const float *res_b, hipStream_t s) {
     float *aux = layer_aux(e, l);
-    const float *next_norm = (l + 1 < e->layers) ? layer_aux(e, l + 1) + kAuxAttnNorm : final_norm(e);
-    hipLaunchKernelGGL((k_qkvg<C, kRbQkvg>), dim3(4 * kH / kRbQkvg + 1), dim3(kT), 0, s,
-                       e->w_qkvg[l], e->xn, e->i_qkvg[l], aux, layer_tails(e, l), e->qkv, e->gate,
-                       e->ab);
+    Epi q{};
+    q.y = e->qkv;
+    q.y2 = e->gate;
+    q.y3 = e->sgate;
+    q.aux = aux;
+    q.tails = layer_tails(e, l);
+    q.ab = e->ab;
+    q.bd = e->bd;
+    XSrc xq = xsrc(res_a, res_b, nullptr, aux + kAuxAttnNorm, e->resid, nullptr, e->eps);
+    if constexpr (PRO0 == PRO_EMBED) {
+        xq.emb = e->w_emb;
+        xq.tok = e->tok_dev;
+        xq.vocab = e->vocab;
+        xq.aux_out = e->ws + GDN_WS_OFF_X;
+    }
+    hipLaunchKernelGGL((k_gemv<C, kH, kRbQkvg, PRO0, EPI_QKVG>), dim3(4 * kH / kRbQkvg + 1), dim3(kT),
+                       0, s, e->w_qkvg[l], e->i_qkvg[l], xq, q);
+}
+
+template <int C>
+void launch_recur(GDNEngine *e, int l, hipStream_t s) {
     hipLaunchKernelGGL((k_recur<C, kCB>), dim3(kHD / kCB, kNH), dim3(kT), 0, s, e->qkv,
-                       e->qkv + kH, e->qkv + 2 * kH, e->ab, e->ab + kNH, aux + kAuxALog,
-                       aux + kAuxDtBias, layer_state(e, l), e->attn, e->gate, aux + kAuxONorm,
-                       e->og, cnt_recur(e, l), e->eps, 1);
-    hipLaunchKernelGGL((k_gemv_res<C, kH, kRbO>), dim3(kH / kRbO), dim3(kT), 0, s, e->w_o[l],
-                       e->og, e->i_o[l], e->ybuf, e->resid, e->resid_alt, aux + kAuxMlpNorm,
-                       e->xn, cnt_o(e, l), e->eps);
-    hipLaunchKernelGGL((k_gu<C>), dim3(2 * kI / kRbGu), dim3(kT), 0, s, e->w_gu[l], e->xn,
-                       e->i_gu[l], e->hbuf);
-    hipLaunchKernelGGL((k_gemv_res<C, kI, kRbDown>), dim3(kH / kRbDown), dim3(kT), 0, s,
-                       e->w_down[l], e->hbuf, e->i_down[l], e->ybuf, e->resid_alt, e->resid,
-                       next_norm, e->xn, cnt_down(e, l), e->eps);
+                       e->qkv + kH, e->qkv + 2 * kH, e->bd, layer_state(e, l), e->attn);
+}
+
+template <int C>
+void launch_o(GDNEngine *e, int l, hipStream_t s) {
+    Epi st{};
+    st.y = e->ybuf_o;
+    hipLaunchKernelGGL((k_gemv<C, kH, kRbO, PRO_ONORM, EPI_STORE>), dim3(kH / kRbO), dim3(kT), 0, s,
+                       e->w_o[l], e->i_o[l],
+                       xsrc(e->attn, e->gate, e->sgate, layer_aux(e, l) + kAuxONorm, nullptr, nullptr,
+                            e->eps),
+                       st);
+}
+
+template <int C>
+void launch_gu(GDNEngine *e, int l, hipStream_t s) {
+    Epi sw{};
+    sw.y = e->hbuf;
+    hipLaunchKernelGGL((k_gemv<C, kH, kRbGu, PRO_RESNORM, EPI_SWIGLU>), dim3(2 * kI / kRbGu), dim3(kT),
+                       0, s, e->w_gu[l], e->i_gu[l],
+                       xsrc(e->resid, e->ybuf_o, nullptr, layer_aux(e, l) + kAuxMlpNorm, e->resid_alt,
+                            nullptr, e->eps),
+                       sw);
+}
+
+template <int C>
+void launch_down(GDNEngine *e, int l, hipStream_t s) {
+    Epi dn{};
+    dn.y = e->dbuf;
+    hipLaunchKernelGGL((k_gemv<C, kI, kRbDown, PRO_PLAIN, EPI_STORE>), dim3(kH / kRbDown), dim3(kT), 0,
+                       s, e->w_down[l], e->i_down[l],
+                       xsrc(e->hbuf, nullptr, nullptr, nullptr, nullptr, nullptr, e->eps), dn);
+}
+
+template <int C>
+void launch_lm(GDNEngine *e, hipStream_t s) {
+    Epi lm{};
+    lm.y = e->ws + GDN_WS_OFF_LOGITS;
+    lm.part_val = e->lm_val;
+    lm.part_idx = e->lm_idx;
+    hipLaunchKernelGGL((k_gemv<C, kH, kRbLm, PRO_RESNORM, EPI_LM>), dim3(e->vocab / kRbLm), dim3(kT), 0,
+                       s, e->w_lm, e->i_lm,
+                       xsrc(e->resid_alt, e->dbuf, nullptr, final_norm(e), e->resid, e->fhid, e->eps), lm);
+}
+
+void launch_argmax(GDNEngine *e, hipStream_t s) {
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(kT), 0, s, e->lm_val, e->lm_idx, e->vocab / kRbLm,
+                       e->tok_dev + 1, e->ws + GDN_WS_OFF_X_NORM);
+}
+
+template <int C, int PRO0>
+void enqueue_layer(GDNEngine *e, int l, const float *res_a, const float *res_b, hipStream_t s) {
+    launch_qkvg<C, PRO0>(e, l, res_a, res_b, s);
+    launch_recur<C>(e, l, s);
+    launch_o<C>(e, l, s);
+    launch_gu<C>(e, l, s);
+    launch_down<C>(e, l, s);
 }
 
 template <int C>
 void enqueue_step_t(GDNEngine *e, hipStream_t s) {
-    hipLaunchKernelGGL((k_embed<C>), dim3(1), dim3(kT), 0, s, e->tok_dev, e->vocab, e->w_emb,
-                       (const float *)nullptr, e->ws + GDN_WS_OFF_X, e->resid,
-                       layer_aux(e, 0) + kAuxAttnNorm, e->xn, e->eps);
-    for (int l = 0; l < e->layers; ++l) enqueue_layer<C>(e, l, s);
-    hipLaunchKernelGGL((k_lm<C>), dim3(e->vocab / kRbLm), dim3(kT), 0, s, e->w_lm, e->xn, e->i_lm,
-                       e->ws + GDN_WS_OFF_LOGITS, e->lm_val, e->lm_idx, cnt_lm(e), e->tok_dev + 1,
-                       e->ws + GDN_WS_OFF_X_NORM);
+    enqueue_layer<C, PRO_EMBED>(e, 0, nullptr, nullptr, s);
+    for (int l = 1; l < e->layers; ++l) enqueue_layer<C, PRO_RESNORM>(e, l, e->resid_alt, e->dbuf, s);
+    launch_lm<C>(e, s);
+    launch_argmax(e, s);
+}
+
+// Kernel kinds timed by gdn_profile_kernels, in output order.
+constexpr int kProfKinds = 7;
+
+// Average device time per launch of each kernel kind; each kind is launched
+// back to back over every layer's weights, so no launch finds another's
+// weights in cache.  Advances the recurrent and conv state.
+template <int C>
+int profile_t(GDNEngine *e, uint32_t rounds, float *avg_us, uint32_t n) {
+    for (uint32_t id = 0; id < n && id < (uint32_t)kProfKinds; ++id) {
+        GDN_HIP(hipStreamSynchronize(e->stream));
+        GDN_HIP(hipEventRecord(e->ev0, e->stream));
+        uint32_t launches = 0;
+        for (uint32_t r = 0; r < rounds; ++r) {
+            if (id >= 5) {
+                if (id == 5) launch_lm<C>(e, e->stream);
+                else launch_argmax(e, e->stream);
+                ++launches;
+                continue;
+            }
+            for (int l = 0; l < e->layers; ++l, ++launches) {
+                switch (id) {
+                case 0: launch_qkvg<C, PRO_RESNORM>(e, l, e->resid_alt, e->dbuf, e->stream); break;
+                case 1: launch_recur<C>(e, l, e->stream); break;
+                case 2: launch_o<C>(e, l, e->stream); break;
+                case 3: launch_gu<C>(e, l, e->stream); break;
+                default: launch_down<C>(e, l, e->stream); break;
+                }
+            }
+        }
+        GDN_HIP(hipEventRecord(e->ev1, e->stream));
+        GDN_HIP(hipEventSynchronize(e->ev1));
+        GDN_HIP(hipGetLastError());
+        float ms = 0.0f;
+        GDN_HIP(hipEventElapsedTime(&ms, e->ev0, e->ev1));
+        avg_us[id] = launches ? 1000.0f * ms / (float)launches : 0.0f;
+    }
+    return 0;
 }
 
 void enqueue_step(GDNEngine *e, hipStream_t s) {
@@ -1128,7 +1265,6 @@ void destroy_engine(GDNEngine *e) {
     (void)hipFree(e->ws);
     (void)hipFree(e->act);
     (void)hipFree(e->lm_idx);
-    (void)hipFree(e->counters);
     (void)hipFree(e->tok_dev);
     if (e->tok_host) (void)hipHostFree(e->tok_host);
     delete e;
@@ -1223,7 +1359,7 @@ int gdn_read_logits(const GDNRunState *state, float *logits, size_t count) {
 
 int gdn_read_final_hidden(const GDNRunState *state, float *hidden, size_t count) {
     if (count > (size_t)kH) return -1;
-    GDN_HIP(hipMemcpy(hidden, state->engine->xn, count * 4, hipMemcpyDeviceToHost));
+    GDN_HIP(hipMemcpy(hidden, state->engine->fhid, count * 4, hipMemcpyDeviceToHost));
     return 0;
 }
 
@@ -1349,6 +1485,16 @@ int gdn_run_teacher_forced(GDNRunState *state, const int32_t *tokens, uint32_t n
     return 0;
 }
 
+int gdn_profile_kernels(GDNRunState *state, uint32_t rounds, float *avg_us, uint32_t n_kinds) {
+    GDNEngine *e = state->engine;
+    if (!e || rounds == 0) return -1;
+    switch (e->contract) {
+    case kRef: return profile_t<kRef>(e, rounds, avg_us, n_kinds);
+    case kBf16w: return profile_t<kBf16w>(e, rounds, avg_us, n_kinds);
+    default: return profile_t<kFp32>(e, rounds, avg_us, n_kinds);
+    }
+}
+
 // ---------------------------------------------------------------- test hooks
 
 int gdn_test_gemv(int contract, const float *W, const float *x, uint32_t M, uint32_t K, float *y) {
@@ -1368,7 +1514,12 @@ int gdn_test_gemv(int contract, const float *W, const float *x, uint32_t M, uint
     GDN_HIP(hipMemcpy(dx, x, (size_t)K * 4, hipMemcpyHostToDevice));
     const WInfo wi = pk.info();
     const dim3 grid(M / kRbTest), block(kT);
-#define GDN_PLAIN(CC, KK) hipLaunchKernelGGL((k_gemv_plain<CC, KK, kRbTest>), grid, block, 0, 0, dW, dx, wi, dy)
+#define GDN_PLAIN(CC, KK)                                                                     \
+    hipLaunchKernelGGL((k_gemv<CC, KK, kRbTest, PRO_PLAIN, EPI_RAW>), grid, block, 0, 0, dW, wi, xs, ep)
+    XSrc xs{};
+    xs.a = dx;
+    Epi ep{};
+    ep.y = dy;
     if (K == (uint32_t)kH) {
         if (contract == kFp32) GDN_PLAIN(kFp32, kH);
         else GDN_PLAIN(kRef, kH);
@@ -1420,13 +1571,16 @@ int gdn_test_recurrence(int contract, uint32_t n_heads, uint32_t n_steps, const 
     } else {
         GDN_HIP(hipMemcpy(dS, S, nstate * 4, hipMemcpyHostToDevice));
     }
+    float *dbd;
+    GDN_HIP(hipMalloc(&dbd, 2 * ns * 4));
+    hipLaunchKernelGGL(k_head_scalars, dim3((unsigned)((ns + kT - 1) / kT)), dim3(kT), 0, 0, da, db, dal,
+                       ddt, (int)ns, dbd);
     const dim3 grid(kHD / kCB, n_heads), block(kT);
     for (uint32_t s = 0; s < n_steps; ++s) {
         const size_t ov = (size_t)s * n_heads * kHD, os = (size_t)s * n_heads;
-#define GDN_REC(CC)                                                                           \
-    hipLaunchKernelGGL((k_recur<CC, kCB>), grid, block, 0, 0, dq + ov, dk + ov, dv + ov,       \
-                       da + os, db + os, dal + os, ddt + os, dS, dout + ov, (const float *)nullptr, \
-                       (const float *)nullptr, (float *)nullptr, (unsigned *)nullptr, 0.0f, 0)
+#define GDN_REC(CC)                                                                             \
+    hipLaunchKernelGGL((k_recur<CC, kCB>), grid, block, 0, 0, dq + ov, dk + ov, dv + ov, dbd + 2 * os, \
+                       dS, dout + ov)
         if (contract == kRef) GDN_REC(kRef);
         else if (contract == kBf16w) GDN_REC(kBf16w);
         else GDN_REC(kFp32);
@@ -1445,7 +1599,7 @@ int gdn_test_recurrence(int contract, uint32_t n_heads, uint32_t n_steps, const 
     } else {
         GDN_HIP(hipMemcpy(S, dS, nstate * 4, hipMemcpyDeviceToHost));
     }
-    float *bufs[] = {dq, dk, dv, da, db, dal, ddt, dout};
+    float *bufs[] = {dq, dk, dv, da, db, dal, ddt, dout, dbd};
     for (float *p : bufs) GDN_HIP(hipFree(p));
     GDN_HIP(hipFree(dS));
     return 0;
@@ -1462,12 +1616,11 @@ int gdn_test_layer(GDNRunState *state, uint32_t layer, uint32_t n_steps, const f
     for (uint32_t s = 0; s < n_steps; ++s) {
         GDN_HIP(hipMemcpyAsync(din, x_in + (size_t)s * kH, (size_t)kH * 4, hipMemcpyHostToDevice,
                                e->stream));
-        const float *norm0 = layer_aux(e, (int)layer) + kAuxAttnNorm;
 #define GDN_LAYER(CC)                                                                         \
     do {                                                                                      \
-        hipLaunchKernelGGL((k_embed<CC>), dim3(1), dim3(kT), 0, e->stream, e->tok_dev, e->vocab, \
-                           e->w_emb, din, e->ws + GDN_WS_OFF_X, e->resid, norm0, e->xn, e->eps); \
-        enqueue_layer<CC>(e, (int)layer, e->stream);                                          \
+        enqueue_layer<CC, PRO_RESNORM>(e, (int)layer, din, nullptr, e->stream);                 \
+        hipLaunchKernelGGL((k_resadd<CC>), dim3(1), dim3(kT), 0, e->stream, e->resid_alt, e->dbuf, \
+                           e->resid);                                                         \
     } while (0)
         if (e->contract == kRef) GDN_LAYER(kRef);
         else if (e->contract == kBf16w) GDN_LAYER(kBf16w);

@@ -236,6 +236,14 @@ class RunState:
             fptr(inner) if timing else None, fptr(outer) if timing else None), "gdn_run_teacher_forced")
         return am, inner, outer
 
+    KERNEL_KINDS = ("qkvg", "recur", "o_proj", "gate_up", "down", "lm_head", "argmax")
+
+    def profile_kernels(self, rounds: int = 4) -> Dict[str, float]:
+        """Average microseconds per launch of each kernel kind (advances state)."""
+        out = np.zeros(len(self.KERNEL_KINDS), np.float32)
+        _check(L.load().gdn_profile_kernels(self.ptr, rounds, fptr(out), out.size), "gdn_profile_kernels")
+        return {k: float(v) for k, v in zip(self.KERNEL_KINDS, out)}
+
     def layer_steps(self, layer: int, x_in: np.ndarray) -> np.ndarray:
         """gdn_test_layer: run one layer over teacher-forced residual inputs."""
         x = _f32(x_in).reshape(-1, self.model.config.hidden_size)

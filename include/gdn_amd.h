@@ -209,6 +209,14 @@ int gdn_run_teacher_forced(GDNRunState *state, const int32_t *tokens,
                            uint32_t n_tokens, uint32_t n_steps,
                            int32_t *argmax_out, float *inner_ms,
                            float *outer_ms);
+/* Average device time (microseconds) per launch of each kernel kind, in
+ * the order qkvg, recur, o_proj, gate_up, down, lm_head, argmax; each kind
+ * is launched back to back over every layer's weights (HIP events on the
+ * engine stream).  Advances the recurrent and conv state.  No reference
+ * counterpart: the reference times its FPGA calls with compile-time cycle
+ * probes (GDN_CALL_PROBE, gdn_model.h:91-107). */
+int gdn_profile_kernels(GDNRunState *state, uint32_t rounds, float *avg_us,
+                        uint32_t n_kinds);
 /* 0: launch kernels one by one; 1 (default): one captured hipGraph/step. */
 int gdn_set_graph_mode(GDNRunState *state, int use_graph);
 int gdn_get_contract(const GDNRunState *state);

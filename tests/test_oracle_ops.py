@@ -1,0 +1,289 @@
+"""Closed-form and special-case pins of the oracle's operators.
+
+Each expected value below is derived by hand from the mathematics (noted in
+the comment), and the inputs are chosen so that a plausible mistake -- a
+different association, a dropped rounding point, a swapped bank, a wrong tap
+orientation -- changes the result.
+"""
+import numpy as np
+import pytest
+
+F = np.float32
+TWO24 = F(2.0 ** 24)
+
+
+def bf(x):
+    """RNE to BF16 for finite values (the definition, via integers)."""
+    u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32)
+
+
+# ---------------------------------------------------------------- trees
+
+def test_tree16_association(orc):
+    # balanced: (2^24 + 1) -> 2^24 (tie to even), (-2^24 + 1) exact,
+    # (1 + 1) = 2 twice: (2^24 + 2) + (-2^24 + 1 + 2) = 16777218 - 16777213 = 5.
+    # A left-to-right sum gives 3; pairing (p0+p2) would give 4 or 6.
+    p = np.zeros(16, F)
+    p[0], p[1], p[2], p[3] = TWO24, 1, 1, 1
+    p[4], p[5], p[6], p[7] = -TWO24, 1, 1, 1
+    assert orc.tree16(p) == 5.0
+    # integers sum exactly
+    q = np.arange(16, dtype=F)
+    assert orc.tree16(q) == 120.0
+
+
+def test_tree256_association(orc):
+    a = np.zeros(256, F)
+    a[0], a[1], a[128] = TWO24, 1, 1
+    # l128[0] = 2^24 + 1 -> 2^24; the 1 at index 128 joins at the top: 2^24 + 1 -> 2^24
+    assert orc.tree256(a) == float(TWO24)
+    a = np.zeros(256, F)
+    a[0], a[2], a[1] = TWO24, -TWO24, 1
+    # (2^24 + 1) -> 2^24, then + (-2^24) = 0: the 1 is lost.  A sequential
+    # sum would also lose it, a (0,2)-first pairing would keep it.
+    assert orc.tree256(a) == 0.0
+    assert orc.tree256(np.ones(256, F)) == 256.0
+
+
+# ----------------------------------------------------------------- GEMV
+
+@pytest.mark.parametrize("contract", [0, 2])
+def test_gemv_one_hot_selects_column(orc, contract):
+    rng = np.random.default_rng(3)
+    W = bf(rng.normal(0, 0.02, (64, 2048)).astype(F))
+    for k in (0, 17, 1023, 2047):
+        x = np.zeros(2048, F)
+        x[k] = 1.0
+        y = orc.gemv(contract, W, x)
+        assert (y == W[:, k]).all()
+
+
+@pytest.mark.parametrize("K", [2048, 5632])
+def test_gemv_integer_exact(orc, K):
+    rng = np.random.default_rng(4)
+    W = rng.integers(-8, 9, (32, K)).astype(F)
+    x = rng.integers(-8, 9, K).astype(F)
+    want = (W.astype(np.int64) @ x.astype(np.int64)).astype(F)
+    for contract in (0, 2):
+        assert (orc.gemv(contract, W, x) == want).all()
+
+
+def test_gemv_bank_order(orc):
+    # x = 1; the row holds 2^24 at beat 0, -2^24 at beat 4 (both even/lower)
+    # and a 1 at beat 1 (odd/lower) and a 1 at beat 2 lane 16 (even/upper).
+    # Banks: even_lo = (2^24) + (-2^24) = 0, even_hi = 1, odd_lo = 1:
+    # y = (0 + 1) + (1 + 0) = 2.  One running sum over all beats gives 0 or 1;
+    # merging halves per beat before banking gives 1.
+    W = np.zeros((8, 2048), F)
+    W[0, 0] = TWO24
+    W[0, 4 * 32] = -TWO24
+    W[0, 1 * 32] = 1.0
+    W[0, 2 * 32 + 16] = 1.0
+    x = np.ones(2048, F)
+    for contract in (0, 2):
+        assert orc.gemv(contract, W, x)[0] == 2.0
+
+
+def test_gemv_native_rounding_point(orc):
+    # each product (1 + 2^-7)^2 = 1 + 2^-6 + 2^-14 rounds to 1 + 2^-6 in the
+    # native contract (BF16 products) but not in the FP32 control arm.
+    w = F(1 + 2.0 ** -7)
+    W = np.full((8, 2048), w, F)
+    x = np.full(2048, w, F)
+    y_ref = orc.gemv(0, W, x)[0]
+    y_f32 = orc.gemv(2, W, x)[0]
+    assert y_ref == F(2048 * (1 + 2.0 ** -6))
+    assert y_f32 != y_ref
+
+
+def test_gemv_tiny_order(orc):
+    # acc = (acc + lo) + hi per beat: (0 + 2^24) + 1 -> 2^24; then
+    # (2^24 + -2^24) + 0 = 0.  Separate lo/hi banks would give 1.
+    W = np.zeros((1, 2048), F)
+    W[0, 0] = TWO24
+    W[0, 16] = 1.0
+    W[0, 32] = -TWO24
+    x = np.ones(2048, F)
+    assert orc.gemv_tiny(W, x)[0] == 0.0
+
+
+# ----------------------------------------------------------------- norms
+
+def test_rmsnorm_constant(orc):
+    # x = 1: sum = 2048, 1/sqrtf(1 + 1e-6f) = 0.99999952 -> BF16 1.0
+    out = orc.rmsnorm(0, np.ones(2048, F), np.ones(2048, F))
+    assert (out == 1.0).all()
+    # x = 2, w = 0.5: scale ~ 1/2 -> 2 * scale * 0.5 ~ 0.5
+    out = orc.rmsnorm(0, np.full(2048, 2.0, F), np.full(2048, 0.5, F))
+    assert (out == 0.5).all()
+    # FP32 arm keeps the unrounded value
+    out = orc.rmsnorm(2, np.ones(2048, F), np.ones(2048, F))
+    assert (out == F(1.0) / np.sqrt(F(1.0) + F(1e-6))).all()
+
+
+def test_rmsnorm_scale_invariance(orc):
+    rng = np.random.default_rng(5)
+    x = bf(rng.normal(0, 1, 2048).astype(F))
+    w = bf(rng.normal(1, 0.1, 2048).astype(F))
+    a = orc.rmsnorm(2, x, w)
+    b = orc.rmsnorm(2, x * F(4), w)
+    np.testing.assert_allclose(a, b, rtol=1e-5)
+
+
+def test_residual_rmsnorm(orc):
+    x = np.full(2048, 1.0, F)
+    y = np.full(2048, 2.0 ** -9, F)  # 1 + 2^-9 is a tie -> BF16 1.0
+    xo, out = orc.residual_rmsnorm(0, x, y, np.ones(2048, F))
+    assert (xo == 1.0).all() and (out == 1.0).all()
+    xo, _ = orc.residual_rmsnorm(2, x, y, np.ones(2048, F))
+    assert (xo == F(1 + 2.0 ** -9)).all()
+
+
+def test_output_norm_gate(orc):
+    # a = 1 per head -> normalised ~1; g = 0 -> gate g*sigmoid(g) = 0
+    o = np.ones(2048, F)
+    out = orc.output_norm_gate(0, o, np.zeros(2048, F), np.ones(256, F), 8, 256)
+    assert (out == 0).all()
+    # heads normalise independently: head h scaled by (h+1) gives the same row
+    o = np.concatenate([np.full(256, h + 1, F) for h in range(8)])
+    g = np.full(2048, 4.0, F)
+    out = orc.output_norm_gate(2, o, g, np.ones(256, F), 8, 256)
+    s = F(4.0) / (F(1) + np.exp(F(-4.0)))
+    np.testing.assert_allclose(out, np.full(2048, s, F), rtol=2e-6)
+
+
+# ----------------------------------------------------------------- conv
+
+def test_conv_taps_and_shift(orc):
+    C = 2048
+    rng = np.random.default_rng(6)
+    raw = bf(rng.normal(0, 1, C).astype(F))
+    tails = bf(rng.normal(0, 1, (3, C)).astype(F))
+    # tap 3 applies to the newest input
+    w = np.zeros((C, 4), F)
+    w[:, 3] = 1.0
+    out, t2 = orc.conv_silu(0, raw, w, tails, orc.CR)
+    want = bf(np.array([orc.lib().orc_silu(float(v), orc.CR) for v in raw], F))
+    assert (out == want).all()
+    # the tail shifts by one row and appends the raw (pre-conv) input
+    assert (t2[0] == tails[1]).all() and (t2[1] == tails[2]).all() and (t2[2] == raw).all()
+    # tap 0 applies to the oldest row
+    w = np.zeros((C, 4), F)
+    w[:, 0] = 1.0
+    out, _ = orc.conv_silu(0, raw, w, tails, orc.CR)
+    want = bf(np.array([orc.lib().orc_silu(float(v), orc.CR) for v in tails[0]], F))
+    assert (out == want).all()
+    # zero tails and zero weights give silu(0) = 0
+    out, _ = orc.conv_silu(0, raw, np.zeros((C, 4), F), np.zeros((3, C), F))
+    assert (out == 0).all()
+
+
+# ----------------------------------------------------------------- recurrence
+
+def _unit(v):
+    return v / np.sqrt((v.astype(np.float64) ** 2).sum())
+
+
+def test_recurrence_beta_zero(orc):
+    rng = np.random.default_rng(7)
+    S = rng.normal(0, 0.01, (256, 256)).astype(F)
+    q, k, v = (rng.normal(0, 1, 256).astype(F) for _ in range(3))
+    o, S2 = orc.recurrence_head_scalars(2, q, k, v, 0.0, 0.5, S)
+    # beta = 0: S' = decay * S exactly (k * 0 adds +-0)
+    assert (S2 == F(0.5) * S).all()
+    qn = _unit(q.astype(np.float64))
+    np.testing.assert_allclose(o, 0.0625 * 0.5 * (S.astype(np.float64).T @ qn), rtol=2e-5, atol=1e-7)
+
+
+def test_recurrence_one_hot_key_overwrites_row(orc):
+    # decay = 1, beta = 1, k = e_j: S'[j] = v, other rows unchanged.
+    rng = np.random.default_rng(8)
+    S = rng.integers(-4, 5, (256, 256)).astype(F)
+    v = rng.integers(-4, 5, 256).astype(F)
+    k = np.zeros(256, F)
+    k[37] = 3.0  # normalised to 1 (up to the 1e-6 guard): use a power of two scale
+    q = rng.normal(0, 1, 256).astype(F)
+    o, S2 = orc.recurrence_head_scalars(2, q, k, v, 1.0, 1.0, S)
+    knorm = F(3.0) * (F(1.0) / np.sqrt(F(9.0) + F(1e-6)))
+    # row j: S + kn * (v - kn * S_j) ; with kn != 1 exactly, compare to fp64
+    want = S.astype(np.float64).copy()
+    want[37] = S[37] + float(knorm) * (v - float(knorm) * S[37])
+    np.testing.assert_allclose(S2, want, rtol=1e-6, atol=1e-6)
+    others = np.ones(256, bool)
+    others[37] = False
+    assert (S2[others] == S[others]).all()
+
+
+def test_recurrence_plain_ieee_case(orc):
+    # decay = 1 and beta = 0.5 leave only exactly-rounded FP32 arithmetic
+    # (the reference's own cosim setting, slr2_region_cosim/README.md:8-12):
+    # compare to the textbook recurrence in fp64.
+    rng = np.random.default_rng(9)
+    S = rng.normal(0, 0.01, (256, 256)).astype(F)
+    q, k, v = (rng.normal(0, 1, 256).astype(F) for _ in range(3))
+    o, S2 = orc.recurrence_head_scalars(2, q, k, v, 0.5, 1.0, S)
+    qn, kn = _unit(q.astype(np.float64)), _unit(k.astype(np.float64))
+    S64 = S.astype(np.float64)
+    # textbook (chunk.py:688-718): S_t = a S (I - b k k^T) + b v k^T in [V][K];
+    # in [K][V]: S_t = a S + b k (v - a S^T k)^T ; o = S_t^T q / sqrt(dk)
+    St = S64 + np.outer(kn, 0.5 * (v - S64.T @ kn))
+    np.testing.assert_allclose(S2, St, rtol=1e-4, atol=1e-6)
+    np.testing.assert_allclose(o, St.T @ qn / 16.0, rtol=1e-4, atol=1e-6)
+
+
+def test_recurrence_gated_against_fp64(orc):
+    rng = np.random.default_rng(10)
+    S = rng.normal(0, 0.01, (256, 256)).astype(F)
+    for step in range(4):
+        q, k, v = (rng.normal(0, 1, 256).astype(F) for _ in range(3))
+        a, b = float(rng.normal()), float(rng.normal())
+        a_log = float(rng.uniform(0, np.log(16)))
+        o, S2 = orc.recurrence_head(2, q, k, v, a, b, a_log, 0.0, S, orc.CR)
+        beta = 1 / (1 + np.exp(-b))
+        decay = np.exp(-np.exp(a_log) * np.log1p(np.exp(a)))
+        qn, kn = _unit(q.astype(np.float64)), _unit(k.astype(np.float64))
+        S64 = S.astype(np.float64)
+        St = decay * S64 + np.outer(kn, beta * (v - decay * (S64.T @ kn)))
+        np.testing.assert_allclose(S2, St, rtol=1e-4, atol=1e-7)
+        np.testing.assert_allclose(o, St.T @ qn / 16.0, rtol=1e-4, atol=1e-7)
+        S = S2
+
+
+def test_recurrence_ref_rounds_state(orc):
+    rng = np.random.default_rng(11)
+    S = bf(rng.normal(0, 0.01, (256, 256)).astype(F))
+    q, k, v = (bf(rng.normal(0, 1, 256).astype(F)) for _ in range(3))
+    o, S2 = orc.recurrence_head(0, q, k, v, 0.1, 0.2, 0.3, 0.0, S)
+    assert ((S2.view(np.uint32) & 0xFFFF) == 0).all()
+    assert ((o.view(np.uint32) & 0xFFFF) == 0).all()
+    o1, S1 = orc.recurrence_head(1, q, k, v, 0.1, 0.2, 0.3, 0.0, S)
+    assert (o1 == o).all()          # same pass; only the stored state differs
+    assert (bf(S1) == S2).all()
+
+
+def test_head_scalars_closed_form(orc):
+    beta, decay = orc.head_scalars(0.0, 0.0, 0.0, 0.0, orc.CR)
+    assert beta == 0.5
+    assert decay == F(np.exp(-np.log(2.0)))  # exp(-1 * softplus(0)) = 1/2
+    beta, decay = orc.head_scalars(25.0, -30.0, 0.0, 0.0, orc.CR)
+    assert decay == F(np.exp(np.float32(-25.0)))  # softplus(x > 20) = x
+
+
+# ----------------------------------------------------------------- misc
+
+def test_swiglu(orc):
+    g = np.array([0.0, 1.0, -1.0, 4.0], F)
+    u = np.array([5.0, 2.0, 2.0, 0.5], F)
+    h = orc.swiglu(2, g, u, orc.CR)
+    want = g / (1 + np.exp(-g.astype(np.float64))) * u
+    np.testing.assert_allclose(h, want, rtol=1e-6)
+    assert orc.swiglu(0, g, u, orc.CR)[0] == 0.0
+
+
+def test_argmax_rules(orc):
+    assert orc.argmax(np.array([1, 3, 3, 2], F)) == 1              # lowest index wins ties
+    assert orc.argmax(np.array([np.nan, 1, np.nan, 2], F)) == 3     # NaN never wins
+    assert orc.argmax(np.full(5, -np.inf, F)) == 0                  # nothing beats -FLT_MAX
+    assert orc.argmax(np.array([-3.402823466e38, -3.402823466e38], F)) == 0
+    assert orc.argmax(np.array([0, np.inf, np.inf], F)) == 1
