@@ -61,6 +61,13 @@ KERNEL_BYTES = {
     "lm_head": V * H * 2 + H * 2 + V * 4,
     "argmax": (V // 8) * 8,
 }
+# DRAM bytes per launch (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy of
+# known size) from the counter passes summarised in
+# profiles/gemv_qkvg_gdn13b_bf16_decode.md (bf16 arm).
+MEASURED_TRAFFIC = {
+    "qkvg": 34_642_000, "recur": 4_377_000, "o_proj": 8_752_000, "gate_up": 46_549_000,
+    "down": 23_395_000, "lm_head": 131_882_000, "argmax": 35_000,
+}
 LAUNCHES_PER_TOKEN = {"qkvg": L, "recur": L, "o_proj": L, "gate_up": L, "down": L, "lm_head": 1, "argmax": 1}
 
 
@@ -107,7 +114,22 @@ def main():
     ap.add_argument("--profile-rounds", type=int, default=4)
     ap.add_argument("--cpu-tokens", type=int, default=6, help="oracle tokens timed on all cores (0: skip)")
     ap.add_argument("--cpu-single-tokens", type=int, default=1, help="oracle tokens timed on one core")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only copy 256 MiB device to device three times (the known-size copy that scales "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch the step's kernels one by one instead of the captured hipGraph "
+                         "(for rocprofv3 kernel tracing, which aborts the queue on graph launches)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+        a = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": a.numel() * 4, "copies": 3}), flush=True)
+        return
     if args.gpus != 1:
         print("bench.py: this build is a single-GPU decode engine; run with --gpus 1 "
               "(no multi-GPU figure is produced)", file=sys.stderr)
@@ -118,6 +140,8 @@ def main():
     t_setup = time.perf_counter()
     model = g.Model.synth(num_layers=L, seed=0, std=0.02, bf16=(contract != g.CONTRACT_FP32))
     rs = g.RunState(model, contract)
+    if args.eager:
+        rs.set_graph(False)
     prompt = g.synth_tokens(max(args.warmup, 1), 0, 1, V)
     stream = g.synth_tokens(4096, 0, 2, V)
     if args.warmup > 0:
@@ -172,7 +196,8 @@ def main():
                         "fixed 4096-token uniform stream (cyclic), greedy argmax",
             "contract": args.contract,
             "state_dtype": "bf16" if contract == g.CONTRACT_REF else "fp32",
-            "launch": "one hipGraph per token (122 kernels)",
+            "launch": "eager (122 kernel launches per token)" if args.eager
+                      else "one hipGraph per token (122 kernels)",
         },
         "outer_ms_median": round(float(np.median(outer)), 5),
         "inner_ms_median": round(inner_med, 5),
@@ -190,7 +215,7 @@ def main():
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": round(achieved_k / PEAK_HBM_GBPS, 4),
-            "traffic": None,
+            "traffic": MEASURED_TRAFFIC[dom] if contract == g.CONTRACT_BF16W_FP32S else None,
             "algorithmic_bytes_per_launch": kb,
             "avg_launch_us": round(prof[dom], 3),
         },
