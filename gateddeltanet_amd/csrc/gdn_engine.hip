@@ -363,8 +363,10 @@ __device__ __forceinline__ bool fast_verdict(XFlags fl, WInfo wi, float *red, in
 }
 
 // Sum of squares of the hidden vector in LDS in the norm order: 16-value
-// chunks summed sequentially, chunk sums added sequentially.
-__device__ __forceinline__ float hidden_sumsq(const float *xs, float *scratch) {
+// chunks summed sequentially (threads 0..127), chunk sums added sequentially
+// by wave 0 alone -- the other waves wait at the barrier instead of spending
+// issue slots on the same serial chain.  Every thread returns the sum.
+__device__ __forceinline__ float hidden_sumsq(const float *xs, float *scratch, float *bcast) {
     const int t = threadIdx.x;
     if (t < kH / 16) {
         float s = 0.0f;
@@ -376,10 +378,21 @@ __device__ __forceinline__ float hidden_sumsq(const float *xs, float *scratch) {
         scratch[t] = s;
     }
     __syncthreads();
-    float sum = 0.0f;
-#pragma unroll 16
-    for (int i = 0; i < kH / 16; ++i) sum += scratch[i];
-    return sum;
+    if (t < 64) {
+        const f32x4 *s4 = reinterpret_cast<const f32x4 *>(scratch);
+        float sum = 0.0f;
+#pragma unroll 8
+        for (int i = 0; i < kH / 64; ++i) {
+            const f32x4 c = s4[i];
+            sum += c.x;
+            sum += c.y;
+            sum += c.z;
+            sum += c.w;
+        }
+        if (t == 0) bcast[0] = sum;
+    }
+    __syncthreads();
+    return bcast[0];
 }
 
 // ---------------------------------------------------------------- epilogues
@@ -454,8 +467,15 @@ __device__ void ab_block(const float *__restrict__ aux, const float *xs, float *
 
 // ------------------------------------------------------------ the GEMV kernel
 
+// Waves per SIMD each GEMV instantiation must fit (caps its VGPRs): the
+// whole grid is then resident at once (QKVG 1025 blocks <= 5 x 256 CUs,
+// gate/up 1408 <= 6 x 256) and no straggler block runs in a second round.
+constexpr int gemv_min_waves(int C, int EPI) {
+    return C == kFp32 ? 4 : (EPI == EPI_SWIGLU || EPI == EPI_LM) ? 6 : 5;
+}
+
 template <int C, int K, int RB, int PRO, int EPI>
-__global__ __launch_bounds__(kT) void k_gemv(const void *__restrict__ W, WInfo wi, XSrc src,
+__global__ __launch_bounds__(kT, gemv_min_waves(C, EPI)) void k_gemv(const void *__restrict__ W, WInfo wi, XSrc src,
                                              Epi ep) {
     constexpr int HBP = Hb<K>::HBP;
     constexpr int PART = (EPI == EPI_QKVG ? 16 : RB) * HBP;
@@ -464,7 +484,8 @@ __global__ __launch_bounds__(kT) void k_gemv(const void *__restrict__ W, WInfo w
     static_assert(PRO == PRO_PLAIN || K == kH, "normalised inputs are hidden-sized");
     __shared__ __attribute__((aligned(16))) float xs[K];
     __shared__ __attribute__((aligned(16))) float part[PART];
-    __shared__ float scratch[kH / 16];
+    __shared__ __attribute__((aligned(16))) float scratch[kH / 16];
+    __shared__ float bcast[kNH];
     __shared__ float red[4];
     __shared__ int redi[4];
     const int t = threadIdx.x;
@@ -534,7 +555,7 @@ __global__ __launch_bounds__(kT) void k_gemv(const void *__restrict__ W, WInfo w
             if (blk0 && src.res_out) src.res_out[t + kT * m] = r;
         }
         __syncthreads();
-        const float sum = hidden_sumsq(xs, scratch);
+        const float sum = hidden_sumsq(xs, scratch, bcast);
         const float scale = 1.0f / __builtin_sqrtf(sum / (float)kH + src.eps);
 #pragma unroll
         for (int m = 0; m < PER; ++m) {
@@ -546,7 +567,9 @@ __global__ __launch_bounds__(kT) void k_gemv(const void *__restrict__ W, WInfo w
             }
         }
     } else {
-        // per-head sums of squares of the attention output
+        // per-head sums of squares of the attention output: 16-value chunks
+        // (threads 0..127), then each head's 16 chunk sums in order (one lane
+        // of wave 0 per head)
 #pragma unroll
         for (int m = 0; m < PER; ++m) xs[t + kT * m] = va[m];
         __syncthreads();
@@ -560,13 +583,16 @@ __global__ __launch_bounds__(kT) void k_gemv(const void *__restrict__ W, WInfo w
             scratch[t] = s;
         }
         __syncthreads();
-#pragma unroll
-        for (int m = 0; m < PER; ++m) {  // element t + 256 m belongs to head m
+        if (t < kNH) {
             float sum = 0.0f;
 #pragma unroll
-            for (int ch = 0; ch < kHD / 16; ++ch) sum += scratch[m * (kHD / 16) + ch];
-            const float scale = 1.0f / __builtin_sqrtf(sum / (float)kHD + src.eps);
-            const float normalized = va[m] * scale * vw[0];
+            for (int ch = 0; ch < kHD / 16; ++ch) sum += scratch[t * (kHD / 16) + ch];
+            bcast[t] = 1.0f / __builtin_sqrtf(sum / (float)kHD + src.eps);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < PER; ++m) {  // element t + 256 m belongs to head m
+            const float normalized = va[m] * bcast[m] * vw[0];
             const float x = R<C>(normalized * vb[m] * vc[m]);
             xs[t + kT * m] = x;
             fl.add(x);
