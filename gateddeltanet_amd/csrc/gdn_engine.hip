@@ -34,6 +34,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 #include <vector>
 
 #include "gdn_amd.h"
@@ -84,10 +85,14 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
-// Smallest nonzero |w| of a matrix (after DAZ) and whether any is not finite.
+// Smallest nonzero and largest |w| of a matrix (after DAZ) and whether any
+// is not finite.
 struct WInfo {
     float min_abs;
+    float max_abs;
     int nonfinite;
 };
 
@@ -173,19 +178,6 @@ __device__ __forceinline__ float native_exact(uint32_t w, float xf) {
     return u2f(r);
 }
 
-// Two native products when every operand is finite and normal and no
-// product can fall below the flush threshold: the FP32 product is then
-// exact, so one v_cvt_pk_bf16_f32 (round to nearest even) finishes both.
-__device__ __forceinline__ void native_pair_fast(uint32_t w2, float x0, float x1, float &p0,
-                                                 float &p1) {
-    const float a = u2f(w2 << 16) * x0;
-    const float b = u2f(w2 & 0xffff0000u) * x1;
-    const bf16x2 r = __builtin_convertvector((f32x2){a, b}, bf16x2);
-    const uint32_t rb = __builtin_bit_cast(uint32_t, r);
-    p0 = u2f(rb << 16);
-    p1 = u2f(rb & 0xffff0000u);
-}
-
 __device__ __forceinline__ void lds_load16(const float *src, float *v) {
     const f32x4 *s4 = reinterpret_cast<const f32x4 *>(src);
 #pragma unroll
@@ -197,6 +189,74 @@ __device__ __forceinline__ void lds_load16(const float *src, float *v) {
         v[4 * q + 3] = t.w;
     }
 }
+
+__device__ __forceinline__ void lds_load16u(const uint32_t *src, uint32_t *v) {
+    const u32x4 *s4 = reinterpret_cast<const u32x4 *>(src);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const u32x4 t = s4[q];
+        v[4 * q + 0] = t.x;
+        v[4 * q + 1] = t.y;
+        v[4 * q + 2] = t.z;
+        v[4 * q + 3] = t.w;
+    }
+}
+
+// Two FP32 values to a BF16 pair (lo in bits 0..15), round to nearest even
+// (v_cvt_pk_bf16_f32; equal to the integer rounding for every non-NaN input).
+__device__ __forceinline__ uint32_t cvt_pk(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
+}
+
+// Eight BF16 x BF16 products rounded to BF16, packed in pairs: r[j] holds
+// R(w[j].lo * x[2j]) in bits 0..15 and R(w[j].hi * x[2j+1]) in bits 16..31.
+// Each product is one v_dot2_f32_bf16 with a zero accumulator: the
+// activation word carries its BF16 in the lane of the weight it meets and
+// zero in the other lane, so the dot product is the single FP32 product --
+// exact for BF16 operands whose product is a normal FP32 number -- and
+// v_cvt_pk_bf16_f32 rounds two of them to nearest even.  A VALU read of a
+// v_dot2 result needs 3 wait states on gfx950, which the compiler cannot see
+// inside inline assembly: the block issues all eight products, one s_nop,
+// then the conversions, so every read is at least 4 slots after its write.
+__device__ __forceinline__ void dot8_bf16(const uint32_t *w, const uint32_t *x, uint32_t *r) {
+    float t0, t1, t2, t3, t4, t5, t6, t7;
+    asm("v_dot2_f32_bf16 %4, %12, %16, 0\n\t"
+        "v_dot2_f32_bf16 %5, %12, %17, 0\n\t"
+        "v_dot2_f32_bf16 %6, %13, %18, 0\n\t"
+        "v_dot2_f32_bf16 %7, %13, %19, 0\n\t"
+        "v_dot2_f32_bf16 %8, %14, %20, 0\n\t"
+        "v_dot2_f32_bf16 %9, %14, %21, 0\n\t"
+        "v_dot2_f32_bf16 %10, %15, %22, 0\n\t"
+        "v_dot2_f32_bf16 %11, %15, %23, 0\n\t"
+        "s_nop 0\n\t"
+        "v_cvt_pk_bf16_f32 %0, %4, %5\n\t"
+        "v_cvt_pk_bf16_f32 %1, %6, %7\n\t"
+        "v_cvt_pk_bf16_f32 %2, %8, %9\n\t"
+        "v_cvt_pk_bf16_f32 %3, %10, %11"
+        : "=v"(r[0]), "=v"(r[1]), "=v"(r[2]), "=v"(r[3]), "=&v"(t0), "=&v"(t1), "=&v"(t2),
+          "=&v"(t3), "=&v"(t4), "=&v"(t5), "=&v"(t6), "=&v"(t7)
+        : "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]), "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]),
+          "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]));
+}
+
+// Swap values between lane pairs (2i, 2i + 1) with a DPP quad permutation.
+__device__ __forceinline__ float swap_lane_pair(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false));
+}
+
+// Running magnitude statistics of BF16 activation pairs, per 16-bit half:
+// the largest |x| bits and the smallest (|x| bits - 1), where zero wraps to
+// 0xffff and so never wins.
+struct PairStats {
+    uint32_t mx = 0u, mnm1 = 0xffffffffu;
+    __device__ __forceinline__ void add(uint32_t pair) {
+        const u16x2 m = __builtin_bit_cast(u16x2, pair & 0x7fff7fffu);
+        const u16x2 one = {1, 1};
+        mx = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, mx), m));
+        mnm1 = __builtin_bit_cast(uint32_t,
+                                  __builtin_elementwise_min(__builtin_bit_cast(u16x2, mnm1), (u16x2)(m - one)));
+    }
+};
 
 
 // ------------------------------------------------------------------ GEMV core
@@ -215,6 +275,12 @@ __device__ __forceinline__ void lds_load16(const float *src, float *v) {
 // work: the activation prologue (residual add, RMSNorm, output norm * gate)
 // runs while the weight stream is in flight, and s_barrier does not wait
 // on outstanding global loads.
+//
+// The GEMV input lives in LDS as one 32-bit word per element.  BF16
+// contracts: element k's BF16 bits sit in the half of the word that meets
+// weight k in the packed weight pair (low half for even k, high half for odd
+// k) and the other half is zero -- the operand form of dot2_bf16, and for odd
+// k also the FP32 value itself.  FP32 contract: the FP32 value.
 
 template <int K>
 struct Hb {
@@ -223,12 +289,22 @@ struct Hb {
     static constexpr int NB = K / 32;     // 32-column beats per row
 };
 
+// The QKVG kernel's first kAbBlocks workgroups compute the 16 tiny a/b rows
+// (4 each) instead of projection rows.
+constexpr int kAbBlocks = 4;
+constexpr int kAbRows = 2 * kNH / kAbBlocks;
+
+__device__ __forceinline__ float lane_word_value(uint32_t w, int k) {
+    return (k & 1) ? u2f(w) : u2f(w << 16);
+}
+
 template <int K, int RB, int C>
 struct WRegs {
     static constexpr int HB = Hb<K>::HB, HBP = Hb<K>::HBP;
     static constexpr int ITEMS = RB * HB;
     static constexpr int NIT = (ITEMS + kT - 1) / kT;
     static constexpr bool kFull = (ITEMS % kT) == 0;
+    static constexpr bool kSameHb = (kT % HB) == 0;  // every item of a thread has one half-beat
     static constexpr int WPI = (C == kFp32) ? 4 : 2;  // 16-byte loads per item
     u32x4 v[NIT][WPI];
 
@@ -246,38 +322,85 @@ struct WRegs {
         }
     }
 
+    // a/b blocks: kAbRows FP32 rows of the hidden width; items t and t + 256
+    // are rows t / 128 and 2 + t / 128 at half-beat t % 128.
+    __device__ __forceinline__ void load_ab(const float *__restrict__ abw) {
+        static_assert(K == kH && kAbRows == 4 && NIT * WPI >= 8, "a/b rows fit the weight registers");
+        const int t = threadIdx.x;
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) {
+            const int row = (t >> 7) + 2 * ii, hb = t & 127;
+            const u32x4 *src = reinterpret_cast<const u32x4 *>(abw + (size_t)row * kH + hb * 16);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[(4 * ii + q) / WPI][(4 * ii + q) % WPI] = src[q];
+        }
+    }
+
     template <bool FAST>
-    __device__ __forceinline__ void compute(const float *xs, float *part) const {
+    __device__ __forceinline__ void compute(const uint32_t *xs, float *part) const {
+        uint32_t xv[16];
+        if constexpr (kSameHb) lds_load16u(xs + (threadIdx.x % HB) * 16, xv);
 #pragma unroll
         for (int i = 0; i < NIT; ++i) {
             const int f = threadIdx.x + kT * i;
             if (kFull || f < ITEMS) {
                 const int row = f / HB, hb = f - row * HB;
-                float xv[16], p[16];
-                lds_load16(xs + hb * 16, xv);
+                if constexpr (!kSameHb) lds_load16u(xs + hb * 16, xv);
+                float p[16];
                 if constexpr (C == kFp32) {
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
-                        p[4 * q + 0] = u2f(v[i][q].x) * xv[4 * q + 0];
-                        p[4 * q + 1] = u2f(v[i][q].y) * xv[4 * q + 1];
-                        p[4 * q + 2] = u2f(v[i][q].z) * xv[4 * q + 2];
-                        p[4 * q + 3] = u2f(v[i][q].w) * xv[4 * q + 3];
+                        p[4 * q + 0] = u2f(v[i][q].x) * u2f(xv[4 * q + 0]);
+                        p[4 * q + 1] = u2f(v[i][q].y) * u2f(xv[4 * q + 1]);
+                        p[4 * q + 2] = u2f(v[i][q].z) * u2f(xv[4 * q + 2]);
+                        p[4 * q + 3] = u2f(v[i][q].w) * u2f(xv[4 * q + 3]);
                     }
                 } else {
                     const uint32_t w8[8] = {v[i][0].x, v[i][0].y, v[i][0].z, v[i][0].w,
                                             v[i][1].x, v[i][1].y, v[i][1].z, v[i][1].w};
+                    if constexpr (FAST) {
+                        uint32_t rbits[8];
+                        dot8_bf16(w8, xv, rbits);
+                        dot8_bf16(w8 + 4, xv + 8, rbits + 4);
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        if constexpr (FAST) {
-                            native_pair_fast(w8[e], xv[2 * e], xv[2 * e + 1], p[2 * e], p[2 * e + 1]);
-                        } else {
-                            p[2 * e] = native_exact(w8[e] & 0xffffu, xv[2 * e]);
-                            p[2 * e + 1] = native_exact(w8[e] >> 16, xv[2 * e + 1]);
+                        for (int e = 0; e < 8; ++e) {
+                            p[2 * e] = u2f(rbits[e] << 16);
+                            p[2 * e + 1] = u2f(rbits[e] & 0xffff0000u);
+                        }
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            p[2 * e] = native_exact(w8[e] & 0xffffu, u2f(xv[2 * e] << 16));
+                            p[2 * e + 1] = native_exact(w8[e] >> 16, u2f(xv[2 * e + 1]));
                         }
                     }
                 }
                 part[row * HBP + hb] = tree16(p);
             }
+        }
+    }
+
+    // a/b rows: FP32 products x * w, tree16 per half-beat (gdn_gemv_tiny_ab).
+    __device__ __forceinline__ void compute_ab(const uint32_t *xs, float *part) const {
+        const int t = threadIdx.x, hb = t & 127;
+        uint32_t xv[16];
+        lds_load16u(xs + hb * 16, xv);
+        float xf[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) xf[e] = (C == kFp32) ? u2f(xv[e]) : lane_word_value(xv[e], e);
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) {
+            float p[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int n = 4 * ii + q;
+                const u32x4 wq = v[n / WPI][n % WPI];
+                p[4 * q + 0] = xf[4 * q + 0] * u2f(wq.x);
+                p[4 * q + 1] = xf[4 * q + 1] * u2f(wq.y);
+                p[4 * q + 2] = xf[4 * q + 2] * u2f(wq.z);
+                p[4 * q + 3] = xf[4 * q + 3] * u2f(wq.w);
+            }
+            part[((t >> 7) + 2 * ii) * HBP + hb] = tree16(p);
         }
     }
 };
@@ -324,60 +447,80 @@ struct XSrc {
     float eps;
 };
 
-// Fast-path decision for one thread's final inputs: finite, normal or zero.
-struct XFlags {
-    int bad = 0;
-    float mn = INFINITY;
-    __device__ __forceinline__ void add(float v) {
-        const uint32_t m = f2u(v) & 0x7fffffffu;
-        if (m >= 0x7f800000u || (m != 0u && m < 0x00800000u)) bad = 1;
-        else if (m != 0u) mn = fminf(mn, u2f(m));
+// Workgroup barriers for the input prologue.  BlockSync is s_barrier.
+// Wave4Sync joins waves 0..3 only -- the waves that own the input elements
+// in a CU-resident workgroup -- so they never wait for the other waves,
+// which may sit for microseconds issuing their weight loads (a SIMD holds
+// only about one wave's worth of outstanding loads).  Each wave's lane 0
+// adds one to an LDS arrival counter; the waves spin (s_sleep) until it
+// reaches 4 x phase.  The spin is bounded so no wave can hang; the bound
+// (about a second) is never reached while the four waves run.
+struct BlockSync {
+    __device__ __forceinline__ void operator()() { __syncthreads(); }
+};
+
+constexpr int kSpinMax = 1 << 24;
+
+__device__ __forceinline__ void wait_count(int *ctr, int target) {
+    int spins = 0;
+    while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target &&
+           ++spins < kSpinMax)
+        __builtin_amdgcn_s_sleep(1);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+struct Wave4Sync {
+    int *ctr;
+    int phase = 0;
+    __device__ __forceinline__ void operator()() {
+        ++phase;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if ((threadIdx.x & 63) == 0)
+            __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        wait_count(ctr, 4 * phase);
     }
 };
 
-// Block-wide fast-path verdict (BF16 contracts): every input finite and
-// normal or zero, every weight finite, and min|x| * min|w| >= 2^-125 so no
-// product can reach the flush threshold.  Ends with a barrier.
-template <int C>
-__device__ __forceinline__ bool fast_verdict(XFlags fl, WInfo wi, float *red, int *redi) {
-    if constexpr (C == kFp32) {
-        __syncthreads();
-        return false;
-    } else {
-        float mn = fl.mn;
+// Fast-path verdict (BF16 contracts): every input finite and normal or
+// zero, every weight finite, and every product |x| |w| inside
+// [2^-123, 2^126) -- so no product reaches the flush threshold or overflows
+// and dot2_bf16 + v_cvt_pk_bf16_f32 equal the native product.
+// The input-owning waves 0..3 publish their statistics, then any thread
+// decides from the published values.
+__device__ __forceinline__ void publish_stats(PairStats st, uint32_t *red) {
+    uint32_t mx = max(st.mx & 0xffffu, st.mx >> 16);
+    uint32_t mn = min(st.mnm1 & 0xffffu, st.mnm1 >> 16);
 #pragma unroll
-        for (int m = 1; m < 64; m <<= 1) mn = fminf(mn, __shfl_xor(mn, m));
-        const int wbad = __any(fl.bad) ? 1 : 0;
-        const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-        if (lane == 0) {
-            red[w] = mn;
-            redi[w] = wbad;
-        }
-        __syncthreads();
-        const float gm = fminf(fminf(red[0], red[1]), fminf(red[2], red[3]));
-        const int gb = redi[0] | redi[1] | redi[2] | redi[3];
-        if (gb || wi.nonfinite) return false;
-        if (gm == INFINITY || wi.min_abs == INFINITY) return true;
-        return (double)gm * (double)wi.min_abs >= 0x1p-125;
+    for (int m = 1; m < 64; m <<= 1) {
+        mx = max(mx, (uint32_t)__shfl_xor((int)mx, m));
+        mn = min(mn, (uint32_t)__shfl_xor((int)mn, m));
+    }
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    if (lane == 0 && w < 4) {
+        red[w] = mx;
+        red[4 + w] = mn;
     }
 }
 
-// Sum of squares of the hidden vector in LDS in the norm order: 16-value
-// chunks summed sequentially (threads 0..127), chunk sums added sequentially
-// by wave 0 alone -- the other waves wait at the barrier instead of spending
-// issue slots on the same serial chain.  Every thread returns the sum.
-__device__ __forceinline__ float hidden_sumsq(const float *xs, float *scratch, float *bcast) {
+__device__ __forceinline__ bool decide_fast(const uint32_t *red, WInfo wi) {
+    const uint32_t mx = max(max(red[0], red[1]), max(red[2], red[3]));
+    const uint32_t mn = min(min(red[4], red[5]), min(red[6], red[7]));
+    if (mx >= 0x7f80u || wi.nonfinite) return false;  // an input NaN/infinity or a weight
+    if (mn == 0xffffu) return true;                     // every input is zero
+    const uint32_t mn_mag = mn + 1u;
+    if (mn_mag < 0x0080u) return false;                 // a subnormal input
+    const double lo = (double)u2f(mn_mag << 16) * (double)wi.min_abs;
+    const double hi = (double)u2f(mx << 16) * (double)wi.max_abs;
+    return lo >= 0x1p-123 && hi < 0x1p126;
+}
+
+// Serial sum of the 128 chunk sums in scratch by wave 0 (the other waves
+// wait at the barrier instead of spending issue slots on the same chain);
+// every thread returns the total.  Two barriers.
+template <class Sync>
+__device__ __forceinline__ float chunk_total(const float *scratch, float *bcast, Sync &sync) {
+    sync();
     const int t = threadIdx.x;
-    if (t < kH / 16) {
-        float s = 0.0f;
-#pragma unroll
-        for (int kk = 0; kk < 16; ++kk) {
-            const float v = xs[16 * t + kk];
-            s += v * v;
-        }
-        scratch[t] = s;
-    }
-    __syncthreads();
     if (t < 64) {
         const f32x4 *s4 = reinterpret_cast<const f32x4 *>(scratch);
         float sum = 0.0f;
@@ -391,9 +534,359 @@ __device__ __forceinline__ float hidden_sumsq(const float *xs, float *scratch, f
         }
         if (t == 0) bcast[0] = sum;
     }
-    __syncthreads();
+    sync();
     return bcast[0];
 }
+
+// Sum of squares of 16-value chunks in order, when thread 2c holds the first
+// 8 values of chunk c and thread 2c + 1 the last 8: the even lane's running
+// sum moves to the odd lane, which finishes the chunk.  Odd lanes return the
+// chunk sum.
+__device__ __forceinline__ float chunk_sumsq8(const float *r) {
+    float sq[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sq[e] = r[e] * r[e];
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += sq[e];
+    float c = swap_lane_pair(s);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) c += sq[e];
+    return c;
+}
+
+// Store 8 (BF16 pairs ->) lane words for elements [8t, 8t + 8).
+__device__ __forceinline__ void store_pairs8(uint32_t *xs, const uint32_t *pairs, PairStats &st) {
+    u32x4 lo, hi;
+    uint32_t lw[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        st.add(pairs[j]);
+        lw[2 * j] = pairs[j] & 0xffffu;
+        lw[2 * j + 1] = pairs[j] & 0xffff0000u;
+    }
+    lo.x = lw[0]; lo.y = lw[1]; lo.z = lw[2]; lo.w = lw[3];
+    hi.x = lw[4]; hi.y = lw[5]; hi.z = lw[6]; hi.w = lw[7];
+    u32x4 *d = reinterpret_cast<u32x4 *>(xs + 8 * threadIdx.x);
+    d[0] = lo;
+    d[1] = hi;
+}
+
+__device__ __forceinline__ void unpack8(const f32x4 *v, float *o) {
+    o[0] = v[0].x; o[1] = v[0].y; o[2] = v[0].z; o[3] = v[0].w;
+    o[4] = v[1].x; o[5] = v[1].y; o[6] = v[1].z; o[7] = v[1].w;
+}
+
+// The GEMV input for one workgroup.  load() issues the activation reads (the
+// kernel issues the weight stream right after), finish() builds the input in
+// LDS and returns the fast-path verdict (after a barrier).
+//   BF16 contracts: thread t owns elements [PER t, PER t + PER).  Roundings
+//   use v_cvt_pk_bf16_f32; where a NaN may reach a stored BF16 value (the
+//   residual and final-hidden outputs) the integer rounding with its
+//   canonical NaN is used instead.
+//   FP32 contract: thread t owns elements t + 256 m.
+template <int C, int K, int PRO>
+struct Prologue {
+    static constexpr int PER = K / kT;
+    static constexpr bool BF = C != kFp32;
+    static_assert(!BF || PRO == PRO_PLAIN || PER == 8, "normalised inputs: 8 per thread");
+    f32x4 a4[2], b4[2], c4[2], w4[2];
+    f32x2 p2[PER / 2];
+    u32x4 e4;
+    float va[PER], vb[PER], vc[PER], vw[PER];
+    int tok = 0;
+
+    __device__ __forceinline__ void load(const XSrc &src) {
+        const int t = threadIdx.x;
+        if constexpr (PRO == PRO_EMBED) {
+            tok = src.tok[0];
+            if (tok < 0 || tok >= src.vocab) tok = 0;  // the host rejects these first
+        }
+        if constexpr (BF) {
+            if constexpr (PRO == PRO_PLAIN) {
+                const f32x2 *a = reinterpret_cast<const f32x2 *>(src.a) + (size_t)t * (PER / 2);
+#pragma unroll
+                for (int j = 0; j < PER / 2; ++j) p2[j] = a[j];
+            } else if constexpr (PRO == PRO_RESNORM) {
+                const f32x4 *a = reinterpret_cast<const f32x4 *>(src.a) + 2 * t;
+                const f32x4 *w = reinterpret_cast<const f32x4 *>(src.w) + 2 * t;
+                a4[0] = a[0];
+                a4[1] = a[1];
+                if (src.b) {
+                    const f32x4 *b = reinterpret_cast<const f32x4 *>(src.b) + 2 * t;
+                    b4[0] = b[0];
+                    b4[1] = b[1];
+                }
+                w4[0] = w[0];
+                w4[1] = w[1];
+            } else if constexpr (PRO == PRO_EMBED) {
+                e4 = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const uint16_t *>(src.emb) +
+                                                      (size_t)tok * kH + 8 * t);
+                const f32x4 *w = reinterpret_cast<const f32x4 *>(src.w) + 2 * t;
+                w4[0] = w[0];
+                w4[1] = w[1];
+            } else {
+                const f32x4 *a = reinterpret_cast<const f32x4 *>(src.a) + 2 * t;
+                const f32x4 *g = reinterpret_cast<const f32x4 *>(src.b) + 2 * t;
+                const f32x4 *s = reinterpret_cast<const f32x4 *>(src.c) + 2 * t;
+                const f32x4 *w = reinterpret_cast<const f32x4 *>(src.w) + 2 * (t & 31);
+                a4[0] = a[0];
+                a4[1] = a[1];
+                b4[0] = g[0];
+                b4[1] = g[1];
+                c4[0] = s[0];
+                c4[1] = s[1];
+                w4[0] = w[0];
+                w4[1] = w[1];
+            }
+        } else {
+            if constexpr (PRO == PRO_PLAIN) {
+#pragma unroll
+                for (int m = 0; m < PER; ++m) va[m] = src.a[t + kT * m];
+            } else if constexpr (PRO == PRO_RESNORM) {
+#pragma unroll
+                for (int m = 0; m < PER; ++m) {
+                    va[m] = src.a[t + kT * m];
+                    vb[m] = src.b ? src.b[t + kT * m] : 0.0f;
+                    vw[m] = src.w[t + kT * m];
+                }
+            } else if constexpr (PRO == PRO_EMBED) {
+#pragma unroll
+                for (int m = 0; m < PER; ++m) {
+                    va[m] = reinterpret_cast<const float *>(src.emb)[(size_t)tok * kH + t + kT * m];
+                    vw[m] = src.w[t + kT * m];
+                }
+            } else {
+#pragma unroll
+                for (int m = 0; m < PER; ++m) {
+                    va[m] = src.a[t + kT * m];
+                    vb[m] = src.b[t + kT * m];
+                    vc[m] = src.c[t + kT * m];
+                }
+                vw[0] = src.w[t];
+            }
+        }
+    }
+
+    // barriers finish_bf16 passes through
+    static constexpr int kSyncs = (PRO == PRO_PLAIN) ? 1 : 3;
+
+    // BF16 contracts: called by threads 0..255 (the element owners); every
+    // barrier is sync(), kSyncs of them.
+    template <class Sync>
+    __device__ __forceinline__ bool finish_bf16(const XSrc &src, WInfo wi, uint32_t *xs,
+                                                float *scratch, float *bcast, uint32_t *red,
+                                                Sync &sync) {
+        const int t = threadIdx.x;
+        const bool act = t < kT;
+        PairStats st;
+        if constexpr (PRO == PRO_PLAIN) {
+            // the BF16 of each element is its top half (the reference's
+            // activation conversion), placed in its lane
+            if (act) {
+#pragma unroll
+                for (int j = 0; j < PER / 2; ++j) {
+                    const uint32_t b0 = f2u(p2[j].x), b1 = f2u(p2[j].y);
+                    const uint32_t pair = (b1 & 0xffff0000u) | (b0 >> 16);
+                    st.add(pair);
+                    u32x2 lw;
+                    lw.x = pair & 0xffffu;
+                    lw.y = pair & 0xffff0000u;
+                    reinterpret_cast<u32x2 *>(xs + PER * t)[j] = lw;
+                }
+            }
+        } else if constexpr (PRO == PRO_RESNORM || PRO == PRO_EMBED) {
+            float r[8], w[8];
+            if (act) {
+                float a[8], b[8];
+                unpack8(w4, w);
+                if constexpr (PRO == PRO_EMBED) {
+                    const uint32_t e[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        r[2 * j] = u2f(e[j] << 16);
+                        r[2 * j + 1] = u2f(e[j] & 0xffff0000u);
+                    }
+                } else {
+                    unpack8(a4, a);
+                    if (src.b) {
+                        unpack8(b4, b);
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const uint32_t rp = cvt_pk(a[2 * j] + b[2 * j], a[2 * j + 1] + b[2 * j + 1]);
+                            r[2 * j] = u2f(rp << 16);
+                            r[2 * j + 1] = u2f(rp & 0xffff0000u);
+                        }
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) r[e] = a[e];
+                    }
+                }
+                const float cs = chunk_sumsq8(r);
+                if (t & 1) scratch[t >> 1] = cs;
+            }
+            const float sum = chunk_total(scratch, bcast, sync);
+            if (act) {
+                const bool finite = sum <= 3.402823466e38f;
+                if (blockIdx.x == 0) {
+                    // stored BF16 values: exact rounding, canonical NaN (a NaN
+                    // or infinity is rare: the inputs are read again)
+                    float rs[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) rs[e] = r[e];
+                    if (!finite) {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            if constexpr (PRO == PRO_EMBED) rs[e] = rne_bf16(r[e]);
+                            else if (src.b) rs[e] = rne_bf16(src.a[8 * t + e] + src.b[8 * t + e]);
+                        }
+                    }
+                    if (src.res_out) {
+                        f32x4 *d = reinterpret_cast<f32x4 *>(src.res_out) + 2 * t;
+                        d[0] = (f32x4){rs[0], rs[1], rs[2], rs[3]};
+                        d[1] = (f32x4){rs[4], rs[5], rs[6], rs[7]};
+                    }
+                    if constexpr (PRO == PRO_EMBED) {
+                        if (src.aux_out) {  // the FP32 embedding row as read
+                            f32x4 *d = reinterpret_cast<f32x4 *>(src.aux_out) + 2 * t;
+                            d[0] = (f32x4){r[0], r[1], r[2], r[3]};
+                            d[1] = (f32x4){r[4], r[5], r[6], r[7]};
+                        }
+                    }
+                }
+                const float scale = 1.0f / __builtin_sqrtf(sum / (float)kH + src.eps);
+                float xv[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xv[e] = r[e] * scale * w[e];
+                uint32_t pairs[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) pairs[j] = cvt_pk(xv[2 * j], xv[2 * j + 1]);
+                store_pairs8(xs, pairs, st);
+                if constexpr (PRO == PRO_RESNORM) {
+                    if (blockIdx.x == 0 && src.aux_out) {
+                        // x from the rounded residual (a NaN there makes every
+                        // x NaN; only its bits need the canonical form)
+                        f32x4 *d = reinterpret_cast<f32x4 *>(src.aux_out) + 2 * t;
+                        float xo[8];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) xo[e] = rne_bf16(xv[e]);
+                        d[0] = (f32x4){xo[0], xo[1], xo[2], xo[3]};
+                        d[1] = (f32x4){xo[4], xo[5], xo[6], xo[7]};
+                    }
+                }
+            }
+        } else {
+            // per-head sums of squares: 16-value chunks (thread pairs), then
+            // each head's 16 chunk sums in order (one lane of wave 0 per head)
+            float a[8], g[8], s[8], w[8];
+            if (act) {
+                unpack8(a4, a);
+                unpack8(b4, g);
+                unpack8(c4, s);
+                unpack8(w4, w);
+                const float cs = chunk_sumsq8(a);
+                if (t & 1) scratch[t >> 1] = cs;
+            }
+            sync();
+            if (t < kNH) {
+                float sum = 0.0f;
+#pragma unroll
+                for (int ch = 0; ch < kHD / 16; ++ch) sum += scratch[t * (kHD / 16) + ch];
+                bcast[t] = 1.0f / __builtin_sqrtf(sum / (float)kHD + src.eps);
+            }
+            sync();
+            if (act) {
+                const float sc = bcast[t >> 5];  // elements 8t.. belong to head t / 32
+                uint32_t pairs[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float x0 = a[2 * j] * sc * w[2 * j] * g[2 * j] * s[2 * j];
+                    const float x1 = a[2 * j + 1] * sc * w[2 * j + 1] * g[2 * j + 1] * s[2 * j + 1];
+                    pairs[j] = cvt_pk(x0, x1);
+                }
+                store_pairs8(xs, pairs, st);
+            }
+        }
+        publish_stats(st, red);
+        sync();
+        return decide_fast(red, wi);
+    }
+
+    // FP32 contract: the same operators with every rounding point the
+    // identity; products are plain FP32 (no fast path needed).
+    __device__ __forceinline__ bool finish_fp32(const XSrc &src, float *xs, float *scratch,
+                                                float *bcast) {
+        const int t = threadIdx.x;
+        BlockSync sync;
+        if constexpr (PRO == PRO_PLAIN) {
+#pragma unroll
+            for (int m = 0; m < PER; ++m) xs[t + kT * m] = va[m];
+        } else if constexpr (PRO == PRO_RESNORM || PRO == PRO_EMBED) {
+            const bool blk0 = blockIdx.x == 0;
+#pragma unroll
+            for (int m = 0; m < PER; ++m) {
+                float r;
+                if constexpr (PRO == PRO_EMBED) {
+                    r = va[m];
+                    if (blk0 && src.aux_out) src.aux_out[t + kT * m] = va[m];
+                } else {
+                    r = src.b ? va[m] + vb[m] : va[m];
+                }
+                va[m] = r;
+                xs[t + kT * m] = r;
+                if (blk0 && src.res_out) src.res_out[t + kT * m] = r;
+            }
+            __syncthreads();
+            if (t < kH / 16) {
+                float s = 0.0f;
+#pragma unroll
+                for (int kk = 0; kk < 16; ++kk) {
+                    const float v = xs[16 * t + kk];
+                    s += v * v;
+                }
+                scratch[t] = s;
+            }
+            const float sum = chunk_total(scratch, bcast, sync);
+            const float scale = 1.0f / __builtin_sqrtf(sum / (float)kH + src.eps);
+#pragma unroll
+            for (int m = 0; m < PER; ++m) {
+                const float xn = va[m] * scale * vw[m];
+                xs[t + kT * m] = xn;
+                if constexpr (PRO == PRO_RESNORM) {
+                    if (blk0 && src.aux_out) src.aux_out[t + kT * m] = xn;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < PER; ++m) xs[t + kT * m] = va[m];
+            __syncthreads();
+            if (t < kNH * (kHD / 16)) {
+                float s = 0.0f;
+#pragma unroll
+                for (int kk = 0; kk < 16; ++kk) {
+                    const float v = xs[16 * t + kk];
+                    s += v * v;
+                }
+                scratch[t] = s;
+            }
+            __syncthreads();
+            if (t < kNH) {
+                float sum = 0.0f;
+#pragma unroll
+                for (int ch = 0; ch < kHD / 16; ++ch) sum += scratch[t * (kHD / 16) + ch];
+                bcast[t] = 1.0f / __builtin_sqrtf(sum / (float)kHD + src.eps);
+            }
+            __syncthreads();
+#pragma unroll
+            for (int m = 0; m < PER; ++m) {  // element t + 256 m belongs to head m
+                const float normalized = va[m] * bcast[m] * vw[0];
+                xs[t + kT * m] = normalized * vb[m] * vc[m];
+            }
+        }
+        __syncthreads();
+        return false;
+    }
+};
 
 // ---------------------------------------------------------------- epilogues
 
@@ -405,8 +898,7 @@ struct Epi {
     float *y3;         // QKVG: sigmoid(gate)
     const float *aux;  // QKVG: the layer's small weights
     float *tails;      // QKVG: the layer's conv tails (3 stripes)
-    float *ab;         // QKVG: a[8], b[8]
-    float *bd;         // QKVG: (beta, decay) per head
+    float *ab;         // QKVG: a[8], b[8] (BF16-rounded)
     float *part_val;   // LM: per-block argmax
     int *part_idx;
 };
@@ -421,54 +913,10 @@ __device__ __forceinline__ void head_scalars(float a, float b, float a_log, floa
     decay = exp_cr(decay_val);
 }
 
-// The tiny a/b projections (16 rows: a 0..7, b 8..15) with FP32 products
-// and acc = (acc + tree16(lo)) + tree16(hi) per beat (gdn_gemv_tiny_ab),
-// then the per-head scalars.
-template <int C>
-__device__ void ab_block(const float *__restrict__ aux, const float *xs, float *part, float *lds16,
-                         float *__restrict__ ab, float *__restrict__ bd) {
-    constexpr int HB = Hb<kH>::HB, HBP = Hb<kH>::HBP;
-    const float *abw = aux + kAuxAB;
-#pragma unroll
-    for (int i = 0; i < (16 * HB) / kT; ++i) {
-        const int f = threadIdx.x + kT * i;
-        const int row = f / HB, hb = f - row * HB;
-        const f32x4 *w4 = reinterpret_cast<const f32x4 *>(abw + (size_t)row * kH + hb * 16);
-        float p[16];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const f32x4 wq = w4[q];
-            p[4 * q + 0] = xs[hb * 16 + 4 * q + 0] * wq.x;
-            p[4 * q + 1] = xs[hb * 16 + 4 * q + 1] * wq.y;
-            p[4 * q + 2] = xs[hb * 16 + 4 * q + 2] * wq.z;
-            p[4 * q + 3] = xs[hb * 16 + 4 * q + 3] * wq.w;
-        }
-        part[row * HBP + hb] = tree16(p);
-    }
-    __syncthreads();
-    if (threadIdx.x < 16) {
-        const float *pr = part + threadIdx.x * HBP;
-        float acc = 0.0f;
-        for (int j = 0; j < HB / 2; ++j) acc = (acc + pr[2 * j]) + pr[2 * j + 1];
-        const float r = R<C>(acc);
-        ab[threadIdx.x] = r;
-        lds16[threadIdx.x] = r;
-    }
-    __syncthreads();
-    if (threadIdx.x < kNH) {
-        const int hh = threadIdx.x;
-        float beta, decay;
-        head_scalars(lds16[hh], lds16[kNH + hh], aux[kAuxALog + hh], aux[kAuxDtBias + hh], beta,
-                     decay);
-        bd[2 * hh] = beta;
-        bd[2 * hh + 1] = decay;
-    }
-}
-
 // ------------------------------------------------------------ the GEMV kernel
 
 // Waves per SIMD each GEMV instantiation must fit (caps its VGPRs): the
-// whole grid is then resident at once (QKVG 1025 blocks <= 5 x 256 CUs,
+// whole grid is then resident at once (QKVG 1028 blocks <= 5 x 256 CUs,
 // gate/up 1408 <= 6 x 256) and no straggler block runs in a second round.
 constexpr int gemv_min_waves(int C, int EPI) {
     return C == kFp32 ? 4 : (EPI == EPI_SWIGLU || EPI == EPI_LM) ? 6 : 5;
@@ -478,132 +926,44 @@ template <int C, int K, int RB, int PRO, int EPI>
 __global__ __launch_bounds__(kT, gemv_min_waves(C, EPI)) void k_gemv(const void *__restrict__ W, WInfo wi, XSrc src,
                                              Epi ep) {
     constexpr int HBP = Hb<K>::HBP;
-    constexpr int PART = (EPI == EPI_QKVG ? 16 : RB) * HBP;
-    constexpr int PER = K / kT;  // input values per thread
     static_assert(K % kT == 0, "K splits evenly over the workgroup");
     static_assert(PRO == PRO_PLAIN || K == kH, "normalised inputs are hidden-sized");
-    __shared__ __attribute__((aligned(16))) float xs[K];
-    __shared__ __attribute__((aligned(16))) float part[PART];
+    static_assert(EPI != EPI_QKVG || RB >= kAbRows, "a/b rows fit the partial-sum buffer");
+    __shared__ __attribute__((aligned(16))) uint32_t xs[K];
+    __shared__ __attribute__((aligned(16))) float part[RB * HBP];
     __shared__ __attribute__((aligned(16))) float scratch[kH / 16];
     __shared__ float bcast[kNH];
-    __shared__ float red[4];
-    __shared__ int redi[4];
     const int t = threadIdx.x;
-    // QKVG: block 0 is the a/b block (dispatched first: its serial tail is
-    // the longest), blocks 1.. own the projection rows.
-    const bool ab_blk = (EPI == EPI_QKVG) && blockIdx.x == 0;
-    const int rb = (EPI == EPI_QKVG) ? (int)blockIdx.x - 1 : (int)blockIdx.x;
+    // QKVG: blocks 0..kAbBlocks-1 are the a/b blocks, the rest own the
+    // projection rows.
+    const bool ab_blk = (EPI == EPI_QKVG) && blockIdx.x < kAbBlocks;
+    const int rb = (EPI == EPI_QKVG) ? (int)blockIdx.x - kAbBlocks : (int)blockIdx.x;
 
-    // 1. activation loads (issued before the weight stream)
-    float va[PER], vb[PER], vc[PER], vw[PER];
-    int tok = 0;
-    if constexpr (PRO == PRO_PLAIN) {
-#pragma unroll
-        for (int m = 0; m < PER; ++m) va[m] = src.a[t + kT * m];
-    } else if constexpr (PRO == PRO_RESNORM) {
-#pragma unroll
-        for (int m = 0; m < PER; ++m) {
-            va[m] = src.a[t + kT * m];
-            vb[m] = src.b ? src.b[t + kT * m] : 0.0f;
-            vw[m] = src.w[t + kT * m];
-        }
-    } else if constexpr (PRO == PRO_EMBED) {
-        tok = src.tok[0];
-        if (tok < 0 || tok >= src.vocab) tok = 0;  // the host rejects these first
-#pragma unroll
-        for (int m = 0; m < PER; ++m) {
-            const size_t ix = (size_t)tok * kH + t + kT * m;
-            if constexpr (C == kFp32) va[m] = reinterpret_cast<const float *>(src.emb)[ix];
-            else va[m] = bf16_bits_to_f32(reinterpret_cast<const uint16_t *>(src.emb)[ix]);
-            vw[m] = src.w[t + kT * m];
-        }
-    } else {
-#pragma unroll
-        for (int m = 0; m < PER; ++m) {
-            va[m] = src.a[t + kT * m];
-            vb[m] = src.b[t + kT * m];
-            vc[m] = src.c[t + kT * m];
-        }
-        vw[0] = src.w[t];
-    }
-
-    // 2. the weight stream
+    // 1. activation loads, 2. the weight stream, 3. the prologue proper
+    Prologue<C, K, PRO> pro;
+    pro.load(src);
     WRegs<K, RB, C> w;
-    if (!ab_blk) w.load(W, rb);
-
-    // 3. the prologue proper: the GEMV input lands in LDS
-    XFlags fl;
-    if constexpr (PRO == PRO_PLAIN) {
-#pragma unroll
-        for (int m = 0; m < PER; ++m) {
-            xs[t + kT * m] = va[m];
-            fl.add(va[m]);
-        }
-    } else if constexpr (PRO == PRO_RESNORM || PRO == PRO_EMBED) {
-        const bool blk0 = blockIdx.x == 0;
-#pragma unroll
-        for (int m = 0; m < PER; ++m) {
-            float r;
-            if constexpr (PRO == PRO_EMBED) {
-                r = R<C>(va[m]);
-                if (blk0 && src.aux_out) src.aux_out[t + kT * m] = va[m];
-            } else {
-                r = src.b ? R<C>(va[m] + vb[m]) : va[m];
-            }
-            va[m] = r;
-            xs[t + kT * m] = r;
-            if (blk0 && src.res_out) src.res_out[t + kT * m] = r;
-        }
-        __syncthreads();
-        const float sum = hidden_sumsq(xs, scratch, bcast);
-        const float scale = 1.0f / __builtin_sqrtf(sum / (float)kH + src.eps);
-#pragma unroll
-        for (int m = 0; m < PER; ++m) {
-            const float xn = R<C>(va[m] * scale * vw[m]);
-            xs[t + kT * m] = xn;
-            fl.add(xn);
-            if constexpr (PRO == PRO_RESNORM) {
-                if (blk0 && src.aux_out) src.aux_out[t + kT * m] = xn;
-            }
-        }
+    if constexpr (EPI == EPI_QKVG) {
+        if (ab_blk) w.load_ab(ep.aux + kAuxAB + (size_t)blockIdx.x * kAbRows * kH);
+        else w.load(W, rb);
     } else {
-        // per-head sums of squares of the attention output: 16-value chunks
-        // (threads 0..127), then each head's 16 chunk sums in order (one lane
-        // of wave 0 per head)
-#pragma unroll
-        for (int m = 0; m < PER; ++m) xs[t + kT * m] = va[m];
-        __syncthreads();
-        if (t < kNH * (kHD / 16)) {
-            float s = 0.0f;
-#pragma unroll
-            for (int kk = 0; kk < 16; ++kk) {
-                const float v = xs[16 * t + kk];
-                s += v * v;
-            }
-            scratch[t] = s;
-        }
-        __syncthreads();
-        if (t < kNH) {
-            float sum = 0.0f;
-#pragma unroll
-            for (int ch = 0; ch < kHD / 16; ++ch) sum += scratch[t * (kHD / 16) + ch];
-            bcast[t] = 1.0f / __builtin_sqrtf(sum / (float)kHD + src.eps);
-        }
-        __syncthreads();
-#pragma unroll
-        for (int m = 0; m < PER; ++m) {  // element t + 256 m belongs to head m
-            const float normalized = va[m] * bcast[m] * vw[0];
-            const float x = R<C>(normalized * vb[m] * vc[m]);
-            xs[t + kT * m] = x;
-            fl.add(x);
-        }
+        w.load(W, rb);
     }
-    const bool fast = fast_verdict<C>(fl, wi, red, redi);
+    static_assert(C == kFp32, "BF16 contracts use k_gemv_cu");
+    const bool fast = pro.finish_fp32(src, reinterpret_cast<float *>(xs), scratch, bcast);
 
     // 4. products and reduction
     if constexpr (EPI == EPI_QKVG) {
         if (ab_blk) {
-            ab_block<C>(ep.aux, xs, part, scratch, ep.ab, ep.bd);
+            // acc = (acc + tree16(lo)) + tree16(hi) per beat, rounded
+            w.compute_ab(xs, part);
+            __syncthreads();
+            if (t < kAbRows) {
+                const float *pr = part + t * HBP;
+                float acc = 0.0f;
+                for (int j = 0; j < Hb<kH>::NB; ++j) acc = (acc + pr[2 * j]) + pr[2 * j + 1];
+                ep.ab[blockIdx.x * kAbRows + t] = R<C>(acc);
+            }
             return;
         }
     }
@@ -680,6 +1040,278 @@ __global__ __launch_bounds__(kT, gemv_min_waves(C, EPI)) void k_gemv(const void 
     }
 }
 
+// ------------------------------------------------ CU-resident GEMV (BF16)
+//
+// One 1024-thread workgroup per CU (it claims all 512 VGPRs of every SIMD,
+// so no two share one) owns ROWS consecutive rows of the matrix, a
+// contiguous slice of the weight stream, and walks it in chunks of CR rows
+// held in registers (two chunk buffers when there are several chunks: the
+// loads of chunk c + 2 are issued as soon as chunk c has been multiplied).
+// The activation reads are issued, and a barrier passed, before any weight
+// read: the vector memory path of a CU serves requests in order, so an
+// activation read issued after a weight stream waits for all of it.  The
+// prologue (residual add, norms) then runs once per CU while the CU's
+// weights stream in.
+constexpr int kTB = 1024;  // threads per CU-resident workgroup
+// Rows per CU-resident workgroup (grids of 256 workgroups).
+constexpr int kCuQkvg = 32;   // 8192 / 256
+constexpr int kCuO = 8;       // 2048 / 256
+constexpr int kCuGu = 44;     // 22 gate + 22 up rows: 11264 / 256
+constexpr int kCuDown = 8;    // 2048 / 256
+constexpr int kCuLm = 125;    // 32000 / 256, in chunks of 25
+constexpr int kCuLmChunk = 25;
+constexpr int kCuLmSmall = 8; // vocabularies that 125 does not divide
+
+template <int K, int CR, int C>
+struct WChunk {
+    static constexpr int HB = Hb<K>::HB, HBP = Hb<K>::HBP;
+    static constexpr int ITEMS = CR * HB;
+    static constexpr int NIT = (ITEMS + kTB - 1) / kTB;
+    static constexpr bool kFull = (ITEMS % kTB) == 0;
+    static constexpr bool kSameHb = (kTB % HB) == 0;
+    static_assert(C != kFp32, "BF16 weights");
+    u32x4 v[NIT][2];
+
+    // chunk: the chunk's first row; item f is the 16 elements at 16 f
+    __device__ __forceinline__ void load(const uint16_t *__restrict__ chunk) {
+        const u32x4 *wb = reinterpret_cast<const u32x4 *>(chunk);
+#pragma unroll
+        for (int i = 0; i < NIT; ++i) {
+            const int f = threadIdx.x + kTB * i;
+            if (kFull || f < ITEMS) {
+                v[i][0] = __builtin_nontemporal_load(wb + 2 * f);
+                v[i][1] = __builtin_nontemporal_load(wb + 2 * f + 1);
+            }
+        }
+    }
+
+    template <bool FAST>
+    __device__ __forceinline__ void compute(const uint32_t *xs, float *part) const {
+        uint32_t xv[16];
+        if constexpr (kSameHb) lds_load16u(xs + (threadIdx.x % HB) * 16, xv);
+#pragma unroll
+        for (int i = 0; i < NIT; ++i) {
+            const int f = threadIdx.x + kTB * i;
+            if (kFull || f < ITEMS) {
+                const int row = f / HB, hb = f - row * HB;
+                if constexpr (!kSameHb) lds_load16u(xs + hb * 16, xv);
+                const uint32_t w8[8] = {v[i][0].x, v[i][0].y, v[i][0].z, v[i][0].w,
+                                        v[i][1].x, v[i][1].y, v[i][1].z, v[i][1].w};
+                float p[16];
+                if constexpr (FAST) {
+                    uint32_t rbits[8];
+                    dot8_bf16(w8, xv, rbits);
+                    dot8_bf16(w8 + 4, xv + 8, rbits + 4);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        p[2 * e] = u2f(rbits[e] << 16);
+                        p[2 * e + 1] = u2f(rbits[e] & 0xffff0000u);
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        p[2 * e] = native_exact(w8[e] & 0xffffu, u2f(xv[2 * e] << 16));
+                        p[2 * e + 1] = native_exact(w8[e] >> 16, u2f(xv[2 * e + 1]));
+                    }
+                }
+                part[row * HBP + hb] = tree16(p);
+            }
+        }
+    }
+};
+
+// Bank chains of CR rows: thread L < 4 CR runs chain L & 3 of row L >> 2
+// (the waves that hold those threads call this); lane 4r ends with row r.
+template <int K, int CR>
+__device__ __forceinline__ float chain_rows(const float *part) {
+    constexpr int HBP = Hb<K>::HBP, NB = Hb<K>::NB;
+    const int L = threadIdx.x;
+    float acc = 0.0f;
+    if (L < CR * 4) {
+        const int row = L >> 2, parity = (L >> 1) & 1, half = L & 1;
+        const float *pr = part + row * HBP + half;
+#pragma unroll 8
+        for (int b = parity; b < NB; b += 2) acc = acc + pr[2 * b];
+    }
+    const float s = acc + __shfl_xor(acc, 1);
+    return s + __shfl_xor(s, 2);
+}
+
+template <int N>
+using IC = std::integral_constant<int, N>;
+
+// ROWS rows per workgroup (grid = M / ROWS), CR rows per chunk.
+//   EPI_QKVG    rows are q|k|v|g; workgroups 0..15 also run a/b row blockIdx
+//   EPI_SWIGLU  a workgroup's rows are ROWS/2 gate rows then the matching
+//               ROWS/2 up rows
+//   EPI_LM      FP32 logits and the workgroup's argmax
+template <int C, int K, int ROWS, int CR, int PRO, int EPI>
+__global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, WInfo wi, XSrc src,
+                                                   Epi ep) {
+    constexpr int HBP = Hb<K>::HBP, NCH = ROWS / CR, NPART = NCH > 1 ? 2 : 1;
+    constexpr int CHW = (4 * CR + 63) / 64;  // waves that run bank chains
+    static_assert(ROWS % CR == 0 && NCH <= 6, "whole chunks");
+    static_assert(K % kT == 0 && (PRO == PRO_PLAIN || K == kH), "input shape");
+    static_assert(EPI != EPI_QKVG || (ROWS == CR && CHW < 16), "a/b rows use the last wave");
+    __shared__ __attribute__((aligned(16))) uint32_t xs[K];
+    __shared__ __attribute__((aligned(16))) float part[NPART][CR * HBP];
+    __shared__ __attribute__((aligned(16))) float scratch[kH / 16];
+    __shared__ float bcast[kNH];
+    __shared__ uint32_t red[8];
+    __shared__ float ybuf[ROWS];
+    __shared__ float abpart[Hb<kH>::HB];
+    // claim the whole register file (128 VGPRs x 16 waves): one workgroup per CU
+    asm volatile("" ::: "v127");
+    const int t = threadIdx.x, wave = t >> 6;
+    const int row0 = blockIdx.x * ROWS;
+    const uint16_t *wblk = static_cast<const uint16_t *>(W) + (size_t)row0 * K;
+    __shared__ int arrive;  // Wave4Sync arrivals of the prologue waves
+    if (t == 0) arrive = 0;
+    __syncthreads();  // before any load: the waves are just starting
+
+    // 1. activation reads (waves 0..3 own the input elements), issued
+    // before their weight loads
+    Prologue<C, K, PRO> pro;
+    if (t < kT) pro.load(src);
+
+    // 2. the weight stream (and the a/b row of QKVG workgroups 0..15)
+    WChunk<K, CR, C> wa, wb;
+    wa.load(wblk);
+    if constexpr (NCH > 1) wb.load(wblk + (size_t)CR * K);
+    u32x4 abw[4];
+    const bool ab_blk = (EPI == EPI_QKVG) && blockIdx.x < 2 * kNH;
+    if constexpr (EPI == EPI_QKVG) {
+        if (ab_blk && t < Hb<kH>::HB) {
+            const u32x4 *src4 = reinterpret_cast<const u32x4 *>(ep.aux + kAuxAB + (size_t)blockIdx.x * kH + t * 16);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) abw[q] = src4[q];
+        }
+    }
+
+    // 3. the input vector in LDS and the fast-path verdict: waves 0..3 build
+    // it (synchronising only among themselves); the other waves, once their
+    // loads are issued, wait for the prologue's last arrival
+    bool fast;
+    if (t < kT) {
+        Wave4Sync sync{&arrive};
+        fast = pro.finish_bf16(src, wi, xs, scratch, bcast, red, sync);
+    } else {
+        wait_count(&arrive, 4 * Prologue<C, K, PRO>::kSyncs);
+        fast = decide_fast(red, wi);
+    }
+
+    // 4. per chunk: products, barrier, bank chains and the row epilogue
+    auto step = [&](auto &w, auto cidx) {
+        constexpr int c = decltype(cidx)::value;
+        float *pc = part[c % NPART];
+        if (fast) w.template compute<true>(xs, pc);
+        else w.template compute<false>(xs, pc);
+        if constexpr (c + 2 < NCH) w.load(wblk + (size_t)(c + 2) * CR * K);
+        if constexpr (EPI == EPI_QKVG) {
+            if (ab_blk && t < Hb<kH>::HB) {
+                // FP32 products x * w, tree16 per half-beat (gdn_gemv_tiny_ab)
+                uint32_t xv[16];
+                lds_load16u(xs + t * 16, xv);
+                float p[16];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    p[4 * q + 0] = lane_word_value(xv[4 * q + 0], 0) * u2f(abw[q].x);
+                    p[4 * q + 1] = lane_word_value(xv[4 * q + 1], 1) * u2f(abw[q].y);
+                    p[4 * q + 2] = lane_word_value(xv[4 * q + 2], 0) * u2f(abw[q].z);
+                    p[4 * q + 3] = lane_word_value(xv[4 * q + 3], 1) * u2f(abw[q].w);
+                }
+                abpart[t] = tree16(p);
+            }
+        }
+        __syncthreads();
+        if constexpr (EPI == EPI_QKVG) {
+            if (ab_blk && t == kTB - 64) {
+                // acc = (acc + tree16(lo)) + tree16(hi) per beat, rounded
+                float acc = 0.0f;
+                for (int j = 0; j < Hb<kH>::NB; ++j) acc = (acc + abpart[2 * j]) + abpart[2 * j + 1];
+                ep.ab[blockIdx.x] = R<C>(acc);
+            }
+        }
+        if (wave >= CHW) return;
+        const float y = chain_rows<K, CR>(pc);
+        const bool owner = (t & 3) == 0 && (t >> 2) < CR;
+        if (!owner) return;
+        const int rr = c * CR + (t >> 2);  // row within the workgroup
+        const int r = row0 + rr;
+        if constexpr (EPI == EPI_RAW) {
+            ep.y[r] = y;
+        } else if constexpr (EPI == EPI_STORE) {
+            ep.y[r] = R<C>(y);
+        } else if constexpr (EPI == EPI_QKVG) {
+            const float yv = R<C>(y);
+            if (r < 3 * kH) {
+                // causal conv over [t0, t1, t2, x] + SiLU; tails shift to [t1, t2, x]
+                const int kind = r / kH, ch = r - kind * kH;
+                const float *cw = ep.aux + kAuxConv + ((size_t)kind * kH + ch) * 4;
+                uint16_t *tl = reinterpret_cast<uint16_t *>(ep.tails + (size_t)kind * kTailStripe);
+                const uint16_t b0 = tl[ch], b1 = tl[kH + ch], b2 = tl[2 * kH + ch];
+                const float t0 = bf16_bits_to_f32(b0), t1 = bf16_bits_to_f32(b1), t2 = bf16_bits_to_f32(b2);
+                tl[ch] = b1;
+                tl[kH + ch] = b2;
+                tl[2 * kH + ch] = (uint16_t)(f2u(yv) >> 16);
+                const float s = t0 * cw[0] + t1 * cw[1] + t2 * cw[2] + yv * cw[3];
+                ep.y[r] = R<C>(silu_ref(s));
+            } else {
+                ep.y2[r - 3 * kH] = yv;
+                ep.y3[r - 3 * kH] = sigmoid_ref(yv);
+            }
+        } else if constexpr (EPI == EPI_SWIGLU) {
+            ybuf[rr] = R<C>(y);
+        } else {
+            ep.y[r] = y;  // LM: FP32 logits (no rounding point)
+            ybuf[rr] = y;
+        }
+    };
+    step(wa, IC<0>{});
+    if constexpr (NCH > 1) step(wb, IC<1>{});
+    if constexpr (NCH > 2) step(wa, IC<2>{});
+    if constexpr (NCH > 3) step(wb, IC<3>{});
+    if constexpr (NCH > 4) step(wa, IC<4>{});
+    if constexpr (NCH > 5) step(wb, IC<5>{});
+
+    // 5. workgroup epilogues over all rows
+    if constexpr (EPI == EPI_SWIGLU) {
+        __syncthreads();
+        if (t < ROWS / 2) {
+            const float g = ybuf[t], u = ybuf[t + ROWS / 2];
+            ep.y[blockIdx.x * (ROWS / 2) + t] = R<C>(silu_ref(g) * u);
+        }
+    } else if constexpr (EPI == EPI_LM) {
+        // the workgroup's argmax in row order: strict '>' within a lane's
+        // rows, then a merge that keeps the larger value and, on ties, the
+        // lower index (NaN never wins)
+        __syncthreads();
+        if (wave != 0) return;
+        float best = -3.402823466e38f;
+        int idx = 0;
+        for (int i = t; i < ROWS; i += 64) {
+            const float v = ybuf[i];
+            if (v > best) {
+                best = v;
+                idx = row0 + i;
+            }
+        }
+#pragma unroll
+        for (int m = 1; m < 64; m <<= 1) {
+            const float ov = __shfl_xor(best, m);
+            const int oi = __shfl_xor(idx, m);
+            if (ov > best || (ov == best && oi < idx)) {
+                best = ov;
+                idx = oi;
+            }
+        }
+        if (t == 0) {
+            ep.part_val[blockIdx.x] = best;
+            ep.part_idx[blockIdx.x] = idx;
+        }
+    }
+}
+
 // Second argmax stage over the LM head's per-block results, which are in
 // index order: strict '>' within a thread's increasing indices, then a
 // merge that keeps the larger value and, on ties, the lower index.
@@ -734,7 +1366,10 @@ template <int C, int CB>
 __global__ __launch_bounds__(kT) void k_recur(const float *__restrict__ qp,
                                               const float *__restrict__ kp,
                                               const float *__restrict__ vp,
-                                              const float *__restrict__ bd,
+                                              const float *__restrict__ ap,
+                                              const float *__restrict__ bp,
+                                              const float *__restrict__ a_log,
+                                              const float *__restrict__ dt_bias,
                                               void *__restrict__ state, float *__restrict__ attn) {
     static_assert(CB <= 64 && (CB % 8) == 0, "one wave owns the column chains");
     constexpr int PER_ROW = (C == kRef) ? CB / 8 : CB / 4;  // 16-byte loads per tile row
@@ -750,7 +1385,6 @@ __global__ __launch_bounds__(kT) void k_recur(const float *__restrict__ qp,
 
     const float q = qp[h * kHD + t], k = kp[h * kHD + t];
     const float vi = (t < CB) ? vp[h * kHD + c0 + t] : 0.0f;
-    const float beta = bd[2 * h], decay = bd[2 * h + 1];
     u32x4 tr[NLD];
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
@@ -763,6 +1397,10 @@ __global__ __launch_bounds__(kT) void k_recur(const float *__restrict__ qp,
                                                      (size_t)row * kHD + cq * 4);
         }
     }
+
+    // beta/decay from the head's a and b while the tile is in flight
+    float beta, decay;
+    head_scalars(ap[h], bp[h], a_log[h], dt_bias[h], beta, decay);
 
     const float qs = wave_tree64(q * q), ks = wave_tree64(k * k);
     if (lane == 0) {
@@ -777,8 +1415,8 @@ __global__ __launch_bounds__(kT) void k_recur(const float *__restrict__ qp,
     const float qv = q * q_inv, kv = k * k_inv;
     qn[t] = qv;
     kn[t] = kv;
-    const float ap = wave_tree64(qv * kv);
-    if (lane == 0) red2[w] = ap;
+    const float qk = wave_tree64(qv * kv);
+    if (lane == 0) red2[w] = qk;
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
         const int u = t + kT * i, row = u / PER_ROW, cq = u - row * PER_ROW;
@@ -844,20 +1482,6 @@ __global__ __launch_bounds__(kT) void k_recur(const float *__restrict__ qp,
     }
 }
 
-// beta/decay for n heads from raw (a, b, a_log, dt_bias) (isolated-kernel hook).
-__global__ __launch_bounds__(kT) void k_head_scalars(const float *__restrict__ a,
-                                                     const float *__restrict__ b,
-                                                     const float *__restrict__ a_log,
-                                                     const float *__restrict__ dt_bias, int n,
-                                                     float *__restrict__ bd) {
-    const int i = blockIdx.x * kT + threadIdx.x;
-    if (i >= n) return;
-    float beta, decay;
-    head_scalars(a[i], b[i], a_log[i], dt_bias[i], beta, decay);
-    bd[2 * i] = beta;
-    bd[2 * i + 1] = decay;
-}
-
 // out = R(a + b) over the hidden vector (layer output for the layer hook).
 template <int C>
 __global__ __launch_bounds__(kT) void k_resadd(const float *__restrict__ a,
@@ -891,7 +1515,7 @@ struct GDNEngine {
     float *ws = nullptr;
     float *act = nullptr;
     float *resid = nullptr, *resid_alt = nullptr, *fhid = nullptr, *qkv = nullptr,
-          *gate = nullptr, *sgate = nullptr, *ab = nullptr, *bd = nullptr, *attn = nullptr,
+          *gate = nullptr, *sgate = nullptr, *ab = nullptr, *attn = nullptr,
           *ybuf_o = nullptr, *dbuf = nullptr, *hbuf = nullptr, *lm_val = nullptr;
     int *lm_idx = nullptr;
     int *tok_dev = nullptr;   // [0] in, [1] out
@@ -922,25 +1546,27 @@ struct Packer {
     int contract;
     std::vector<unsigned char> staging;
     float min_abs = INFINITY;
+    float max_abs = 0.0f;
     int nonfinite = 0;
     size_t filled = 0;  // elements
 
     void begin(size_t elems) {
         staging.resize(elems * welem(contract));
         min_abs = INFINITY;
+        max_abs = 0.0f;
         nonfinite = 0;
         filled = 0;
     }
     void rows(const float *src, size_t n, bool daz = true) {
-        float mn;
+        float mn, mx;
         int bad;
         if (contract == kFp32) {
             std::memcpy(staging.data() + filled * 4, src, n * 4);
-            gdn_scan_fp32(src, n, &mn, &bad);
+            gdn_scan_fp32(src, n, &mn, &mx, &bad);
         } else {
             uint16_t *d = reinterpret_cast<uint16_t *>(staging.data()) + filled;
             if (daz) {
-                gdn_pack_bf16_daz(src, d, n, &mn, &bad);
+                gdn_pack_bf16_daz(src, d, n, &mn, &mx, &bad);
             } else {
                 for (size_t i = 0; i < n; ++i) {
                     uint32_t b;
@@ -948,10 +1574,12 @@ struct Packer {
                     d[i] = (uint16_t)(b >> 16);
                 }
                 mn = INFINITY;
+                mx = 0.0f;
                 bad = 0;
             }
         }
         if (mn < min_abs) min_abs = mn;
+        if (mx > max_abs) max_abs = mx;
         nonfinite |= bad;
         filled += n;
     }
@@ -959,7 +1587,7 @@ struct Packer {
         GDN_HIP(hipMemcpy(dst, staging.data(), filled * welem(contract), hipMemcpyHostToDevice));
         return 0;
     }
-    WInfo info() const { return WInfo{min_abs, nonfinite}; }
+    WInfo info() const { return WInfo{min_abs, max_abs, nonfinite}; }
 };
 
 int check_shape(const GDNWeightHeader *c) {
@@ -1008,10 +1636,13 @@ int upload_weights(GDNEngine *e, const GDNModel *m) {
         if (pk.upload(p)) return -1;
         p += H * H * es;
 
+        // gate/up rows interleaved per workgroup: G gate rows, then the
+        // matching G up rows
         pk.begin(2 * I * H);
-        for (size_t blk = 0; blk < I / (kRbGu / 2); ++blk) {
-            pk.rows(w.mlp_gate_proj + blk * (kRbGu / 2) * H, (kRbGu / 2) * H);
-            pk.rows(w.mlp_up_proj + blk * (kRbGu / 2) * H, (kRbGu / 2) * H);
+        const size_t G = (e->contract == kFp32) ? kRbGu / 2 : kCuGu / 2;
+        for (size_t blk = 0; blk < I / G; ++blk) {
+            pk.rows(w.mlp_gate_proj + blk * G * H, G * H);
+            pk.rows(w.mlp_up_proj + blk * G * H, G * H);
         }
         e->w_gu[l] = p;
         e->i_gu[l] = pk.info();
@@ -1066,7 +1697,7 @@ int alloc_buffers(GDNEngine *e) {
     GDN_HIP(hipMalloc(&e->ws, (size_t)GDN_WS_FLOATS * 4));
     GDN_HIP(hipMemset(e->ws, 0, (size_t)GDN_WS_FLOATS * 4));
     const size_t nblk_lm = (size_t)e->vocab / kRbLm;
-    const size_t act_floats = 3 * kH + 3 * kH + 2 * kH + 16 + 2 * kNH + 3 * kH + kI + nblk_lm;
+    const size_t act_floats = 3 * kH + 3 * kH + 2 * kH + 16 + 3 * kH + kI + nblk_lm;
     GDN_HIP(hipMalloc(&e->act, act_floats * 4));
     GDN_HIP(hipMemset(e->act, 0, act_floats * 4));
     float *p = e->act;
@@ -1077,7 +1708,6 @@ int alloc_buffers(GDNEngine *e) {
     e->gate = p; p += kH;
     e->sgate = p; p += kH;
     e->ab = p; p += 16;
-    e->bd = p; p += 2 * kNH;
     e->attn = p; p += kH;
     e->ybuf_o = p; p += kH;
     e->dbuf = p; p += kH;
@@ -1109,7 +1739,9 @@ XSrc xsrc(const float *a, const float *b, const float *c, const float *w, float 
 
 // Per-kernel launches.  The QKVG prologue (PRO0) takes the embedding row
 // (first layer of a step), the previous layer's residual (res_b = its down
-// output), or a caller-given residual (res_b = nullptr).
+// output), or a caller-given residual (res_b = nullptr).  BF16 contracts use
+// the CU-resident kernels (grids of 256), the FP32 control arm the
+// row-block kernels.
 template <int C, int PRO0>
 void launch_qkvg(GDNEngine *e, int l, const float *res_a, const float *res_b, hipStream_t s) {
     float *aux = layer_aux(e, l);
@@ -1120,7 +1752,6 @@ void launch_qkvg(GDNEngine *e, int l, const float *res_a, const float *res_b, hi
     q.aux = aux;
     q.tails = layer_tails(e, l);
     q.ab = e->ab;
-    q.bd = e->bd;
     XSrc xq = xsrc(res_a, res_b, nullptr, aux + kAuxAttnNorm, e->resid, nullptr, e->eps);
     if constexpr (PRO0 == PRO_EMBED) {
         xq.emb = e->w_emb;
@@ -1128,45 +1759,70 @@ void launch_qkvg(GDNEngine *e, int l, const float *res_a, const float *res_b, hi
         xq.vocab = e->vocab;
         xq.aux_out = e->ws + GDN_WS_OFF_X;
     }
-    hipLaunchKernelGGL((k_gemv<C, kH, kRbQkvg, PRO0, EPI_QKVG>), dim3(4 * kH / kRbQkvg + 1), dim3(kT),
-                       0, s, e->w_qkvg[l], e->i_qkvg[l], xq, q);
+    if constexpr (C == kFp32) {
+        hipLaunchKernelGGL((k_gemv<C, kH, kRbQkvg, PRO0, EPI_QKVG>), dim3(4 * kH / kRbQkvg + kAbBlocks),
+                           dim3(kT), 0, s, e->w_qkvg[l], e->i_qkvg[l], xq, q);
+    } else {
+        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuQkvg, kCuQkvg, PRO0, EPI_QKVG>), dim3(4 * kH / kCuQkvg),
+                           dim3(kTB), 0, s, e->w_qkvg[l], e->i_qkvg[l], xq, q);
+    }
 }
 
 template <int C>
 void launch_recur(GDNEngine *e, int l, hipStream_t s) {
+    const float *aux = layer_aux(e, l);
     hipLaunchKernelGGL((k_recur<C, kCB>), dim3(kHD / kCB, kNH), dim3(kT), 0, s, e->qkv,
-                       e->qkv + kH, e->qkv + 2 * kH, e->bd, layer_state(e, l), e->attn);
+                       e->qkv + kH, e->qkv + 2 * kH, e->ab, e->ab + kNH, aux + kAuxALog,
+                       aux + kAuxDtBias, layer_state(e, l), e->attn);
 }
 
 template <int C>
 void launch_o(GDNEngine *e, int l, hipStream_t s) {
     Epi st{};
     st.y = e->ybuf_o;
-    hipLaunchKernelGGL((k_gemv<C, kH, kRbO, PRO_ONORM, EPI_STORE>), dim3(kH / kRbO), dim3(kT), 0, s,
-                       e->w_o[l], e->i_o[l],
-                       xsrc(e->attn, e->gate, e->sgate, layer_aux(e, l) + kAuxONorm, nullptr, nullptr,
-                            e->eps),
-                       st);
+    const XSrc xo = xsrc(e->attn, e->gate, e->sgate, layer_aux(e, l) + kAuxONorm, nullptr, nullptr, e->eps);
+    if constexpr (C == kFp32) {
+        hipLaunchKernelGGL((k_gemv<C, kH, kRbO, PRO_ONORM, EPI_STORE>), dim3(kH / kRbO), dim3(kT), 0, s,
+                           e->w_o[l], e->i_o[l], xo, st);
+    } else {
+        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuO, kCuO, PRO_ONORM, EPI_STORE>), dim3(kH / kCuO), dim3(kTB),
+                           0, s, e->w_o[l], e->i_o[l], xo, st);
+    }
 }
 
 template <int C>
 void launch_gu(GDNEngine *e, int l, hipStream_t s) {
     Epi sw{};
     sw.y = e->hbuf;
-    hipLaunchKernelGGL((k_gemv<C, kH, kRbGu, PRO_RESNORM, EPI_SWIGLU>), dim3(2 * kI / kRbGu), dim3(kT),
-                       0, s, e->w_gu[l], e->i_gu[l],
-                       xsrc(e->resid, e->ybuf_o, nullptr, layer_aux(e, l) + kAuxMlpNorm, e->resid_alt,
-                            nullptr, e->eps),
-                       sw);
+    const XSrc xg = xsrc(e->resid, e->ybuf_o, nullptr, layer_aux(e, l) + kAuxMlpNorm, e->resid_alt,
+                         nullptr, e->eps);
+    if constexpr (C == kFp32) {
+        hipLaunchKernelGGL((k_gemv<C, kH, kRbGu, PRO_RESNORM, EPI_SWIGLU>), dim3(2 * kI / kRbGu), dim3(kT),
+                           0, s, e->w_gu[l], e->i_gu[l], xg, sw);
+    } else {
+        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuGu, kCuGu, PRO_RESNORM, EPI_SWIGLU>), dim3(2 * kI / kCuGu),
+                           dim3(kTB), 0, s, e->w_gu[l], e->i_gu[l], xg, sw);
+    }
 }
 
 template <int C>
 void launch_down(GDNEngine *e, int l, hipStream_t s) {
     Epi dn{};
     dn.y = e->dbuf;
-    hipLaunchKernelGGL((k_gemv<C, kI, kRbDown, PRO_PLAIN, EPI_STORE>), dim3(kH / kRbDown), dim3(kT), 0,
-                       s, e->w_down[l], e->i_down[l],
-                       xsrc(e->hbuf, nullptr, nullptr, nullptr, nullptr, nullptr, e->eps), dn);
+    const XSrc xd = xsrc(e->hbuf, nullptr, nullptr, nullptr, nullptr, nullptr, e->eps);
+    if constexpr (C == kFp32) {
+        hipLaunchKernelGGL((k_gemv<C, kI, kRbDown, PRO_PLAIN, EPI_STORE>), dim3(kH / kRbDown), dim3(kT), 0,
+                           s, e->w_down[l], e->i_down[l], xd, dn);
+    } else {
+        hipLaunchKernelGGL((k_gemv_cu<C, kI, kCuDown, kCuDown, PRO_PLAIN, EPI_STORE>), dim3(kH / kCuDown),
+                           dim3(kTB), 0, s, e->w_down[l], e->i_down[l], xd, dn);
+    }
+}
+
+// LM-head workgroups (= first-stage argmax results) of a contract/vocabulary.
+int lm_blocks(const GDNEngine *e) {
+    if (e->contract == kFp32) return e->vocab / kRbLm;
+    return (e->vocab % kCuLm) == 0 ? e->vocab / kCuLm : e->vocab / kCuLmSmall;
 }
 
 template <int C>
@@ -1175,13 +1831,22 @@ void launch_lm(GDNEngine *e, hipStream_t s) {
     lm.y = e->ws + GDN_WS_OFF_LOGITS;
     lm.part_val = e->lm_val;
     lm.part_idx = e->lm_idx;
-    hipLaunchKernelGGL((k_gemv<C, kH, kRbLm, PRO_RESNORM, EPI_LM>), dim3(e->vocab / kRbLm), dim3(kT), 0,
-                       s, e->w_lm, e->i_lm,
-                       xsrc(e->resid_alt, e->dbuf, nullptr, final_norm(e), e->resid, e->fhid, e->eps), lm);
+    const XSrc xl = xsrc(e->resid_alt, e->dbuf, nullptr, final_norm(e), e->resid, e->fhid, e->eps);
+    const dim3 grid(lm_blocks(e));
+    if constexpr (C == kFp32) {
+        hipLaunchKernelGGL((k_gemv<C, kH, kRbLm, PRO_RESNORM, EPI_LM>), grid, dim3(kT), 0, s, e->w_lm,
+                           e->i_lm, xl, lm);
+    } else if ((e->vocab % kCuLm) == 0) {
+        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuLm, kCuLmChunk, PRO_RESNORM, EPI_LM>), grid, dim3(kTB), 0, s,
+                           e->w_lm, e->i_lm, xl, lm);
+    } else {
+        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuLmSmall, kCuLmSmall, PRO_RESNORM, EPI_LM>), grid, dim3(kTB),
+                           0, s, e->w_lm, e->i_lm, xl, lm);
+    }
 }
 
 void launch_argmax(GDNEngine *e, hipStream_t s) {
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(kT), 0, s, e->lm_val, e->lm_idx, e->vocab / kRbLm,
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(kT), 0, s, e->lm_val, e->lm_idx, lm_blocks(e),
                        e->tok_dev + 1, e->ws + GDN_WS_OFF_X_NORM);
 }
 
@@ -1542,18 +2207,22 @@ int gdn_test_gemv(int contract, const float *W, const float *x, uint32_t M, uint
     const dim3 grid(M / kRbTest), block(kT);
 #define GDN_PLAIN(CC, KK)                                                                     \
     hipLaunchKernelGGL((k_gemv<CC, KK, kRbTest, PRO_PLAIN, EPI_RAW>), grid, block, 0, 0, dW, wi, xs, ep)
+#define GDN_PLAIN_CU(KK)                                                                      \
+    hipLaunchKernelGGL((k_gemv_cu<kRef, KK, kRbTest, kRbTest, PRO_PLAIN, EPI_RAW>), grid, dim3(kTB), 0, 0, \
+                       dW, wi, xs, ep)
     XSrc xs{};
     xs.a = dx;
     Epi ep{};
     ep.y = dy;
     if (K == (uint32_t)kH) {
         if (contract == kFp32) GDN_PLAIN(kFp32, kH);
-        else GDN_PLAIN(kRef, kH);
+        else GDN_PLAIN_CU(kH);
     } else {
         if (contract == kFp32) GDN_PLAIN(kFp32, kI);
-        else GDN_PLAIN(kRef, kI);
+        else GDN_PLAIN_CU(kI);
     }
 #undef GDN_PLAIN
+#undef GDN_PLAIN_CU
     GDN_HIP(hipGetLastError());
     GDN_HIP(hipMemcpy(y, dy, (size_t)M * 4, hipMemcpyDeviceToHost));
     GDN_HIP(hipFree(dW));
@@ -1597,16 +2266,12 @@ int gdn_test_recurrence(int contract, uint32_t n_heads, uint32_t n_steps, const 
     } else {
         GDN_HIP(hipMemcpy(dS, S, nstate * 4, hipMemcpyHostToDevice));
     }
-    float *dbd;
-    GDN_HIP(hipMalloc(&dbd, 2 * ns * 4));
-    hipLaunchKernelGGL(k_head_scalars, dim3((unsigned)((ns + kT - 1) / kT)), dim3(kT), 0, 0, da, db, dal,
-                       ddt, (int)ns, dbd);
     const dim3 grid(kHD / kCB, n_heads), block(kT);
     for (uint32_t s = 0; s < n_steps; ++s) {
         const size_t ov = (size_t)s * n_heads * kHD, os = (size_t)s * n_heads;
 #define GDN_REC(CC)                                                                             \
-    hipLaunchKernelGGL((k_recur<CC, kCB>), grid, block, 0, 0, dq + ov, dk + ov, dv + ov, dbd + 2 * os, \
-                       dS, dout + ov)
+    hipLaunchKernelGGL((k_recur<CC, kCB>), grid, block, 0, 0, dq + ov, dk + ov, dv + ov, da + os,  \
+                       db + os, dal + os, ddt + os, dS, dout + ov)
         if (contract == kRef) GDN_REC(kRef);
         else if (contract == kBf16w) GDN_REC(kBf16w);
         else GDN_REC(kFp32);
@@ -1625,7 +2290,7 @@ int gdn_test_recurrence(int contract, uint32_t n_heads, uint32_t n_steps, const 
     } else {
         GDN_HIP(hipMemcpy(S, dS, nstate * 4, hipMemcpyDeviceToHost));
     }
-    float *bufs[] = {dq, dk, dv, da, db, dal, ddt, dout, dbd};
+    float *bufs[] = {dq, dk, dv, da, db, dal, ddt, dout};
     for (float *p : bufs) GDN_HIP(hipFree(p));
     GDN_HIP(hipFree(dS));
     return 0;

@@ -344,11 +344,11 @@ uint16_t gdn_native_product_bits_host(uint16_t w, uint16_t x) {
     return r;
 }
 
-void gdn_pack_bf16_daz(const float *src, uint16_t *dst, size_t n, float *min_abs,
+void gdn_pack_bf16_daz(const float *src, uint16_t *dst, size_t n, float *min_abs, float *max_abs,
                        int *nonfinite) {
-    float mn = INFINITY;
+    float mn = INFINITY, mx = 0.0f;
     int bad = 0;
-#pragma omp parallel for schedule(static) reduction(min : mn) reduction(| : bad)
+#pragma omp parallel for schedule(static) reduction(min : mn) reduction(max : mx) reduction(| : bad)
     for (long long i = 0; i < (long long)n; ++i) {
         uint16_t b = (uint16_t)(f2u(src[i]) >> 16);
         const uint16_t e = (uint16_t)((b >> 7) & 0xffu);
@@ -356,22 +356,29 @@ void gdn_pack_bf16_daz(const float *src, uint16_t *dst, size_t n, float *min_abs
         if (e == 0xffu) bad = 1;
         dst[i] = b;
         const float a = std::fabs(u2f((uint32_t)b << 16));
+        if (e != 0xffu && a > mx) mx = a;
         if (a != 0.0f && a < mn) mn = a;
     }
     *min_abs = mn;
+    *max_abs = mx;
     *nonfinite = bad;
 }
 
-void gdn_scan_fp32(const float *src, size_t n, float *min_abs, int *nonfinite) {
-    float mn = INFINITY;
+void gdn_scan_fp32(const float *src, size_t n, float *min_abs, float *max_abs, int *nonfinite) {
+    float mn = INFINITY, mx = 0.0f;
     int bad = 0;
-#pragma omp parallel for schedule(static) reduction(min : mn) reduction(| : bad)
+#pragma omp parallel for schedule(static) reduction(min : mn) reduction(max : mx) reduction(| : bad)
     for (long long i = 0; i < (long long)n; ++i) {
         const float a = std::fabs(src[i]);
-        if (!std::isfinite(a)) bad = 1;
-        else if (a != 0.0f && a < mn) mn = a;
+        if (!std::isfinite(a)) {
+            bad = 1;
+        } else {
+            if (a != 0.0f && a < mn) mn = a;
+            if (a > mx) mx = a;
+        }
     }
     *min_abs = mn;
+    *max_abs = mx;
     *nonfinite = bad;
 }
 

@@ -16,11 +16,12 @@ uint16_t gdn_native_product_bits_host(uint16_t w, uint16_t x);
 
 // Convert n BF16-exact FP32 words to BF16 bits with subnormals flushed to
 // signed zero (the native product treats them as zero), and report the
-// smallest nonzero magnitude and whether any value is not finite.
-void gdn_pack_bf16_daz(const float *src, uint16_t *dst, size_t n, float *min_abs,
+// smallest nonzero and the largest finite magnitude and whether any value is
+// not finite.
+void gdn_pack_bf16_daz(const float *src, uint16_t *dst, size_t n, float *min_abs, float *max_abs,
                        int *nonfinite);
 // Same statistics for an FP32 matrix (no conversion).
-void gdn_scan_fp32(const float *src, size_t n, float *min_abs, int *nonfinite);
+void gdn_scan_fp32(const float *src, size_t n, float *min_abs, float *max_abs, int *nonfinite);
 
 #ifdef __cplusplus
 }
