@@ -67,7 +67,7 @@ constexpr int kRbGu = 8;   // 4 gate rows + the 4 matching up rows
 constexpr int kRbDown = 4;
 constexpr int kRbLm = 8;
 constexpr int kRbTest = 8;
-constexpr int kCB = 64;    // state columns per recurrence workgroup
+constexpr int kCB = 16;    // state columns per recurrence workgroup
 
 enum { kRef = GDN_CONTRACT_REF, kBf16w = GDN_CONTRACT_BF16W_FP32S, kFp32 = GDN_CONTRACT_FP32 };
 
@@ -289,10 +289,10 @@ struct Hb {
     static constexpr int NB = K / 32;     // 32-column beats per row
 };
 
-// The QKVG kernel's first kAbBlocks workgroups compute the 16 tiny a/b rows
-// (4 each) instead of projection rows.
-constexpr int kAbBlocks = 4;
-constexpr int kAbRows = 2 * kNH / kAbBlocks;
+// The row-block QKVG kernel's first kAbBlocks workgroups compute head h's
+// tiny a and b rows (workgroup h) instead of projection rows.
+constexpr int kAbBlocks = kNH;
+constexpr int kAbRows = 2;
 
 __device__ __forceinline__ float lane_word_value(uint32_t w, int k) {
     return (k & 1) ? u2f(w) : u2f(w << 16);
@@ -322,18 +322,15 @@ struct WRegs {
         }
     }
 
-    // a/b blocks: kAbRows FP32 rows of the hidden width; items t and t + 256
-    // are rows t / 128 and 2 + t / 128 at half-beat t % 128.
-    __device__ __forceinline__ void load_ab(const float *__restrict__ abw) {
-        static_assert(K == kH && kAbRows == 4 && NIT * WPI >= 8, "a/b rows fit the weight registers");
+    // a/b workgroup h: rows a_h (item t < 128) and b_h (item t >= 128) of
+    // the FP32 a/b block, half-beat t % 128.
+    __device__ __forceinline__ void load_ab(const float *__restrict__ abw, int h) {
+        static_assert(K == kH && kAbRows == 2 && NIT * WPI >= 4, "a/b rows fit the weight registers");
         const int t = threadIdx.x;
+        const int row = (t >> 7) * kNH + h, hb = t & 127;
+        const u32x4 *src = reinterpret_cast<const u32x4 *>(abw + (size_t)row * kH + hb * 16);
 #pragma unroll
-        for (int ii = 0; ii < 2; ++ii) {
-            const int row = (t >> 7) + 2 * ii, hb = t & 127;
-            const u32x4 *src = reinterpret_cast<const u32x4 *>(abw + (size_t)row * kH + hb * 16);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) v[(4 * ii + q) / WPI][(4 * ii + q) % WPI] = src[q];
-        }
+        for (int q = 0; q < 4; ++q) v[q / WPI][q % WPI] = src[q];
     }
 
     template <bool FAST>
@@ -385,23 +382,16 @@ struct WRegs {
         const int t = threadIdx.x, hb = t & 127;
         uint32_t xv[16];
         lds_load16u(xs + hb * 16, xv);
-        float xf[16];
+        float p[16];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) xf[e] = (C == kFp32) ? u2f(xv[e]) : lane_word_value(xv[e], e);
-#pragma unroll
-        for (int ii = 0; ii < 2; ++ii) {
-            float p[16];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int n = 4 * ii + q;
-                const u32x4 wq = v[n / WPI][n % WPI];
-                p[4 * q + 0] = xf[4 * q + 0] * u2f(wq.x);
-                p[4 * q + 1] = xf[4 * q + 1] * u2f(wq.y);
-                p[4 * q + 2] = xf[4 * q + 2] * u2f(wq.z);
-                p[4 * q + 3] = xf[4 * q + 3] * u2f(wq.w);
-            }
-            part[((t >> 7) + 2 * ii) * HBP + hb] = tree16(p);
+        for (int q = 0; q < 4; ++q) {
+            const u32x4 wq = v[q / WPI][q % WPI];
+            p[4 * q + 0] = u2f(xv[4 * q + 0]) * u2f(wq.x);
+            p[4 * q + 1] = u2f(xv[4 * q + 1]) * u2f(wq.y);
+            p[4 * q + 2] = u2f(xv[4 * q + 2]) * u2f(wq.z);
+            p[4 * q + 3] = u2f(xv[4 * q + 3]) * u2f(wq.w);
         }
+        part[(t >> 7) * HBP + hb] = tree16(p);
     }
 };
 
@@ -899,6 +889,7 @@ struct Epi {
     const float *aux;  // QKVG: the layer's small weights
     float *tails;      // QKVG: the layer's conv tails (3 stripes)
     float *ab;         // QKVG: a[8], b[8] (BF16-rounded)
+    float *bd;         // QKVG: (beta, decay) per head
     float *part_val;   // LM: per-block argmax
     int *part_idx;
 };
@@ -944,7 +935,7 @@ __global__ __launch_bounds__(kT, gemv_min_waves(C, EPI)) void k_gemv(const void 
     pro.load(src);
     WRegs<K, RB, C> w;
     if constexpr (EPI == EPI_QKVG) {
-        if (ab_blk) w.load_ab(ep.aux + kAuxAB + (size_t)blockIdx.x * kAbRows * kH);
+        if (ab_blk) w.load_ab(ep.aux + kAuxAB, blockIdx.x);
         else w.load(W, rb);
     } else {
         w.load(W, rb);
@@ -955,14 +946,25 @@ __global__ __launch_bounds__(kT, gemv_min_waves(C, EPI)) void k_gemv(const void 
     // 4. products and reduction
     if constexpr (EPI == EPI_QKVG) {
         if (ab_blk) {
-            // acc = (acc + tree16(lo)) + tree16(hi) per beat, rounded
+            // acc = (acc + tree16(lo)) + tree16(hi) per beat, rounded; then
+            // beta_h and decay_h
             w.compute_ab(xs, part);
             __syncthreads();
+            if (t >= 64) return;
+            float acc = 0.0f;
             if (t < kAbRows) {
                 const float *pr = part + t * HBP;
-                float acc = 0.0f;
                 for (int j = 0; j < Hb<kH>::NB; ++j) acc = (acc + pr[2 * j]) + pr[2 * j + 1];
-                ep.ab[blockIdx.x * kAbRows + t] = R<C>(acc);
+            }
+            const float a = R<C>(acc);
+            const float b = R<C>(__shfl(acc, 1));
+            if (t == 0) {
+                float beta, decay;
+                head_scalars(a, b, ep.aux[kAuxALog + blockIdx.x], ep.aux[kAuxDtBias + blockIdx.x], beta, decay);
+                ep.ab[blockIdx.x] = a;
+                ep.ab[kNH + blockIdx.x] = b;
+                ep.bd[2 * blockIdx.x] = beta;
+                ep.bd[2 * blockIdx.x + 1] = decay;
             }
             return;
         }
@@ -1152,14 +1154,14 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     constexpr int CHW = (4 * CR + 63) / 64;  // waves that run bank chains
     static_assert(ROWS % CR == 0 && NCH <= 6, "whole chunks");
     static_assert(K % kT == 0 && (PRO == PRO_PLAIN || K == kH), "input shape");
-    static_assert(EPI != EPI_QKVG || (ROWS == CR && CHW < 16), "a/b rows use the last wave");
+    static_assert(EPI != EPI_QKVG || (ROWS == CR && K == kH), "a/b rows: one chunk, hidden input");
     __shared__ __attribute__((aligned(16))) uint32_t xs[K];
     __shared__ __attribute__((aligned(16))) float part[NPART][CR * HBP];
     __shared__ __attribute__((aligned(16))) float scratch[kH / 16];
     __shared__ float bcast[kNH];
     __shared__ uint32_t red[8];
     __shared__ float ybuf[ROWS];
-    __shared__ float abpart[Hb<kH>::HB];
+    __shared__ float abpart[2 * Hb<kH>::HB];
     // claim the whole register file (128 VGPRs x 16 waves): one workgroup per CU
     asm volatile("" ::: "v127");
     const int t = threadIdx.x, wave = t >> 6;
@@ -1174,19 +1176,23 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     Prologue<C, K, PRO> pro;
     if (t < kT) pro.load(src);
 
-    // 2. the weight stream (and the a/b row of QKVG workgroups 0..15)
-    WChunk<K, CR, C> wa, wb;
-    wa.load(wblk);
-    if constexpr (NCH > 1) wb.load(wblk + (size_t)CR * K);
+    // QKVG workgroup h < 8 also owns head h's a and b rows (FP32 weights,
+    // read by the input waves ahead of their weight stream)
     u32x4 abw[4];
-    const bool ab_blk = (EPI == EPI_QKVG) && blockIdx.x < 2 * kNH;
+    const bool ab_blk = (EPI == EPI_QKVG) && blockIdx.x < kNH;
     if constexpr (EPI == EPI_QKVG) {
-        if (ab_blk && t < Hb<kH>::HB) {
-            const u32x4 *src4 = reinterpret_cast<const u32x4 *>(ep.aux + kAuxAB + (size_t)blockIdx.x * kH + t * 16);
+        if (ab_blk && t < kT) {
+            const int abrow = (t >> 7) * kNH + blockIdx.x, hb = t & 127;
+            const u32x4 *src4 = reinterpret_cast<const u32x4 *>(ep.aux + kAuxAB + (size_t)abrow * kH + hb * 16);
 #pragma unroll
             for (int q = 0; q < 4; ++q) abw[q] = src4[q];
         }
     }
+
+    // 2. the weight stream
+    WChunk<K, CR, C> wa, wb;
+    wa.load(wblk);
+    if constexpr (NCH > 1) wb.load(wblk + (size_t)CR * K);
 
     // 3. the input vector in LDS and the fast-path verdict: waves 0..3 build
     // it (synchronising only among themselves); the other waves, once their
@@ -1195,6 +1201,46 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     if (t < kT) {
         Wave4Sync sync{&arrive};
         fast = pro.finish_bf16(src, wi, xs, scratch, bcast, red, sync);
+        if constexpr (EPI == EPI_QKVG) {
+            if (ab_blk) {
+                // a_h and b_h: FP32 products x * w, tree16 per half-beat, then
+                // acc = (acc + tree16(lo)) + tree16(hi) per beat, rounded
+                // (gdn_gemv_tiny_ab); then beta_h and decay_h -- all while the
+                // weight stream is in flight
+                const int hb = t & 127;
+                uint32_t xv[16];
+                lds_load16u(xs + hb * 16, xv);
+                float p[16];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    p[4 * q + 0] = lane_word_value(xv[4 * q + 0], 0) * u2f(abw[q].x);
+                    p[4 * q + 1] = lane_word_value(xv[4 * q + 1], 1) * u2f(abw[q].y);
+                    p[4 * q + 2] = lane_word_value(xv[4 * q + 2], 0) * u2f(abw[q].z);
+                    p[4 * q + 3] = lane_word_value(xv[4 * q + 3], 1) * u2f(abw[q].w);
+                }
+                abpart[t] = tree16(p);
+                sync();
+                if (wave == 3) {
+                    const int lane = t & 63;
+                    float acc = 0.0f;
+                    if (lane < 2) {
+                        const float *pr = abpart + lane * Hb<kH>::HB;
+                        for (int j = 0; j < Hb<kH>::NB; ++j) acc = (acc + pr[2 * j]) + pr[2 * j + 1];
+                    }
+                    const float a = R<C>(acc);
+                    const float b = R<C>(__shfl(acc, 1));
+                    if (lane == 0) {
+                        float beta, decay;
+                        head_scalars(a, b, ep.aux[kAuxALog + blockIdx.x], ep.aux[kAuxDtBias + blockIdx.x], beta,
+                                     decay);
+                        ep.ab[blockIdx.x] = a;
+                        ep.ab[kNH + blockIdx.x] = b;
+                        ep.bd[2 * blockIdx.x] = beta;
+                        ep.bd[2 * blockIdx.x + 1] = decay;
+                    }
+                }
+            }
+        }
     } else {
         wait_count(&arrive, 4 * Prologue<C, K, PRO>::kSyncs);
         fast = decide_fast(red, wi);
@@ -1207,31 +1253,7 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
         if (fast) w.template compute<true>(xs, pc);
         else w.template compute<false>(xs, pc);
         if constexpr (c + 2 < NCH) w.load(wblk + (size_t)(c + 2) * CR * K);
-        if constexpr (EPI == EPI_QKVG) {
-            if (ab_blk && t < Hb<kH>::HB) {
-                // FP32 products x * w, tree16 per half-beat (gdn_gemv_tiny_ab)
-                uint32_t xv[16];
-                lds_load16u(xs + t * 16, xv);
-                float p[16];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    p[4 * q + 0] = lane_word_value(xv[4 * q + 0], 0) * u2f(abw[q].x);
-                    p[4 * q + 1] = lane_word_value(xv[4 * q + 1], 1) * u2f(abw[q].y);
-                    p[4 * q + 2] = lane_word_value(xv[4 * q + 2], 0) * u2f(abw[q].z);
-                    p[4 * q + 3] = lane_word_value(xv[4 * q + 3], 1) * u2f(abw[q].w);
-                }
-                abpart[t] = tree16(p);
-            }
-        }
         __syncthreads();
-        if constexpr (EPI == EPI_QKVG) {
-            if (ab_blk && t == kTB - 64) {
-                // acc = (acc + tree16(lo)) + tree16(hi) per beat, rounded
-                float acc = 0.0f;
-                for (int j = 0; j < Hb<kH>::NB; ++j) acc = (acc + abpart[2 * j]) + abpart[2 * j + 1];
-                ep.ab[blockIdx.x] = R<C>(acc);
-            }
-        }
         if (wave >= CHW) return;
         const float y = chain_rows<K, CR>(pc);
         const bool owner = (t & 3) == 0 && (t >> 2) < CR;
@@ -1357,50 +1379,64 @@ __global__ __launch_bounds__(kT) void k_argmax(const float *__restrict__ part_va
     }
 }
 
-// Gated delta rule for one head and CB state columns.
+// Gated delta rule for one head and CB state columns (beta/decay per head
+// come from the QKVG kernel).
 //   q/k L2 norms in gdn_tree_reduce_256 order (four wave butterflies, then
 //   (w0 + w1) + (w2 + w3)), alpha = tree256(qn * kn);
-//   read pass: r_i, p_i column chains over the 256 rows in order, one lane
-//   per column; delta and o; update pass S' = decay * S + k (x) delta.
+//   every product S[j][i] * kn[j] and S[j][i] * qn[j] is formed in parallel
+//   into column-major LDS tiles, then lane i runs the r_i chain and lane
+//   CB + i the p_i chain over j = 0..255 in order (only the dependent adds
+//   are serial); delta and o; the update S' = decay * S + kn (x) delta is
+//   applied to the tile still held in registers.
 template <int C, int CB>
 __global__ __launch_bounds__(kT) void k_recur(const float *__restrict__ qp,
                                               const float *__restrict__ kp,
                                               const float *__restrict__ vp,
-                                              const float *__restrict__ ap,
-                                              const float *__restrict__ bp,
-                                              const float *__restrict__ a_log,
-                                              const float *__restrict__ dt_bias,
+                                              const float *__restrict__ bd,
                                               void *__restrict__ state, float *__restrict__ attn) {
-    static_assert(CB <= 64 && (CB % 8) == 0, "one wave owns the column chains");
-    constexpr int PER_ROW = (C == kRef) ? CB / 8 : CB / 4;  // 16-byte loads per tile row
-    constexpr int NLD = (kHD * PER_ROW) / kT;
-    static_assert((kHD * PER_ROW) % kT == 0, "tile loads split evenly");
+    static_assert(2 * CB <= 64 && (CB % 8) == 0, "one wave runs both chains of every column");
+    constexpr int EPT = kHD * CB / kT;                  // state elements per thread
+    constexpr int PER_ROW = CB / EPT;                   // threads per tile row
+    constexpr int LDT = kHD + 4;                        // padded column stride of the product tiles
+    static_assert(EPT == 8 || EPT == 16 || EPT == 4, "whole 16-byte pieces per thread");
     __shared__ float qn[kHD], kn[kHD];
-    __shared__ __attribute__((aligned(16))) float tile[kHD * CB];
+    __shared__ __attribute__((aligned(16))) float pk_t[CB * LDT];  // S[j][i] * kn[j] at [i][j]
+    __shared__ __attribute__((aligned(16))) float pq_t[CB * LDT];  // S[j][i] * qn[j] at [i][j]
     __shared__ float dl[CB];
     __shared__ float red[8], red2[4];
     const int h = blockIdx.y, c0 = blockIdx.x * CB, t = threadIdx.x;
     const int lane = t & 63, w = t >> 6;
-    const size_t sbase = (size_t)h * kHD * kHD + c0;
+    const int row = t / PER_ROW, col = (t - row * PER_ROW) * EPT;  // this thread's tile piece
+    const size_t sidx = (size_t)h * kHD * kHD + (size_t)row * kHD + c0 + col;
 
     const float q = qp[h * kHD + t], k = kp[h * kHD + t];
     const float vi = (t < CB) ? vp[h * kHD + c0 + t] : 0.0f;
-    u32x4 tr[NLD];
+    float sv[EPT];  // S[row][c0 + col + e]
+    {
+        constexpr int NV = (C == kRef) ? EPT / 8 : EPT / 4;
+        u32x4 tr[NV];
 #pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-        const int u = t + kT * i, row = u / PER_ROW, cq = u - row * PER_ROW;
-        if constexpr (C == kRef) {
-            tr[i] = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const uint16_t *>(state) + sbase +
-                                                     (size_t)row * kHD + cq * 8);
-        } else {
-            tr[i] = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const float *>(state) + sbase +
-                                                     (size_t)row * kHD + cq * 4);
+        for (int i = 0; i < NV; ++i) {
+            if constexpr (C == kRef)
+                tr[i] = reinterpret_cast<const u32x4 *>(reinterpret_cast<const uint16_t *>(state) + sidx)[i];
+            else
+                tr[i] = reinterpret_cast<const u32x4 *>(reinterpret_cast<const float *>(state) + sidx)[i];
+        }
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t wv[4] = {tr[i].x, tr[i].y, tr[i].z, tr[i].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if constexpr (C == kRef) {
+                    sv[8 * i + 2 * e] = u2f(wv[e] << 16);
+                    sv[8 * i + 2 * e + 1] = u2f(wv[e] & 0xffff0000u);
+                } else {
+                    sv[4 * i + e] = u2f(wv[e]);
+                }
+            }
         }
     }
-
-    // beta/decay from the head's a and b while the tile is in flight
-    float beta, decay;
-    head_scalars(ap[h], bp[h], a_log[h], dt_bias[h], beta, decay);
+    const float beta = bd[2 * h], decay = bd[2 * h + 1];
 
     const float qs = wave_tree64(q * q), ks = wave_tree64(k * k);
     if (lane == 0) {
@@ -1417,69 +1453,90 @@ __global__ __launch_bounds__(kT) void k_recur(const float *__restrict__ qp,
     kn[t] = kv;
     const float qk = wave_tree64(qv * kv);
     if (lane == 0) red2[w] = qk;
-#pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-        const int u = t + kT * i, row = u / PER_ROW, cq = u - row * PER_ROW;
-        if constexpr (C == kRef) {
-            const u32x4 v = tr[i];
-            f32x4 lo, hi;
-            lo.x = u2f(v.x << 16); lo.y = u2f(v.x & 0xffff0000u);
-            lo.z = u2f(v.y << 16); lo.w = u2f(v.y & 0xffff0000u);
-            hi.x = u2f(v.z << 16); hi.y = u2f(v.z & 0xffff0000u);
-            hi.z = u2f(v.w << 16); hi.w = u2f(v.w & 0xffff0000u);
-            f32x4 *dst = reinterpret_cast<f32x4 *>(tile + row * CB + cq * 8);
-            dst[0] = lo;
-            dst[1] = hi;
-        } else {
-            *reinterpret_cast<u32x4 *>(tile + row * CB + cq * 4) = tr[i];
-        }
-    }
     __syncthreads();
     const float alpha = (red2[0] + red2[1]) + (red2[2] + red2[3]);
-
-    if (t < CB) {
-        float r = 0.0f, p = 0.0f;
-#pragma unroll 16
-        for (int j = 0; j < kHD; ++j) {
-            const float s = tile[j * CB + t];
-            r = r + s * kn[j];
-            p = p + s * qn[j];
-        }
-        const float delta = beta * (vi - decay * r);
-        const float o = 0.0625f * (decay * p + alpha * delta);
-        dl[t] = delta;
-        attn[h * kHD + c0 + t] = R<C>(o);
+    const float kj = kn[row], qj = qn[row];
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+        pk_t[(col + e) * LDT + row] = sv[e] * kj;
+        pq_t[(col + e) * LDT + row] = sv[e] * qj;
     }
     __syncthreads();
 
+    if (t < 2 * CB) {
+        // lane i: r_i = sum_j S[j][i] kn[j]; lane CB + i: p_i (same order)
+        const bool is_p = t >= CB;
+        const int ci = is_p ? t - CB : t;
+        const f32x4 *src = reinterpret_cast<const f32x4 *>((is_p ? pq_t : pk_t) + ci * LDT);
+        f32x4 col_v[kHD / 4];  // the whole column, read ahead of the serial adds
 #pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-        const int u = t + kT * i, row = u / PER_ROW, cq = u - row * PER_ROW;
-        const float kj = kn[row];
-        if constexpr (C == kRef) {
-            uint32_t packed[4];
+        for (int j4 = 0; j4 < kHD / 4; ++j4) col_v[j4] = src[j4];
+        float acc = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int col = cq * 8 + 2 * e;
-                const float n0 = decay * tile[row * CB + col] + kj * dl[col];
-                const float n1 = decay * tile[row * CB + col + 1] + kj * dl[col + 1];
-                packed[e] = (f2u(rne_bf16(n0)) >> 16) | (f2u(rne_bf16(n1)) & 0xffff0000u);
-            }
-            u32x4 v;
-            v.x = packed[0]; v.y = packed[1]; v.z = packed[2]; v.w = packed[3];
-            *reinterpret_cast<u32x4 *>(reinterpret_cast<uint16_t *>(state) + sbase + (size_t)row * kHD +
-                                       cq * 8) = v;
-        } else {
-            const f32x4 old = *reinterpret_cast<const f32x4 *>(tile + row * CB + cq * 4);
-            f32x4 nv;
-            nv.x = decay * old.x + kj * dl[cq * 4 + 0];
-            nv.y = decay * old.y + kj * dl[cq * 4 + 1];
-            nv.z = decay * old.z + kj * dl[cq * 4 + 2];
-            nv.w = decay * old.w + kj * dl[cq * 4 + 3];
-            *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(state) + sbase + (size_t)row * kHD +
-                                       cq * 4) = nv;
+        for (int j4 = 0; j4 < kHD / 4; ++j4) {
+            acc = acc + col_v[j4].x;
+            acc = acc + col_v[j4].y;
+            acc = acc + col_v[j4].z;
+            acc = acc + col_v[j4].w;
+        }
+        const float pv = __shfl(acc, (lane + CB) & 63);
+        if (!is_p) {
+            const float r = acc;
+            const float delta = beta * (vi - decay * r);
+            const float o = 0.0625f * (decay * pv + alpha * delta);
+            dl[t] = delta;
+            attn[h * kHD + c0 + t] = R<C>(o);
         }
     }
+    __syncthreads();
+
+    float nv[EPT];
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) nv[e] = decay * sv[e] + kj * dl[col + e];
+    if constexpr (C == kRef) {
+#pragma unroll
+        for (int i = 0; i < EPT / 8; ++i) {
+            u32x4 v;
+            v.x = cvt_pk(nv[8 * i + 0], nv[8 * i + 1]);
+            v.y = cvt_pk(nv[8 * i + 2], nv[8 * i + 3]);
+            v.z = cvt_pk(nv[8 * i + 4], nv[8 * i + 5]);
+            v.w = cvt_pk(nv[8 * i + 6], nv[8 * i + 7]);
+            if (!(fabsf(nv[8 * i + 0]) <= 3.402823466e38f) || !(fabsf(nv[8 * i + 1]) <= 3.402823466e38f) ||
+                !(fabsf(nv[8 * i + 2]) <= 3.402823466e38f) || !(fabsf(nv[8 * i + 3]) <= 3.402823466e38f) ||
+                !(fabsf(nv[8 * i + 4]) <= 3.402823466e38f) || !(fabsf(nv[8 * i + 5]) <= 3.402823466e38f) ||
+                !(fabsf(nv[8 * i + 6]) <= 3.402823466e38f) || !(fabsf(nv[8 * i + 7]) <= 3.402823466e38f)) {
+                // a NaN or infinity: the integer rounding (canonical NaN)
+                uint32_t pk[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    pk[e] = (f2u(rne_bf16(nv[8 * i + 2 * e])) >> 16) |
+                            (f2u(rne_bf16(nv[8 * i + 2 * e + 1])) & 0xffff0000u);
+                v.x = pk[0]; v.y = pk[1]; v.z = pk[2]; v.w = pk[3];
+            }
+            reinterpret_cast<u32x4 *>(reinterpret_cast<uint16_t *>(state) + sidx)[i] = v;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < EPT / 4; ++i) {
+            f32x4 v;
+            v.x = nv[4 * i + 0]; v.y = nv[4 * i + 1]; v.z = nv[4 * i + 2]; v.w = nv[4 * i + 3];
+            reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(state) + sidx)[i] = v;
+        }
+    }
+}
+
+// beta/decay for n heads from raw (a, b, a_log, dt_bias) (recurrence hook).
+__global__ __launch_bounds__(kT) void k_head_scalars(const float *__restrict__ a,
+                                                     const float *__restrict__ b,
+                                                     const float *__restrict__ a_log,
+                                                     const float *__restrict__ dt_bias, int n,
+                                                     float *__restrict__ bd) {
+    const int i = blockIdx.x * kT + threadIdx.x;
+    if (i >= n) return;
+    float beta, decay;
+    head_scalars(a[i], b[i], a_log[i], dt_bias[i], beta, decay);
+    bd[2 * i] = beta;
+    bd[2 * i + 1] = decay;
 }
 
 // out = R(a + b) over the hidden vector (layer output for the layer hook).
@@ -1515,7 +1572,7 @@ struct GDNEngine {
     float *ws = nullptr;
     float *act = nullptr;
     float *resid = nullptr, *resid_alt = nullptr, *fhid = nullptr, *qkv = nullptr,
-          *gate = nullptr, *sgate = nullptr, *ab = nullptr, *attn = nullptr,
+          *gate = nullptr, *sgate = nullptr, *ab = nullptr, *bd = nullptr, *attn = nullptr,
           *ybuf_o = nullptr, *dbuf = nullptr, *hbuf = nullptr, *lm_val = nullptr;
     int *lm_idx = nullptr;
     int *tok_dev = nullptr;   // [0] in, [1] out
@@ -1697,7 +1754,7 @@ int alloc_buffers(GDNEngine *e) {
     GDN_HIP(hipMalloc(&e->ws, (size_t)GDN_WS_FLOATS * 4));
     GDN_HIP(hipMemset(e->ws, 0, (size_t)GDN_WS_FLOATS * 4));
     const size_t nblk_lm = (size_t)e->vocab / kRbLm;
-    const size_t act_floats = 3 * kH + 3 * kH + 2 * kH + 16 + 3 * kH + kI + nblk_lm;
+    const size_t act_floats = 3 * kH + 3 * kH + 2 * kH + 16 + 2 * kNH + 3 * kH + kI + nblk_lm;
     GDN_HIP(hipMalloc(&e->act, act_floats * 4));
     GDN_HIP(hipMemset(e->act, 0, act_floats * 4));
     float *p = e->act;
@@ -1708,6 +1765,7 @@ int alloc_buffers(GDNEngine *e) {
     e->gate = p; p += kH;
     e->sgate = p; p += kH;
     e->ab = p; p += 16;
+    e->bd = p; p += 2 * kNH;
     e->attn = p; p += kH;
     e->ybuf_o = p; p += kH;
     e->dbuf = p; p += kH;
@@ -1752,6 +1810,7 @@ void launch_qkvg(GDNEngine *e, int l, const float *res_a, const float *res_b, hi
     q.aux = aux;
     q.tails = layer_tails(e, l);
     q.ab = e->ab;
+    q.bd = e->bd;
     XSrc xq = xsrc(res_a, res_b, nullptr, aux + kAuxAttnNorm, e->resid, nullptr, e->eps);
     if constexpr (PRO0 == PRO_EMBED) {
         xq.emb = e->w_emb;
@@ -1770,10 +1829,8 @@ void launch_qkvg(GDNEngine *e, int l, const float *res_a, const float *res_b, hi
 
 template <int C>
 void launch_recur(GDNEngine *e, int l, hipStream_t s) {
-    const float *aux = layer_aux(e, l);
     hipLaunchKernelGGL((k_recur<C, kCB>), dim3(kHD / kCB, kNH), dim3(kT), 0, s, e->qkv,
-                       e->qkv + kH, e->qkv + 2 * kH, e->ab, e->ab + kNH, aux + kAuxALog,
-                       aux + kAuxDtBias, layer_state(e, l), e->attn);
+                       e->qkv + kH, e->qkv + 2 * kH, e->bd, layer_state(e, l), e->attn);
 }
 
 template <int C>
@@ -2266,12 +2323,16 @@ int gdn_test_recurrence(int contract, uint32_t n_heads, uint32_t n_steps, const 
     } else {
         GDN_HIP(hipMemcpy(dS, S, nstate * 4, hipMemcpyHostToDevice));
     }
+    float *dbd;
+    GDN_HIP(hipMalloc(&dbd, 2 * ns * 4));
+    hipLaunchKernelGGL(k_head_scalars, dim3((unsigned)((ns + kT - 1) / kT)), dim3(kT), 0, 0, da, db, dal,
+                       ddt, (int)ns, dbd);
     const dim3 grid(kHD / kCB, n_heads), block(kT);
     for (uint32_t s = 0; s < n_steps; ++s) {
         const size_t ov = (size_t)s * n_heads * kHD, os = (size_t)s * n_heads;
 #define GDN_REC(CC)                                                                             \
-    hipLaunchKernelGGL((k_recur<CC, kCB>), grid, block, 0, 0, dq + ov, dk + ov, dv + ov, da + os,  \
-                       db + os, dal + os, ddt + os, dS, dout + ov)
+    hipLaunchKernelGGL((k_recur<CC, kCB>), grid, block, 0, 0, dq + ov, dk + ov, dv + ov, dbd + 2 * os, \
+                       dS, dout + ov)
         if (contract == kRef) GDN_REC(kRef);
         else if (contract == kBf16w) GDN_REC(kBf16w);
         else GDN_REC(kFp32);
@@ -2290,7 +2351,7 @@ int gdn_test_recurrence(int contract, uint32_t n_heads, uint32_t n_steps, const 
     } else {
         GDN_HIP(hipMemcpy(S, dS, nstate * 4, hipMemcpyDeviceToHost));
     }
-    float *bufs[] = {dq, dk, dv, da, db, dal, ddt, dout};
+    float *bufs[] = {dq, dk, dv, da, db, dal, ddt, dout, dbd};
     for (float *p : bufs) GDN_HIP(hipFree(p));
     GDN_HIP(hipFree(dS));
     return 0;
