@@ -1064,6 +1064,20 @@ constexpr int kCuLm = 125;    // 32000 / 256, in chunks of 25
 constexpr int kCuLmChunk = 25;
 constexpr int kCuLmSmall = 8; // vocabularies that 125 does not divide
 
+// Partial sums of the CU-resident GEMV, bank-contiguous: row r, bank
+// (beat parity, half) = 2 * (beat & 1) + half, position beat / 2.  A bank
+// segment is padded to 4 (mod 32) words so the four chain lanes of a row
+// read distinct LDS banks.
+template <int K>
+struct BankLayout {
+    static constexpr int NB2 = Hb<K>::NB / 2;                       // beats per bank chain
+    static constexpr int BSTR = ((NB2 + 3) / 4) * 4 + ((((NB2 + 3) / 4) * 4) % 32 == 4 ? 0 : 4);
+    static constexpr int RSTR = 4 * BSTR;
+    __device__ static constexpr int index(int row, int hb) {
+        return row * RSTR + (2 * ((hb >> 1) & 1) + (hb & 1)) * BSTR + (hb >> 2);
+    }
+};
+
 template <int K, int CR, int C>
 struct WChunk {
     static constexpr int HB = Hb<K>::HB, HBP = Hb<K>::HBP;
@@ -1116,7 +1130,7 @@ struct WChunk {
                         p[2 * e + 1] = native_exact(w8[e] >> 16, u2f(xv[2 * e + 1]));
                     }
                 }
-                part[row * HBP + hb] = tree16(p);
+                part[BankLayout<K>::index(row, hb)] = tree16(p);
             }
         }
     }
@@ -1124,16 +1138,25 @@ struct WChunk {
 
 // Bank chains of CR rows: thread L < 4 CR runs chain L & 3 of row L >> 2
 // (the waves that hold those threads call this); lane 4r ends with row r.
+// The chain's whole bank segment is read before its serial adds.
 template <int K, int CR>
 __device__ __forceinline__ float chain_rows(const float *part) {
-    constexpr int HBP = Hb<K>::HBP, NB = Hb<K>::NB;
+    using BL = BankLayout<K>;
+    constexpr int NV = (BL::NB2 + 3) / 4;
     const int L = threadIdx.x;
     float acc = 0.0f;
     if (L < CR * 4) {
-        const int row = L >> 2, parity = (L >> 1) & 1, half = L & 1;
-        const float *pr = part + row * HBP + half;
-#pragma unroll 8
-        for (int b = parity; b < NB; b += 2) acc = acc + pr[2 * b];
+        const f32x4 *seg = reinterpret_cast<const f32x4 *>(part + (L >> 2) * BL::RSTR + (L & 3) * BL::BSTR);
+        f32x4 v[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) v[i] = seg[i];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            if (4 * i + 0 < BL::NB2) acc = acc + v[i].x;
+            if (4 * i + 1 < BL::NB2) acc = acc + v[i].y;
+            if (4 * i + 2 < BL::NB2) acc = acc + v[i].z;
+            if (4 * i + 3 < BL::NB2) acc = acc + v[i].w;
+        }
     }
     const float s = acc + __shfl_xor(acc, 1);
     return s + __shfl_xor(s, 2);
@@ -1150,13 +1173,13 @@ using IC = std::integral_constant<int, N>;
 template <int C, int K, int ROWS, int CR, int PRO, int EPI>
 __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, WInfo wi, XSrc src,
                                                    Epi ep) {
-    constexpr int HBP = Hb<K>::HBP, NCH = ROWS / CR, NPART = NCH > 1 ? 2 : 1;
+    constexpr int NCH = ROWS / CR, NPART = NCH > 1 ? 2 : 1;
     constexpr int CHW = (4 * CR + 63) / 64;  // waves that run bank chains
     static_assert(ROWS % CR == 0 && NCH <= 6, "whole chunks");
     static_assert(K % kT == 0 && (PRO == PRO_PLAIN || K == kH), "input shape");
     static_assert(EPI != EPI_QKVG || (ROWS == CR && K == kH), "a/b rows: one chunk, hidden input");
     __shared__ __attribute__((aligned(16))) uint32_t xs[K];
-    __shared__ __attribute__((aligned(16))) float part[NPART][CR * HBP];
+    __shared__ __attribute__((aligned(16))) float part[NPART][CR * BankLayout<K>::RSTR];
     __shared__ __attribute__((aligned(16))) float scratch[kH / 16];
     __shared__ float bcast[kNH];
     __shared__ uint32_t red[8];
@@ -1176,6 +1199,23 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     Prologue<C, K, PRO> pro;
     if (t < kT) pro.load(src);
 
+    // QKVG: the owner lane of each q/k/v row reads its conv tails and taps
+    // now, ahead of the weight stream (the epilogue would otherwise wait on
+    // them after the chains)
+    const bool owner = wave < CHW && (t & 3) == 0 && (t >> 2) < CR;
+    uint16_t tail_b[3] = {0, 0, 0};
+    f32x4 taps = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (EPI == EPI_QKVG) {
+        const int r = row0 + (t >> 2);
+        if (owner && r < 3 * kH) {
+            const int kind = r / kH, ch = r - kind * kH;
+            const uint16_t *tl = reinterpret_cast<const uint16_t *>(ep.tails + (size_t)kind * kTailStripe);
+            tail_b[0] = tl[ch];
+            tail_b[1] = tl[kH + ch];
+            tail_b[2] = tl[2 * kH + ch];
+            taps = *reinterpret_cast<const f32x4 *>(ep.aux + kAuxConv + ((size_t)kind * kH + ch) * 4);
+        }
+    }
     // QKVG workgroup h < 8 also owns head h's a and b rows (FP32 weights,
     // read by the input waves ahead of their weight stream)
     u32x4 abw[4];
@@ -1256,7 +1296,6 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
         __syncthreads();
         if (wave >= CHW) return;
         const float y = chain_rows<K, CR>(pc);
-        const bool owner = (t & 3) == 0 && (t >> 2) < CR;
         if (!owner) return;
         const int rr = c * CR + (t >> 2);  // row within the workgroup
         const int r = row0 + rr;
@@ -1269,14 +1308,13 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
             if (r < 3 * kH) {
                 // causal conv over [t0, t1, t2, x] + SiLU; tails shift to [t1, t2, x]
                 const int kind = r / kH, ch = r - kind * kH;
-                const float *cw = ep.aux + kAuxConv + ((size_t)kind * kH + ch) * 4;
                 uint16_t *tl = reinterpret_cast<uint16_t *>(ep.tails + (size_t)kind * kTailStripe);
-                const uint16_t b0 = tl[ch], b1 = tl[kH + ch], b2 = tl[2 * kH + ch];
-                const float t0 = bf16_bits_to_f32(b0), t1 = bf16_bits_to_f32(b1), t2 = bf16_bits_to_f32(b2);
-                tl[ch] = b1;
-                tl[kH + ch] = b2;
+                const float t0 = bf16_bits_to_f32(tail_b[0]), t1 = bf16_bits_to_f32(tail_b[1]),
+                            t2 = bf16_bits_to_f32(tail_b[2]);
+                tl[ch] = tail_b[1];
+                tl[kH + ch] = tail_b[2];
                 tl[2 * kH + ch] = (uint16_t)(f2u(yv) >> 16);
-                const float s = t0 * cw[0] + t1 * cw[1] + t2 * cw[2] + yv * cw[3];
+                const float s = t0 * taps.x + t1 * taps.y + t2 * taps.z + yv * taps.w;
                 ep.y[r] = R<C>(silu_ref(s));
             } else {
                 ep.y2[r - 3 * kH] = yv;
