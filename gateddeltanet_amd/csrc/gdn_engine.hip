@@ -1060,9 +1060,11 @@ constexpr int kCuQkvg = 32;   // 8192 / 256
 constexpr int kCuO = 8;       // 2048 / 256
 constexpr int kCuGu = 44;     // 22 gate + 22 up rows: 11264 / 256
 constexpr int kCuDown = 8;    // 2048 / 256
-constexpr int kCuLm = 125;    // 32000 / 256, in chunks of 25
-constexpr int kCuLmChunk = 25;
+constexpr int kCuLm = 125;    // 32000 / 256
 constexpr int kCuLmSmall = 8; // vocabularies that 125 does not divide
+// Items in flight per thread (16 = every item issued up front).
+constexpr int kDepthAll = 16;
+constexpr int kDepthLm = 3;
 
 // Partial sums of the CU-resident GEMV, bank-contiguous: row r, bank
 // (beat parity, half) = 2 * (beat & 1) + half, position beat / 2.  A bank
@@ -1078,41 +1080,60 @@ struct BankLayout {
     }
 };
 
-template <int K, int CR, int C>
-struct WChunk {
-    static constexpr int HB = Hb<K>::HB, HBP = Hb<K>::HBP;
-    static constexpr int ITEMS = CR * HB;
+// A workgroup's weight rows as a stream of 16-element items: item f (row
+// f / (K/16), half-beat f % (K/16)) sits at element 16 f of the workgroup's
+// slice and thread t takes items t + 1024 i.  prime() issues the loads of
+// the first DEPTH items; run() walks the items in order, issuing item
+// i + DEPTH before multiplying item i, so a wave never has more than DEPTH
+// items in flight (a SIMD holds only about one wave's worth of outstanding
+// loads; a wave that asks for more stalls at issue and cannot multiply the
+// items it already has).
+template <int K, int ROWS, int C, int D>
+struct WStream {
+    static constexpr int HB = Hb<K>::HB;
+    static constexpr int ITEMS = ROWS * HB;
     static constexpr int NIT = (ITEMS + kTB - 1) / kTB;
+    static constexpr int DEPTH = D < NIT ? D : NIT;
     static constexpr bool kFull = (ITEMS % kTB) == 0;
     static constexpr bool kSameHb = (kTB % HB) == 0;
     static_assert(C != kFp32, "BF16 weights");
+    const u32x4 *wb;
     u32x4 v[NIT][2];
 
-    // chunk: the chunk's first row; item f is the 16 elements at 16 f
-    __device__ __forceinline__ void load(const uint16_t *__restrict__ chunk) {
-        const u32x4 *wb = reinterpret_cast<const u32x4 *>(chunk);
-#pragma unroll
-        for (int i = 0; i < NIT; ++i) {
-            const int f = threadIdx.x + kTB * i;
-            if (kFull || f < ITEMS) {
-                v[i][0] = __builtin_nontemporal_load(wb + 2 * f);
-                v[i][1] = __builtin_nontemporal_load(wb + 2 * f + 1);
-            }
+    template <int I>
+    __device__ __forceinline__ void load() {
+        const int f = threadIdx.x + kTB * I;
+        if (kFull || f < ITEMS) {
+            v[I][0] = __builtin_nontemporal_load(wb + 2 * f);
+            v[I][1] = __builtin_nontemporal_load(wb + 2 * f + 1);
         }
     }
 
-    template <bool FAST>
-    __device__ __forceinline__ void compute(const uint32_t *xs, float *part) const {
-        uint32_t xv[16];
-        if constexpr (kSameHb) lds_load16u(xs + (threadIdx.x % HB) * 16, xv);
-#pragma unroll
-        for (int i = 0; i < NIT; ++i) {
-            const int f = threadIdx.x + kTB * i;
+    template <int I>
+    __device__ __forceinline__ void prime_from() {
+        if constexpr (I < DEPTH) {
+            load<I>();
+            prime_from<I + 1>();
+        }
+    }
+
+    __device__ __forceinline__ void prime(const uint16_t *__restrict__ slice) {
+        wb = reinterpret_cast<const u32x4 *>(slice);
+        prime_from<0>();
+    }
+
+    // Item I (compile-time, so the item registers stay registers), then the
+    // rest.
+    template <bool FAST, int I>
+    __device__ __forceinline__ void run_from(const uint32_t *xs, float *part, uint32_t *xv) {
+        if constexpr (I < NIT) {
+            if constexpr (I + DEPTH < NIT) load<I + DEPTH>();
+            const int f = threadIdx.x + kTB * I;
             if (kFull || f < ITEMS) {
                 const int row = f / HB, hb = f - row * HB;
                 if constexpr (!kSameHb) lds_load16u(xs + hb * 16, xv);
-                const uint32_t w8[8] = {v[i][0].x, v[i][0].y, v[i][0].z, v[i][0].w,
-                                        v[i][1].x, v[i][1].y, v[i][1].z, v[i][1].w};
+                const uint32_t w8[8] = {v[I][0].x, v[I][0].y, v[I][0].z, v[I][0].w,
+                                        v[I][1].x, v[I][1].y, v[I][1].z, v[I][1].w};
                 float p[16];
                 if constexpr (FAST) {
                     uint32_t rbits[8];
@@ -1132,7 +1153,18 @@ struct WChunk {
                 }
                 part[BankLayout<K>::index(row, hb)] = tree16(p);
             }
+            // keep the scheduler from hoisting later loads above this item
+            // (their registers would all be live at once)
+            if constexpr (DEPTH < NIT) __builtin_amdgcn_sched_barrier(0);
+            run_from<FAST, I + 1>(xs, part, xv);
         }
+    }
+
+    template <bool FAST>
+    __device__ __forceinline__ void run(const uint32_t *xs, float *part) {
+        uint32_t xv[16];
+        if constexpr (kSameHb) lds_load16u(xs + (threadIdx.x % HB) * 16, xv);
+        run_from<FAST, 0>(xs, part, xv);
     }
 };
 
@@ -1165,21 +1197,22 @@ __device__ __forceinline__ float chain_rows(const float *part) {
 template <int N>
 using IC = std::integral_constant<int, N>;
 
-// ROWS rows per workgroup (grid = M / ROWS), CR rows per chunk.
-//   EPI_QKVG    rows are q|k|v|g; workgroups 0..15 also run a/b row blockIdx
+// ROWS rows per workgroup (grid = M / ROWS), at most D items in flight per
+// thread.
+//   EPI_QKVG    rows are q|k|v|g; workgroups 0..7 also run head h's a/b rows
 //   EPI_SWIGLU  a workgroup's rows are ROWS/2 gate rows then the matching
 //               ROWS/2 up rows
 //   EPI_LM      FP32 logits and the workgroup's argmax
-template <int C, int K, int ROWS, int CR, int PRO, int EPI>
+template <int C, int K, int ROWS, int D, int PRO, int EPI>
 __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, WInfo wi, XSrc src,
                                                    Epi ep) {
-    constexpr int NCH = ROWS / CR, NPART = NCH > 1 ? 2 : 1;
+    constexpr int CR = ROWS;
     constexpr int CHW = (4 * CR + 63) / 64;  // waves that run bank chains
-    static_assert(ROWS % CR == 0 && NCH <= 6, "whole chunks");
+    static_assert(CHW <= 16, "one chain lane per bank");
     static_assert(K % kT == 0 && (PRO == PRO_PLAIN || K == kH), "input shape");
-    static_assert(EPI != EPI_QKVG || (ROWS == CR && K == kH), "a/b rows: one chunk, hidden input");
+    static_assert(EPI != EPI_QKVG || K == kH, "a/b rows: hidden input");
     __shared__ __attribute__((aligned(16))) uint32_t xs[K];
-    __shared__ __attribute__((aligned(16))) float part[NPART][CR * BankLayout<K>::RSTR];
+    __shared__ __attribute__((aligned(16))) float part[CR * BankLayout<K>::RSTR];
     __shared__ __attribute__((aligned(16))) float scratch[kH / 16];
     __shared__ float bcast[kNH];
     __shared__ uint32_t red[8];
@@ -1230,9 +1263,8 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     }
 
     // 2. the weight stream
-    WChunk<K, CR, C> wa, wb;
-    wa.load(wblk);
-    if constexpr (NCH > 1) wb.load(wblk + (size_t)CR * K);
+    WStream<K, ROWS, C, D> ws;
+    ws.prime(wblk);
 
     // 3. the input vector in LDS and the fast-path verdict: waves 0..3 build
     // it (synchronising only among themselves); the other waves, once their
@@ -1286,53 +1318,44 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
         fast = decide_fast(red, wi);
     }
 
-    // 4. per chunk: products, barrier, bank chains and the row epilogue
-    auto step = [&](auto &w, auto cidx) {
-        constexpr int c = decltype(cidx)::value;
-        float *pc = part[c % NPART];
-        if (fast) w.template compute<true>(xs, pc);
-        else w.template compute<false>(xs, pc);
-        if constexpr (c + 2 < NCH) w.load(wblk + (size_t)(c + 2) * CR * K);
-        __syncthreads();
-        if (wave >= CHW) return;
-        const float y = chain_rows<K, CR>(pc);
-        if (!owner) return;
-        const int rr = c * CR + (t >> 2);  // row within the workgroup
-        const int r = row0 + rr;
-        if constexpr (EPI == EPI_RAW) {
-            ep.y[r] = y;
-        } else if constexpr (EPI == EPI_STORE) {
-            ep.y[r] = R<C>(y);
-        } else if constexpr (EPI == EPI_QKVG) {
-            const float yv = R<C>(y);
-            if (r < 3 * kH) {
-                // causal conv over [t0, t1, t2, x] + SiLU; tails shift to [t1, t2, x]
-                const int kind = r / kH, ch = r - kind * kH;
-                uint16_t *tl = reinterpret_cast<uint16_t *>(ep.tails + (size_t)kind * kTailStripe);
-                const float t0 = bf16_bits_to_f32(tail_b[0]), t1 = bf16_bits_to_f32(tail_b[1]),
-                            t2 = bf16_bits_to_f32(tail_b[2]);
-                tl[ch] = tail_b[1];
-                tl[kH + ch] = tail_b[2];
-                tl[2 * kH + ch] = (uint16_t)(f2u(yv) >> 16);
-                const float s = t0 * taps.x + t1 * taps.y + t2 * taps.z + yv * taps.w;
-                ep.y[r] = R<C>(silu_ref(s));
+    // 4. products, barrier, bank chains and the row epilogue
+    if (fast) ws.template run<true>(xs, part);
+    else ws.template run<false>(xs, part);
+    __syncthreads();
+    if (wave < CHW) {
+        const float y = chain_rows<K, CR>(part);
+        if (owner) {
+            const int rr = t >> 2;  // row within the workgroup
+            const int r = row0 + rr;
+            if constexpr (EPI == EPI_RAW) {
+                ep.y[r] = y;
+            } else if constexpr (EPI == EPI_STORE) {
+                ep.y[r] = R<C>(y);
+            } else if constexpr (EPI == EPI_QKVG) {
+                const float yv = R<C>(y);
+                if (r < 3 * kH) {
+                    // causal conv over [t0, t1, t2, x] + SiLU; tails shift to [t1, t2, x]
+                    const int kind = r / kH, ch = r - kind * kH;
+                    uint16_t *tl = reinterpret_cast<uint16_t *>(ep.tails + (size_t)kind * kTailStripe);
+                    const float t0 = bf16_bits_to_f32(tail_b[0]), t1 = bf16_bits_to_f32(tail_b[1]),
+                                t2 = bf16_bits_to_f32(tail_b[2]);
+                    tl[ch] = tail_b[1];
+                    tl[kH + ch] = tail_b[2];
+                    tl[2 * kH + ch] = (uint16_t)(f2u(yv) >> 16);
+                    const float s = t0 * taps.x + t1 * taps.y + t2 * taps.z + yv * taps.w;
+                    ep.y[r] = R<C>(silu_ref(s));
+                } else {
+                    ep.y2[r - 3 * kH] = yv;
+                    ep.y3[r - 3 * kH] = sigmoid_ref(yv);
+                }
+            } else if constexpr (EPI == EPI_SWIGLU) {
+                ybuf[rr] = R<C>(y);
             } else {
-                ep.y2[r - 3 * kH] = yv;
-                ep.y3[r - 3 * kH] = sigmoid_ref(yv);
+                ep.y[r] = y;  // LM: FP32 logits (no rounding point)
+                ybuf[rr] = y;
             }
-        } else if constexpr (EPI == EPI_SWIGLU) {
-            ybuf[rr] = R<C>(y);
-        } else {
-            ep.y[r] = y;  // LM: FP32 logits (no rounding point)
-            ybuf[rr] = y;
         }
-    };
-    step(wa, IC<0>{});
-    if constexpr (NCH > 1) step(wb, IC<1>{});
-    if constexpr (NCH > 2) step(wa, IC<2>{});
-    if constexpr (NCH > 3) step(wb, IC<3>{});
-    if constexpr (NCH > 4) step(wa, IC<4>{});
-    if constexpr (NCH > 5) step(wb, IC<5>{});
+    }
 
     // 5. workgroup epilogues over all rows
     if constexpr (EPI == EPI_SWIGLU) {
@@ -1436,7 +1459,7 @@ __global__ __launch_bounds__(kT) void k_recur(const float *__restrict__ qp,
     constexpr int EPT = kHD * CB / kT;                  // state elements per thread
     constexpr int PER_ROW = CB / EPT;                   // threads per tile row
     constexpr int LDT = kHD + 4;                        // padded column stride of the product tiles
-    static_assert(EPT == 8 || EPT == 16 || EPT == 4, "whole 16-byte pieces per thread");
+    static_assert(EPT % 8 == 0 && PER_ROW * EPT == CB, "whole 16-byte pieces per thread");
     __shared__ float qn[kHD], kn[kHD];
     __shared__ __attribute__((aligned(16))) float pk_t[CB * LDT];  // S[j][i] * kn[j] at [i][j]
     __shared__ __attribute__((aligned(16))) float pq_t[CB * LDT];  // S[j][i] * qn[j] at [i][j]
@@ -1860,7 +1883,7 @@ void launch_qkvg(GDNEngine *e, int l, const float *res_a, const float *res_b, hi
         hipLaunchKernelGGL((k_gemv<C, kH, kRbQkvg, PRO0, EPI_QKVG>), dim3(4 * kH / kRbQkvg + kAbBlocks),
                            dim3(kT), 0, s, e->w_qkvg[l], e->i_qkvg[l], xq, q);
     } else {
-        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuQkvg, kCuQkvg, PRO0, EPI_QKVG>), dim3(4 * kH / kCuQkvg),
+        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuQkvg, kDepthAll, PRO0, EPI_QKVG>), dim3(4 * kH / kCuQkvg),
                            dim3(kTB), 0, s, e->w_qkvg[l], e->i_qkvg[l], xq, q);
     }
 }
@@ -1880,7 +1903,7 @@ void launch_o(GDNEngine *e, int l, hipStream_t s) {
         hipLaunchKernelGGL((k_gemv<C, kH, kRbO, PRO_ONORM, EPI_STORE>), dim3(kH / kRbO), dim3(kT), 0, s,
                            e->w_o[l], e->i_o[l], xo, st);
     } else {
-        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuO, kCuO, PRO_ONORM, EPI_STORE>), dim3(kH / kCuO), dim3(kTB),
+        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuO, kDepthAll, PRO_ONORM, EPI_STORE>), dim3(kH / kCuO), dim3(kTB),
                            0, s, e->w_o[l], e->i_o[l], xo, st);
     }
 }
@@ -1895,7 +1918,7 @@ void launch_gu(GDNEngine *e, int l, hipStream_t s) {
         hipLaunchKernelGGL((k_gemv<C, kH, kRbGu, PRO_RESNORM, EPI_SWIGLU>), dim3(2 * kI / kRbGu), dim3(kT),
                            0, s, e->w_gu[l], e->i_gu[l], xg, sw);
     } else {
-        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuGu, kCuGu, PRO_RESNORM, EPI_SWIGLU>), dim3(2 * kI / kCuGu),
+        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuGu, kDepthAll, PRO_RESNORM, EPI_SWIGLU>), dim3(2 * kI / kCuGu),
                            dim3(kTB), 0, s, e->w_gu[l], e->i_gu[l], xg, sw);
     }
 }
@@ -1909,7 +1932,7 @@ void launch_down(GDNEngine *e, int l, hipStream_t s) {
         hipLaunchKernelGGL((k_gemv<C, kI, kRbDown, PRO_PLAIN, EPI_STORE>), dim3(kH / kRbDown), dim3(kT), 0,
                            s, e->w_down[l], e->i_down[l], xd, dn);
     } else {
-        hipLaunchKernelGGL((k_gemv_cu<C, kI, kCuDown, kCuDown, PRO_PLAIN, EPI_STORE>), dim3(kH / kCuDown),
+        hipLaunchKernelGGL((k_gemv_cu<C, kI, kCuDown, kDepthAll, PRO_PLAIN, EPI_STORE>), dim3(kH / kCuDown),
                            dim3(kTB), 0, s, e->w_down[l], e->i_down[l], xd, dn);
     }
 }
@@ -1932,10 +1955,10 @@ void launch_lm(GDNEngine *e, hipStream_t s) {
         hipLaunchKernelGGL((k_gemv<C, kH, kRbLm, PRO_RESNORM, EPI_LM>), grid, dim3(kT), 0, s, e->w_lm,
                            e->i_lm, xl, lm);
     } else if ((e->vocab % kCuLm) == 0) {
-        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuLm, kCuLmChunk, PRO_RESNORM, EPI_LM>), grid, dim3(kTB), 0, s,
+        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuLm, kDepthLm, PRO_RESNORM, EPI_LM>), grid, dim3(kTB), 0, s,
                            e->w_lm, e->i_lm, xl, lm);
     } else {
-        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuLmSmall, kCuLmSmall, PRO_RESNORM, EPI_LM>), grid, dim3(kTB),
+        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuLmSmall, kDepthAll, PRO_RESNORM, EPI_LM>), grid, dim3(kTB),
                            0, s, e->w_lm, e->i_lm, xl, lm);
     }
 }
@@ -2303,7 +2326,7 @@ int gdn_test_gemv(int contract, const float *W, const float *x, uint32_t M, uint
 #define GDN_PLAIN(CC, KK)                                                                     \
     hipLaunchKernelGGL((k_gemv<CC, KK, kRbTest, PRO_PLAIN, EPI_RAW>), grid, block, 0, 0, dW, wi, xs, ep)
 #define GDN_PLAIN_CU(KK)                                                                      \
-    hipLaunchKernelGGL((k_gemv_cu<kRef, KK, kRbTest, kRbTest, PRO_PLAIN, EPI_RAW>), grid, dim3(kTB), 0, 0, \
+    hipLaunchKernelGGL((k_gemv_cu<kRef, KK, kRbTest, kDepthAll, PRO_PLAIN, EPI_RAW>), grid, dim3(kTB), 0, 0, \
                        dW, wi, xs, ep)
     XSrc xs{};
     xs.a = dx;
