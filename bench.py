@@ -53,20 +53,22 @@ BYTES_PER_TOKEN = {
 # Algorithmic bytes per launch of each kernel kind (bf16 arm): weights at
 # BF16 plus the state / conv-tail traffic the kernel must move.
 KERNEL_BYTES = {
-    "qkvg": 4 * H * H * 2 + 2 * 8 * H * 2 + 3 * H * 4 * 2 + 3 * 3 * H * 2 * 2 + 2 * H * 2,
+    "qkvg": 4 * H * H * 2 + 2 * 8 * H * 4 + 3 * H * 4 * 4 + 3 * 3 * H * 2 * 2 + 2 * H * 2,
     "recur": 8 * 256 * 256 * 4 * 2,
     "o_proj": H * H * 2 + 256 * 2,
     "gate_up": 2 * I * H * 2 + H * 2,
     "down": H * I * 2,
     "lm_head": V * H * 2 + H * 2 + V * 4,
-    "argmax": (V // 8) * 8,
+    "argmax": (V // 125) * 8,
 }
 # DRAM bytes per launch (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy of
 # known size) from the counter passes summarised in
-# profiles/gemv_qkvg_gdn13b_bf16_decode.md (bf16 arm).
+# profiles/k_gemv_cu_gdn13b_bf16w_decode.md (bf16w_fp32s arm).  The
+# recurrence moves 2.1 MB more than its state: each 16-column workgroup
+# writes half of every 128-byte line, which the L2 fills before merging.
 MEASURED_TRAFFIC = {
-    "qkvg": 34_642_000, "recur": 4_377_000, "o_proj": 8_752_000, "gate_up": 46_549_000,
-    "down": 23_395_000, "lm_head": 131_882_000, "argmax": 35_000,
+    "qkvg": 34_470_000, "recur": 6_529_000, "o_proj": 8_680_000, "gate_up": 46_562_000,
+    "down": 23_349_000, "lm_head": 136_951_000, "argmax": 7_000,
 }
 LAUNCHES_PER_TOKEN = {"qkvg": L, "recur": L, "o_proj": L, "gate_up": L, "down": L, "lm_head": 1, "argmax": 1}
 

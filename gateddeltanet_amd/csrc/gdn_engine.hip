@@ -3,24 +3,23 @@
 // state, the captured per-token hipGraph, and the run-state entry points of
 // include/gdn_amd.h.
 //
-// One decode step (token id -> argmax token id), per layer l:
-//   k_qkvg     bf16 GEMV [4H x H] (q,k,v,g) + per-channel causal conv/SiLU
-//              with the conv-tail shift, plus one extra workgroup for the
-//              tiny a/b projections          gdn_model.cpp:3785-3797, :1501-1536,
-//                                            :1543-1667, :5043-5130
-//   k_recur    per (head, 64-column block): q/k L2 norm, beta/decay, the
-//              fused Sk / Sq read pass, delta, o, and the rank-1 state update;
-//              the last block of a head applies the output RMSNorm * gate
-//                                            :2376-2933, :3226-3349
-//   k_gemv_res o_proj GEMV; the last block adds the residual and applies the
-//              MLP RMSNorm                   :3803-3814, :3379-3450
-//   k_gu       gate/up GEMV (rows interleaved 4+4) with the SwiGLU epilogue
-//                                            :3815-3826, :4751-4767
-//   k_gemv_res down GEMV; the last block adds the residual and applies the
-//              next layer's attention RMSNorm (the final norm after the last)
-//                                            :3827-3842
-// then k_lm: LM-head GEMV writing FP32 logits and a two-stage argmax
-// (:3857-3890, :4778-4931).  k_embed opens the step (:3716-3740, :1394-1474).
+// One decode step (token id -> argmax token id) is one captured hipGraph of
+// 122 launches.  Per layer l (BF16 contracts; the FP32 control arm runs the
+// same steps with the row-block k_gemv):
+//   QKVG    k_gemv_cu: residual add + attention RMSNorm prologue (the
+//           embedding import in layer 0), BF16 GEMV [4H x H] (q,k,v,g),
+//           per-channel causal conv/SiLU with the conv-tail shift, gate and
+//           sigmoid(gate); workgroup h < 8 also runs head h's tiny a/b rows
+//           and beta/decay               gdn_model.cpp:3716-3740, :3785-3797,
+//                                        :1394-1474, :1501-1667, :2461-2465
+//   recur   k_recur per (head, 16 columns): q/k L2 norms, the Sk / Sq column
+//           chains, delta, o and the rank-1 state update  :2376-2933, :3226-3349
+//   o_proj  k_gemv_cu: per-head output RMSNorm * gate prologue, GEMV  :3803-3814
+//   GU      k_gemv_cu: residual add + MLP RMSNorm prologue, gate/up GEMV
+//           (22 + 22 rows per workgroup), SwiGLU  :3815-3826, :4751-4767, :3379-3450
+//   down    k_gemv_cu: GEMV [H x I]      :3827-3842
+// then the LM head (final norm prologue, FP32 logits, per-workgroup argmax)
+// and k_argmax (:3857-3890, :4778-4931).
 //
 // Arithmetic follows the reference's all-BF16 contract bit for bit (products
 // rounded to BF16 with DAZ/FTZ, tree16 + four-bank reduction, every operator
