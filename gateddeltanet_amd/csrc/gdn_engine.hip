@@ -1209,7 +1209,7 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     constexpr int CHW = (4 * CR + 63) / 64;  // waves that run bank chains
     static_assert(CHW <= 16, "one chain lane per bank");
     static_assert(K % kT == 0 && (PRO == PRO_PLAIN || K == kH), "input shape");
-    static_assert(EPI != EPI_QKVG || K == kH, "a/b rows: hidden input");
+    static_assert(EPI != EPI_QKVG || (K == kH && CHW < 16), "a/b rows: hidden input, a free wave");
     __shared__ __attribute__((aligned(16))) uint32_t xs[K];
     __shared__ __attribute__((aligned(16))) float part[CR * BankLayout<K>::RSTR];
     __shared__ __attribute__((aligned(16))) float scratch[kH / 16];
@@ -1231,12 +1231,20 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     Prologue<C, K, PRO> pro;
     if (t < kT) pro.load(src);
 
-    // QKVG: the owner lane of each q/k/v row reads its conv tails and taps
-    // now, ahead of the weight stream (the epilogue would otherwise wait on
-    // them after the chains)
+    // 2. the weight stream
+    WStream<K, ROWS, C, D> ws;
+    ws.prime(wblk);
+
+    // QKVG extras, read behind the weight loads so they take no load-queue
+    // slot ahead of the stream: the conv tails and taps of each q/k/v row
+    // (its owner lane), and in workgroup h < 8 head h's a and b rows (FP32,
+    // waves 12..15)
     const bool owner = wave < CHW && (t & 3) == 0 && (t >> 2) < CR;
     uint16_t tail_b[3] = {0, 0, 0};
     f32x4 taps = {0.0f, 0.0f, 0.0f, 0.0f};
+    u32x4 abw[4];
+    const bool ab_blk = (EPI == EPI_QKVG) && blockIdx.x < kNH;
+    constexpr int kAbT0 = kTB - kT;  // first a/b thread
     if constexpr (EPI == EPI_QKVG) {
         const int r = row0 + (t >> 2);
         if (owner && r < 3 * kH) {
@@ -1247,23 +1255,13 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
             tail_b[2] = tl[2 * kH + ch];
             taps = *reinterpret_cast<const f32x4 *>(ep.aux + kAuxConv + ((size_t)kind * kH + ch) * 4);
         }
-    }
-    // QKVG workgroup h < 8 also owns head h's a and b rows (FP32 weights,
-    // read by the input waves ahead of their weight stream)
-    u32x4 abw[4];
-    const bool ab_blk = (EPI == EPI_QKVG) && blockIdx.x < kNH;
-    if constexpr (EPI == EPI_QKVG) {
-        if (ab_blk && t < kT) {
-            const int abrow = (t >> 7) * kNH + blockIdx.x, hb = t & 127;
+        if (ab_blk && t >= kAbT0) {
+            const int u = t - kAbT0, abrow = (u >> 7) * kNH + blockIdx.x, hb = u & 127;
             const u32x4 *src4 = reinterpret_cast<const u32x4 *>(ep.aux + kAuxAB + (size_t)abrow * kH + hb * 16);
 #pragma unroll
             for (int q = 0; q < 4; ++q) abw[q] = src4[q];
         }
     }
-
-    // 2. the weight stream
-    WStream<K, ROWS, C, D> ws;
-    ws.prime(wblk);
 
     // 3. the input vector in LDS and the fast-path verdict: waves 0..3 build
     // it (synchronising only among themselves); the other waves, once their
@@ -1272,46 +1270,6 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     if (t < kT) {
         Wave4Sync sync{&arrive};
         fast = pro.finish_bf16(src, wi, xs, scratch, bcast, red, sync);
-        if constexpr (EPI == EPI_QKVG) {
-            if (ab_blk) {
-                // a_h and b_h: FP32 products x * w, tree16 per half-beat, then
-                // acc = (acc + tree16(lo)) + tree16(hi) per beat, rounded
-                // (gdn_gemv_tiny_ab); then beta_h and decay_h -- all while the
-                // weight stream is in flight
-                const int hb = t & 127;
-                uint32_t xv[16];
-                lds_load16u(xs + hb * 16, xv);
-                float p[16];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    p[4 * q + 0] = lane_word_value(xv[4 * q + 0], 0) * u2f(abw[q].x);
-                    p[4 * q + 1] = lane_word_value(xv[4 * q + 1], 1) * u2f(abw[q].y);
-                    p[4 * q + 2] = lane_word_value(xv[4 * q + 2], 0) * u2f(abw[q].z);
-                    p[4 * q + 3] = lane_word_value(xv[4 * q + 3], 1) * u2f(abw[q].w);
-                }
-                abpart[t] = tree16(p);
-                sync();
-                if (wave == 3) {
-                    const int lane = t & 63;
-                    float acc = 0.0f;
-                    if (lane < 2) {
-                        const float *pr = abpart + lane * Hb<kH>::HB;
-                        for (int j = 0; j < Hb<kH>::NB; ++j) acc = (acc + pr[2 * j]) + pr[2 * j + 1];
-                    }
-                    const float a = R<C>(acc);
-                    const float b = R<C>(__shfl(acc, 1));
-                    if (lane == 0) {
-                        float beta, decay;
-                        head_scalars(a, b, ep.aux[kAuxALog + blockIdx.x], ep.aux[kAuxDtBias + blockIdx.x], beta,
-                                     decay);
-                        ep.ab[blockIdx.x] = a;
-                        ep.ab[kNH + blockIdx.x] = b;
-                        ep.bd[2 * blockIdx.x] = beta;
-                        ep.bd[2 * blockIdx.x + 1] = decay;
-                    }
-                }
-            }
-        }
     } else {
         wait_count(&arrive, 4 * Prologue<C, K, PRO>::kSyncs);
         fast = decide_fast(red, wi);
@@ -1320,7 +1278,47 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     // 4. products, barrier, bank chains and the row epilogue
     if (fast) ws.template run<true>(xs, part);
     else ws.template run<false>(xs, part);
+    if constexpr (EPI == EPI_QKVG) {
+        if (ab_blk && t >= kAbT0) {
+            // a_h and b_h: FP32 products x * w, tree16 per half-beat
+            // (gdn_gemv_tiny_ab)
+            const int hb = (t - kAbT0) & 127;
+            uint32_t xv[16];
+            lds_load16u(xs + hb * 16, xv);
+            float p[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                p[4 * q + 0] = lane_word_value(xv[4 * q + 0], 0) * u2f(abw[q].x);
+                p[4 * q + 1] = lane_word_value(xv[4 * q + 1], 1) * u2f(abw[q].y);
+                p[4 * q + 2] = lane_word_value(xv[4 * q + 2], 0) * u2f(abw[q].z);
+                p[4 * q + 3] = lane_word_value(xv[4 * q + 3], 1) * u2f(abw[q].w);
+            }
+            abpart[t - kAbT0] = tree16(p);
+        }
+    }
     __syncthreads();
+    if constexpr (EPI == EPI_QKVG) {
+        if (ab_blk && wave == CHW) {
+            // acc = (acc + tree16(lo)) + tree16(hi) per beat, rounded; then
+            // beta_h and decay_h -- beside the bank chains of waves 0..CHW-1
+            const int lane = t & 63;
+            float acc = 0.0f;
+            if (lane < 2) {
+                const float *pr = abpart + lane * Hb<kH>::HB;
+                for (int j = 0; j < Hb<kH>::NB; ++j) acc = (acc + pr[2 * j]) + pr[2 * j + 1];
+            }
+            const float a = R<C>(acc);
+            const float b = R<C>(__shfl(acc, 1));
+            if (lane == 0) {
+                float beta, decay;
+                head_scalars(a, b, ep.aux[kAuxALog + blockIdx.x], ep.aux[kAuxDtBias + blockIdx.x], beta, decay);
+                ep.ab[blockIdx.x] = a;
+                ep.ab[kNH + blockIdx.x] = b;
+                ep.bd[2 * blockIdx.x] = beta;
+                ep.bd[2 * blockIdx.x + 1] = decay;
+            }
+        }
+    }
     if (wave < CHW) {
         const float y = chain_rows<K, CR>(part);
         if (owner) {
