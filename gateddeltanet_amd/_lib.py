@@ -91,8 +91,31 @@ class GDNRunState(ctypes.Structure):
     ]
 
 
+class GDNLogitsParity(ctypes.Structure):
+    _fields_ = [
+        ("checked_steps", c_uint32),
+        ("argmax_mismatches", c_uint32),
+        ("compared_values", c_uint64),
+        ("exact_mismatches", c_uint64),
+        ("nonfinite_mismatches", c_uint64),
+        ("tolerance_failures", c_uint64),
+        ("min_top5_overlap", c_uint32),
+        ("reserved", c_uint32),
+        ("max_abs_error", ctypes.c_double),
+        ("max_rel_error", ctypes.c_double),
+        ("squared_error_sum", ctypes.c_double),
+        ("candidate_squared_sum", ctypes.c_double),
+        ("reference_squared_sum", ctypes.c_double),
+        ("dot_product_sum", ctypes.c_double),
+        ("worst_step_nrmse", ctypes.c_double),
+        ("min_step_cosine", ctypes.c_double),
+        ("worst_max_abs_over_reference_rms", ctypes.c_double),
+    ]
+
+
 FP = POINTER(c_float)
 IP = POINTER(c_int32)
+LP = POINTER(GDNLogitsParity)
 
 # name -> (restype, argtypes).  Every symbol include/gdn_amd.h declares.
 SIGNATURES = {
@@ -133,6 +156,13 @@ SIGNATURES = {
     "gdn_test_gemv": (c_int, [c_int, FP, FP, c_uint32, c_uint32, FP]),
     "gdn_test_recurrence": (c_int, [c_int, c_uint32, c_uint32, FP, FP, FP, FP, FP, FP, FP, FP, FP]),
     "gdn_test_layer": (c_int, [POINTER(GDNRunState), c_uint32, c_uint32, FP, FP]),
+    "gdn_logits_parity_init": (None, [LP]),
+    "gdn_logits_parity_step": (None, [LP, FP, FP, c_uint32, c_uint32, c_int]),
+    "gdn_logits_parity_nrmse": (ctypes.c_double, [LP]),
+    "gdn_logits_parity_cosine": (ctypes.c_double, [LP]),
+    "gdn_logits_gate_passes": (c_int, [LP]),
+    "gdn_token_logprob": (ctypes.c_double, [FP, c_uint32, c_int32]),
+    "gdn_strict_argmax": (c_uint32, [FP, c_uint32]),
 }
 
 _lib = None

@@ -270,6 +270,55 @@ int gdn_test_recurrence(int contract, uint32_t n_heads, uint32_t n_steps,
 int gdn_test_layer(GDNRunState *state, uint32_t layer, uint32_t n_steps,
                    const float *x_in, float *x_out);
 
+/* ===== logit tooling (host only): the reference host's scoring and
+ *       GPU-logit vector gate, as reusable calls ===== */
+
+/* Parity of one logit stream against a reference stream, accumulated over
+ * decode steps: exact / non-finite / FP32-tolerance mismatches, global and
+ * per-step NRMSE and cosine, max |error| and its ratio to the reference RMS,
+ * top-5 overlap and argmax agreement (host.cpp:61-110, :1412-1586).  No
+ * counterpart in gdn_model.h. */
+typedef struct GDNLogitsParity {
+    uint32_t checked_steps;
+    uint32_t argmax_mismatches;
+    uint64_t compared_values;
+    uint64_t exact_mismatches;
+    uint64_t nonfinite_mismatches;
+    uint64_t tolerance_failures;
+    uint32_t min_top5_overlap;
+    uint32_t reserved;
+    double max_abs_error;
+    double max_rel_error;
+    double squared_error_sum;
+    double candidate_squared_sum;
+    double reference_squared_sum;
+    double dot_product_sum;
+    double worst_step_nrmse;
+    double min_step_cosine;
+    double worst_max_abs_over_reference_rms;
+} GDNLogitsParity;
+
+void gdn_logits_parity_init(GDNLogitsParity *parity);
+/* One step: actual[vocab] (the engine's logits), reference[vocab], and the
+ * token the run selected.  apply_fp32_tolerance counts values outside
+ * 1e-3 + 1e-4 |reference| as tolerance failures. */
+void gdn_logits_parity_step(GDNLogitsParity *parity, const float *actual,
+                            const float *reference, uint32_t vocab,
+                            uint32_t selected_token, int apply_fp32_tolerance);
+double gdn_logits_parity_nrmse(const GDNLogitsParity *parity);
+double gdn_logits_parity_cosine(const GDNLogitsParity *parity);
+/* 1 when the accumulated parity meets the GPU-logit envelope (global NRMSE
+ * <= 0.01, worst step NRMSE <= 0.04, min step cosine >= 0.9995, worst
+ * max|err| / ref RMS <= 0.10, max|err| <= 0.5, top-5 overlap 5, no argmax or
+ * non-finite mismatch; host.cpp:77-110). */
+int gdn_logits_gate_passes(const GDNLogitsParity *parity);
+/* log softmax(logits)[target] in double (host.cpp:1954-1995, :2361-2382);
+ * NaN when target is out of range. */
+double gdn_token_logprob(const float *logits, uint32_t vocab, int32_t target);
+/* First index of the maximum under strict '>' from index 0
+ * (host.cpp:2348-2359). */
+uint32_t gdn_strict_argmax(const float *logits, uint32_t n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,200 @@
+"""gdn_eval_amd end to end on the GPU (gpu): the command-line driver against
+the same model stepped through the library in this process.
+
+* decode-from-state (gdn_eval.cpp:269-529): the trajectory, the GDNLOG1
+  logits and GDNHID1 hidden dumps and the post-decode .gdnstate equal the
+  in-process run bit for bit; the host check passes (exit 0); a second run
+  against the first run's logits dump reports no exact mismatch and passes
+  the vector gate.
+* the steady teacher-forced benchmark (host.cpp:2150-2256) reports every
+  step it was asked for.
+* rolling scoring (host.cpp:1943-2070) over a kind-3 fixture, with the model
+  read from a .gdnw file, gives the log-likelihood of a blank-state
+  teacher-forced run scored with float64 log-softmax in numpy.
+
+The CLI builds its model with --synth=1 (seed 0, std 0.02, BF16-rounded),
+the same call as Model.synth(num_layers=1) here.
+"""
+import json
+import os
+import shutil
+import struct
+import subprocess
+
+import numpy as np
+import pytest
+from scipy.special import log_softmax
+
+import gateddeltanet_amd as g
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CLI = os.path.join(ROOT, "gateddeltanet_amd", "gdn_eval_amd")
+N_DECODE = 6
+PROMPT = [11, 2222, 333, 31999, 0, 7, 7, 1234]
+
+
+def same_bits(a, b):
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    return a.shape == b.shape and bool((a.view(np.uint32) == b.view(np.uint32)).all())
+
+
+def run_cli(*args, timeout=300):
+    print(f"[cli] {' '.join(args)}", flush=True)
+    r = subprocess.run([CLI, *args], capture_output=True, text=True, timeout=timeout)
+    return r
+
+
+def read_dump(path, magic):
+    raw = open(path, "rb").read()
+    assert raw[:8] == magic
+    version, width, steps = struct.unpack("<III", raw[8:20])
+    assert version == 1
+    return np.frombuffer(raw[20:], np.float32).reshape(steps, width)
+
+
+@pytest.fixture(scope="module")
+def model():
+    m = g.Model.synth(num_layers=1, seed=0, std=0.02, bf16=True)
+    yield m
+    m.free()
+
+
+@pytest.fixture(scope="module")
+def decoded(model, tmp_path_factory):
+    """A .gdnstate after PROMPT, and the in-process decode from it."""
+    d = tmp_path_factory.mktemp("cli")
+    state = str(d / "prompt.gdnstate")
+    rs = g.RunState(model)
+    try:
+        for t in PROMPT:
+            seed = rs.decode_step(t)
+        rs.save_gdnstate(state, PROMPT, seed)
+        traj, logits, hidden = [seed], [], []
+        for _ in range(1, N_DECODE):
+            traj.append(rs.decode_step(traj[-1]))
+            logits.append(rs.logits())
+            hidden.append(rs.final_hidden())
+        rec, conv = rs.save_state()
+    finally:
+        rs.free()
+    return dict(dir=d, state=state, traj=traj, logits=np.stack(logits), hidden=np.stack(hidden),
+                rec=rec, conv=conv)
+
+
+def test_decode_from_state_matches_library(model, decoded):
+    d = decoded["dir"]
+    out, ldump, hdump, sdump = (str(d / n) for n in ("dec.json", "l.gdnlog", "h.gdnhid", "after.gdnstate"))
+    r = run_cli("--synth=1", out, "--decode-from-state", decoded["state"], "--decode-len", str(N_DECODE),
+                "--logits-dump", ldump, "--hidden-dump", hdump, "--dump-state", sdump)
+    assert r.returncode == 0, r.stderr
+    res = json.load(open(out))
+    ex = res["examples"][0]
+    assert res["kind"] == 2 and res["decode_len"] == N_DECODE
+    assert ex["gen_traj"] == decoded["traj"] and ex["tf_argmax"] == decoded["traj"]
+    assert len(ex["per_step_tpot_ms"]) == N_DECODE and ex["per_step_tpot_ms"][0] == 0.0
+    lp = res["logits_parity"]
+    assert lp["checked_steps"] == N_DECODE - 1 and lp["compared_values"] == (N_DECODE - 1) * 32000
+    assert lp["cpu_tolerance_failures"] == 0 and lp["argmax_mismatches"] == 0
+    assert same_bits(read_dump(ldump, b"GDNLOG1\0"), decoded["logits"])
+    assert same_bits(read_dump(hdump, b"GDNHID1\0"), decoded["hidden"])
+    rs = g.RunState(model)
+    try:
+        pl, seed = rs.load_gdnstate(sdump)
+        rec, conv = rs.save_state()
+    finally:
+        rs.free()
+    assert seed == decoded["traj"][-1]
+    assert same_bits(rec, decoded["rec"]) and same_bits(conv, decoded["conv"])
+
+    # the same run against its own dump: exact, and inside the vector gate
+    out2 = str(d / "dec2.json")
+    r = run_cli("--synth=1", out2, "--decode-from-state", decoded["state"], "--decode-len", str(N_DECODE),
+                "--logits-reference", ldump, "--no-host-check")
+    assert r.returncode == 0, r.stderr
+    res2 = json.load(open(out2))
+    assert res2["logits_parity"]["exact_reference_mismatches"] == 0
+    vg = res2["vector_gate"]
+    assert vg["passes"] is True and vg["global_nrmse"] == 0.0 and vg["min_top5_overlap"] == 5
+    assert res2["examples"][0]["gen_traj"] == decoded["traj"]
+
+
+def test_decode_length_from_ll_fixture(decoded):
+    """With no --decode-len, N is the first golden continuation length."""
+    d = decoded["dir"]
+    fx = d / "ll.gdnreq"
+    ctx, cont = PROMPT, decoded["traj"][:4]
+    with open(fx, "wb") as f:
+        f.write(b"GDNREQ1\0" + struct.pack("<III", 1, 2, 1))
+        f.write(struct.pack(f"<II{len(ctx)}i{len(cont)}i", len(ctx), len(cont), *ctx, *cont))
+    out = str(d / "ll.json")
+    r = run_cli("--synth=1", str(fx), out, "--decode-from-state", decoded["state"], "--no-host-check")
+    assert r.returncode == 0, r.stderr
+    assert json.load(open(out))["examples"][0]["gen_traj"] == decoded["traj"][:4]
+
+
+def test_benchmark_mode(decoded):
+    d = decoded["dir"]
+    toks = d / "tokens.txt"
+    toks.write_text(" ".join(str(t) for t in PROMPT) + "\n")
+    out = str(d / "bench.json")
+    r = run_cli("--synth=1", out, "--decode-from-state", decoded["state"], "--benchmark-tokens", str(toks),
+                "--benchmark-steps", "40", "--benchmark-warmup", "8")
+    assert r.returncode == 0, r.stderr
+    res = json.load(open(out))
+    assert res["schema"] == "gdn-steady-tpot-v1" and res["token_stream_length"] == len(PROMPT)
+    iv = res["intervals"][0]
+    assert iv["steps"] == 40 and iv["tokens_per_second"] > 0
+    for k in ("production_tpot", "kernel"):
+        s = iv[k]
+        assert 0 < s["min_ms"] <= s["median_ms"] <= s["p95_ms"] <= s["max_ms"]
+    assert iv["kernel"]["median_ms"] <= iv["production_tpot"]["median_ms"]
+
+
+def test_rolling_score_matches_library(model, tmp_path):
+    fx = tmp_path / "rolling.gdnreq"
+    docs = [
+        (12, 40, [([5, 6, 7], [8, 9])]),
+        (30, 120, [([100, 200], [300]), ([31999, 1, 2, 3], [4, 5, 6])]),
+    ]
+    with open(fx, "wb") as f:
+        f.write(b"GDNREQ1\0" + struct.pack("<III", 1, 3, len(docs)))
+        for words, nbytes, windows in docs:
+            f.write(struct.pack("<III", words, nbytes, len(windows)))
+            for ctx, cont in windows:
+                f.write(struct.pack(f"<II{len(ctx)}i{len(cont)}i", len(ctx), len(cont), *ctx, *cont))
+    if shutil.disk_usage(tmp_path).free < 3 * model.total_floats * 4:
+        pytest.skip("not enough scratch disk for a one-layer .gdnw")
+    weights = str(tmp_path / "m.gdnw")
+    model.save(weights)
+    out = str(tmp_path / "score.json")
+    r = run_cli(weights, str(fx), out, "--score")
+    assert r.returncode == 0, r.stderr
+    res = json.load(open(out))
+
+    total, scored = 0.0, 0
+    rs = g.RunState(model)
+    try:
+        for _, _, windows in docs:
+            for ctx, cont in windows:
+                rs.load_state(np.zeros(rs.n_state, np.float32), np.zeros(rs.n_conv, np.float32))
+                toks = ctx + cont
+                for i in range(len(toks) - 1):
+                    rs.decode_step(toks[i])
+                    if i + 1 < len(ctx):
+                        continue
+                    total += log_softmax(rs.logits().astype(np.float64))[toks[i + 1]]
+                    scored += 1
+    finally:
+        rs.free()
+    assert res["documents"] == 2 and res["windows"] == 3 and res["scored_tokens"] == scored == 6
+    assert res["words"] == 42 and res["bytes"] == 160
+    assert abs(res["total_logprob"] - total) <= 1e-9 * abs(total)
+    assert abs(res["word_perplexity"] - np.exp(-total / 42)) <= 1e-9 * np.exp(-total / 42)
+
+    # --score-doc-limit keeps the first document only
+    r = run_cli(weights, str(fx), out, "--score", "--score-doc-limit", "1")
+    assert r.returncode == 0, r.stderr
+    assert json.load(open(out))["scored_tokens"] == 2
