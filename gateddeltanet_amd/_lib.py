@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libgdn_amd.
 CONTRACT_REF = 0
 CONTRACT_BF16W_FP32S = 1
 CONTRACT_FP32 = 2
+MAX_STREAMS = 64  # GDN_MAX_STREAMS
 CONTRACT_NAMES = {CONTRACT_REF: "ref", CONTRACT_BF16W_FP32S: "bf16w_fp32s", CONTRACT_FP32: "fp32"}
 
 # Workspace layout in floats (gdn_model.h:54-75 of the reference).
@@ -113,9 +114,18 @@ class GDNLogitsParity(ctypes.Structure):
     ]
 
 
+class GDNBatchState(ctypes.Structure):
+    _fields_ = [
+        ("engine", c_void_p),
+        ("n_streams", c_uint32),
+        ("reserved", c_uint32),
+    ]
+
+
 FP = POINTER(c_float)
 IP = POINTER(c_int32)
 LP = POINTER(GDNLogitsParity)
+BP = POINTER(GDNBatchState)
 
 # name -> (restype, argtypes).  Every symbol include/gdn_amd.h declares.
 SIGNATURES = {
@@ -163,6 +173,18 @@ SIGNATURES = {
     "gdn_logits_gate_passes": (c_int, [LP]),
     "gdn_token_logprob": (ctypes.c_double, [FP, c_uint32, c_int32]),
     "gdn_strict_argmax": (c_uint32, [FP, c_uint32]),
+    "gdn_batch_init": (c_int, [BP, POINTER(GDNModel), c_uint32]),
+    "gdn_batch_free": (None, [BP]),
+    "gdn_batch_decode_step": (c_int, [BP, IP, IP]),
+    "gdn_batch_read_tokens": (c_int, [BP, IP]),
+    "gdn_batch_read_logits": (c_int, [BP, c_uint32, FP, c_size_t]),
+    "gdn_batch_read_final_hidden": (c_int, [BP, c_uint32, FP, c_size_t]),
+    "gdn_batch_load_stream_state": (c_int, [BP, c_uint32, FP, c_size_t, FP, c_size_t]),
+    "gdn_batch_save_stream_state": (c_int, [BP, c_uint32, FP, c_size_t, FP, c_size_t]),
+    "gdn_batch_run_teacher_forced": (c_int, [BP, IP, c_uint32, IP, FP, FP]),
+    "gdn_batch_profile_kernels": (c_int, [BP, c_uint32, FP, c_uint32]),
+    "gdn_batch_set_graph_mode": (c_int, [BP, c_int]),
+    "gdn_test_batch_gemm": (c_int, [FP, FP, c_uint32, c_uint32, FP]),
 }
 
 _lib = None

@@ -1,0 +1,1181 @@
+// gdn_batch.hip -- multi-stream decode: up to 64 independent token streams,
+// each with its own recurrent and conv state, advanced one token per stream
+// per step.  The reference decodes a single stream (README.md:75-77); this
+// path keeps its per-stream arithmetic and moves the projections onto the
+// matrix cores.
+//
+// Arithmetic.  Every operator outside the projections is the BF16W_FP32S
+// arithmetic of the batch-1 engine (the same device functions): embedding
+// import, residual adds and RMSNorms in chunk order, the tiny a/b rows in
+// FP32 products, conv + SiLU with the tail shift, beta/decay, the recurrence
+// on an FP32 state, the output norm * gate, SwiGLU, FP32 logits and the
+// strict-'>' argmax.  The projections take the same BF16 operands (weights
+// and activations at their BF16 rounding points, subnormals flushed) but form
+// exact products and accumulate them in FP32 on v_mfma_f32_16x16x32_bf16, in
+// the matrix cores' order instead of the reference's tree16 + four banks.
+// Results therefore agree with the batch-1 engine to rounding, not bit for
+// bit; outputs are rounded to BF16 at the same points.
+//
+// Layout.  A projection W [N][K] is stored as MFMA A-operand tiles (16 rows x
+// 32 columns, gdn_tile_bf16).  The activations of all streams enter as the B
+// operand: X [64 streams][K] BF16 in tiles of 32 columns x 16 streams, lane l
+// holding stream l % 16 and columns 8 (l / 16) .. + 7.  Stream s of a GEMM
+// output is column s of D = W X^T, so streams never mix.
+//
+// Per layer (8 launches):
+//   k_bgemm<QKVG>  q,k,v,g rows; epilogue: BF16 rounding, conv + SiLU with
+//                  each stream's tails, gate and sigmoid(gate)
+//   k_brecur       the recurrence per (head, stream), state in registers
+//   k_bonorm       per (head, stream) output RMSNorm * gate -> X
+//   k_bgemm<STORE> o_proj -> y (BF16)
+//   k_bnorm        h = R(h + y), MLP RMSNorm -> X
+//   k_bgemm<SWIGLU> gate/up row pairs, SwiGLU -> X (K = 5632)
+//   k_bgemm<STORE> down -> y
+//   k_bnorm        h = R(h + y), next attention RMSNorm (or the final norm)
+//                  -> X, with the next layer's a/b rows and beta/decay
+// plus the embedding norm before layer 0, the LM head with a per-workgroup
+// argmax, and the per-stream argmax merge.
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "gdn_amd.h"
+#include "gdn_device.h"
+#include "gdn_internal.h"
+
+namespace gdn {
+namespace bt {
+
+constexpr int kMaxB = GDN_MAX_STREAMS;  // streams = the 64 B-operand columns
+static_assert(kMaxB == 64, "four 16-stream groups per MFMA B operand");
+constexpr int kSplitO = 4;              // K splits of o_proj (16 k tiles each)
+constexpr int kSplitDown = 11;          // K splits of the down projection (16 k tiles each)
+constexpr int kKtH = kH / 32;           // k tiles of a K = 2048 projection
+constexpr int kKtI = kI / 32;           // k tiles of the down projection
+constexpr size_t kLayerState = (size_t)kNH * kHD * kHD;  // floats per (layer, stream)
+constexpr size_t kStreamTails = (size_t)3 * 3 * kH;      // floats per (layer, stream)
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+enum { EPI_RAW = 0, EPI_STORE = 1, EPI_QKVG = 2, EPI_SWIGLU = 3, EPI_LM = 4 };
+
+// BF16 bits of a value already at a BF16 rounding point, subnormals flushed
+// to a signed zero (the reference's products treat them as zero).
+__device__ __forceinline__ uint32_t bf16_daz_bits(float v) {
+    const uint32_t b = f2u(v);
+    return ((b & 0x7f800000u) == 0u) ? ((b >> 16) & 0x8000u) : (b >> 16);
+}
+
+// Offset (BF16 elements) of (stream m, column k) in an X tile buffer.
+__device__ __forceinline__ int xt_index(int m, int k) {
+    const int kt = k >> 5, kk = k & 31;
+    return (((kt * 4 + (m >> 4)) * 64 + ((kk >> 3) << 4) + (m & 15)) << 3) + (kk & 7);
+}
+
+// Eight consecutive columns k..k+7 (k % 8 == 0) of stream m, one 16-byte store.
+__device__ __forceinline__ void store_x8(uint16_t *x, int m, int k, const float *v) {
+    u32x4 w;
+    w.x = bf16_daz_bits(v[0]) | (bf16_daz_bits(v[1]) << 16);
+    w.y = bf16_daz_bits(v[2]) | (bf16_daz_bits(v[3]) << 16);
+    w.z = bf16_daz_bits(v[4]) | (bf16_daz_bits(v[5]) << 16);
+    w.w = bf16_daz_bits(v[6]) | (bf16_daz_bits(v[7]) << 16);
+    *reinterpret_cast<u32x4 *>(x + xt_index(m, k)) = w;
+}
+
+// ------------------------------------------------------------ the GEMM
+
+struct BEpi {
+    int n_streams;
+    int n_rows;          // N: row stride of y / logits
+    float *y;            // EPI_RAW / EPI_STORE: [64][N]
+    float *qkv;          // EPI_QKVG: [64][3][kH] after conv + SiLU
+    float *gate;         // [64][kH] R(g)
+    float *sgate;        // [64][kH] sigmoid(R(g))
+    float *tails;        // this layer's [n_streams][3][3][kH]
+    const float *conv_w; // [3][kH][4]
+    uint16_t *x_next;    // EPI_SWIGLU: X tiles of the down projection
+    float *logits;       // EPI_LM: [64][N]
+    float *part_val;     // [gridDim.x][64]
+    int *part_idx;
+};
+
+// D[rows][64 streams] = W[rows][K] X^T for 16 * RT rows per workgroup and
+// KT / S k tiles (split S of the K range: grid (N / (16 RT), S)).  The NW
+// waves split the workgroup's k tiles (wave w takes tiles w, w + NW, ...),
+// keep up to four tiles of operands in flight, and the per-wave sums are
+// added in wave order through LDS; the epilogue then runs on the reduced
+// tile.  Split partial sums (EPI_RAW with S > 1) are added in split order by
+// the consumer.
+template <int RT, int KT, int NW, int S, int EPI>
+__global__ __launch_bounds__(NW * 64) void k_bgemm(const u32x4 *__restrict__ W, const u32x4 *__restrict__ X,
+                                                   BEpi ep) {
+    constexpr int KTS = KT / S, KTW = KTS / NW, GT = NW * 64;
+    static_assert(KT % S == 0 && KTS % NW == 0, "whole k tiles per wave");
+    static_assert(EPI != EPI_SWIGLU || RT == 2, "SwiGLU pairs a gate and an up row tile");
+    static_assert(S == 1 || EPI == EPI_RAW, "split sums leave the GEMM unrounded");
+    constexpr int D = KTW < 4 ? KTW : 4;
+    constexpr size_t WSTEP = (size_t)NW * RT * 64, XSTEP = (size_t)NW * 4 * 64;
+    __shared__ f32x4 red[NW * RT * 4 * 64];
+    __shared__ float lm_v[RT * 4][64];
+    __shared__ int lm_i[RT * 4][64];
+    const int t = threadIdx.x, w = t >> 6, l = t & 63, rb = blockIdx.x, sp = blockIdx.y;
+    const int kt0 = sp * KTS + w;
+    const u32x4 *wp = W + ((size_t)rb * KT + kt0) * (RT * 64) + l;
+    const u32x4 *xp = X + (size_t)kt0 * (4 * 64) + l;
+
+    // QKVG epilogue operands (each stream's conv tails and the taps) are
+    // read ahead of the weight stream
+    constexpr int QE = (EPI == EPI_QKVG) ? (RT * 16 * 64) / GT : 1;
+    f32x4 qtl[QE], qcw[QE];
+    if constexpr (EPI == EPI_QKVG) {
+#pragma unroll
+        for (int j = 0; j < QE; ++j) {
+            const int q = t + GT * j, cl = q & (RT * 16 - 1), m = q / (RT * 16);
+            const int row = rb * 16 * RT + cl, which = row / kH, c = row - which * kH;
+            qtl[j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+            qcw[j] = qtl[j];
+            if (which < 3 && m < ep.n_streams) {
+                const float *tl = ep.tails + ((size_t)m * 3 + which) * 3 * kH + c;
+                qtl[j] = (f32x4){tl[0], tl[kH], tl[2 * kH], 0.0f};
+                qcw[j] = *reinterpret_cast<const f32x4 *>(ep.conv_w + ((size_t)which * kH + c) * 4);
+            }
+        }
+    }
+
+    f32x4 acc[RT][4];
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) acc[r][g] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    u32x4 a[D][RT], b[D][4];
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+#pragma unroll
+        for (int r = 0; r < RT; ++r) a[i][r] = wp[i * WSTEP + r * 64];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) b[i][g] = xp[i * XSTEP + g * 64];
+    }
+#pragma unroll
+    for (int i = 0; i < KTW; ++i) {
+        const int s = i % D;
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                acc[r][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[s][r]),
+                                                                    __builtin_bit_cast(bf16x8, b[s][g]),
+                                                                    acc[r][g], 0, 0, 0);
+        if (i + D < KTW) {
+#pragma unroll
+            for (int r = 0; r < RT; ++r) a[s][r] = wp[(i + D) * WSTEP + r * 64];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) b[s][g] = xp[(i + D) * XSTEP + g * 64];
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) red[((w * RT + r) * 4 + g) * 64 + l] = acc[r][g];
+    __syncthreads();
+
+    // Task (rt, nq, m): rows rt * 16 + nq * 4 + 0..3 of stream m, held by lane
+    // nq * 16 + m % 16 of stream group m / 16 in every wave's D tile.  Plain
+    // stores take a task per thread; the transcendental epilogues take one
+    // row (component e) of a task per thread.
+    auto red_index = [&](int rt, int nq, int m) { return (rt * 4 + (m >> 4)) * 64 + nq * 16 + (m & 15); };
+    auto reduced = [&](int rt, int nq, int m) {
+        const int idx = red_index(rt, nq, m);
+        f32x4 v = red[idx];
+#pragma unroll
+        for (int ww = 1; ww < NW; ++ww) v = v + red[ww * RT * 4 * 64 + idx];
+        return v;
+    };
+    auto reduced1 = [&](int rt, int nq, int m, int e) {
+        const float *rf = reinterpret_cast<const float *>(red) + 4 * red_index(rt, nq, m) + e;
+        float v = rf[0];
+#pragma unroll
+        for (int ww = 1; ww < NW; ++ww) v = v + rf[4 * ww * RT * 4 * 64];
+        return v;
+    };
+    if constexpr (EPI == EPI_RAW || EPI == EPI_STORE || EPI == EPI_LM) {
+#pragma unroll
+        for (int q = t; q < RT * 4 * 64; q += GT) {
+            const int m = q & 63, nq = (q >> 6) & 3, rt = q >> 8;
+            const f32x4 v = reduced(rt, nq, m);
+            const int row = rb * 16 * RT + rt * 16 + nq * 4;
+            if constexpr (EPI == EPI_LM) {
+                *reinterpret_cast<f32x4 *>(ep.logits + (size_t)m * ep.n_rows + row) = v;
+                float best = -3.402823466e38f;
+                int idx = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (v[e] > best) {
+                        best = v[e];
+                        idx = row + e;
+                    }
+                lm_v[rt * 4 + nq][m] = best;
+                lm_i[rt * 4 + nq][m] = idx;
+            } else {
+                f32x4 o = v;
+                if constexpr (EPI == EPI_STORE) {
+                    o.x = rne_bf16(v.x);
+                    o.y = rne_bf16(v.y);
+                    o.z = rne_bf16(v.z);
+                    o.w = rne_bf16(v.w);
+                }
+                *reinterpret_cast<f32x4 *>(ep.y + ((size_t)sp * 64 + m) * ep.n_rows + row) = o;
+            }
+        }
+    } else if constexpr (EPI == EPI_QKVG) {
+        // one element per thread and pass, channels fastest (coalesced tails)
+#pragma unroll
+        for (int j = 0; j < QE; ++j) {
+            const int q = t + GT * j, cl = q & (RT * 16 - 1), m = q / (RT * 16);
+            if (m >= ep.n_streams) continue;
+            const int row = rb * 16 * RT + cl;
+            const int which = row / kH, c = row - which * kH;  // q, k, v, g sections
+            const float raw = rne_bf16(reduced1(cl >> 4, (cl >> 2) & 3, m, cl & 3));
+            if (which < 3) {
+                // gdn_depthwise_conv_silu_head_kind, gdn_model.cpp:1543-1667
+                float *tl = ep.tails + ((size_t)m * 3 + which) * 3 * kH + c;
+                const f32x4 tv = qtl[j], cw = qcw[j];
+                const float sum = tv.x * cw.x + tv.y * cw.y + tv.z * cw.z + raw * cw.w;
+                tl[0] = tv.y;
+                tl[kH] = tv.z;
+                tl[2 * kH] = raw;
+                ep.qkv[((size_t)m * 3 + which) * kH + c] = rne_bf16(silu_ref(sum));
+            } else {
+                ep.gate[(size_t)m * kH + c] = raw;
+                ep.sgate[(size_t)m * kH + c] = sigmoid_ref(raw);
+            }
+        }
+    } else {  // EPI_SWIGLU, gemv32_store SwiGLU branch, gdn_model.cpp:4751-4767
+        // one channel x stream per thread and pass, packed through LDS into
+        // 16-byte stores of eight channels
+        __shared__ __attribute__((aligned(16))) uint16_t hb[64][16];
+#pragma unroll
+        for (int q = t; q < 16 * 64; q += GT) {
+            const int cl = q & 15, m = q >> 4;
+            const float g = rne_bf16(reduced1(0, cl >> 2, m, cl & 3)), u = rne_bf16(reduced1(1, cl >> 2, m, cl & 3));
+            hb[m][cl] = (uint16_t)bf16_daz_bits(rne_bf16(silu_ref(g) * u));
+        }
+        __syncthreads();
+        if (t < 128) {
+            const int mm = t >> 1, half = t & 1;
+            if (mm < ep.n_streams)
+                *reinterpret_cast<u32x4 *>(ep.x_next + xt_index(mm, rb * 16 + 8 * half)) =
+                    *reinterpret_cast<const u32x4 *>(&hb[mm][8 * half]);
+        }
+    }
+    if constexpr (EPI == EPI_LM) {
+        __syncthreads();
+        if (t < 64) {
+            // row quads in index order: strict '>' keeps the lowest index of
+            // equal maxima (NaN never wins)
+            float best = lm_v[0][t];
+            int idx = lm_i[0][t];
+#pragma unroll
+            for (int q = 1; q < RT * 4; ++q)
+                if (lm_v[q][t] > best) {
+                    best = lm_v[q][t];
+                    idx = lm_i[q][t];
+                }
+            ep.part_val[(size_t)rb * 64 + t] = best;
+            ep.part_idx[(size_t)rb * 64 + t] = idx;
+        }
+    }
+}
+
+// Per-stream merge of the LM head's per-workgroup results (in index order):
+// strict '>' within a thread's increasing blocks, then larger value / lower
+// index across threads -- the reference's first-maximum scan.
+__global__ __launch_bounds__(kT) void k_bargmax(const float *__restrict__ part_val,
+                                                const int *__restrict__ part_idx, int n_blocks,
+                                                int *__restrict__ tok_out) {
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    const int m = blockIdx.x, t = threadIdx.x;
+    float best = -3.402823466e38f;
+    int idx = 0;
+    for (int i = t; i < n_blocks; i += kT) {
+        const float v = part_val[(size_t)i * 64 + m];
+        if (v > best) {
+            best = v;
+            idx = part_idx[(size_t)i * 64 + m];
+        }
+    }
+#pragma unroll
+    for (int s = 1; s < 64; s <<= 1) {
+        const float ov = __shfl_xor(best, s);
+        const int oi = __shfl_xor(idx, s);
+        if (ov > best || (ov == best && oi < idx)) {
+            best = ov;
+            idx = oi;
+        }
+    }
+    if ((t & 63) == 0) {
+        bv[t >> 6] = best;
+        bi[t >> 6] = idx;
+    }
+    __syncthreads();
+    if (t == 0) {
+        for (int i = 1; i < 4; ++i)
+            if (bv[i] > best || (bv[i] == best && bi[i] < idx)) {
+                best = bv[i];
+                idx = bi[i];
+            }
+        tok_out[m] = idx;
+    }
+}
+
+// ------------------------------------------------------ per-stream kernels
+
+struct BNorm {
+    float *h;              // [64][kH] residual stream, updated in place
+    const float *y;        // [splits][64][kH] partial sums: h = R(h + R(sum)) first
+    const uint16_t *emb;   // embedding rows (BF16): h = R(emb[tok[m]]) (EMBED)
+    const int *tok;
+    const float *w;        // norm weight [kH]
+    uint16_t *x_out;       // X tiles of the next projection
+    float *xn_out;         // optional [64][kH] copy of the normalized vector
+    const float *ab_w;     // a_proj (8 x kH) then b_proj (8 x kH) (AB)
+    const float *a_log;
+    const float *dt_bias;
+    float *bd;             // [64][16]: beta, decay per head
+    float eps;
+};
+
+// One workgroup per stream: the residual add (or embedding import), the
+// RMSNorm in chunk order (gdn_rmsnorm_rows_bf16 / gdn_residual_rmsnorm_bf16,
+// gdn_model.cpp:1394-1474, :3351-3450) and, before an attention block, the
+// tiny a/b rows and beta/decay (gdn_gemv_tiny_ab :1501-1536, :2461-2465).
+// Thread t holds elements 8t..8t+7; a 16-element chunk is the sequential sum
+// of thread 2c's eight squares continued by thread 2c + 1.  SPLITS partial
+// sums of the preceding projection are added in split order (0: no residual
+// add; EMBED: the embedding row instead).  Every global operand, the a/b
+// rows included, is requested before the first dependent use.
+template <int SPLITS, bool EMBED, bool AB>
+__global__ __launch_bounds__(kT) void k_bnorm(BNorm p) {
+    __shared__ __attribute__((aligned(16))) float xs[kH];
+    __shared__ __attribute__((aligned(16))) float cs[kH / 16];
+    __shared__ __attribute__((aligned(16))) float tab[16][64][2];
+    __shared__ float abv[16];
+    __shared__ float scale_s;
+    const int m = blockIdx.x, t = threadIdx.x, e0 = 8 * t;
+    constexpr int ABN = AB ? 32 : 1;
+    f32x4 wq[ABN];
+    if constexpr (AB) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            const int q = t + kT * i, grp = q >> 3, sub = q & 7;
+            wq[i] = *reinterpret_cast<const f32x4 *>(p.ab_w + (size_t)(grp >> 6) * kH + 32 * (grp & 63) + 4 * sub);
+        }
+    }
+    const f32x4 *w4 = reinterpret_cast<const f32x4 *>(p.w + e0);
+    const f32x4 wa = w4[0], wb = w4[1];
+    float hv[8];
+    if constexpr (EMBED) {
+        const u32x4 raw = *reinterpret_cast<const u32x4 *>(p.emb + (size_t)p.tok[m] * kH + e0);
+        const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            hv[2 * j] = rne_bf16(u2f(wv[j] << 16));
+            hv[2 * j + 1] = rne_bf16(u2f(wv[j] & 0xffff0000u));
+        }
+    } else {
+        const f32x4 *h4 = reinterpret_cast<const f32x4 *>(p.h + (size_t)m * kH + e0);
+        const f32x4 a0 = h4[0], a1 = h4[1];
+        hv[0] = a0.x; hv[1] = a0.y; hv[2] = a0.z; hv[3] = a0.w;
+        hv[4] = a1.x; hv[5] = a1.y; hv[6] = a1.z; hv[7] = a1.w;
+        if constexpr (SPLITS > 0) {
+            // the projection's split sums in split order, then its rounding
+            f32x4 yp[SPLITS][2];
+#pragma unroll
+            for (int sp = 0; sp < SPLITS; ++sp) {
+                const f32x4 *y4 = reinterpret_cast<const f32x4 *>(p.y + ((size_t)sp * kMaxB + m) * kH + e0);
+                yp[sp][0] = y4[0];
+                yp[sp][1] = y4[1];
+            }
+            f32x4 y0 = yp[0][0], y1 = yp[0][1];
+#pragma unroll
+            for (int sp = 1; sp < SPLITS; ++sp) {
+                y0 = y0 + yp[sp][0];
+                y1 = y1 + yp[sp][1];
+            }
+            const float yv[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) hv[e] = rne_bf16(hv[e] + rne_bf16(yv[e]));
+        }
+    }
+    if constexpr (EMBED || SPLITS > 0) {
+        f32x4 *d = reinterpret_cast<f32x4 *>(p.h + (size_t)m * kH + e0);
+        d[0] = (f32x4){hv[0], hv[1], hv[2], hv[3]};
+        d[1] = (f32x4){hv[4], hv[5], hv[6], hv[7]};
+    }
+    // chunk sums: the even thread's partial continues in the odd thread
+    float part = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) part += hv[e] * hv[e];
+    const float lead = __shfl_xor(part, 1);
+    if (t & 1) {
+        float s = lead;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += hv[e] * hv[e];
+        cs[t >> 1] = s;
+    }
+    __syncthreads();
+    if (t == 0) {
+        // every chunk sum read ahead of the sequential adds
+        float v[kH / 16];
+#pragma unroll
+        for (int c = 0; c < kH / 64; ++c) {
+            const f32x4 q = reinterpret_cast<const f32x4 *>(cs)[c];
+            v[4 * c] = q.x;
+            v[4 * c + 1] = q.y;
+            v[4 * c + 2] = q.z;
+            v[4 * c + 3] = q.w;
+        }
+        float sum = 0.0f;
+#pragma unroll
+        for (int c = 0; c < kH / 16; ++c) sum += v[c];
+        scale_s = 1.0f / __builtin_sqrtf(sum / (float)kH + p.eps);
+    }
+    __syncthreads();
+    const float sc = scale_s;
+    const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+    float xv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xv[e] = rne_bf16(hv[e] * sc * wv[e]);
+    store_x8(p.x_out, m, e0, xv);
+    if (p.xn_out) {
+        f32x4 *d = reinterpret_cast<f32x4 *>(p.xn_out + (size_t)m * kH + e0);
+        d[0] = (f32x4){xv[0], xv[1], xv[2], xv[3]};
+        d[1] = (f32x4){xv[4], xv[5], xv[6], xv[7]};
+    }
+    if constexpr (AB) {
+        {
+            f32x4 *d = reinterpret_cast<f32x4 *>(xs + e0);
+            d[0] = (f32x4){xv[0], xv[1], xv[2], xv[3]};
+            d[1] = (f32x4){xv[4], xv[5], xv[6], xv[7]};
+        }
+        __syncthreads();
+        // rows 0..7 = a heads, 8..15 = b heads.  Eight lanes per (row,
+        // 32-column beat), four products each: lanes 0-3 form tree16 of the
+        // lower half, lanes 4-7 of the upper (pairs, then lane pairs, then
+        // lane quads), so a wave's loads cover eight consecutive beats of one
+        // row.
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            const int q = t + kT * i, grp = q >> 3, sub = q & 7;
+            const f32x4 xq = *reinterpret_cast<const f32x4 *>(xs + 32 * (grp & 63) + 4 * sub);
+            const f32x4 w = wq[i];
+            float s = (xq.x * w.x + xq.y * w.y) + (xq.z * w.z + xq.w * w.w);
+            s = s + __shfl_xor(s, 1);
+            s = s + __shfl_xor(s, 2);
+            if ((sub & 3) == 0) tab[grp >> 6][grp & 63][sub >> 2] = s;
+        }
+        __syncthreads();
+        if (t < 16) {
+            float v[128];
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                const f32x4 q = reinterpret_cast<const f32x4 *>(&tab[t][0][0])[i];
+                v[4 * i] = q.x;
+                v[4 * i + 1] = q.y;
+                v[4 * i + 2] = q.z;
+                v[4 * i + 3] = q.w;
+            }
+            float acc = 0.0f;
+#pragma unroll
+            for (int bt = 0; bt < 64; ++bt) acc = (acc + v[2 * bt]) + v[2 * bt + 1];
+            abv[t] = rne_bf16(acc);
+        }
+        __syncthreads();
+        if (t < kNH) {
+            float beta, decay;
+            head_scalars(abv[t], abv[kNH + t], p.a_log[t], p.dt_bias[t], beta, decay);
+            p.bd[m * 16 + 2 * t] = beta;
+            p.bd[m * 16 + 2 * t + 1] = decay;
+        }
+    }
+}
+
+// Per (head, stream): the output RMSNorm times the gate and sigmoid(gate)
+// (gdn_output_norm_and_gate, gdn_model.cpp:3226-3349) into X tiles.
+__global__ __launch_bounds__(kT) void k_bonorm(const float *__restrict__ attn, const float *__restrict__ gate,
+                                               const float *__restrict__ sgate, const float *__restrict__ w,
+                                               float eps, uint16_t *__restrict__ x_out) {
+    __shared__ float as[kHD];
+    __shared__ float cs[kHD / 16];
+    __shared__ float xs[kHD];
+    __shared__ float scale_s;
+    const int h = blockIdx.x, m = blockIdx.y, t = threadIdx.x, c = h * kHD + t;
+    const float a = attn[(size_t)m * kH + c];
+    as[t] = a;
+    __syncthreads();
+    if (t < kHD / 16) {
+        float s = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) {
+            const float v = as[16 * t + kk];
+            s += v * v;
+        }
+        cs[t] = s;
+    }
+    __syncthreads();
+    if (t == 0) {
+        float v[kHD / 16];
+#pragma unroll
+        for (int i = 0; i < kHD / 16; ++i) v[i] = cs[i];
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kHD / 16; ++i) sum += v[i];
+        scale_s = 1.0f / __builtin_sqrtf(sum / (float)kHD + eps);
+    }
+    __syncthreads();
+    xs[t] = rne_bf16(a * scale_s * w[t] * gate[(size_t)m * kH + c] * sgate[(size_t)m * kH + c]);
+    __syncthreads();
+    if (t < kHD / 8) store_x8(x_out, m, h * kHD + 8 * t, xs + 8 * t);
+}
+
+// The recurrence of one (head, stream) per workgroup of 512 threads, with
+// the batch-1 arithmetic (gdn_island_prep / read / update,
+// gdn_model.cpp:2376-2933).  Wave w owns state column 64 (w % 4) + lane and
+// rows 128 (w / 4) .. + 127, held in registers from load to store: waves 0-3
+// run the r and p chains over rows 0..127, hand the partial sums to waves
+// 4-7 through LDS, which continue over rows 128..255 (the chain order is
+// j = 0..255 as in the reference) and form delta and o; every wave then
+// writes its rows of S' = decay * S + kn (x) delta.  The q/k norms and alpha
+// use the batch-1 tree order (four wave butterflies, (w0 + w1) + (w2 + w3)).
+__global__ __launch_bounds__(2 * kT) void k_brecur(const float *__restrict__ qkv, const float *__restrict__ bd,
+                                                   float *__restrict__ state, float *__restrict__ attn) {
+    constexpr int RH = kHD / 2;  // rows per wave
+    __shared__ float qn[kHD], kn[kHD], rpart[kHD], ppart[kHD], dl[kHD];
+    __shared__ float red[8], red2[4];
+    const int h = blockIdx.x, m = blockIdx.y, t = threadIdx.x, w = t >> 6, lane = t & 63;
+    const int col = (w & 3) * 64 + lane, r0 = (w >> 2) * RH;
+    const float *qp = qkv + (size_t)m * 3 * kH + h * kHD;
+    float *S = state + (size_t)m * kLayerState + (size_t)h * kHD * kHD + col;
+    float sv[RH];
+#pragma unroll
+    for (int j = 0; j < RH; ++j) sv[j] = S[(size_t)(r0 + j) * kHD];
+    const float beta = bd[m * 16 + 2 * h], decay = bd[m * 16 + 2 * h + 1];
+    float q = 0.0f, k = 0.0f;
+    if (t < kHD) {
+        q = qp[t];
+        k = qp[kH + t];
+        const float qs = wave_tree64(q * q), ks = wave_tree64(k * k);
+        if (lane == 0) {
+            red[w] = qs;
+            red[4 + w] = ks;
+        }
+    }
+    __syncthreads();
+    if (t < kHD) {
+        const float q_sq = (red[0] + red[1]) + (red[2] + red[3]);
+        const float k_sq = (red[4] + red[5]) + (red[6] + red[7]);
+        const float qv = q * (1.0f / __builtin_sqrtf(q_sq + 1e-6f));
+        const float kv = k * (1.0f / __builtin_sqrtf(k_sq + 1e-6f));
+        qn[t] = qv;
+        kn[t] = kv;
+        const float qk = wave_tree64(qv * kv);
+        if (lane == 0) red2[w] = qk;
+    }
+    __syncthreads();
+    if (w < 4) {
+        float r = 0.0f, p = 0.0f;
+#pragma unroll
+        for (int j = 0; j < RH; ++j) {
+            r = r + sv[j] * kn[j];
+            p = p + sv[j] * qn[j];
+        }
+        rpart[col] = r;
+        ppart[col] = p;
+    }
+    __syncthreads();
+    if (w >= 4) {
+        float r = rpart[col], p = ppart[col];
+#pragma unroll
+        for (int j = 0; j < RH; ++j) {
+            r = r + sv[j] * kn[RH + j];
+            p = p + sv[j] * qn[RH + j];
+        }
+        const float alpha = (red2[0] + red2[1]) + (red2[2] + red2[3]);
+        const float delta = beta * (qp[2 * kH + col] - decay * r);
+        const float o = 0.0625f * (decay * p + alpha * delta);
+        dl[col] = delta;
+        attn[(size_t)m * kH + h * kHD + col] = rne_bf16(o);
+    }
+    __syncthreads();
+    const float d = dl[col];
+#pragma unroll
+    for (int j = 0; j < RH; ++j) S[(size_t)(r0 + j) * kHD] = decay * sv[j] + kn[r0 + j] * d;
+}
+
+}  // namespace bt
+}  // namespace gdn
+
+// ===================================================================== engine
+
+using namespace gdn;
+using namespace gdn::bt;
+
+struct GDNBatchEngine {
+    int layers = 0, vocab = 0, streams = 0;
+    float eps = 1e-6f;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    void *wmem = nullptr;
+    const u32x4 *w_qkvg[kMaxLayers] = {}, *w_o[kMaxLayers] = {}, *w_gu[kMaxLayers] = {},
+                *w_down[kMaxLayers] = {}, *w_lm = nullptr;
+    uint16_t *emb = nullptr;
+    float *aux = nullptr;      // [layers][kAuxLayer] + final_norm[kH]
+    float *state = nullptr;    // [layers][streams][kNH][kHD][kHD]
+    float *tails = nullptr;    // [layers][streams][3][3][kH]
+    float *act = nullptr;
+    float *h = nullptr, *qkv = nullptr, *gate = nullptr, *sgate = nullptr, *bd = nullptr,
+          *attn = nullptr, *ypart = nullptr, *xn = nullptr, *logits = nullptr, *part_val = nullptr;
+    int *part_idx = nullptr;
+    uint16_t *x_h = nullptr, *x_o = nullptr, *x_d = nullptr;  // X tiles, K = 2048 / 2048 / 5632
+    int *tok_dev = nullptr;   // [0..63] in, [64..127] out
+    int *tok_host = nullptr;  // pinned, same layout
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    bool use_graph = true;
+};
+
+namespace {
+
+float *b_aux(GDNBatchEngine *e, int l) { return e->aux + (size_t)l * kAuxLayer; }
+float *b_tails(GDNBatchEngine *e, int l) { return e->tails + (size_t)l * e->streams * kStreamTails; }
+float *b_state(GDNBatchEngine *e, int l) { return e->state + (size_t)l * e->streams * kLayerState; }
+int lm_wgs(const GDNBatchEngine *e) { return e->vocab / 32; }
+
+int b_check_shape(const GDNWeightHeader *c) {
+    if (c->hidden_size != (uint32_t)kH || c->num_heads != (uint32_t)kNH || c->num_v_heads != (uint32_t)kNH ||
+        c->head_dim != (uint32_t)kHD || c->intermediate_size != (uint32_t)kI || c->conv_size != 4u) {
+        gdn_error("gdn: the engine is specialised for hidden 2048, 8x256 heads, intermediate 5632, conv 4");
+        return -1;
+    }
+    if (c->num_layers < 1 || c->num_layers > (uint32_t)kMaxLayers) {
+        gdn_error("gdn: num_layers must be 1..24");
+        return -1;
+    }
+    if (c->vocab_size == 0 || (c->vocab_size % 32) != 0) {
+        gdn_error("gdn: the multi-stream engine needs a vocabulary that is a multiple of 32");
+        return -1;
+    }
+    return 0;
+}
+
+// BF16 bits (subnormals flushed) of n BF16-exact floats.
+void to_bf16(const float *src, size_t n, std::vector<uint16_t> &dst) {
+    dst.resize(n);
+    float mn, mx;
+    int bad;
+    gdn_pack_bf16_daz(src, dst.data(), n, &mn, &mx, &bad);
+}
+
+int upload_tiled(const std::vector<uint16_t> &rows, size_t n_rows, size_t k, int rt, char *&p,
+                 const u32x4 *&out) {
+    std::vector<uint16_t> tiled(n_rows * k);
+    gdn_tile_bf16(rows.data(), n_rows, k, rt, tiled.data());
+    GDN_HIP(hipMemcpy(p, tiled.data(), tiled.size() * 2, hipMemcpyHostToDevice));
+    out = reinterpret_cast<const u32x4 *>(p);
+    p += tiled.size() * 2;
+    return 0;
+}
+
+int b_upload(GDNBatchEngine *e, const GDNModel *m) {
+    const size_t H = kH, I = kI, V = (size_t)e->vocab, L = (size_t)e->layers;
+    const size_t per_layer = 4 * H * H + H * H + 2 * I * H + H * I;
+    GDN_HIP(hipMalloc(&e->wmem, (L * per_layer + V * H) * 2));
+    char *p = static_cast<char *>(e->wmem);
+    std::vector<uint16_t> rows, part;
+    for (size_t l = 0; l < L; ++l) {
+        const GDNLayerWeights &w = m->layers[l];
+        rows.resize(4 * H * H);
+        const float *src[4] = {w.q_proj, w.k_proj, w.v_proj, w.g_proj};
+        for (int s = 0; s < 4; ++s) {
+            to_bf16(src[s], H * H, part);
+            std::memcpy(rows.data() + s * H * H, part.data(), H * H * 2);
+        }
+        if (upload_tiled(rows, 4 * H, H, 2, p, e->w_qkvg[l])) return -1;
+        to_bf16(w.o_proj, H * H, rows);
+        if (upload_tiled(rows, H, H, 2, p, e->w_o[l])) return -1;
+        // gate rows c..c+15 then up rows c..c+15: one SwiGLU row pair per
+        // workgroup row block
+        std::vector<uint16_t> g16, u16;
+        to_bf16(w.mlp_gate_proj, I * H, g16);
+        to_bf16(w.mlp_up_proj, I * H, u16);
+        rows.resize(2 * I * H);
+        for (size_t blk = 0; blk < I / 16; ++blk) {
+            std::memcpy(rows.data() + (2 * blk) * 16 * H, g16.data() + blk * 16 * H, 16 * H * 2);
+            std::memcpy(rows.data() + (2 * blk + 1) * 16 * H, u16.data() + blk * 16 * H, 16 * H * 2);
+        }
+        if (upload_tiled(rows, 2 * I, H, 2, p, e->w_gu[l])) return -1;
+        to_bf16(w.mlp_down_proj, H * I, rows);
+        if (upload_tiled(rows, H, I, 2, p, e->w_down[l])) return -1;
+    }
+    to_bf16(m->lm_head, V * H, rows);
+    if (upload_tiled(rows, V, H, 2, p, e->w_lm)) return -1;
+    // embeddings keep their top 16 bits (the batch-1 engine's import)
+    std::vector<uint16_t> emb(V * H);
+    for (size_t i = 0; i < V * H; ++i) {
+        uint32_t b;
+        std::memcpy(&b, m->embeddings + i, 4);
+        emb[i] = (uint16_t)(b >> 16);
+    }
+    GDN_HIP(hipMalloc(&e->emb, emb.size() * 2));
+    GDN_HIP(hipMemcpy(e->emb, emb.data(), emb.size() * 2, hipMemcpyHostToDevice));
+
+    std::vector<float> aux(L * kAuxLayer + H, 0.0f);
+    for (size_t l = 0; l < L; ++l) {
+        const GDNLayerWeights &w = m->layers[l];
+        float *a = aux.data() + l * kAuxLayer;
+        std::memcpy(a + kAuxAttnNorm, w.attn_norm, H * 4);
+        std::memcpy(a + kAuxMlpNorm, w.mlp_norm, H * 4);
+        std::memcpy(a + kAuxONorm, w.o_norm, kHD * 4);
+        std::memcpy(a + kAuxALog, w.a_log, kNH * 4);
+        std::memcpy(a + kAuxDtBias, w.dt_bias, kNH * 4);
+        std::memcpy(a + kAuxAB, w.a_proj, kNH * H * 4);
+        std::memcpy(a + kAuxAB + kNH * H, w.b_proj, kNH * H * 4);
+        std::memcpy(a + kAuxConv, w.q_conv, H * 4 * 4);
+        std::memcpy(a + kAuxConv + H * 4, w.k_conv, H * 4 * 4);
+        std::memcpy(a + kAuxConv + 2 * H * 4, w.v_conv, H * 4 * 4);
+    }
+    std::memcpy(aux.data() + L * kAuxLayer, m->final_norm, H * 4);
+    GDN_HIP(hipMalloc(&e->aux, aux.size() * 4));
+    GDN_HIP(hipMemcpy(e->aux, aux.data(), aux.size() * 4, hipMemcpyHostToDevice));
+    return 0;
+}
+
+int b_alloc(GDNBatchEngine *e) {
+    const size_t L = (size_t)e->layers, B = (size_t)e->streams, V = (size_t)e->vocab;
+    GDN_HIP(hipMalloc(&e->state, L * B * kLayerState * 4));
+    GDN_HIP(hipMemset(e->state, 0, L * B * kLayerState * 4));
+    GDN_HIP(hipMalloc(&e->tails, L * B * kStreamTails * 4));
+    GDN_HIP(hipMemset(e->tails, 0, L * B * kStreamTails * 4));
+    const size_t G = (size_t)lm_wgs(e);
+    const size_t act = kMaxB * (kH + 3 * kH + kH + kH + 16 + kH + kSplitDown * kH + kH + V) + G * kMaxB;
+    GDN_HIP(hipMalloc(&e->act, act * 4));
+    GDN_HIP(hipMemset(e->act, 0, act * 4));
+    float *p = e->act;
+    e->h = p; p += kMaxB * kH;
+    e->qkv = p; p += kMaxB * 3 * kH;
+    e->gate = p; p += kMaxB * kH;
+    e->sgate = p; p += kMaxB * kH;
+    e->bd = p; p += kMaxB * 16;
+    e->attn = p; p += kMaxB * kH;
+    e->ypart = p; p += (size_t)kSplitDown * kMaxB * kH;
+    e->xn = p; p += kMaxB * kH;
+    e->logits = p; p += kMaxB * V;
+    e->part_val = p; p += G * kMaxB;
+    GDN_HIP(hipMalloc(&e->part_idx, G * kMaxB * sizeof(int)));
+    // X tiles: streams beyond n_streams stay zero
+    GDN_HIP(hipMalloc(&e->x_h, (size_t)kMaxB * kH * 2));
+    GDN_HIP(hipMalloc(&e->x_o, (size_t)kMaxB * kH * 2));
+    GDN_HIP(hipMalloc(&e->x_d, (size_t)kMaxB * kI * 2));
+    GDN_HIP(hipMemset(e->x_h, 0, (size_t)kMaxB * kH * 2));
+    GDN_HIP(hipMemset(e->x_o, 0, (size_t)kMaxB * kH * 2));
+    GDN_HIP(hipMemset(e->x_d, 0, (size_t)kMaxB * kI * 2));
+    GDN_HIP(hipMalloc(&e->tok_dev, 2 * kMaxB * sizeof(int)));
+    GDN_HIP(hipMemset(e->tok_dev, 0, 2 * kMaxB * sizeof(int)));
+    GDN_HIP(hipHostMalloc(&e->tok_host, 2 * kMaxB * sizeof(int), hipHostMallocDefault));
+    std::memset(e->tok_host, 0, 2 * kMaxB * sizeof(int));
+    GDN_HIP(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
+    GDN_HIP(hipEventCreate(&e->ev0));
+    GDN_HIP(hipEventCreate(&e->ev1));
+    GDN_HIP(hipDeviceSynchronize());
+    return 0;
+}
+
+BNorm bnorm(GDNBatchEngine *e, const float *y, const float *w, uint16_t *x_out, int ab_layer) {
+    BNorm p{};
+    p.h = e->h;
+    p.y = y;
+    p.w = w;
+    p.x_out = x_out;
+    p.eps = e->eps;
+    if (ab_layer >= 0) {
+        float *a = b_aux(e, ab_layer);
+        p.ab_w = a + kAuxAB;
+        p.a_log = a + kAuxALog;
+        p.dt_bias = a + kAuxDtBias;
+        p.bd = e->bd;
+    }
+    return p;
+}
+
+// Kernel kinds of gdn_batch_profile_kernels, in output order.
+enum { KB_EMBED, KB_QKVG, KB_RECUR, KB_ONORM, KB_O, KB_NORM, KB_GU, KB_DOWN, KB_LM, KB_ARGMAX, KB_KINDS };
+
+void launch_embed(GDNBatchEngine *e, hipStream_t s) {
+    BNorm p = bnorm(e, nullptr, b_aux(e, 0) + kAuxAttnNorm, e->x_h, 0);
+    p.emb = e->emb;
+    p.tok = e->tok_dev;
+    hipLaunchKernelGGL((k_bnorm<0, true, true>), dim3(e->streams), dim3(kT), 0, s, p);
+}
+void launch_qkvg(GDNBatchEngine *e, int l, hipStream_t s) {
+    BEpi ep{};
+    ep.n_streams = e->streams;
+    ep.n_rows = 4 * kH;
+    ep.qkv = e->qkv;
+    ep.gate = e->gate;
+    ep.sgate = e->sgate;
+    ep.tails = b_tails(e, l);
+    ep.conv_w = b_aux(e, l) + kAuxConv;
+    hipLaunchKernelGGL((k_bgemm<2, kKtH, 8, 1, EPI_QKVG>), dim3(4 * kH / 32), dim3(8 * 64), 0, s, e->w_qkvg[l],
+                       reinterpret_cast<const u32x4 *>(e->x_h), ep);
+}
+void launch_recur(GDNBatchEngine *e, int l, hipStream_t s) {
+    hipLaunchKernelGGL(k_brecur, dim3(kNH, e->streams), dim3(2 * kT), 0, s, e->qkv, e->bd, b_state(e, l), e->attn);
+}
+void launch_onorm(GDNBatchEngine *e, int l, hipStream_t s) {
+    hipLaunchKernelGGL(k_bonorm, dim3(kNH, e->streams), dim3(kT), 0, s, e->attn, e->gate, e->sgate,
+                       b_aux(e, l) + kAuxONorm, e->eps, e->x_o);
+}
+void launch_o(GDNBatchEngine *e, int l, hipStream_t s) {
+    BEpi ep{};
+    ep.n_streams = e->streams;
+    ep.n_rows = kH;
+    ep.y = e->ypart;
+    hipLaunchKernelGGL((k_bgemm<2, kKtH, 4, kSplitO, EPI_RAW>), dim3(kH / 32, kSplitO), dim3(kT), 0, s, e->w_o[l],
+                       reinterpret_cast<const u32x4 *>(e->x_o), ep);
+}
+void launch_mlp_norm(GDNBatchEngine *e, int l, hipStream_t s) {
+    const BNorm p = bnorm(e, e->ypart, b_aux(e, l) + kAuxMlpNorm, e->x_h, -1);
+    hipLaunchKernelGGL((k_bnorm<kSplitO, false, false>), dim3(e->streams), dim3(kT), 0, s, p);
+}
+void launch_gu(GDNBatchEngine *e, int l, hipStream_t s) {
+    BEpi ep{};
+    ep.n_streams = e->streams;
+    ep.x_next = e->x_d;
+    hipLaunchKernelGGL((k_bgemm<2, kKtH, 4, 1, EPI_SWIGLU>), dim3(2 * kI / 32), dim3(kT), 0, s, e->w_gu[l],
+                       reinterpret_cast<const u32x4 *>(e->x_h), ep);
+}
+void launch_down(GDNBatchEngine *e, int l, hipStream_t s) {
+    BEpi ep{};
+    ep.n_streams = e->streams;
+    ep.n_rows = kH;
+    ep.y = e->ypart;
+    hipLaunchKernelGGL((k_bgemm<2, kKtI, 4, kSplitDown, EPI_RAW>), dim3(kH / 32, kSplitDown), dim3(kT), 0, s,
+                       e->w_down[l], reinterpret_cast<const u32x4 *>(e->x_d), ep);
+}
+// After layer l's down projection: h = R(h + y), then the next layer's
+// attention norm with its a/b rows, or the final norm.
+void launch_layer_norm(GDNBatchEngine *e, int l, hipStream_t s) {
+    if (l + 1 < e->layers) {
+        const BNorm p = bnorm(e, e->ypart, b_aux(e, l + 1) + kAuxAttnNorm, e->x_h, l + 1);
+        hipLaunchKernelGGL((k_bnorm<kSplitDown, false, true>), dim3(e->streams), dim3(kT), 0, s, p);
+    } else {
+        BNorm p = bnorm(e, e->ypart, e->aux + (size_t)e->layers * kAuxLayer, e->x_h, -1);
+        p.xn_out = e->xn;
+        hipLaunchKernelGGL((k_bnorm<kSplitDown, false, false>), dim3(e->streams), dim3(kT), 0, s, p);
+    }
+}
+void launch_lm(GDNBatchEngine *e, hipStream_t s) {
+    BEpi ep{};
+    ep.n_streams = e->streams;
+    ep.n_rows = e->vocab;
+    ep.logits = e->logits;
+    ep.part_val = e->part_val;
+    ep.part_idx = e->part_idx;
+    hipLaunchKernelGGL((k_bgemm<2, kKtH, 4, 1, EPI_LM>), dim3(lm_wgs(e)), dim3(kT), 0, s, e->w_lm,
+                       reinterpret_cast<const u32x4 *>(e->x_h), ep);
+}
+void launch_argmax(GDNBatchEngine *e, hipStream_t s) {
+    hipLaunchKernelGGL(k_bargmax, dim3(e->streams), dim3(kT), 0, s, e->part_val, e->part_idx, lm_wgs(e),
+                       e->tok_dev + kMaxB);
+}
+
+void b_enqueue_step(GDNBatchEngine *e, hipStream_t s) {
+    launch_embed(e, s);
+    for (int l = 0; l < e->layers; ++l) {
+        launch_qkvg(e, l, s);
+        launch_recur(e, l, s);
+        launch_onorm(e, l, s);
+        launch_o(e, l, s);
+        launch_mlp_norm(e, l, s);
+        launch_gu(e, l, s);
+        launch_down(e, l, s);
+        launch_layer_norm(e, l, s);
+    }
+    launch_lm(e, s);
+    launch_argmax(e, s);
+}
+
+int b_ensure_graph(GDNBatchEngine *e) {
+    if (e->exec) return 0;
+    GDN_HIP(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+    b_enqueue_step(e, e->stream);
+    GDN_HIP(hipStreamEndCapture(e->stream, &e->graph));
+    GDN_HIP(hipGraphInstantiate(&e->exec, e->graph, nullptr, nullptr, 0));
+    return 0;
+}
+
+// tokens[n_streams] in (host) -> step -> next tokens out (host).
+int b_run_step(GDNBatchEngine *e, const int32_t *tokens, int32_t *next, float *inner_ms) {
+    for (int i = 0; i < e->streams; ++i) {
+        if (tokens[i] < 0 || tokens[i] >= e->vocab) {
+            gdn_error("token id out of range");
+            return -1;
+        }
+    }
+    if (e->use_graph && b_ensure_graph(e) != 0) return -1;
+    std::memcpy(e->tok_host, tokens, (size_t)e->streams * sizeof(int));
+    GDN_HIP(hipMemcpyAsync(e->tok_dev, e->tok_host, (size_t)e->streams * sizeof(int), hipMemcpyHostToDevice,
+                           e->stream));
+    if (inner_ms) GDN_HIP(hipEventRecord(e->ev0, e->stream));
+    if (e->use_graph) {
+        GDN_HIP(hipGraphLaunch(e->exec, e->stream));
+    } else {
+        b_enqueue_step(e, e->stream);
+        GDN_HIP(hipGetLastError());
+    }
+    if (inner_ms) GDN_HIP(hipEventRecord(e->ev1, e->stream));
+    GDN_HIP(hipMemcpyAsync(e->tok_host + kMaxB, e->tok_dev + kMaxB, (size_t)e->streams * sizeof(int),
+                           hipMemcpyDeviceToHost, e->stream));
+    GDN_HIP(hipStreamSynchronize(e->stream));
+    if (next) std::memcpy(next, e->tok_host + kMaxB, (size_t)e->streams * sizeof(int));
+    if (inner_ms) GDN_HIP(hipEventElapsedTime(inner_ms, e->ev0, e->ev1));
+    return 0;
+}
+
+void b_destroy(GDNBatchEngine *e) {
+    if (!e) return;
+    if (e->exec) (void)hipGraphExecDestroy(e->exec);
+    if (e->graph) (void)hipGraphDestroy(e->graph);
+    if (e->ev0) (void)hipEventDestroy(e->ev0);
+    if (e->ev1) (void)hipEventDestroy(e->ev1);
+    if (e->stream) (void)hipStreamDestroy(e->stream);
+    (void)hipFree(e->wmem);
+    (void)hipFree(e->emb);
+    (void)hipFree(e->aux);
+    (void)hipFree(e->state);
+    (void)hipFree(e->tails);
+    (void)hipFree(e->act);
+    (void)hipFree(e->part_idx);
+    (void)hipFree(e->x_h);
+    (void)hipFree(e->x_o);
+    (void)hipFree(e->x_d);
+    (void)hipFree(e->tok_dev);
+    if (e->tok_host) (void)hipHostFree(e->tok_host);
+    delete e;
+}
+
+GDNBatchEngine *engine_of(const GDNBatchState *s) {
+    if (!s || !s->engine) gdn_error("gdn: multi-stream state not initialised");
+    return s ? s->engine : nullptr;
+}
+
+// Copy between one stream's [layers][per] block and the strided device array.
+int stream_copy(float *dev, size_t per, int streams, int layers, uint32_t stream, float *host, bool to_dev) {
+    const size_t width = per * 4, dpitch = (size_t)streams * per * 4;
+    float *d = dev + (size_t)stream * per;
+    if (to_dev)
+        GDN_HIP(hipMemcpy2D(d, dpitch, host, width, width, (size_t)layers, hipMemcpyHostToDevice));
+    else
+        GDN_HIP(hipMemcpy2D(host, width, d, dpitch, width, (size_t)layers, hipMemcpyDeviceToHost));
+    return 0;
+}
+
+}  // namespace
+
+// ================================================================== C ABI
+
+extern "C" {
+
+int gdn_batch_init(GDNBatchState *state, const GDNModel *model, uint32_t n_streams) {
+    std::memset(state, 0, sizeof(*state));
+    if (n_streams == 0 || n_streams > (uint32_t)kMaxB) {
+        gdn_error("gdn: n_streams must be 1..64");
+        return -1;
+    }
+    if (b_check_shape(&model->config) != 0) return -1;
+    if (gdn_validate_bf16_exact_weights(model->weight_data, &model->config) != 0) {
+        gdn_error("gdn: the multi-stream engine needs a BF16-exact checkpoint");
+        return -1;
+    }
+    GDNBatchEngine *e = new GDNBatchEngine();
+    e->layers = (int)model->config.num_layers;
+    e->vocab = (int)model->config.vocab_size;
+    e->streams = (int)n_streams;
+    e->eps = model->config.norm_eps;
+    if (b_alloc(e) != 0 || b_upload(e, model) != 0) {
+        b_destroy(e);
+        return -1;
+    }
+    state->engine = e;
+    state->n_streams = n_streams;
+    return 0;
+}
+
+void gdn_batch_free(GDNBatchState *state) {
+    b_destroy(state->engine);
+    std::memset(state, 0, sizeof(*state));
+}
+
+int gdn_batch_set_graph_mode(GDNBatchState *state, int use_graph) {
+    GDNBatchEngine *e = engine_of(state);
+    if (!e) return -1;
+    e->use_graph = use_graph != 0;
+    return 0;
+}
+
+int gdn_batch_decode_step(GDNBatchState *state, const int32_t *tokens, int32_t *next_tokens) {
+    GDNBatchEngine *e = engine_of(state);
+    if (!e) return -1;
+    return b_run_step(e, tokens, next_tokens, nullptr);
+}
+
+int gdn_batch_read_tokens(const GDNBatchState *state, int32_t *tokens) {
+    GDNBatchEngine *e = engine_of(state);
+    if (!e) return -1;
+    GDN_HIP(hipMemcpy(tokens, e->tok_dev + kMaxB, (size_t)e->streams * sizeof(int), hipMemcpyDeviceToHost));
+    return 0;
+}
+
+int gdn_batch_read_logits(const GDNBatchState *state, uint32_t stream, float *logits, size_t count) {
+    GDNBatchEngine *e = engine_of(state);
+    if (!e || stream >= (uint32_t)e->streams || count > (size_t)e->vocab) return -1;
+    GDN_HIP(hipMemcpy(logits, e->logits + (size_t)stream * e->vocab, count * 4, hipMemcpyDeviceToHost));
+    return 0;
+}
+
+int gdn_batch_read_final_hidden(const GDNBatchState *state, uint32_t stream, float *hidden, size_t count) {
+    GDNBatchEngine *e = engine_of(state);
+    if (!e || stream >= (uint32_t)e->streams || count > (size_t)kH) return -1;
+    GDN_HIP(hipMemcpy(hidden, e->xn + (size_t)stream * kH, count * 4, hipMemcpyDeviceToHost));
+    return 0;
+}
+
+int gdn_batch_load_stream_state(GDNBatchState *state, uint32_t stream, const float *recurrent,
+                                size_t recurrent_floats, const float *conv_tails, size_t conv_floats) {
+    GDNBatchEngine *e = engine_of(state);
+    if (!e || stream >= (uint32_t)e->streams) return -1;
+    if (recurrent && recurrent_floats != (size_t)e->layers * kLayerState) return -1;
+    if (conv_tails && conv_floats != (size_t)e->layers * kStreamTails) return -1;
+    if (recurrent && stream_copy(e->state, kLayerState, e->streams, e->layers, stream,
+                                 const_cast<float *>(recurrent), true))
+        return -1;
+    if (conv_tails && stream_copy(e->tails, kStreamTails, e->streams, e->layers, stream,
+                                  const_cast<float *>(conv_tails), true))
+        return -1;
+    return 0;
+}
+
+int gdn_batch_save_stream_state(const GDNBatchState *state, uint32_t stream, float *recurrent,
+                                size_t recurrent_floats, float *conv_tails, size_t conv_floats) {
+    GDNBatchEngine *e = engine_of(state);
+    if (!e || stream >= (uint32_t)e->streams) return -1;
+    if (recurrent && recurrent_floats != (size_t)e->layers * kLayerState) return -1;
+    if (conv_tails && conv_floats != (size_t)e->layers * kStreamTails) return -1;
+    if (recurrent && stream_copy(e->state, kLayerState, e->streams, e->layers, stream, recurrent, false)) return -1;
+    if (conv_tails && stream_copy(e->tails, kStreamTails, e->streams, e->layers, stream, conv_tails, false))
+        return -1;
+    return 0;
+}
+
+int gdn_batch_run_teacher_forced(GDNBatchState *state, const int32_t *tokens, uint32_t n_steps,
+                                 int32_t *argmax_out, float *inner_ms, float *outer_ms) {
+    GDNBatchEngine *e = engine_of(state);
+    if (!e) return -1;
+    const size_t B = (size_t)e->streams;
+    std::vector<int32_t> next(B);
+    for (uint32_t i = 0; i < n_steps; ++i) {
+        const auto t0 = std::chrono::steady_clock::now();
+        if (b_run_step(e, tokens + (size_t)i * B, next.data(), inner_ms ? inner_ms + i : nullptr) != 0) return -1;
+        const auto t1 = std::chrono::steady_clock::now();
+        if (outer_ms) outer_ms[i] = std::chrono::duration<float, std::milli>(t1 - t0).count();
+        if (argmax_out) std::memcpy(argmax_out + (size_t)i * B, next.data(), B * sizeof(int32_t));
+    }
+    return 0;
+}
+
+int gdn_batch_profile_kernels(GDNBatchState *state, uint32_t rounds, float *avg_us, uint32_t n_kinds) {
+    GDNBatchEngine *e = engine_of(state);
+    if (!e) return -1;
+    for (uint32_t id = 0; id < n_kinds && id < (uint32_t)KB_KINDS; ++id) {
+        GDN_HIP(hipStreamSynchronize(e->stream));
+        GDN_HIP(hipEventRecord(e->ev0, e->stream));
+        uint32_t launches = 0;
+        for (uint32_t r = 0; r < rounds; ++r) {
+            const int per_layer = (id == KB_EMBED || id == KB_LM || id == KB_ARGMAX) ? 1 : e->layers;
+            for (int l = 0; l < per_layer; ++l, ++launches) {
+                switch (id) {
+                case KB_EMBED: launch_embed(e, e->stream); break;
+                case KB_QKVG: launch_qkvg(e, l, e->stream); break;
+                case KB_RECUR: launch_recur(e, l, e->stream); break;
+                case KB_ONORM: launch_onorm(e, l, e->stream); break;
+                case KB_O: launch_o(e, l, e->stream); break;
+                case KB_NORM: launch_layer_norm(e, l, e->stream); break;
+                case KB_GU: launch_gu(e, l, e->stream); break;
+                case KB_DOWN: launch_down(e, l, e->stream); break;
+                case KB_LM: launch_lm(e, e->stream); break;
+                default: launch_argmax(e, e->stream); break;
+                }
+            }
+        }
+        GDN_HIP(hipEventRecord(e->ev1, e->stream));
+        GDN_HIP(hipEventSynchronize(e->ev1));
+        GDN_HIP(hipGetLastError());
+        float ms = 0.0f;
+        GDN_HIP(hipEventElapsedTime(&ms, e->ev0, e->ev1));
+        avg_us[id] = launches ? 1000.0f * ms / (float)launches : 0.0f;
+    }
+    return 0;
+}
+
+int gdn_test_batch_gemm(const float *W, const float *X, uint32_t N, uint32_t K, float *Y) {
+    const bool k_hidden = K == (uint32_t)kH;
+    if (!(k_hidden || K == (uint32_t)kI) || N == 0 || (N % 32u) != 0) {
+        gdn_error("gdn_test_batch_gemm: K must be 2048 or 5632 and N a multiple of 32");
+        return -1;
+    }
+    // the production configurations: o_proj's for K = 2048, down's for 5632
+    const int splits = k_hidden ? kSplitO : kSplitDown;
+    std::vector<uint16_t> wb, wt((size_t)N * K), xb;
+    to_bf16(W, (size_t)N * K, wb);
+    gdn_tile_bf16(wb.data(), N, K, 2, wt.data());
+    // X [64][K] in B-operand tiles: the A tiling of 64 rows in 4 row tiles
+    to_bf16(X, (size_t)kMaxB * K, xb);
+    std::vector<uint16_t> xt((size_t)kMaxB * K);
+    gdn_tile_bf16(xb.data(), kMaxB, K, 4, xt.data());
+    void *dw = nullptr, *dx = nullptr;
+    float *dy = nullptr;
+    GDN_HIP(hipMalloc(&dw, wt.size() * 2));
+    GDN_HIP(hipMalloc(&dx, xt.size() * 2));
+    GDN_HIP(hipMalloc(&dy, (size_t)splits * kMaxB * N * 4));
+    GDN_HIP(hipMemcpy(dw, wt.data(), wt.size() * 2, hipMemcpyHostToDevice));
+    GDN_HIP(hipMemcpy(dx, xt.data(), xt.size() * 2, hipMemcpyHostToDevice));
+    BEpi ep{};
+    ep.n_streams = kMaxB;
+    ep.n_rows = (int)N;
+    ep.y = dy;
+    if (k_hidden)
+        hipLaunchKernelGGL((k_bgemm<2, kKtH, 4, kSplitO, EPI_RAW>), dim3(N / 32, kSplitO), dim3(kT), 0, 0,
+                           static_cast<const u32x4 *>(dw), static_cast<const u32x4 *>(dx), ep);
+    else
+        hipLaunchKernelGGL((k_bgemm<2, kKtI, 4, kSplitDown, EPI_RAW>), dim3(N / 32, kSplitDown), dim3(kT), 0, 0,
+                           static_cast<const u32x4 *>(dw), static_cast<const u32x4 *>(dx), ep);
+    GDN_HIP(hipGetLastError());
+    std::vector<float> parts((size_t)splits * kMaxB * N);
+    GDN_HIP(hipMemcpy(parts.data(), dy, parts.size() * 4, hipMemcpyDeviceToHost));
+    // split sums in split order, as the consumers add them
+    for (size_t i = 0; i < (size_t)kMaxB * N; ++i) {
+        float v = parts[i];
+        for (int sp = 1; sp < splits; ++sp) v = v + parts[(size_t)sp * kMaxB * N + i];
+        Y[i] = v;
+    }
+    (void)hipFree(dw);
+    (void)hipFree(dx);
+    (void)hipFree(dy);
+    return 0;
+}
+
+}  // extern "C"

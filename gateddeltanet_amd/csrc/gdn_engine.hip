@@ -37,27 +37,10 @@
 #include <vector>
 
 #include "gdn_amd.h"
+#include "gdn_device.h"
 #include "gdn_internal.h"
 
-#define GDN_HIP(call)                                                              \
-    do {                                                                           \
-        hipError_t e_ = (call);                                                    \
-        if (e_ != hipSuccess) {                                                    \
-            std::fprintf(stderr, "gdn: %s failed: %s (%s:%d)\n", #call,            \
-                         hipGetErrorString(e_), __FILE__, __LINE__);               \
-            return -1;                                                             \
-        }                                                                          \
-    } while (0)
-
 namespace gdn {
-
-constexpr int kH = 2048;   // hidden
-constexpr int kNH = 8;     // heads
-constexpr int kHD = 256;   // head dim (dk = dv)
-constexpr int kI = 5632;   // MLP intermediate
-constexpr int kT = 256;    // threads per workgroup (4 wave64)
-constexpr int kMaxLayers = 24;
-constexpr int kTailStripe = 6144;  // floats reserved per (layer, q|k|v) conv-tail stripe
 
 // Row blocking per GEMV (rows per workgroup).
 constexpr int kRbQkvg = 8;
@@ -68,25 +51,6 @@ constexpr int kRbLm = 8;
 constexpr int kRbTest = 8;
 constexpr int kCB = 16;    // state columns per recurrence workgroup
 
-enum { kRef = GDN_CONTRACT_REF, kBf16w = GDN_CONTRACT_BF16W_FP32S, kFp32 = GDN_CONTRACT_FP32 };
-
-// Per-layer block of small FP32 weights (norms, scalars, a/b rows, conv taps).
-constexpr int kAuxAttnNorm = 0;
-constexpr int kAuxMlpNorm = kH;
-constexpr int kAuxONorm = 2 * kH;
-constexpr int kAuxALog = 2 * kH + kHD;
-constexpr int kAuxDtBias = kAuxALog + kNH;
-constexpr int kAuxAB = kAuxALog + 16;
-constexpr int kAuxConv = kAuxAB + 2 * kNH * kH;
-constexpr int kAuxLayer = kAuxConv + 3 * kH * 4;
-
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-
 // Smallest nonzero and largest |w| of a matrix (after DAZ) and whether any
 // is not finite.
 struct WInfo {
@@ -94,66 +58,6 @@ struct WInfo {
     float max_abs;
     int nonfinite;
 };
-
-// ---------------------------------------------------------------- scalar math
-
-__device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
-__device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
-
-// fp32_to_bf16_rne, gdn_model.cpp:309-320 (canonical NaN, infinities kept).
-__device__ __forceinline__ float rne_bf16(float x) {
-    const uint32_t b = f2u(x), mag = b & 0x7fffffffu;
-    if (mag >= 0x7f800000u) {
-        if (mag == 0x7f800000u) return x;
-        return u2f((b & 0x80000000u) ? 0xffc00000u : 0x7fc00000u);
-    }
-    return u2f((b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u);
-}
-
-template <int C>
-__device__ __forceinline__ float R(float x) {
-    if constexpr (C == kFp32) return x;
-    else return rne_bf16(x);
-}
-
-__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b16) { return u2f(b16 << 16); }
-
-// exp and log1p through double: correctly rounded float results.
-__device__ __forceinline__ float exp_cr(float x) { return (float)exp((double)x); }
-__device__ __forceinline__ float log1p_cr(float x) { return (float)log1p((double)x); }
-
-// gdn_sigmoid / gdn_silu / gdn_softplus, gdn_model.cpp:1307-1330.
-__device__ __forceinline__ float sigmoid_ref(float x) {
-    if (x >= 0.0f) {
-        const float z = exp_cr(-x);
-        return 1.0f / (1.0f + z);
-    }
-    const float z = exp_cr(x);
-    return z / (1.0f + z);
-}
-__device__ __forceinline__ float silu_ref(float x) { return x * sigmoid_ref(x); }
-__device__ __forceinline__ float softplus_ref(float x) {
-    if (x > 20.0f) return x;
-    if (x < -20.0f) return exp_cr(x);
-    return log1p_cr(exp_cr(x));
-}
-
-// Balanced pairwise sum of 16 contiguous values (gemv32_tree16).
-__device__ __forceinline__ float tree16(const float *p) {
-    const float s0 = p[0] + p[1], s1 = p[2] + p[3], s2 = p[4] + p[5], s3 = p[6] + p[7];
-    const float s4 = p[8] + p[9], s5 = p[10] + p[11], s6 = p[12] + p[13], s7 = p[14] + p[15];
-    const float a0 = s0 + s1, a1 = s2 + s3, a2 = s4 + s5, a3 = s6 + s7;
-    const float b0 = a0 + a1, b1 = a2 + a3;
-    return b0 + b1;
-}
-
-// XOR butterfly over a wave64: every lane ends with the balanced pairwise
-// sum of the 64 values (the lower six levels of gdn_tree_reduce_256).
-__device__ __forceinline__ float wave_tree64(float v) {
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) v = v + __shfl_xor(v, m);
-    return v;
-}
 
 // The native BF16 product with every special case of gdn_model.cpp:401-462:
 // DAZ inputs, canonical NaN, signed infinities/zeros, FTZ below 0x007fc000.
@@ -199,12 +103,6 @@ __device__ __forceinline__ void lds_load16u(const uint32_t *src, uint32_t *v) {
         v[4 * q + 2] = t.z;
         v[4 * q + 3] = t.w;
     }
-}
-
-// Two FP32 values to a BF16 pair (lo in bits 0..15), round to nearest even
-// (v_cvt_pk_bf16_f32; equal to the integer rounding for every non-NaN input).
-__device__ __forceinline__ uint32_t cvt_pk(float lo, float hi) {
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
 }
 
 // Eight BF16 x BF16 products rounded to BF16, packed in pairs: r[j] holds
@@ -893,16 +791,6 @@ struct Epi {
     int *part_idx;
 };
 
-// beta = sigmoid(b); decay = expf(-expf(a_log) * softplus(a + dt_bias))
-// (gdn_island_prep, gdn_model.cpp:2461-2465).
-__device__ __forceinline__ void head_scalars(float a, float b, float a_log, float dt_bias,
-                                             float &beta, float &decay) {
-    beta = sigmoid_ref(b);
-    const float decay_in = a + dt_bias;
-    const float decay_val = -exp_cr(a_log) * softplus_ref(decay_in);
-    decay = exp_cr(decay_val);
-}
-
 // ------------------------------------------------------------ the GEMV kernel
 
 // Waves per SIMD each GEMV instantiation must fit (caps its VGPRs): the
@@ -1437,150 +1325,14 @@ __global__ __launch_bounds__(kT) void k_argmax(const float *__restrict__ part_va
     }
 }
 
-// Gated delta rule for one head and CB state columns (beta/decay per head
-// come from the QKVG kernel).
-//   q/k L2 norms in gdn_tree_reduce_256 order (four wave butterflies, then
-//   (w0 + w1) + (w2 + w3)), alpha = tree256(qn * kn);
-//   every product S[j][i] * kn[j] and S[j][i] * qn[j] is formed in parallel
-//   into column-major LDS tiles, then lane i runs the r_i chain and lane
-//   CB + i the p_i chain over j = 0..255 in order (only the dependent adds
-//   are serial); delta and o; the update S' = decay * S + kn (x) delta is
-//   applied to the tile still held in registers.
+// One workgroup per (16 state columns, head): grid (kHD / CB, kNH).
 template <int C, int CB>
 __global__ __launch_bounds__(kT) void k_recur(const float *__restrict__ qp,
                                               const float *__restrict__ kp,
                                               const float *__restrict__ vp,
                                               const float *__restrict__ bd,
                                               void *__restrict__ state, float *__restrict__ attn) {
-    static_assert(2 * CB <= 64 && (CB % 8) == 0, "one wave runs both chains of every column");
-    constexpr int EPT = kHD * CB / kT;                  // state elements per thread
-    constexpr int PER_ROW = CB / EPT;                   // threads per tile row
-    constexpr int LDT = kHD + 4;                        // padded column stride of the product tiles
-    static_assert(EPT % 8 == 0 && PER_ROW * EPT == CB, "whole 16-byte pieces per thread");
-    __shared__ float qn[kHD], kn[kHD];
-    __shared__ __attribute__((aligned(16))) float pk_t[CB * LDT];  // S[j][i] * kn[j] at [i][j]
-    __shared__ __attribute__((aligned(16))) float pq_t[CB * LDT];  // S[j][i] * qn[j] at [i][j]
-    __shared__ float dl[CB];
-    __shared__ float red[8], red2[4];
-    const int h = blockIdx.y, c0 = blockIdx.x * CB, t = threadIdx.x;
-    const int lane = t & 63, w = t >> 6;
-    const int row = t / PER_ROW, col = (t - row * PER_ROW) * EPT;  // this thread's tile piece
-    const size_t sidx = (size_t)h * kHD * kHD + (size_t)row * kHD + c0 + col;
-
-    const float q = qp[h * kHD + t], k = kp[h * kHD + t];
-    const float vi = (t < CB) ? vp[h * kHD + c0 + t] : 0.0f;
-    float sv[EPT];  // S[row][c0 + col + e]
-    {
-        constexpr int NV = (C == kRef) ? EPT / 8 : EPT / 4;
-        u32x4 tr[NV];
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            if constexpr (C == kRef)
-                tr[i] = reinterpret_cast<const u32x4 *>(reinterpret_cast<const uint16_t *>(state) + sidx)[i];
-            else
-                tr[i] = reinterpret_cast<const u32x4 *>(reinterpret_cast<const float *>(state) + sidx)[i];
-        }
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const uint32_t wv[4] = {tr[i].x, tr[i].y, tr[i].z, tr[i].w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                if constexpr (C == kRef) {
-                    sv[8 * i + 2 * e] = u2f(wv[e] << 16);
-                    sv[8 * i + 2 * e + 1] = u2f(wv[e] & 0xffff0000u);
-                } else {
-                    sv[4 * i + e] = u2f(wv[e]);
-                }
-            }
-        }
-    }
-    const float beta = bd[2 * h], decay = bd[2 * h + 1];
-
-    const float qs = wave_tree64(q * q), ks = wave_tree64(k * k);
-    if (lane == 0) {
-        red[w] = qs;
-        red[4 + w] = ks;
-    }
-    __syncthreads();
-    const float q_sq = (red[0] + red[1]) + (red[2] + red[3]);
-    const float k_sq = (red[4] + red[5]) + (red[6] + red[7]);
-    const float q_inv = 1.0f / __builtin_sqrtf(q_sq + 1e-6f);
-    const float k_inv = 1.0f / __builtin_sqrtf(k_sq + 1e-6f);
-    const float qv = q * q_inv, kv = k * k_inv;
-    qn[t] = qv;
-    kn[t] = kv;
-    const float qk = wave_tree64(qv * kv);
-    if (lane == 0) red2[w] = qk;
-    __syncthreads();
-    const float alpha = (red2[0] + red2[1]) + (red2[2] + red2[3]);
-    const float kj = kn[row], qj = qn[row];
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-        pk_t[(col + e) * LDT + row] = sv[e] * kj;
-        pq_t[(col + e) * LDT + row] = sv[e] * qj;
-    }
-    __syncthreads();
-
-    if (t < 2 * CB) {
-        // lane i: r_i = sum_j S[j][i] kn[j]; lane CB + i: p_i (same order)
-        const bool is_p = t >= CB;
-        const int ci = is_p ? t - CB : t;
-        const f32x4 *src = reinterpret_cast<const f32x4 *>((is_p ? pq_t : pk_t) + ci * LDT);
-        f32x4 col_v[kHD / 4];  // the whole column, read ahead of the serial adds
-#pragma unroll
-        for (int j4 = 0; j4 < kHD / 4; ++j4) col_v[j4] = src[j4];
-        float acc = 0.0f;
-#pragma unroll
-        for (int j4 = 0; j4 < kHD / 4; ++j4) {
-            acc = acc + col_v[j4].x;
-            acc = acc + col_v[j4].y;
-            acc = acc + col_v[j4].z;
-            acc = acc + col_v[j4].w;
-        }
-        const float pv = __shfl(acc, (lane + CB) & 63);
-        if (!is_p) {
-            const float r = acc;
-            const float delta = beta * (vi - decay * r);
-            const float o = 0.0625f * (decay * pv + alpha * delta);
-            dl[t] = delta;
-            attn[h * kHD + c0 + t] = R<C>(o);
-        }
-    }
-    __syncthreads();
-
-    float nv[EPT];
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) nv[e] = decay * sv[e] + kj * dl[col + e];
-    if constexpr (C == kRef) {
-#pragma unroll
-        for (int i = 0; i < EPT / 8; ++i) {
-            u32x4 v;
-            v.x = cvt_pk(nv[8 * i + 0], nv[8 * i + 1]);
-            v.y = cvt_pk(nv[8 * i + 2], nv[8 * i + 3]);
-            v.z = cvt_pk(nv[8 * i + 4], nv[8 * i + 5]);
-            v.w = cvt_pk(nv[8 * i + 6], nv[8 * i + 7]);
-            if (!(fabsf(nv[8 * i + 0]) <= 3.402823466e38f) || !(fabsf(nv[8 * i + 1]) <= 3.402823466e38f) ||
-                !(fabsf(nv[8 * i + 2]) <= 3.402823466e38f) || !(fabsf(nv[8 * i + 3]) <= 3.402823466e38f) ||
-                !(fabsf(nv[8 * i + 4]) <= 3.402823466e38f) || !(fabsf(nv[8 * i + 5]) <= 3.402823466e38f) ||
-                !(fabsf(nv[8 * i + 6]) <= 3.402823466e38f) || !(fabsf(nv[8 * i + 7]) <= 3.402823466e38f)) {
-                // a NaN or infinity: the integer rounding (canonical NaN)
-                uint32_t pk[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    pk[e] = (f2u(rne_bf16(nv[8 * i + 2 * e])) >> 16) |
-                            (f2u(rne_bf16(nv[8 * i + 2 * e + 1])) & 0xffff0000u);
-                v.x = pk[0]; v.y = pk[1]; v.z = pk[2]; v.w = pk[3];
-            }
-            reinterpret_cast<u32x4 *>(reinterpret_cast<uint16_t *>(state) + sidx)[i] = v;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < EPT / 4; ++i) {
-            f32x4 v;
-            v.x = nv[4 * i + 0]; v.y = nv[4 * i + 1]; v.z = nv[4 * i + 2]; v.w = nv[4 * i + 3];
-            reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(state) + sidx)[i] = v;
-        }
-    }
+    recur_block<C, CB>(qp, kp, vp, bd, state, attn, blockIdx.y, blockIdx.x * CB);
 }
 
 // beta/decay for n heads from raw (a, b, a_log, dt_bias) (recurrence hook).

@@ -215,6 +215,22 @@ int gdn_model_save(const GDNModel *model, const char *path) {
     return ok ? 0 : -1;
 }
 
+void gdn_tile_bf16(const uint16_t *src, size_t n_rows, size_t k, int rt, uint16_t *dst) {
+    const size_t kt_n = k / 32, blocks = n_rows / (16 * (size_t)rt);
+#pragma omp parallel for schedule(static)
+    for (long long bi = 0; bi < (long long)blocks; ++bi) {
+        const size_t b = (size_t)bi;
+        for (size_t kt = 0; kt < kt_n; ++kt)
+            for (size_t r = 0; r < (size_t)rt; ++r) {
+                uint16_t *tile = dst + (((b * kt_n + kt) * rt + r) * 64) * 8;
+                for (size_t l = 0; l < 64; ++l) {
+                    const uint16_t *row = src + (b * 16 * rt + r * 16 + l % 16) * k + kt * 32 + 8 * (l / 16);
+                    std::memcpy(tile + l * 8, row, 16);
+                }
+            }
+    }
+}
+
 int gdn_validate_bf16_exact_weights(const float *wd, const GDNWeightHeader *c) {
     const size_t n = gdn_total_weight_floats(c);
     for (size_t i = 0; i < n; ++i) {

@@ -263,6 +263,97 @@ class RunState:
             pass
 
 
+class BatchState:
+    """Multi-stream decode (gdn_batch_*): n_streams independent streams, each
+    with its own FP32 state, one token per stream per step; projections on
+    the matrix cores.  No reference counterpart (the reference is batch-1)."""
+
+    def __init__(self, model: Model, n_streams: int) -> None:
+        self.model = model
+        self._s = L.GDNBatchState()
+        self._live = False
+        _check(L.load().gdn_batch_init(ctypes.byref(self._s), model.ptr, n_streams), "gdn_batch_init")
+        self._live = True
+        self.n_streams = n_streams
+        c = model.config
+        self.n_state = c.num_layers * c.num_heads * c.head_dim * c.head_dim
+        self.n_conv = c.num_layers * 3 * (c.conv_size - 1) * c.hidden_size
+
+    @property
+    def ptr(self):
+        return ctypes.byref(self._s)
+
+    def set_graph(self, use_graph: bool) -> None:
+        _check(L.load().gdn_batch_set_graph_mode(self.ptr, 1 if use_graph else 0), "gdn_batch_set_graph_mode")
+
+    def step(self, tokens: Sequence[int]) -> np.ndarray:
+        """One token per stream in; the greedy next tokens out."""
+        t = np.ascontiguousarray(np.asarray(tokens, np.int32))
+        assert t.size == self.n_streams
+        out = np.empty(self.n_streams, np.int32)
+        _check(L.load().gdn_batch_decode_step(self.ptr, iptr(t), iptr(out)), "gdn_batch_decode_step")
+        return out
+
+    def logits(self, stream: int) -> np.ndarray:
+        out = np.empty(self.model.config.vocab_size, np.float32)
+        _check(L.load().gdn_batch_read_logits(self.ptr, stream, fptr(out), out.size), "gdn_batch_read_logits")
+        return out
+
+    def final_hidden(self, stream: int) -> np.ndarray:
+        out = np.empty(self.model.config.hidden_size, np.float32)
+        _check(L.load().gdn_batch_read_final_hidden(self.ptr, stream, fptr(out), out.size),
+               "gdn_batch_read_final_hidden")
+        return out
+
+    def load_stream_state(self, stream: int, recurrent: Optional[np.ndarray] = None,
+                          conv: Optional[np.ndarray] = None) -> None:
+        r = _f32(recurrent).reshape(-1) if recurrent is not None else None
+        cv = _f32(conv).reshape(-1) if conv is not None else None
+        _check(L.load().gdn_batch_load_stream_state(
+            self.ptr, stream, fptr(r) if r is not None else None, r.size if r is not None else 0,
+            fptr(cv) if cv is not None else None, cv.size if cv is not None else 0), "gdn_batch_load_stream_state")
+
+    def save_stream_state(self, stream: int) -> Tuple[np.ndarray, np.ndarray]:
+        r = np.empty(self.n_state, np.float32)
+        cv = np.empty(self.n_conv, np.float32)
+        _check(L.load().gdn_batch_save_stream_state(self.ptr, stream, fptr(r), r.size, fptr(cv), cv.size),
+               "gdn_batch_save_stream_state")
+        return r, cv
+
+    def teacher_forced(self, tokens: np.ndarray, timing: bool = True):
+        """tokens [steps][n_streams]; returns (argmax [steps][n_streams], inner_ms, outer_ms)."""
+        tk = np.ascontiguousarray(np.asarray(tokens, np.int32))
+        steps = tk.shape[0]
+        assert tk.shape == (steps, self.n_streams)
+        am = np.empty((steps, self.n_streams), np.int32)
+        inner = np.empty(steps, np.float32) if timing else None
+        outer = np.empty(steps, np.float32) if timing else None
+        _check(L.load().gdn_batch_run_teacher_forced(
+            self.ptr, iptr(tk), steps, iptr(am), fptr(inner) if timing else None,
+            fptr(outer) if timing else None), "gdn_batch_run_teacher_forced")
+        return am, inner, outer
+
+    KERNEL_KINDS = ("embed", "qkvg", "recur", "onorm", "o_proj", "layer_norm", "gate_up", "down",
+                    "lm_head", "argmax")
+
+    def profile_kernels(self, rounds: int = 2) -> Dict[str, float]:
+        out = np.zeros(len(self.KERNEL_KINDS), np.float32)
+        _check(L.load().gdn_batch_profile_kernels(self.ptr, rounds, fptr(out), out.size),
+               "gdn_batch_profile_kernels")
+        return {k: float(v) for k, v in zip(self.KERNEL_KINDS, out)}
+
+    def free(self) -> None:
+        if self._live:
+            L.load().gdn_batch_free(self.ptr)
+            self._live = False
+
+    def __del__(self) -> None:
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 # ---- seeded generators (counter-based SplitMix64 + Box-Muller) ----
 
 def synth_normal(n: int, seed: int, stream: int, mean: float = 0.0, std: float = 1.0,
@@ -300,6 +391,17 @@ def gemv(contract: int, W: np.ndarray, x: np.ndarray) -> np.ndarray:
     y = np.empty(M, np.float32)
     _check(L.load().gdn_test_gemv(contract, fptr(W), fptr(x), M, K, fptr(y)), "gdn_test_gemv")
     return y
+
+
+def batch_gemm(W: np.ndarray, X: np.ndarray) -> np.ndarray:
+    """gdn_test_batch_gemm: Y [64][N] = X [64][K] W[N][K]^T on the matrix cores."""
+    W = _f32(W)
+    X = _f32(X)
+    N, K = W.shape
+    assert X.shape == (L.MAX_STREAMS, K)
+    Y = np.empty((L.MAX_STREAMS, N), np.float32)
+    _check(L.load().gdn_test_batch_gemm(fptr(W), fptr(X), N, K, fptr(Y)), "gdn_test_batch_gemm")
+    return Y
 
 
 def recurrence(contract: int, q, k, v, a, b, a_log, dt_bias, S):

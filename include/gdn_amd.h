@@ -319,6 +319,57 @@ double gdn_token_logprob(const float *logits, uint32_t vocab, int32_t target);
  * (host.cpp:2348-2359). */
 uint32_t gdn_strict_argmax(const float *logits, uint32_t n);
 
+/* ===== multi-stream decode =====
+ * No counterpart in the reference, which decodes one stream (README.md:75-77;
+ * SURVEY config 5 asks for 64).  Up to GDN_MAX_STREAMS independent streams,
+ * each with its own FP32 recurrent state and conv tails, advance one token
+ * each per step.  Arithmetic is the BF16W_FP32S contract's except inside the
+ * projections, which form exact products of the same BF16 operands and sum
+ * them in FP32 on the matrix cores; results agree with gdn_decode_step_host
+ * under GDN_CONTRACT_BF16W_FP32S to rounding, not bit for bit.  Stream s's
+ * results never depend on the other streams. */
+#define GDN_MAX_STREAMS 64
+
+struct GDNBatchEngine;
+typedef struct {
+    struct GDNBatchEngine *engine;
+    uint32_t n_streams;
+    uint32_t reserved;
+} GDNBatchState;
+
+/* Upload the weights (BF16-exact checkpoint) and zero every stream's state.
+ * n_streams in 1..GDN_MAX_STREAMS; the vocabulary must be a multiple of 32. */
+int gdn_batch_init(GDNBatchState *state, const GDNModel *model, uint32_t n_streams);
+void gdn_batch_free(GDNBatchState *state);
+/* One step of every stream: tokens[n_streams] in; the greedy next tokens
+ * out (next_tokens may be NULL).  -1 for a token outside [0, vocab). */
+int gdn_batch_decode_step(GDNBatchState *state, const int32_t *tokens, int32_t *next_tokens);
+int gdn_batch_read_tokens(const GDNBatchState *state, int32_t *tokens);
+int gdn_batch_read_logits(const GDNBatchState *state, uint32_t stream, float *logits, size_t count);
+int gdn_batch_read_final_hidden(const GDNBatchState *state, uint32_t stream, float *hidden, size_t count);
+/* One stream's state in the .gdnstate section layouts (as
+ * gdn_load_recurrent_state / gdn_load_conv_tails); either pointer may be
+ * NULL.  Sizes must be the full per-stream sizes. */
+int gdn_batch_load_stream_state(GDNBatchState *state, uint32_t stream, const float *recurrent,
+                                size_t recurrent_floats, const float *conv_tails, size_t conv_floats);
+int gdn_batch_save_stream_state(const GDNBatchState *state, uint32_t stream, float *recurrent,
+                                size_t recurrent_floats, float *conv_tails, size_t conv_floats);
+/* n_steps steps with tokens[step][n_streams] fed; per-step argmax
+ * [step][n_streams], inner ms (HIP events around the step graph) and outer
+ * ms (host tokens in -> host tokens out).  Output pointers may be NULL. */
+int gdn_batch_run_teacher_forced(GDNBatchState *state, const int32_t *tokens, uint32_t n_steps,
+                                 int32_t *argmax_out, float *inner_ms, float *outer_ms);
+/* Average microseconds per launch of each kernel kind, in the order embed,
+ * qkvg, recur, onorm, o_proj, layer_norm, gate_up, down, lm_head, argmax
+ * (each kind launched back to back over every layer).  Advances state. */
+int gdn_batch_profile_kernels(GDNBatchState *state, uint32_t rounds, float *avg_us, uint32_t n_kinds);
+/* 0: launch kernels one by one; 1 (default): one captured hipGraph/step. */
+int gdn_batch_set_graph_mode(GDNBatchState *state, int use_graph);
+/* Test hook: Y[64][N] = X[64][K] W[N][K]^T on the multi-stream GEMM (no
+ * rounding of the sums); W and X BF16-exact, K = 2048 (N % 32 == 0) or
+ * K = 5632 (N % 16 == 0). */
+int gdn_test_batch_gemm(const float *W, const float *X, uint32_t N, uint32_t K, float *Y);
+
 #ifdef __cplusplus
 }
 #endif

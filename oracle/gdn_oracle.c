@@ -171,14 +171,14 @@ float orc_tree256(const float *a) {
  * reduced with tree16; four banks (lower/upper x even/odd beat) accumulate
  * those sums in beat order starting from +0.0f; the row result is
  * (even_lo + even_hi) + (odd_lo + odd_hi).  Products are native BF16
- * (ORC_REF, ORC_BF16W_FP32S) or plain FP32 (ORC_FP32). */
+ * (ORC_REF, ORC_BF16W_FP32S) or plain FP32 (ORC_FP32, ORC_BF16X). */
 static float gemv_row(int contract, const float *w, const float *x, int K) {
     float bank[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     float p[32];
     for (int b = 0; b < K / 32; ++b) {
         for (int l = 0; l < 32; ++l) {
             const float wv = w[32 * b + l], xv = x[32 * b + l];
-            p[l] = contract == ORC_FP32 ? wv * xv : native_mul(wv, xv);
+            p[l] = (contract == ORC_FP32 || contract == ORC_BF16X) ? wv * xv : native_mul(wv, xv);
         }
         const float lo = orc_tree16(p), hi = orc_tree16(p + 16);
         const int e = (b & 1) * 2;

@@ -17,6 +17,11 @@
  *   ORC_FP32         control arm: FP32 weights/activations/state, plain FP32
  *                    products, no rounding point anywhere, same reduction
  *                    orders.
+ *   ORC_BF16X        as ORC_BF16W_FP32S except the dense GEMV products are
+ *                    exact FP32 products of the BF16 operands (no product
+ *                    rounding): the arithmetic of the multi-stream engine's
+ *                    matrix-core projections up to summation order.  Not a
+ *                    reference contract.
  *
  * Transcendental modes:
  *   ORC_LIBM  glibc expf/log1pf, as the reference calls them.
@@ -38,7 +43,7 @@
 extern "C" {
 #endif
 
-enum { ORC_REF = 0, ORC_BF16W_FP32S = 1, ORC_FP32 = 2 };
+enum { ORC_REF = 0, ORC_BF16W_FP32S = 1, ORC_FP32 = 2, ORC_BF16X = 3 };
 enum { ORC_LIBM = 0, ORC_CR = 1 };
 
 /* Same 60-byte layout as the reference GDNWeightHeader. */

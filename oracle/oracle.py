@@ -17,7 +17,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
-REF, BF16W_FP32S, FP32 = 0, 1, 2
+REF, BF16W_FP32S, FP32, BF16X = 0, 1, 2, 3
 LIBM, CR = 0, 1
 
 FP = POINTER(c_float)
