@@ -119,6 +119,10 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 256 MiB device to device three times (the known-size copy that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
+    ap.add_argument("--config", type=int, default=3, choices=(3, 5),
+                    help="3: batch-1 decode (the headline); 5: --streams independent streams per step "
+                         "(multi-stream engine, matrix-core projections)")
+    ap.add_argument("--streams", type=int, default=64, help="streams per step for --config 5")
     ap.add_argument("--eager", action="store_true",
                     help="launch the step's kernels one by one instead of the captured hipGraph "
                          "(for rocprofv3 kernel tracing, which aborts the queue on graph launches)")
@@ -137,6 +141,8 @@ def main():
               "(no multi-GPU figure is produced)", file=sys.stderr)
         sys.exit(2)
 
+    if args.config == 5:
+        return main_streams(args)
     import gateddeltanet_amd as g
     contract = {"ref": g.CONTRACT_REF, "bf16w_fp32s": g.CONTRACT_BF16W_FP32S, "fp32": g.CONTRACT_FP32}[args.contract]
     t_setup = time.perf_counter()
@@ -226,6 +232,102 @@ def main():
         "vs_baseline_note": "value / 8.233 ms (U55C FPGA outer ms/token, real checkpoint, same arithmetic volume)",
     }
     rs.free()
+    model.free()
+    print(json.dumps(out), flush=True)
+
+
+# Multi-stream decode: per step every stream reads the
+# weights once between them and its own FP32 state and conv tails.
+PER_STREAM = 102_565_120  # state read + write, conv tails, embedding row, logits (config 5 figure)
+STREAM_KERNEL_BYTES = {  # per launch, per stream where the traffic is per stream
+    "recur": 8 * 256 * 256 * 4 * 2,
+}
+
+
+def main_streams(args):
+    """--streams independent streams (default 64), each
+    with its own FP32 recurrent state and conv tails, one token per stream
+    per step; --warmup untimed steps then --steps timed steps, teacher-forced
+    with uniform-random tokens.  `value` is aggregate tokens/s (streams x
+    steps / wall time of the timed loop, host tokens in -> host tokens out)."""
+    import gateddeltanet_amd as g
+    B = args.streams
+    steps = args.steps if args.steps != 4096 else 1024
+    warm = args.warmup if args.warmup != 4096 else 64
+    t_setup = time.perf_counter()
+    model = g.Model.synth(num_layers=L, seed=0, std=0.02, bf16=True)
+    bs = g.BatchState(model, B)
+    if args.eager:
+        bs.set_graph(False)
+    toks = g.synth_tokens((warm + steps) * B, 0, 3, V).reshape(warm + steps, B)
+    if warm:
+        bs.teacher_forced(toks[:warm], timing=False)
+    setup_s = time.perf_counter() - t_setup
+    sync()
+    t0 = time.perf_counter()
+    _, inner, outer = bs.teacher_forced(toks[warm:])
+    sync()
+    wall = time.perf_counter() - t0
+    ms_step = wall * 1000.0 / steps
+    inner_med = float(np.median(inner))
+    bytes_step = DENSE + AUX + B * PER_STREAM
+    prof = bs.profile_kernels(args.profile_rounds)
+    per_step = {k: v * (1 if k in ("embed", "lm_head", "argmax") else L) for k, v in prof.items()}
+    rb = STREAM_KERNEL_BYTES["recur"] * B
+    cpu = None
+    if args.cpu_tokens > 0:
+        threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+        st = np.zeros(L * 8 * 256 * 256, np.float32)
+        cv = np.zeros(L * 3 * 3 * H, np.float32)
+        ms_cpu, n_cpu, _ = cpu_baseline(model, g.CONTRACT_BF16W_FP32S, st, cv, toks[:args.cpu_tokens + 1, 0],
+                                        threads, 0)
+        cpu = {"value": round(1000.0 / ms_cpu, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+               "sample": f"{n_cpu} tokens of one stream of the same 24-layer model, CPU oracle (gdn_model.cpp "
+                         f"arithmetic, glibc expf/log1pf, OpenMP rows), {threads} threads; streams are "
+                         "independent, so the CPU's aggregate rate is this rate"}
+    out = {
+        "metric": "aggregate tokens/s, 64-stream GDN-1.3B decode (BASELINE config 5)",
+        "value": round(B * steps / (wall), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warm,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded random-init weights, uniform random token streams)",
+        "config": {
+            "workload": f"BASELINE config 5: {B} independent GatedDeltaNet-1.3B streams, 24 layers, FP32 "
+                        f"states, {steps} teacher-forced steps (one token per stream per step)",
+            "streams": B,
+            "arithmetic": "BF16 operands, exact products summed in FP32 on the matrix cores for the "
+                          "projections; batch-1 BF16W_FP32S arithmetic elsewhere",
+            "launch": "eager" if args.eager else "one hipGraph per step (195 kernels)",
+        },
+        "inner_ms_median": round(inner_med, 5),
+        "outer_ms_median": round(float(np.median(outer)), 5),
+        "bytes_per_step": bytes_step,
+        "achieved_GBps_inner": round(bytes_step / (inner_med * 1e-3) / 1e9, 1),
+        "hbm_frac_inner": round(bytes_step / (inner_med * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+        "kernel_us_per_launch": {k: round(v, 3) for k, v in prof.items()},
+        "kernel_us_per_step": {k: round(v, 1) for k, v in per_step.items()},
+        "roofline": {
+            "kernel": "recur",
+            "bound": "hbm",
+            "achieved": round(rb / (prof["recur"] * 1e-6) / 1e9, 1),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(rb / (prof["recur"] * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_launch": rb,
+            "avg_launch_us": round(prof["recur"], 3),
+        },
+        "cpu_baseline": cpu,
+        "setup_s": round(setup_s, 1),
+    }
+    bs.free()
     model.free()
     print(json.dumps(out), flush=True)
 

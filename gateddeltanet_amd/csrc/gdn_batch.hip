@@ -356,8 +356,8 @@ struct BNorm {
 // Thread t holds elements 8t..8t+7; a 16-element chunk is the sequential sum
 // of thread 2c's eight squares continued by thread 2c + 1.  SPLITS partial
 // sums of the preceding projection are added in split order (0: no residual
-// add; EMBED: the embedding row instead).  Every global operand, the a/b
-// rows included, is requested before the first dependent use.
+// add; EMBED: the embedding row instead).  The a/b rows are requested
+// before the norm's first wait on memory.
 template <int SPLITS, bool EMBED, bool AB>
 __global__ __launch_bounds__(kT) void k_bnorm(BNorm p) {
     __shared__ __attribute__((aligned(16))) float xs[kH];
@@ -366,15 +366,6 @@ __global__ __launch_bounds__(kT) void k_bnorm(BNorm p) {
     __shared__ float abv[16];
     __shared__ float scale_s;
     const int m = blockIdx.x, t = threadIdx.x, e0 = 8 * t;
-    constexpr int ABN = AB ? 32 : 1;
-    f32x4 wq[ABN];
-    if constexpr (AB) {
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            const int q = t + kT * i, grp = q >> 3, sub = q & 7;
-            wq[i] = *reinterpret_cast<const f32x4 *>(p.ab_w + (size_t)(grp >> 6) * kH + 32 * (grp & 63) + 4 * sub);
-        }
-    }
     const f32x4 *w4 = reinterpret_cast<const f32x4 *>(p.w + e0);
     const f32x4 wa = w4[0], wb = w4[1];
     float hv[8];
@@ -409,6 +400,17 @@ __global__ __launch_bounds__(kT) void k_bnorm(BNorm p) {
             const float yv[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
 #pragma unroll
             for (int e = 0; e < 8; ++e) hv[e] = rne_bf16(hv[e] + rne_bf16(yv[e]));
+        }
+    }
+    // the a/b rows are requested behind the operands of the norm (loads
+    // return in order)
+    constexpr int ABN = AB ? 32 : 1;
+    f32x4 wq[ABN];
+    if constexpr (AB) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            const int q = t + kT * i, grp = q >> 3, sub = q & 7;
+            wq[i] = *reinterpret_cast<const f32x4 *>(p.ab_w + (size_t)(grp >> 6) * kH + 32 * (grp & 63) + 4 * sub);
         }
     }
     if constexpr (EMBED || SPLITS > 0) {
