@@ -182,6 +182,7 @@ SIGNATURES = {
     "gdn_batch_load_stream_state": (c_int, [BP, c_uint32, FP, c_size_t, FP, c_size_t]),
     "gdn_batch_save_stream_state": (c_int, [BP, c_uint32, FP, c_size_t, FP, c_size_t]),
     "gdn_batch_run_teacher_forced": (c_int, [BP, IP, c_uint32, IP, FP, FP]),
+    "gdn_batch_prefill": (c_int, [BP, c_uint32, IP, c_uint32, IP]),
     "gdn_batch_profile_kernels": (c_int, [BP, c_uint32, FP, c_uint32]),
     "gdn_batch_set_graph_mode": (c_int, [BP, c_int]),
     "gdn_test_batch_gemm": (c_int, [FP, FP, c_uint32, c_uint32, FP]),

@@ -37,6 +37,7 @@
 // argmax, and the per-stream argmax merge.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -618,6 +619,197 @@ __global__ __launch_bounds__(2 * kT) void k_brecur(const float *__restrict__ qkv
     for (int j = 0; j < RH; ++j) S[(size_t)(r0 + j) * kHD] = decay * sv[j] + kn[r0 + j] * d;
 }
 
+// ---------------------------------------------------------------- prefill
+//
+// A prompt runs through one stream's state in chunks of up to 64 tokens, the
+// tokens taking the place of the streams: each layer's projections take the
+// whole chunk (the same GEMMs and reduction order as the step), the causal
+// conv reads its taps from the neighbouring tokens of the chunk, and one
+// workgroup per head runs the recurrence over the chunk's tokens in order
+// with the state held in registers.  Every token sees the arithmetic of a
+// multi-stream step, so a prefill of n tokens equals n steps bit for bit.
+
+// The causal conv of one 64-channel block over a chunk of n tokens.  raw is
+// [64 tokens][4 kH] (the unrounded q, k, v, g sums); the tails are the
+// prefilled stream's for this layer, [q,k,v][3 oldest..newest][kH].  Token
+// m's window is (s[m], s[m+1], s[m+2]) and its input s[m+3] in the sequence
+// s = tails ++ R(raw[0..n)); the new tails are s[n], s[n+1], s[n+2].
+__global__ __launch_bounds__(kT) void k_pconv(const float *__restrict__ raw, int n, float *__restrict__ tails,
+                                              const float *__restrict__ conv_w, float *__restrict__ qkv,
+                                              float *__restrict__ gate, float *__restrict__ sgate) {
+    __shared__ float xs[kMaxB + 3][64];
+    const int row0 = blockIdx.x * 64, t = threadIdx.x, cl = t & 63, mg = t >> 6;
+    const int row = row0 + cl, which = row0 / kH, c = row - which * kH;
+    if (which < 3) {
+        float *tl = tails + (size_t)which * 3 * kH + c;
+        if (t < 64) {
+            xs[0][cl] = tl[0];
+            xs[1][cl] = tl[kH];
+            xs[2][cl] = tl[2 * kH];
+        }
+        for (int m = mg; m < n; m += 4) xs[3 + m][cl] = rne_bf16(raw[(size_t)m * 4 * kH + row]);
+        __syncthreads();
+        const f32x4 cw = *reinterpret_cast<const f32x4 *>(conv_w + ((size_t)which * kH + c) * 4);
+        for (int m = mg; m < n; m += 4) {
+            // gdn_depthwise_conv_silu_head_kind, gdn_model.cpp:1543-1667
+            const float sum = xs[m][cl] * cw.x + xs[m + 1][cl] * cw.y + xs[m + 2][cl] * cw.z + xs[m + 3][cl] * cw.w;
+            qkv[((size_t)m * 3 + which) * kH + c] = rne_bf16(silu_ref(sum));
+        }
+        if (t < 64) {
+            tl[0] = xs[n][cl];
+            tl[kH] = xs[n + 1][cl];
+            tl[2 * kH] = xs[n + 2][cl];
+        }
+    } else {
+        for (int m = mg; m < n; m += 4) {
+            const float g = rne_bf16(raw[(size_t)m * 4 * kH + row]);
+            gate[(size_t)m * kH + c] = g;
+            sgate[(size_t)m * kH + c] = sigmoid_ref(g);
+        }
+    }
+}
+
+// Per (head, token): the q/k L2 norms and alpha of the recurrence, in the
+// batch-1 tree order (k_brecur's first phase).
+__global__ __launch_bounds__(kT) void k_pqk(const float *__restrict__ qkv, float *__restrict__ qn_out,
+                                            float *__restrict__ kn_out, float *__restrict__ alpha_out) {
+    __shared__ float red[8], red2[4];
+    const int h = blockIdx.x, m = blockIdx.y, t = threadIdx.x, w = t >> 6, lane = t & 63;
+    const float *qp = qkv + (size_t)m * 3 * kH + h * kHD;
+    const float q = qp[t], k = qp[kH + t];
+    const float qs = wave_tree64(q * q), ks = wave_tree64(k * k);
+    if (lane == 0) {
+        red[w] = qs;
+        red[4 + w] = ks;
+    }
+    __syncthreads();
+    const float q_sq = (red[0] + red[1]) + (red[2] + red[3]);
+    const float k_sq = (red[4] + red[5]) + (red[6] + red[7]);
+    const float qv = q * (1.0f / __builtin_sqrtf(q_sq + 1e-6f));
+    const float kv = k * (1.0f / __builtin_sqrtf(k_sq + 1e-6f));
+    qn_out[(size_t)m * kH + h * kHD + t] = qv;
+    kn_out[(size_t)m * kH + h * kHD + t] = kv;
+    const float qk = wave_tree64(qv * kv);
+    if (lane == 0) red2[w] = qk;
+    __syncthreads();
+    if (t == 0) alpha_out[m * kNH + h] = (red2[0] + red2[1]) + (red2[2] + red2[3]);
+}
+
+// r = r + S[j] kn[j] and p = p + S[j] qn[j] over 8 * NB rows in order.  The
+// operands come from LDS 8 rows at a time, the next block requested before
+// the current one is used; a fence that consumes each block's sums keeps at
+// most two blocks of operands live beside the state.
+template <int NB>
+__device__ __forceinline__ void chains8(const float *sv, const float *kn, const float *qn, float &r, float &p) {
+    f32x4 k0 = reinterpret_cast<const f32x4 *>(kn)[0], k1 = reinterpret_cast<const f32x4 *>(kn)[1];
+    f32x4 q0 = reinterpret_cast<const f32x4 *>(qn)[0], q1 = reinterpret_cast<const f32x4 *>(qn)[1];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        f32x4 nk0 = k0, nk1 = k1, nq0 = q0, nq1 = q1;
+        if (b + 1 < NB) {
+            nk0 = reinterpret_cast<const f32x4 *>(kn + 8 * (b + 1))[0];
+            nk1 = reinterpret_cast<const f32x4 *>(kn + 8 * (b + 1))[1];
+            nq0 = reinterpret_cast<const f32x4 *>(qn + 8 * (b + 1))[0];
+            nq1 = reinterpret_cast<const f32x4 *>(qn + 8 * (b + 1))[1];
+        }
+        const float kv[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+        const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            r = r + sv[8 * b + j] * kv[j];
+            p = p + sv[8 * b + j] * qv[j];
+        }
+        asm volatile("" : "+v"(r), "+v"(p) : : "memory");
+        k0 = nk0;
+        k1 = nk1;
+        q0 = nq0;
+        q1 = nq1;
+    }
+}
+
+// The recurrence over a chunk's n tokens in order, for one head and 64 state
+// columns per workgroup (grid (4 column groups, heads)): columns are
+// independent, so four workgroups share a head.  Wave w owns rows 64 w ..
+// 64 w + 63 of column 64 blockIdx.x + lane, held in registers for the whole
+// chunk; a token's r and p chains pass through the four waves in row order
+// (j = 0..255, the reference's chain order) with the partial sums handed on
+// through LDS, and wave 3 forms delta and o.  The chunk's normalized k and
+// q, v of the workgroup's columns and the per-token scalars are staged in
+// LDS first.
+__global__ __launch_bounds__(kT) void k_pscan(const float *__restrict__ qkv, const float *__restrict__ qn_all,
+                                              const float *__restrict__ kn_all, const float *__restrict__ alpha_all,
+                                              const float *__restrict__ bd, int n, float *__restrict__ state,
+                                              float *__restrict__ attn) {
+    constexpr int RQ = kHD / 4;  // rows per wave
+    __shared__ __attribute__((aligned(16))) float kq[kMaxB][2][kHD];
+    __shared__ float vs[kMaxB][64];
+    __shared__ float sc[kMaxB][3];  // beta, decay, alpha
+    __shared__ float rpart[64], ppart[64], dl[64];
+    const int cg = blockIdx.x, h = blockIdx.y, t = threadIdx.x, w = t >> 6, lane = t & 63;
+    const int col = cg * 64 + lane, r0 = w * RQ;
+    float *S = state + (size_t)h * kHD * kHD + col;
+    float sv[RQ];
+#pragma unroll
+    for (int j = 0; j < RQ; ++j) sv[j] = S[(size_t)(r0 + j) * kHD];
+    for (int i = t; i < n * kHD; i += kT) {
+        const int m = i / kHD, j = i - m * kHD;
+        kq[m][0][j] = kn_all[(size_t)m * kH + h * kHD + j];
+        kq[m][1][j] = qn_all[(size_t)m * kH + h * kHD + j];
+    }
+    for (int i = t; i < n * 64; i += kT) {
+        const int m = i >> 6, c = i & 63;
+        vs[m][c] = qkv[((size_t)m * 3 + 2) * kH + h * kHD + cg * 64 + c];
+    }
+    if (t < n) {
+        sc[t][0] = bd[t * 16 + 2 * h];
+        sc[t][1] = bd[t * 16 + 2 * h + 1];
+        sc[t][2] = alpha_all[t * kNH + h];
+    }
+    __syncthreads();
+    for (int m = 0; m < n; ++m) {
+        const float *kn = kq[m][0], *qn = kq[m][1];
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+            if (w == qd) {
+                float r = 0.0f, p = 0.0f;
+                if (qd > 0) {
+                    r = rpart[lane];
+                    p = ppart[lane];
+                }
+                chains8<RQ / 8>(sv, kn + r0, qn + r0, r, p);
+                if (qd < 3) {
+                    rpart[lane] = r;
+                    ppart[lane] = p;
+                } else {
+                    const float beta = sc[m][0], decay = sc[m][1], alpha = sc[m][2];
+                    const float delta = beta * (vs[m][lane] - decay * r);
+                    const float o = 0.0625f * (decay * p + alpha * delta);
+                    dl[lane] = delta;
+                    attn[(size_t)m * kH + h * kHD + col] = rne_bf16(o);
+                }
+            }
+            __syncthreads();
+        }
+        const float d = dl[lane], decay = sc[m][1];
+#pragma unroll
+        for (int b = 0; b < RQ / 8; ++b) {
+            const f32x4 *k4 = reinterpret_cast<const f32x4 *>(kn + r0 + 8 * b);
+            const f32x4 ka = k4[0], kb = k4[1];
+            const float kv[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
+            float *u = sv + 8 * b;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) u[j] = decay * u[j] + kv[j] * d;
+            asm volatile("" : "+v"(u[0]), "+v"(u[1]), "+v"(u[2]), "+v"(u[3]), "+v"(u[4]), "+v"(u[5]), "+v"(u[6]),
+                         "+v"(u[7]) : : "memory");
+        }
+    }
+    // the store addresses are formed after the token loop, not kept across it
+    float *Sw = S;
+    asm volatile("" : "+v"(Sw));
+#pragma unroll
+    for (int j = 0; j < RQ; ++j) Sw[(size_t)(r0 + j) * kHD] = sv[j];
+}
+
 }  // namespace bt
 }  // namespace gdn
 
@@ -645,6 +837,11 @@ struct GDNBatchEngine {
     uint16_t *x_h = nullptr, *x_o = nullptr, *x_d = nullptr;  // X tiles, K = 2048 / 2048 / 5632
     int *tok_dev = nullptr;   // [0..63] in, [64..127] out
     int *tok_host = nullptr;  // pinned, same layout
+    // prefill: the chunk's normalized q / k, alpha, its logits, final hidden
+    // vectors and argmax tokens (per-token buffers of their own, so a
+    // prefill leaves the other streams' last step readable)
+    float *p_qn = nullptr, *p_kn = nullptr, *p_alpha = nullptr, *p_logits = nullptr, *p_xn = nullptr;
+    int *p_tok = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     bool use_graph = true;
@@ -785,6 +982,12 @@ int b_alloc(GDNBatchEngine *e) {
     GDN_HIP(hipMemset(e->x_h, 0, (size_t)kMaxB * kH * 2));
     GDN_HIP(hipMemset(e->x_o, 0, (size_t)kMaxB * kH * 2));
     GDN_HIP(hipMemset(e->x_d, 0, (size_t)kMaxB * kI * 2));
+    GDN_HIP(hipMalloc(&e->p_qn, (size_t)kMaxB * kH * 4));
+    GDN_HIP(hipMalloc(&e->p_kn, (size_t)kMaxB * kH * 4));
+    GDN_HIP(hipMalloc(&e->p_alpha, (size_t)kMaxB * kNH * 4));
+    GDN_HIP(hipMalloc(&e->p_logits, (size_t)kMaxB * V * 4));
+    GDN_HIP(hipMalloc(&e->p_xn, (size_t)kMaxB * kH * 4));
+    GDN_HIP(hipMalloc(&e->p_tok, (size_t)kMaxB * sizeof(int)));
     GDN_HIP(hipMalloc(&e->tok_dev, 2 * kMaxB * sizeof(int)));
     GDN_HIP(hipMemset(e->tok_dev, 0, 2 * kMaxB * sizeof(int)));
     GDN_HIP(hipHostMalloc(&e->tok_host, 2 * kMaxB * sizeof(int), hipHostMallocDefault));
@@ -948,6 +1151,103 @@ int b_run_step(GDNBatchEngine *e, const int32_t *tokens, int32_t *next, float *i
     return 0;
 }
 
+// One prefill chunk of n tokens (already in tok_dev[0..n)) through stream
+// `slot`'s state: the step's kernels with the tokens as the streams, the
+// conv over the chunk (k_pconv) and the in-order recurrence (k_pqk, k_pscan).
+void enqueue_prefill_chunk(GDNBatchEngine *e, int slot, int n, bool last, hipStream_t s) {
+    BNorm p0 = bnorm(e, nullptr, b_aux(e, 0) + kAuxAttnNorm, e->x_h, 0);
+    p0.emb = e->emb;
+    p0.tok = e->tok_dev;
+    hipLaunchKernelGGL((k_bnorm<0, true, true>), dim3(n), dim3(kT), 0, s, p0);
+    for (int l = 0; l < e->layers; ++l) {
+        float *st = b_state(e, l) + (size_t)slot * kLayerState;
+        float *tl = b_tails(e, l) + (size_t)slot * kStreamTails;
+        BEpi raw{};
+        raw.n_streams = n;
+        raw.n_rows = 4 * kH;
+        raw.y = e->ypart;
+        hipLaunchKernelGGL((k_bgemm<2, kKtH, 8, 1, EPI_RAW>), dim3(4 * kH / 32), dim3(8 * 64), 0, s, e->w_qkvg[l],
+                           reinterpret_cast<const u32x4 *>(e->x_h), raw);
+        hipLaunchKernelGGL(k_pconv, dim3(4 * kH / 64), dim3(kT), 0, s, e->ypart, n, tl, b_aux(e, l) + kAuxConv,
+                           e->qkv, e->gate, e->sgate);
+        hipLaunchKernelGGL(k_pqk, dim3(kNH, n), dim3(kT), 0, s, e->qkv, e->p_qn, e->p_kn, e->p_alpha);
+        hipLaunchKernelGGL(k_pscan, dim3(kHD / 64, kNH), dim3(kT), 0, s, e->qkv, e->p_qn, e->p_kn, e->p_alpha,
+                           e->bd, n, st, e->attn);
+        hipLaunchKernelGGL(k_bonorm, dim3(kNH, n), dim3(kT), 0, s, e->attn, e->gate, e->sgate,
+                           b_aux(e, l) + kAuxONorm, e->eps, e->x_o);
+        BEpi eo{};
+        eo.n_streams = n;
+        eo.n_rows = kH;
+        eo.y = e->ypart;
+        hipLaunchKernelGGL((k_bgemm<2, kKtH, 4, kSplitO, EPI_RAW>), dim3(kH / 32, kSplitO), dim3(kT), 0, s,
+                           e->w_o[l], reinterpret_cast<const u32x4 *>(e->x_o), eo);
+        const BNorm pm = bnorm(e, e->ypart, b_aux(e, l) + kAuxMlpNorm, e->x_h, -1);
+        hipLaunchKernelGGL((k_bnorm<kSplitO, false, false>), dim3(n), dim3(kT), 0, s, pm);
+        BEpi eg{};
+        eg.n_streams = n;
+        eg.x_next = e->x_d;
+        hipLaunchKernelGGL((k_bgemm<2, kKtH, 4, 1, EPI_SWIGLU>), dim3(2 * kI / 32), dim3(kT), 0, s, e->w_gu[l],
+                           reinterpret_cast<const u32x4 *>(e->x_h), eg);
+        BEpi ed{};
+        ed.n_streams = n;
+        ed.n_rows = kH;
+        ed.y = e->ypart;
+        hipLaunchKernelGGL((k_bgemm<2, kKtI, 4, kSplitDown, EPI_RAW>), dim3(kH / 32, kSplitDown), dim3(kT), 0, s,
+                           e->w_down[l], reinterpret_cast<const u32x4 *>(e->x_d), ed);
+        if (l + 1 < e->layers) {
+            const BNorm pa = bnorm(e, e->ypart, b_aux(e, l + 1) + kAuxAttnNorm, e->x_h, l + 1);
+            hipLaunchKernelGGL((k_bnorm<kSplitDown, false, true>), dim3(n), dim3(kT), 0, s, pa);
+        } else {
+            BNorm pf = bnorm(e, e->ypart, e->aux + (size_t)e->layers * kAuxLayer, e->x_h, -1);
+            pf.xn_out = e->p_xn;
+            hipLaunchKernelGGL((k_bnorm<kSplitDown, false, false>), dim3(n), dim3(kT), 0, s, pf);
+        }
+    }
+    if (!last) return;
+    BEpi lm{};
+    lm.n_streams = n;
+    lm.n_rows = e->vocab;
+    lm.logits = e->p_logits;
+    lm.part_val = e->part_val;
+    lm.part_idx = e->part_idx;
+    hipLaunchKernelGGL((k_bgemm<2, kKtH, 4, 1, EPI_LM>), dim3(lm_wgs(e)), dim3(kT), 0, s, e->w_lm,
+                       reinterpret_cast<const u32x4 *>(e->x_h), lm);
+    hipLaunchKernelGGL(k_bargmax, dim3(n), dim3(kT), 0, s, e->part_val, e->part_idx, lm_wgs(e), e->p_tok);
+}
+
+int b_prefill(GDNBatchEngine *e, int slot, const int32_t *prompt, uint32_t n_tokens, int32_t *seed) {
+    for (uint32_t i = 0; i < n_tokens; ++i) {
+        if (prompt[i] < 0 || prompt[i] >= e->vocab) {
+            gdn_error("token id out of range");
+            return -1;
+        }
+    }
+    int n = 0;
+    for (uint32_t off = 0; off < n_tokens; off += (uint32_t)kMaxB) {
+        n = (int)std::min<uint32_t>((uint32_t)kMaxB, n_tokens - off);
+        // the pinned staging word is reused only after the previous chunk's
+        // copy has left it
+        GDN_HIP(hipStreamSynchronize(e->stream));
+        std::memcpy(e->tok_host, prompt + off, (size_t)n * sizeof(int));
+        GDN_HIP(hipMemcpyAsync(e->tok_dev, e->tok_host, (size_t)n * sizeof(int), hipMemcpyHostToDevice, e->stream));
+        enqueue_prefill_chunk(e, slot, n, off + (uint32_t)n == n_tokens, e->stream);
+        GDN_HIP(hipGetLastError());
+    }
+    // the last position's logits, final hidden vector and token into the
+    // stream's rows of the step buffers
+    GDN_HIP(hipMemcpyAsync(e->logits + (size_t)slot * e->vocab, e->p_logits + (size_t)(n - 1) * e->vocab,
+                           (size_t)e->vocab * 4, hipMemcpyDeviceToDevice, e->stream));
+    GDN_HIP(hipMemcpyAsync(e->xn + (size_t)slot * kH, e->p_xn + (size_t)(n - 1) * kH, (size_t)kH * 4,
+                           hipMemcpyDeviceToDevice, e->stream));
+    GDN_HIP(hipMemcpyAsync(e->tok_dev + kMaxB + slot, e->p_tok + (n - 1), sizeof(int), hipMemcpyDeviceToDevice,
+                           e->stream));
+    GDN_HIP(hipMemcpyAsync(e->tok_host + kMaxB + slot, e->p_tok + (n - 1), sizeof(int), hipMemcpyDeviceToHost,
+                           e->stream));
+    GDN_HIP(hipStreamSynchronize(e->stream));
+    if (seed) *seed = e->tok_host[kMaxB + slot];
+    return 0;
+}
+
 void b_destroy(GDNBatchEngine *e) {
     if (!e) return;
     if (e->exec) (void)hipGraphExecDestroy(e->exec);
@@ -966,6 +1266,12 @@ void b_destroy(GDNBatchEngine *e) {
     (void)hipFree(e->x_o);
     (void)hipFree(e->x_d);
     (void)hipFree(e->tok_dev);
+    (void)hipFree(e->p_qn);
+    (void)hipFree(e->p_kn);
+    (void)hipFree(e->p_alpha);
+    (void)hipFree(e->p_logits);
+    (void)hipFree(e->p_xn);
+    (void)hipFree(e->p_tok);
     if (e->tok_host) (void)hipHostFree(e->tok_host);
     delete e;
 }
@@ -1081,6 +1387,13 @@ int gdn_batch_save_stream_state(const GDNBatchState *state, uint32_t stream, flo
     if (conv_tails && stream_copy(e->tails, kStreamTails, e->streams, e->layers, stream, conv_tails, false))
         return -1;
     return 0;
+}
+
+int gdn_batch_prefill(GDNBatchState *state, uint32_t stream, const int32_t *prompt, uint32_t n_tokens,
+                      int32_t *seed_token) {
+    GDNBatchEngine *e = engine_of(state);
+    if (!e || stream >= (uint32_t)e->streams || n_tokens == 0 || !prompt) return -1;
+    return b_prefill(e, (int)stream, prompt, n_tokens, seed_token);
 }
 
 int gdn_batch_run_teacher_forced(GDNBatchState *state, const int32_t *tokens, uint32_t n_steps,

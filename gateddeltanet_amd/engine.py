@@ -294,6 +294,14 @@ class BatchState:
         _check(L.load().gdn_batch_decode_step(self.ptr, iptr(t), iptr(out)), "gdn_batch_decode_step")
         return out
 
+    def prefill(self, stream: int, prompt: Sequence[int]) -> int:
+        """gdn_batch_prefill: the prompt through one stream's state; returns
+        the argmax of the last position (the .gdnstate seed token)."""
+        p = np.ascontiguousarray(np.asarray(prompt, np.int32))
+        seed = np.zeros(1, np.int32)
+        _check(L.load().gdn_batch_prefill(self.ptr, stream, iptr(p), p.size, iptr(seed)), "gdn_batch_prefill")
+        return int(seed[0])
+
     def logits(self, stream: int) -> np.ndarray:
         out = np.empty(self.model.config.vocab_size, np.float32)
         _check(L.load().gdn_batch_read_logits(self.ptr, stream, fptr(out), out.size), "gdn_batch_read_logits")

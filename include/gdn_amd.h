@@ -354,6 +354,18 @@ int gdn_batch_load_stream_state(GDNBatchState *state, uint32_t stream, const flo
                                 size_t recurrent_floats, const float *conv_tails, size_t conv_floats);
 int gdn_batch_save_stream_state(const GDNBatchState *state, uint32_t stream, float *recurrent,
                                 size_t recurrent_floats, float *conv_tails, size_t conv_floats);
+/* Prefill: run n_tokens prompt tokens through one stream's state as
+ * n_tokens gdn_batch_decode_step calls would feed them to that stream (the
+ * GPU prompt pass that produces a .gdnstate, export_gdn_state.py:157-201,
+ * :325-330),
+ * in chunks of 64 tokens: token-parallel projections on the matrix cores, the
+ * causal conv across the chunk, the recurrence in token order with the state
+ * held on chip.  Results equal the steps bit for bit.  *seed_token (may be
+ * NULL) receives the argmax of the last position; that position's logits and
+ * final hidden vector become the stream's readable ones.  Other streams'
+ * states are untouched. */
+int gdn_batch_prefill(GDNBatchState *state, uint32_t stream, const int32_t *prompt, uint32_t n_tokens,
+                      int32_t *seed_token);
 /* n_steps steps with tokens[step][n_streams] fed; per-step argmax
  * [step][n_streams], inner ms (HIP events around the step graph) and outer
  * ms (host tokens in -> host tokens out).  Output pointers may be NULL. */

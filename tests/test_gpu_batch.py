@@ -312,3 +312,81 @@ def test_random_one_layer_against_exact_product_oracle(orc):
     finally:
         bs.free()
         m.free()
+
+
+# ------------------------------------------------------------------ prefill
+
+def stepped_reference(m, prompt):
+    """One stream stepped token by token through the multi-stream engine."""
+    bs = g.BatchState(m, 1)
+    try:
+        for t in prompt:
+            last = int(bs.step([t])[0])
+        return last, bs.logits(0), bs.final_hidden(0), bs.save_stream_state(0)
+    finally:
+        bs.free()
+
+
+@pytest.mark.parametrize("n", [1, 2, 150])
+def test_prefill_equals_steps(model, n):
+    """Prefill of n tokens (chunks of 64; n < 3 exercises the conv tails
+    alone) equals n single-stream steps bit for bit, and leaves the other
+    streams' states alone."""
+    prompt = g.synth_tokens(n, 40 + n, 0)
+    seed_ref, logits_ref, hidden_ref, (rec_ref, conv_ref) = stepped_reference(model, prompt)
+    bs = g.BatchState(model, 3)
+    try:
+        seed = bs.prefill(1, prompt)
+        assert seed == seed_ref
+        assert same_bits(bs.logits(1), logits_ref) and same_bits(bs.final_hidden(1), hidden_ref)
+        rec, conv = bs.save_stream_state(1)
+        assert same_bits(rec, rec_ref) and same_bits(conv, conv_ref)
+        for other in (0, 2):
+            r, c = bs.save_stream_state(other)
+            assert not r.any() and not c.any()
+        # decoding continues from the prefilled state like the stepped stream
+        nxt = bs.step([0, seed, 0])
+        ref = g.BatchState(model, 1)
+        try:
+            for t in prompt:
+                ref.step([t])
+            assert int(ref.step([seed])[0]) == nxt[1]
+            assert same_bits(ref.logits(0), bs.logits(1))
+        finally:
+            ref.free()
+    finally:
+        bs.free()
+
+
+def test_prefill_one_hot_matches_batch1(onehot):
+    """On the one-hot model the prefill equals batch-1 decode steps
+    (BF16W_FP32S) too: state, conv tails, seed token and last logits."""
+    m = onehot
+    prompt = g.synth_tokens(70, 41, 0)
+    rs = g.RunState(m, g.CONTRACT_BF16W_FP32S)
+    try:
+        for t in prompt:
+            seed_ref = rs.decode_step(int(t))
+        logits_ref = rs.logits()
+        rec_ref, conv_ref = rs.save_state()
+    finally:
+        rs.free()
+    bs = g.BatchState(m, 2)
+    try:
+        assert bs.prefill(0, prompt) == seed_ref
+        assert equal_values(bs.logits(0), logits_ref)
+        rec, conv = bs.save_stream_state(0)
+        assert equal_values(rec, rec_ref) and equal_values(conv, conv_ref)
+    finally:
+        bs.free()
+
+
+def test_prefill_rejects_bad_tokens(model):
+    bs = g.BatchState(model, 1)
+    try:
+        with pytest.raises(g.GDNError):
+            bs.prefill(0, [1, model.config.vocab_size])
+        with pytest.raises(g.GDNError):
+            bs.prefill(0, [])
+    finally:
+        bs.free()
