@@ -123,6 +123,9 @@ def main():
                     help="3: batch-1 decode (the headline); 5: --streams independent streams per step "
                          "(multi-stream engine, matrix-core projections)")
     ap.add_argument("--streams", type=int, default=64, help="streams per step for --config 5")
+    ap.add_argument("--prefill", type=int, default=0,
+                    help="instead: time the on-device prefill of an N-token uniform prompt (the GPU prompt pass "
+                         "that produces a .gdnstate) against N batch-1 decode steps")
     ap.add_argument("--eager", action="store_true",
                     help="launch the step's kernels one by one instead of the captured hipGraph "
                          "(for rocprofv3 kernel tracing, which aborts the queue on graph launches)")
@@ -141,6 +144,8 @@ def main():
               "(no multi-GPU figure is produced)", file=sys.stderr)
         sys.exit(2)
 
+    if args.prefill > 0:
+        return main_prefill(args)
     if args.config == 5:
         return main_streams(args)
     import gateddeltanet_amd as g
@@ -329,6 +334,56 @@ def main_streams(args):
     }
     bs.free()
     model.free()
+    print(json.dumps(out), flush=True)
+
+
+def main_prefill(args):
+    """The prompt pass: an N-token uniform prompt through one stream's state
+    (gdn_batch_prefill: 64-token chunks, token-parallel matrix-core
+    projections, in-order recurrence on chip), timed against the same prompt
+    as N batch-1 decode steps (BF16W_FP32S); `value` is prefill tokens/s."""
+    import gateddeltanet_amd as g
+    n = args.prefill
+    model = g.Model.synth(num_layers=L, seed=0, std=0.02, bf16=True)
+    prompt = g.synth_tokens(n, 0, 1, V)
+    bs = g.BatchState(model, 1)
+    bs.prefill(0, prompt[:min(n, 128)])  # warm
+    sync()
+    t0 = time.perf_counter()
+    seed = bs.prefill(0, prompt)
+    sync()
+    pre_s = time.perf_counter() - t0
+    bs.free()
+    rs = g.RunState(model, g.CONTRACT_BF16W_FP32S)
+    rs.teacher_forced(prompt[:16], 16, timing=False)
+    rs.load_state(np.zeros(rs.n_state, np.float32), np.zeros(rs.n_conv, np.float32))
+    sync()
+    t0 = time.perf_counter()
+    rs.teacher_forced(prompt, n, timing=False)
+    sync()
+    dec_s = time.perf_counter() - t0
+    rs.free()
+    model.free()
+    out = {
+        "metric": "prefill tokens/s, GDN-1.3B prompt pass (the .gdnstate producer)",
+        "value": round(n / pre_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": n,
+        "warmup": 0,
+        "ms_per_step": round(pre_s * 1000.0 / n, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded random-init weights, uniform random prompt)",
+        "config": {"workload": f"{n}-token prompt through one stream, 24 layers, FP32 state, chunks of 64",
+                   "arithmetic": "the multi-stream step's, bit for bit"},
+        "prefill_ms": round(pre_s * 1000.0, 2),
+        "decode_steps_ms": round(dec_s * 1000.0, 2),
+        "speedup_vs_decode_steps": round(dec_s / pre_s, 2),
+        "seed_token": seed,
+    }
     print(json.dumps(out), flush=True)
 
 

@@ -152,6 +152,7 @@ SIGNATURES = {
                                   POINTER(c_uint32), IP]),
     "gdn_save_gdnstate": (c_int, [POINTER(GDNRunState), POINTER(GDNModel), ctypes.c_char_p, IP,
                                   c_uint32, c_int32]),
+    "gdn_write_gdnstate": (c_int, [POINTER(GDNWeightHeader), ctypes.c_char_p, FP, FP, IP, c_uint32, c_int32]),
     "gdn_run_teacher_forced": (c_int, [POINTER(GDNRunState), IP, c_uint32, c_uint32, IP, FP, FP]),
     "gdn_set_graph_mode": (c_int, [POINTER(GDNRunState), c_int]),
     "gdn_profile_kernels": (c_int, [POINTER(GDNRunState), c_uint32, FP, c_uint32]),

@@ -14,6 +14,16 @@
 //       [--benchmark-warmup N]
 //   gdn_eval_amd <weights.gdnw> <rolling.gdnreq> [output.json] --score
 //       [--score-doc-limit N]
+//   gdn_eval_amd <weights.gdnw> [output.json] --prefill <prompt.txt|ll.gdnreq>
+//       [--example N] --dump-state <out.gdnstate> [--round-bf16]
+//
+// --prefill is the GPU prompt pass that produces a .gdnstate
+// (export_gdn_state.py:157-201, :290-366): the prompt (a whitespace token
+// file, or the context of example N of an LL fixture) runs through the
+// multi-stream engine's prefill; the state, conv tails, prompt and the argmax
+// of the last position (the seed token) are written as a .gdnstate.  The
+// state is the BF16W_FP32S arm's (FP32); --round-bf16 rounds it and the
+// tails to BF16 (RNE) once at the end, so the REF contract can load it.
 //
 // Common options: --contract ref|bf16w|fp32 (default ref, the reference's
 // all-BF16 arithmetic), --synth[=LAYERS] in place of a weights file (the
@@ -53,9 +63,10 @@ double now_ms() {
 
 struct Options {
     std::string weights, fixture, output, state, logits_dump, logits_ref, hidden_dump, dump_state,
-        bench_tokens;
+        bench_tokens, prefill;
     uint32_t decode_len = 0, bench_steps = 0, bench_warmup = 64, score_limit = 0, synth_layers = 0;
-    bool synth = false, host_check = true, score = false;
+    uint32_t example = 0;
+    bool synth = false, host_check = true, score = false, round_bf16 = false;
     int contract = GDN_CONTRACT_REF;
 };
 
@@ -87,6 +98,9 @@ Options parse(int argc, char **argv) {
         else if (a == "--benchmark-steps") o.bench_steps = parse_u32(next("--benchmark-steps"), "--benchmark-steps");
         else if (a == "--benchmark-warmup") o.bench_warmup = parse_u32(next("--benchmark-warmup"), "--benchmark-warmup");
         else if (a == "--score") o.score = true;
+        else if (a == "--prefill") o.prefill = next("--prefill");
+        else if (a == "--example") o.example = parse_u32(next("--example"), "--example");
+        else if (a == "--round-bf16") o.round_bf16 = true;
         else if (a == "--score-doc-limit") o.score_limit = parse_u32(next("--score-doc-limit"), "--score-doc-limit");
         else if (a == "--contract") {
             const std::string c = next("--contract");
@@ -106,6 +120,8 @@ Options parse(int argc, char **argv) {
                 "  gdn_eval_amd <weights|--synth[=L]> [out.json] --decode-from-state S --benchmark-tokens T "
                 "[--benchmark-steps N] [--benchmark-warmup N]\n"
                 "  gdn_eval_amd <weights|--synth[=L]> <rolling.gdnreq> [out.json] --score [--score-doc-limit N]\n"
+                "  gdn_eval_amd <weights|--synth[=L]> [out.json] --prefill <prompt.txt|ll.gdnreq> [--example N] "
+                "--dump-state S [--round-bf16]\n"
                 "  common: --contract ref|bf16w|fp32\n");
             std::exit(0);
         } else if (!a.empty() && a[0] == '-') {
@@ -133,7 +149,9 @@ Options parse(int argc, char **argv) {
         else o.fixture = p;
     }
     if (o.score && o.fixture.empty()) die("--score requires a rolling fixture (GDNREQ1, kind 3)");
-    if (!o.score && o.state.empty()) die("a mode is required: --decode-from-state S or --score; see --help");
+    if (!o.prefill.empty() && o.dump_state.empty()) die("--prefill requires --dump-state <out.gdnstate>");
+    if (!o.score && o.state.empty() && o.prefill.empty())
+        die("a mode is required: --decode-from-state S, --score or --prefill P; see --help");
     if (!o.bench_tokens.empty() && o.state.empty()) die("--benchmark-tokens requires --decode-from-state");
     return o;
 }
@@ -378,18 +396,23 @@ int run_decode(const Options &o, const Fixture *fx, const GDNModel &model, GDNRu
 
 // ---------------------------------------------------------- benchmark mode
 
-int run_benchmark(const Options &o, const GDNModel &model, GDNRunState &rs) {
-    const uint32_t V = model.config.vocab_size;
-    std::ifstream f(o.bench_tokens);
-    if (!f) die("cannot open benchmark token file " + o.bench_tokens);
+// Whitespace-separated token ids in [0, vocab) (host.cpp:2116-2139).
+std::vector<int32_t> load_token_file(const std::string &path, uint32_t V, const char *what) {
+    std::ifstream f(path);
+    if (!f) die(std::string("cannot open ") + what + " token file " + path);
     std::vector<int32_t> tokens;
     long long v;
     while (f >> v) {
-        if (v < 0 || (unsigned long long)v >= V) die("benchmark token out of vocabulary range");
+        if (v < 0 || (unsigned long long)v >= V) die(std::string(what) + " token out of vocabulary range");
         tokens.push_back((int32_t)v);
     }
-    if (!f.eof()) die("benchmark token file must hold whitespace-separated integers");
-    if (tokens.empty()) die("benchmark token stream is empty");
+    if (!f.eof()) die(std::string(what) + " token file must hold whitespace-separated integers");
+    if (tokens.empty()) die(std::string(what) + " token stream is empty");
+    return tokens;
+}
+
+int run_benchmark(const Options &o, const GDNModel &model, GDNRunState &rs) {
+    const std::vector<int32_t> tokens = load_token_file(o.bench_tokens, model.config.vocab_size, "benchmark");
     uint32_t prompt_len = 0;
     int32_t seed = 0;
     if (gdn_load_gdnstate(&rs, &model, o.state.c_str(), &prompt_len, &seed) != 0) die("cannot load " + o.state);
@@ -493,6 +516,58 @@ int run_score(const Options &o, const Fixture &fx, const GDNModel &model, GDNRun
     return 0;
 }
 
+// ----------------------------------------------------------- prefill mode
+
+int run_prefill(const Options &o, const Fixture *fx, const GDNModel &model) {
+    const GDNWeightHeader &c = model.config;
+    std::vector<int32_t> prompt;
+    if (fx) {
+        if (fx->kind != 2 || o.example >= fx->docs.size()) die("--prefill needs an LL fixture example (kind 2)");
+        prompt = fx->docs[o.example].windows[0].ctx;
+        if (prompt.empty()) die("cannot export state for an empty prompt");
+        for (int32_t t : prompt)
+            if (t < 0 || (uint32_t)t >= c.vocab_size) die("prompt token out of vocabulary range");
+    } else {
+        prompt = load_token_file(o.prefill, c.vocab_size, "prompt");
+    }
+    GDNBatchState bs;
+    std::memset(&bs, 0, sizeof(bs));
+    if (gdn_batch_init(&bs, &model, 1) != 0) die("multi-stream engine init failed (BF16-exact weights needed)");
+    std::fprintf(stderr, "[progress] prefill of %zu tokens\n", prompt.size());
+    int32_t seed = 0;
+    const double t0 = now_ms();
+    if (gdn_batch_prefill(&bs, 0, prompt.data(), (uint32_t)prompt.size(), &seed) != 0) die("prefill failed");
+    const double ms = now_ms() - t0;
+    const size_t rec = (size_t)c.num_layers * c.num_heads * c.head_dim * c.head_dim;
+    const size_t conv = (size_t)c.num_layers * 3 * (c.conv_size - 1) * c.hidden_size;
+    std::vector<float> r(rec), cv(conv);
+    if (gdn_batch_save_stream_state(&bs, 0, r.data(), rec, cv.data(), conv) != 0) die("cannot read the state");
+    gdn_batch_free(&bs);
+    if (o.round_bf16) {
+        for (auto *vec : {&r, &cv})
+            for (float &x : *vec) {
+                uint32_t b;
+                std::memcpy(&b, &x, 4);
+                b = (uint32_t)gdn_test_fp32_to_bf16_rne_bits(b) << 16;
+                std::memcpy(&x, &b, 4);
+            }
+    }
+    if (gdn_write_gdnstate(&c, o.dump_state.c_str(), r.data(), cv.data(), prompt.data(), (uint32_t)prompt.size(),
+                           seed) != 0)
+        die("cannot write " + o.dump_state);
+    std::fprintf(stderr, "[prefill] prompt_len=%zu seed_token=%d %.1f ms (%.0f tokens/s) -> %s\n", prompt.size(), seed,
+                 ms, 1000.0 * prompt.size() / ms, o.dump_state.c_str());
+    FILE *out = open_output(o.output);
+    std::fprintf(out,
+                 "{\"mode\": \"prefill\", \"prompt_len\": %zu, \"seed_token\": %d, \"prefill_ms\": %.3f, "
+                 "\"tokens_per_second\": %.1f, \"state\": \"%s\", \"state_rounding\": \"%s\", "
+                 "\"engine\": \"libgdn_amd multi-stream prefill\"}\n",
+                 prompt.size(), seed, ms, 1000.0 * prompt.size() / ms, o.dump_state.c_str(),
+                 o.round_bf16 ? "bf16" : "fp32");
+    if (out != stdout) std::fclose(out);
+    return 0;
+}
+
 }  // namespace
 
 int main(int argc, char **argv) {
@@ -511,6 +586,14 @@ int main(int argc, char **argv) {
         const int rc = (o.contract == GDN_CONTRACT_FP32) ? gdn_model_load_fp32(&model, o.weights.c_str())
                                                           : gdn_model_load(&model, o.weights.c_str());
         if (rc != 0) die("cannot load " + o.weights);
+    }
+    if (!o.prefill.empty()) {
+        const bool is_fixture = o.prefill.size() > 7 && o.prefill.compare(o.prefill.size() - 7, 7, ".gdnreq") == 0;
+        Fixture pf;
+        if (is_fixture) pf = load_fixture(o.prefill);
+        const int rc = run_prefill(o, is_fixture ? &pf : nullptr, model);
+        gdn_model_free(&model);
+        return rc;
     }
     GDNRunState rs;
     std::memset(&rs, 0, sizeof(rs));

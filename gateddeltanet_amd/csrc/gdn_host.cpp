@@ -459,15 +459,10 @@ int gdn_load_gdnstate(GDNRunState *state, const GDNModel *model, const char *pat
     return 0;
 }
 
-int gdn_save_gdnstate(const GDNRunState *state, const GDNModel *model, const char *path,
-                      const int32_t *prompt, uint32_t prompt_len, int32_t seed_token) {
-    const GDNWeightHeader *c = &model->config;
+int gdn_write_gdnstate(const GDNWeightHeader *c, const char *path, const float *recurrent, const float *conv_tails,
+                       const int32_t *prompt, uint32_t prompt_len, int32_t seed_token) {
     const size_t rec = (size_t)c->num_layers * c->num_heads * c->head_dim * c->head_dim;
     const size_t conv = (size_t)c->num_layers * 3u * (c->conv_size - 1u) * c->hidden_size;
-    std::vector<float> r(rec), cv(conv);
-    if (gdn_save_recurrent_state(state, r.data(), rec) != 0 ||
-        gdn_save_conv_tails(state, cv.data(), conv) != 0)
-        return -1;
     FILE *f = std::fopen(path, "wb");
     if (!f) {
         gdn_error("cannot create .gdnstate file");
@@ -477,10 +472,22 @@ int gdn_save_gdnstate(const GDNRunState *state, const GDNModel *model, const cha
                            c->hidden_size, c->conv_size, prompt_len, (uint32_t)seed_token};
     bool ok = std::fwrite("GDNSTAT1", 1, 8, f) == 8 && std::fwrite(v, 4, 9, f) == 9;
     if (ok && prompt_len) ok = std::fwrite(prompt, 4, prompt_len, f) == prompt_len;
-    ok = ok && std::fwrite(r.data(), 4, rec, f) == rec && std::fwrite(cv.data(), 4, conv, f) == conv;
-    std::fclose(f);
+    ok = ok && std::fwrite(recurrent, 4, rec, f) == rec && std::fwrite(conv_tails, 4, conv, f) == conv;
+    ok = (std::fclose(f) == 0) && ok;
     if (!ok) gdn_error(".gdnstate write failed");
     return ok ? 0 : -1;
+}
+
+int gdn_save_gdnstate(const GDNRunState *state, const GDNModel *model, const char *path,
+                      const int32_t *prompt, uint32_t prompt_len, int32_t seed_token) {
+    const GDNWeightHeader *c = &model->config;
+    const size_t rec = (size_t)c->num_layers * c->num_heads * c->head_dim * c->head_dim;
+    const size_t conv = (size_t)c->num_layers * 3u * (c->conv_size - 1u) * c->hidden_size;
+    std::vector<float> r(rec), cv(conv);
+    if (gdn_save_recurrent_state(state, r.data(), rec) != 0 ||
+        gdn_save_conv_tails(state, cv.data(), conv) != 0)
+        return -1;
+    return gdn_write_gdnstate(c, path, r.data(), cv.data(), prompt, prompt_len, seed_token);
 }
 
 }  // extern "C"

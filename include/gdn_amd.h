@@ -200,6 +200,12 @@ int gdn_save_gdnstate(const GDNRunState *state, const GDNModel *model,
                       const char *path, const int32_t *prompt,
                       uint32_t prompt_len, int32_t seed_token);
 
+/* Write a .gdnstate from host arrays in the section layouts above (the
+ * writer of gdn_save_gdnstate; used to export a prefilled stream). */
+int gdn_write_gdnstate(const GDNWeightHeader *config, const char *path, const float *recurrent,
+                       const float *conv_tails, const int32_t *prompt, uint32_t prompt_len,
+                       int32_t seed_token);
+
 /* Steady teacher-forced benchmark, host.cpp:2150-2256: tokens[i % n_tokens]
  * is fed at step i for n_steps steps.  Per step: outer = host token in ->
  * host token out (H2D of 4 bytes, graph launch, D2H of 4 bytes); inner =

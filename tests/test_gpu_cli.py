@@ -198,3 +198,62 @@ def test_rolling_score_matches_library(model, tmp_path):
     r = run_cli(weights, str(fx), out, "--score", "--score-doc-limit", "1")
     assert r.returncode == 0, r.stderr
     assert json.load(open(out))["scored_tokens"] == 2
+
+
+def read_gdnstate(path, layers=1):
+    raw = open(path, "rb").read()
+    assert raw[:8] == b"GDNSTAT1"
+    v = struct.unpack("<9I", raw[8:44])
+    plen = v[7]
+    prompt = list(struct.unpack(f"<{plen}i", raw[44:44 + 4 * plen]))
+    off = 44 + 4 * plen
+    n_rec = layers * 8 * 256 * 256
+    rec = np.frombuffer(raw[off:off + 4 * n_rec], np.float32)
+    conv = np.frombuffer(raw[off + 4 * n_rec:], np.float32)
+    return v, prompt, rec, conv
+
+
+def test_prefill_mode_writes_the_stepped_state(model, tmp_path):
+    """--prefill (the GPU prompt pass of export_gdn_state.py) writes the
+    state, tails, prompt and seed of the prompt stepped through the
+    multi-stream engine; --round-bf16 makes it loadable by the REF
+    contract; a decode-from-state run continues from it."""
+    prompt = [int(t) for t in g.synth_tokens(100, 50, 0)]
+    ptxt = tmp_path / "prompt.txt"
+    ptxt.write_text(" ".join(map(str, prompt)) + "\n")
+    st, out = str(tmp_path / "p.gdnstate"), str(tmp_path / "p.json")
+    r = run_cli("--synth=1", out, "--prefill", str(ptxt), "--dump-state", st)
+    assert r.returncode == 0, r.stderr
+    res = json.load(open(out))
+    v, got_prompt, rec, conv = read_gdnstate(st)
+    bs = g.BatchState(model, 1)
+    try:
+        for t in prompt:
+            seed = int(bs.step([t])[0])
+        rec_ref, conv_ref = bs.save_stream_state(0)
+    finally:
+        bs.free()
+    assert res["prompt_len"] == 100 and res["seed_token"] == seed == v[8] and got_prompt == prompt
+    assert same_bits(rec, rec_ref) and same_bits(conv, conv_ref)
+
+    # an LL fixture's context as the prompt, rounded for the REF contract
+    fx = tmp_path / "ll.gdnreq"
+    ctx, cont = prompt[:37], [1, 2]
+    with open(fx, "wb") as f:
+        f.write(b"GDNREQ1\0" + struct.pack("<III", 1, 2, 1))
+        f.write(struct.pack(f"<II{len(ctx)}i{len(cont)}i", len(ctx), len(cont), *ctx, *cont))
+    st2 = str(tmp_path / "p2.gdnstate")
+    r = run_cli("--synth=1", str(tmp_path / "p2.json"), "--prefill", str(fx), "--dump-state", st2, "--round-bf16")
+    assert r.returncode == 0, r.stderr
+    v2, p2, rec2, conv2 = read_gdnstate(st2)
+    assert p2 == ctx and v2[7] == 37
+    assert ((rec2.view(np.uint32) & 0xFFFF) == 0).all() and ((conv2.view(np.uint32) & 0xFFFF) == 0).all()
+    rs = g.RunState(model, g.CONTRACT_REF)
+    try:
+        assert rs.load_gdnstate(st2) == (37, v2[8])
+    finally:
+        rs.free()
+    r = run_cli("--synth=1", str(tmp_path / "d.json"), "--decode-from-state", st, "--decode-len", "4",
+                "--contract", "bf16w")
+    assert r.returncode == 0, r.stderr
+    assert json.load(open(tmp_path / "d.json"))["examples"][0]["gen_traj"][0] == seed
