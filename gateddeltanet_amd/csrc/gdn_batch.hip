@@ -160,6 +160,9 @@ __global__ __launch_bounds__(NW * 64) void k_bgemm(const u32x4 *__restrict__ W, 
 #pragma unroll
         for (int g = 0; g < 4; ++g) b[i][g] = xp[i * XSTEP + g * 64];
     }
+    // the scheduler keeps every prefetch where it is issued: D k tiles stay
+    // in flight instead of one
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < KTW; ++i) {
         const int s = i % D;
@@ -176,6 +179,7 @@ __global__ __launch_bounds__(NW * 64) void k_bgemm(const u32x4 *__restrict__ W, 
 #pragma unroll
             for (int g = 0; g < 4; ++g) b[s][g] = xp[(i + D) * XSTEP + g * 64];
         }
+        __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int r = 0; r < RT; ++r)
