@@ -699,67 +699,54 @@ __global__ __launch_bounds__(kT) void k_pqk(const float *__restrict__ qkv, float
     if (t == 0) alpha_out[m * kNH + h] = (red2[0] + red2[1]) + (red2[2] + red2[3]);
 }
 
-// r = r + S[j] kn[j] and p = p + S[j] qn[j] over 8 * NB rows in order.  The
-// operands come from LDS 8 rows at a time, the next block requested before
-// the current one is used; a fence that consumes each block's sums keeps at
-// most two blocks of operands live beside the state.
-template <int NB>
-__device__ __forceinline__ void chains8(const float *sv, const float *kn, const float *qn, float &r, float &p) {
-    f32x4 k0 = reinterpret_cast<const f32x4 *>(kn)[0], k1 = reinterpret_cast<const f32x4 *>(kn)[1];
-    f32x4 q0 = reinterpret_cast<const f32x4 *>(qn)[0], q1 = reinterpret_cast<const f32x4 *>(qn)[1];
+// Sequential sum acc = acc + col[j * 64] over 256 rows of one LDS column in
+// row order; the reads run 16 rows ahead of the adds, a fence per block
+// bounding the registers they hold.
+__device__ __forceinline__ float column_chain(const float *col) {
+    float acc = 0.0f;
+    float cur[16];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        f32x4 nk0 = k0, nk1 = k1, nq0 = q0, nq1 = q1;
-        if (b + 1 < NB) {
-            nk0 = reinterpret_cast<const f32x4 *>(kn + 8 * (b + 1))[0];
-            nk1 = reinterpret_cast<const f32x4 *>(kn + 8 * (b + 1))[1];
-            nq0 = reinterpret_cast<const f32x4 *>(qn + 8 * (b + 1))[0];
-            nq1 = reinterpret_cast<const f32x4 *>(qn + 8 * (b + 1))[1];
-        }
-        const float kv[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-        const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    for (int j = 0; j < 16; ++j) cur[j] = col[j * 64];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            r = r + sv[8 * b + j] * kv[j];
-            p = p + sv[8 * b + j] * qv[j];
-        }
-        asm volatile("" : "+v"(r), "+v"(p) : : "memory");
-        k0 = nk0;
-        k1 = nk1;
-        q0 = nq0;
-        q1 = nq1;
+    for (int b = 0; b < kHD / 16; ++b) {
+        float nxt[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) nxt[j] = (b + 1 < kHD / 16) ? col[(16 * (b + 1) + j) * 64] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc = acc + cur[j];
+        asm volatile("" : "+v"(acc) : : "memory");
+#pragma unroll
+        for (int j = 0; j < 16; ++j) cur[j] = nxt[j];
     }
+    return acc;
 }
 
 // The recurrence over a chunk's n tokens in order, for one head and 64 state
 // columns per workgroup (grid (4 column groups, heads)): columns are
 // independent, so four workgroups share a head.  Wave w owns rows 64 w ..
 // 64 w + 63 of column 64 blockIdx.x + lane, held in registers for the whole
-// chunk; a token's r and p chains pass through the four waves in row order
-// (j = 0..255, the reference's chain order) with the partial sums handed on
-// through LDS, and wave 3 forms delta and o.  The chunk's normalized k and
-// q, v of the workgroup's columns and the per-token scalars are staged in
-// LDS first.
+// chunk.  Per token: every wave forms its rows' products S[j][i] * kn[j] and
+// S[j][i] * qn[j] into LDS (row-major, a column per lane); wave 0 then sums
+// the r column chains and wave 1 the p chains, each in row order j = 0..255
+// (the reference's chain order, adds only), while waves 2-3 stage the next
+// token's k and q; every wave forms delta from the two sums and updates its
+// rows, and wave 0 writes o.
 __global__ __launch_bounds__(kT) void k_pscan(const float *__restrict__ qkv, const float *__restrict__ qn_all,
                                               const float *__restrict__ kn_all, const float *__restrict__ alpha_all,
                                               const float *__restrict__ bd, int n, float *__restrict__ state,
                                               float *__restrict__ attn) {
     constexpr int RQ = kHD / 4;  // rows per wave
-    __shared__ __attribute__((aligned(16))) float kq[kMaxB][2][kHD];
+    __shared__ float prod[2][kHD][64];                              // [k|q][row][column]
+    __shared__ __attribute__((aligned(16))) float kq[2][2][kHD];    // [token parity][k|q][row]
+    __shared__ float rp[2][64];
     __shared__ float vs[kMaxB][64];
     __shared__ float sc[kMaxB][3];  // beta, decay, alpha
-    __shared__ float rpart[64], ppart[64], dl[64];
     const int cg = blockIdx.x, h = blockIdx.y, t = threadIdx.x, w = t >> 6, lane = t & 63;
     const int col = cg * 64 + lane, r0 = w * RQ;
     float *S = state + (size_t)h * kHD * kHD + col;
     float sv[RQ];
 #pragma unroll
     for (int j = 0; j < RQ; ++j) sv[j] = S[(size_t)(r0 + j) * kHD];
-    for (int i = t; i < n * kHD; i += kT) {
-        const int m = i / kHD, j = i - m * kHD;
-        kq[m][0][j] = kn_all[(size_t)m * kH + h * kHD + j];
-        kq[m][1][j] = qn_all[(size_t)m * kH + h * kHD + j];
-    }
     for (int i = t; i < n * 64; i += kT) {
         const int m = i >> 6, c = i & 63;
         vs[m][c] = qkv[((size_t)m * 3 + 2) * kH + h * kHD + cg * 64 + c];
@@ -769,43 +756,38 @@ __global__ __launch_bounds__(kT) void k_pscan(const float *__restrict__ qkv, con
         sc[t][1] = bd[t * 16 + 2 * h + 1];
         sc[t][2] = alpha_all[t * kNH + h];
     }
+    kq[0][0][t] = kn_all[h * kHD + t];
+    kq[0][1][t] = qn_all[h * kHD + t];
     __syncthreads();
     for (int m = 0; m < n; ++m) {
-        const float *kn = kq[m][0], *qn = kq[m][1];
+        const float *kn = kq[m & 1][0], *qn = kq[m & 1][1];
+        // products of this wave's rows
 #pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-            if (w == qd) {
-                float r = 0.0f, p = 0.0f;
-                if (qd > 0) {
-                    r = rpart[lane];
-                    p = ppart[lane];
-                }
-                chains8<RQ / 8>(sv, kn + r0, qn + r0, r, p);
-                if (qd < 3) {
-                    rpart[lane] = r;
-                    ppart[lane] = p;
-                } else {
-                    const float beta = sc[m][0], decay = sc[m][1], alpha = sc[m][2];
-                    const float delta = beta * (vs[m][lane] - decay * r);
-                    const float o = 0.0625f * (decay * p + alpha * delta);
-                    dl[lane] = delta;
-                    attn[(size_t)m * kH + h * kHD + col] = rne_bf16(o);
-                }
-            }
-            __syncthreads();
+        for (int j = 0; j < RQ; ++j) {
+            prod[0][r0 + j][lane] = sv[j] * kn[r0 + j];
+            prod[1][r0 + j][lane] = sv[j] * qn[r0 + j];
         }
-        const float d = dl[lane], decay = sc[m][1];
+        __syncthreads();
+        if (w < 2) {
+            rp[w][lane] = column_chain(&prod[w][0][lane]);
+        } else if (m + 1 < n) {
+            const int i = t - 128;  // 128 threads stage 512 values
+            const float *src = (i < 64 ? kn_all : qn_all) + (size_t)(m + 1) * kH + h * kHD;
+            float *dst = kq[(m + 1) & 1][i < 64 ? 0 : 1];
+            const int b0 = (i & 63) * 4;
 #pragma unroll
-        for (int b = 0; b < RQ / 8; ++b) {
-            const f32x4 *k4 = reinterpret_cast<const f32x4 *>(kn + r0 + 8 * b);
-            const f32x4 ka = k4[0], kb = k4[1];
-            const float kv[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
-            float *u = sv + 8 * b;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) u[j] = decay * u[j] + kv[j] * d;
-            asm volatile("" : "+v"(u[0]), "+v"(u[1]), "+v"(u[2]), "+v"(u[3]), "+v"(u[4]), "+v"(u[5]), "+v"(u[6]),
-                         "+v"(u[7]) : : "memory");
+            for (int e = 0; e < 4; ++e) dst[b0 + e] = src[b0 + e];
         }
+        __syncthreads();
+        const float beta = sc[m][0], decay = sc[m][1];
+        const float r = rp[0][lane], p = rp[1][lane];
+        const float delta = beta * (vs[m][lane] - decay * r);
+        if (w == 0) {
+            const float o = 0.0625f * (decay * p + sc[m][2] * delta);
+            attn[(size_t)m * kH + h * kHD + col] = rne_bf16(o);
+        }
+#pragma unroll
+        for (int j = 0; j < RQ; ++j) sv[j] = decay * sv[j] + kn[r0 + j] * delta;
     }
     // the store addresses are formed after the token loop, not kept across it
     float *Sw = S;
