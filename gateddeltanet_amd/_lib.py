@@ -187,6 +187,7 @@ SIGNATURES = {
     "gdn_batch_profile_kernels": (c_int, [BP, c_uint32, FP, c_uint32]),
     "gdn_batch_set_graph_mode": (c_int, [BP, c_int]),
     "gdn_test_batch_gemm": (c_int, [FP, FP, c_uint32, c_uint32, FP]),
+    "gdn_test_tile_bf16": (None, [POINTER(c_uint16), c_size_t, c_size_t, c_int, POINTER(c_uint16)]),
 }
 
 _lib = None

@@ -231,6 +231,10 @@ void gdn_tile_bf16(const uint16_t *src, size_t n_rows, size_t k, int rt, uint16_
     }
 }
 
+void gdn_test_tile_bf16(const uint16_t *src, size_t n_rows, size_t k, int rt, uint16_t *dst) {
+    gdn_tile_bf16(src, n_rows, k, rt, dst);
+}
+
 int gdn_validate_bf16_exact_weights(const float *wd, const GDNWeightHeader *c) {
     const size_t n = gdn_total_weight_floats(c);
     for (size_t i = 0; i < n; ++i) {

@@ -383,6 +383,11 @@ int gdn_batch_run_teacher_forced(GDNBatchState *state, const int32_t *tokens, ui
 int gdn_batch_profile_kernels(GDNBatchState *state, uint32_t rounds, float *avg_us, uint32_t n_kinds);
 /* 0: launch kernels one by one; 1 (default): one captured hipGraph/step. */
 int gdn_batch_set_graph_mode(GDNBatchState *state, int use_graph);
+/* Host helper (test hook): the multi-stream GEMM's operand tiling of a
+ * row-major BF16 matrix [n_rows][k] (16-row x 32-column tiles of 64 lanes x
+ * 8 values; lane l carries row l % 16 and columns 8 (l / 16) .. + 7; tiles
+ * ordered by (block of 16 rt rows, k tile, row tile)). */
+void gdn_test_tile_bf16(const uint16_t *src, size_t n_rows, size_t k, int rt, uint16_t *dst);
 /* Test hook: Y[64][N] = X[64][K] W[N][K]^T on the multi-stream GEMM (no
  * rounding of the sums); W and X BF16-exact, K = 2048 (N % 32 == 0) or
  * K = 5632 (N % 16 == 0). */

@@ -136,3 +136,25 @@ def test_host_compute_logits_matches_oracle(orc):
     ours = m.compute_logits(h)
     ref = orc.compute_logits(orc.header_from(m.config), m.blob, h)
     assert (ours.view(np.uint32) == ref.view(np.uint32)).all()
+
+
+@pytest.mark.parametrize("rows,k,rt", [(32, 64, 2), (64, 96, 4), (16, 32, 1)])
+def test_mfma_tiling_layout(rows, k, rt):
+    """The multi-stream GEMM's A-operand tiling (v_mfma_f32_16x16x32_bf16:
+    lane l holds row l % 16, columns 8 (l / 16) .. + 7 of a 16 x 32 tile),
+    checked element by element against the layout rule; every source value
+    lands exactly once."""
+    src = np.arange(rows * k, dtype=np.uint32).astype(np.uint16).reshape(rows, k)
+    dst = np.empty(rows * k, np.uint16)
+    _lib.load().gdn_test_tile_bf16(src.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), rows, k, rt,
+                                   dst.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)))
+    kt_n = k // 32
+    for blk in range(rows // (16 * rt)):
+        for kt in range(kt_n):
+            for r in range(rt):
+                base = (((blk * kt_n + kt) * rt + r) * 64) * 8
+                for lane in range(64):
+                    row = blk * 16 * rt + r * 16 + lane % 16
+                    c0 = kt * 32 + 8 * (lane // 16)
+                    assert (dst[base + lane * 8: base + lane * 8 + 8] == src[row, c0:c0 + 8]).all()
+    assert sorted(dst.tolist()) == sorted(src.ravel().tolist())
