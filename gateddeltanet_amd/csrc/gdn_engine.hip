@@ -969,27 +969,29 @@ struct BankLayout {
 
 // A workgroup's weight rows as a stream of 16-element items: item f (row
 // f / (K/16), half-beat f % (K/16)) sits at element 16 f of the workgroup's
-// slice and thread t takes items t + 1024 i.  prime() issues the loads of
-// the first DEPTH items; run() walks the items in order, issuing item
-// i + DEPTH before multiplying item i, so a wave never has more than DEPTH
-// items in flight (a SIMD holds only about one wave's worth of outstanding
-// loads; a wave that asks for more stalls at issue and cannot multiply the
-// items it already has).
-template <int K, int ROWS, int C, int D>
+// slice and stream thread u = threadIdx.x - T0 takes items u + (kTB - T0) i
+// (T0 = 256 when waves 0..3 build the input and own no items).  prime()
+// issues the loads of the first DEPTH items; run() walks the items in order,
+// issuing item i + DEPTH before multiplying item i, so a wave never has more
+// than DEPTH items in flight (a SIMD holds only about one wave's worth of
+// outstanding loads; a wave that asks for more stalls at issue and cannot
+// multiply the items it already has).
+template <int K, int ROWS, int C, int D, int T0>
 struct WStream {
+    static constexpr int NT = kTB - T0;  // stream threads
     static constexpr int HB = Hb<K>::HB;
     static constexpr int ITEMS = ROWS * HB;
-    static constexpr int NIT = (ITEMS + kTB - 1) / kTB;
+    static constexpr int NIT = (ITEMS + NT - 1) / NT;
     static constexpr int DEPTH = D < NIT ? D : NIT;
-    static constexpr bool kFull = (ITEMS % kTB) == 0;
-    static constexpr bool kSameHb = (kTB % HB) == 0;
+    static constexpr bool kFull = (ITEMS % NT) == 0;
+    static constexpr bool kSameHb = (NT % HB) == 0;
     static_assert(C != kFp32, "BF16 weights");
     const u32x4 *wb;
     u32x4 v[NIT][2];
 
     template <int I>
     __device__ __forceinline__ void load() {
-        const int f = threadIdx.x + kTB * I;
+        const int f = (int)threadIdx.x - T0 + NT * I;
         if (kFull || f < ITEMS) {
             v[I][0] = __builtin_nontemporal_load(wb + 2 * f);
             v[I][1] = __builtin_nontemporal_load(wb + 2 * f + 1);
@@ -1015,7 +1017,7 @@ struct WStream {
     __device__ __forceinline__ void run_from(const uint32_t *xs, float *part, uint32_t *xv) {
         if constexpr (I < NIT) {
             if constexpr (I + DEPTH < NIT) load<I + DEPTH>();
-            const int f = threadIdx.x + kTB * I;
+            const int f = (int)threadIdx.x - T0 + NT * I;
             if (kFull || f < ITEMS) {
                 const int row = f / HB, hb = f - row * HB;
                 if constexpr (!kSameHb) lds_load16u(xs + hb * 16, xv);
@@ -1050,7 +1052,7 @@ struct WStream {
     template <bool FAST>
     __device__ __forceinline__ void run(const uint32_t *xs, float *part) {
         uint32_t xv[16];
-        if constexpr (kSameHb) lds_load16u(xs + (threadIdx.x % HB) * 16, xv);
+        if constexpr (kSameHb) lds_load16u(xs + ((threadIdx.x - T0) % HB) * 16, xv);
         run_from<FAST, 0>(xs, part, xv);
     }
 };
@@ -1097,7 +1099,7 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     constexpr int CHW = (4 * CR + 63) / 64;  // waves that run bank chains
     static_assert(CHW <= 16, "one chain lane per bank");
     static_assert(K % kT == 0 && (PRO == PRO_PLAIN || K == kH), "input shape");
-    static_assert(EPI != EPI_QKVG || (K == kH && CHW < 16), "a/b rows: hidden input, a free wave");
+    static_assert(EPI != EPI_QKVG || (K == kH && CHW <= 3), "a/b rows: hidden input; wave 3 runs no bank chain");
     __shared__ __attribute__((aligned(16))) uint32_t xs[K];
     __shared__ __attribute__((aligned(16))) float part[CR * BankLayout<K>::RSTR];
     __shared__ __attribute__((aligned(16))) float scratch[kH / 16];
@@ -1114,25 +1116,41 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     if (t == 0) arrive = 0;
     __syncthreads();  // before any load: the waves are just starting
 
-    // 1. activation reads (waves 0..3 own the input elements), issued
-    // before their weight loads
+    // 1. activation reads (waves 0..3 own the input elements).  A CU serves
+    // its vector memory requests in issue order.  Input-first kernels (QKVG,
+    // o_proj, LM head: measured faster so) issue every activation read
+    // before any weight load (s_barrier, which waits for no memory), so the
+    // input arrives ahead of the CU's weight slice, and stream their weights
+    // from waves 4..15 only (a wave stalls at load issue while its SIMD's
+    // queue is full, which would hold the prologue back).  gate/up and down
+    // (measured faster so) let all 16 waves issue weights at once, the input
+    // waves after their activation reads.
+    constexpr bool kActFirst = EPI == EPI_QKVG || PRO == PRO_ONORM || EPI == EPI_LM;
+    constexpr int T0 = kActFirst ? kT : 0;
     Prologue<C, K, PRO> pro;
     if (t < kT) pro.load(src);
+    // QKVG workgroup h < 8: head h's FP32 a and b rows (half-beat t & 127 of
+    // row t >> 7), needed right after the input is built
+    const bool ab_blk = (EPI == EPI_QKVG) && blockIdx.x < kNH;
+    u32x4 abw[4];
+    if (ab_blk && t < kT) {
+        const int abrow = (t >> 7) * kNH + blockIdx.x, hb = t & 127;
+        const u32x4 *src4 = reinterpret_cast<const u32x4 *>(ep.aux + kAuxAB + (size_t)abrow * kH + hb * 16);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) abw[q] = src4[q];
+    }
+    if constexpr (kActFirst) __builtin_amdgcn_s_barrier();
 
     // 2. the weight stream
-    WStream<K, ROWS, C, D> ws;
-    ws.prime(wblk);
+    WStream<K, ROWS, C, D, T0> ws;
+    if (t >= T0) ws.prime(wblk);
 
     // QKVG extras, read behind the weight loads so they take no load-queue
     // slot ahead of the stream: the conv tails and taps of each q/k/v row
-    // (its owner lane), and in workgroup h < 8 head h's a and b rows (FP32,
-    // waves 12..15)
+    // (its owner lane)
     const bool owner = wave < CHW && (t & 3) == 0 && (t >> 2) < CR;
     uint16_t tail_b[3] = {0, 0, 0};
     f32x4 taps = {0.0f, 0.0f, 0.0f, 0.0f};
-    u32x4 abw[4];
-    const bool ab_blk = (EPI == EPI_QKVG) && blockIdx.x < kNH;
-    constexpr int kAbT0 = kTB - kT;  // first a/b thread
     if constexpr (EPI == EPI_QKVG) {
         const int r = row0 + (t >> 2);
         if (owner && r < 3 * kH) {
@@ -1143,12 +1161,6 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
             tail_b[2] = tl[2 * kH + ch];
             taps = *reinterpret_cast<const f32x4 *>(ep.aux + kAuxConv + ((size_t)kind * kH + ch) * 4);
         }
-        if (ab_blk && t >= kAbT0) {
-            const int u = t - kAbT0, abrow = (u >> 7) * kNH + blockIdx.x, hb = u & 127;
-            const u32x4 *src4 = reinterpret_cast<const u32x4 *>(ep.aux + kAuxAB + (size_t)abrow * kH + hb * 16);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) abw[q] = src4[q];
-        }
     }
 
     // 3. the input vector in LDS and the fast-path verdict: waves 0..3 build
@@ -1158,55 +1170,58 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     if (t < kT) {
         Wave4Sync sync{&arrive};
         fast = pro.finish_bf16(src, wi, xs, scratch, bcast, red, sync);
+        if constexpr (EPI == EPI_QKVG) {
+            if (ab_blk) {
+                // a_h and b_h while the weights stream (gdn_gemv_tiny_ab):
+                // FP32 products x * w, tree16 per half-beat; then wave 3 runs
+                // acc = (acc + tree16(lo)) + tree16(hi) per beat, rounded,
+                // and beta_h, decay_h (its double-precision exp/log1p would
+                // otherwise trail the workgroup's epilogue)
+                const int hb = t & 127;
+                uint32_t xv[16];
+                lds_load16u(xs + hb * 16, xv);
+                float p[16];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    p[4 * q + 0] = lane_word_value(xv[4 * q + 0], 0) * u2f(abw[q].x);
+                    p[4 * q + 1] = lane_word_value(xv[4 * q + 1], 1) * u2f(abw[q].y);
+                    p[4 * q + 2] = lane_word_value(xv[4 * q + 2], 0) * u2f(abw[q].z);
+                    p[4 * q + 3] = lane_word_value(xv[4 * q + 3], 1) * u2f(abw[q].w);
+                }
+                abpart[t] = tree16(p);
+                sync();
+                if (wave == 3) {
+                    const int lane = t & 63;
+                    float acc = 0.0f;
+                    if (lane < 2) {
+                        const float *pr = abpart + lane * Hb<kH>::HB;
+                        for (int j = 0; j < Hb<kH>::NB; ++j) acc = (acc + pr[2 * j]) + pr[2 * j + 1];
+                    }
+                    const float a = R<C>(acc);
+                    const float b = R<C>(__shfl(acc, 1));
+                    if (lane == 0) {
+                        float beta, decay;
+                        head_scalars(a, b, ep.aux[kAuxALog + blockIdx.x], ep.aux[kAuxDtBias + blockIdx.x], beta,
+                                     decay);
+                        ep.ab[blockIdx.x] = a;
+                        ep.ab[kNH + blockIdx.x] = b;
+                        ep.bd[2 * blockIdx.x] = beta;
+                        ep.bd[2 * blockIdx.x + 1] = decay;
+                    }
+                }
+            }
+        }
     } else {
         wait_count(&arrive, 4 * Prologue<C, K, PRO>::kSyncs);
         fast = decide_fast(red, wi);
     }
 
     // 4. products, barrier, bank chains and the row epilogue
-    if (fast) ws.template run<true>(xs, part);
-    else ws.template run<false>(xs, part);
-    if constexpr (EPI == EPI_QKVG) {
-        if (ab_blk && t >= kAbT0) {
-            // a_h and b_h: FP32 products x * w, tree16 per half-beat
-            // (gdn_gemv_tiny_ab)
-            const int hb = (t - kAbT0) & 127;
-            uint32_t xv[16];
-            lds_load16u(xs + hb * 16, xv);
-            float p[16];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                p[4 * q + 0] = lane_word_value(xv[4 * q + 0], 0) * u2f(abw[q].x);
-                p[4 * q + 1] = lane_word_value(xv[4 * q + 1], 1) * u2f(abw[q].y);
-                p[4 * q + 2] = lane_word_value(xv[4 * q + 2], 0) * u2f(abw[q].z);
-                p[4 * q + 3] = lane_word_value(xv[4 * q + 3], 1) * u2f(abw[q].w);
-            }
-            abpart[t - kAbT0] = tree16(p);
-        }
+    if (t >= T0) {
+        if (fast) ws.template run<true>(xs, part);
+        else ws.template run<false>(xs, part);
     }
     __syncthreads();
-    if constexpr (EPI == EPI_QKVG) {
-        if (ab_blk && wave == CHW) {
-            // acc = (acc + tree16(lo)) + tree16(hi) per beat, rounded; then
-            // beta_h and decay_h -- beside the bank chains of waves 0..CHW-1
-            const int lane = t & 63;
-            float acc = 0.0f;
-            if (lane < 2) {
-                const float *pr = abpart + lane * Hb<kH>::HB;
-                for (int j = 0; j < Hb<kH>::NB; ++j) acc = (acc + pr[2 * j]) + pr[2 * j + 1];
-            }
-            const float a = R<C>(acc);
-            const float b = R<C>(__shfl(acc, 1));
-            if (lane == 0) {
-                float beta, decay;
-                head_scalars(a, b, ep.aux[kAuxALog + blockIdx.x], ep.aux[kAuxDtBias + blockIdx.x], beta, decay);
-                ep.ab[blockIdx.x] = a;
-                ep.ab[kNH + blockIdx.x] = b;
-                ep.bd[2 * blockIdx.x] = beta;
-                ep.bd[2 * blockIdx.x + 1] = decay;
-            }
-        }
-    }
     if (wave < CHW) {
         const float y = chain_rows<K, CR>(part);
         if (owner) {
