@@ -35,7 +35,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "ms/token batch-1 GDN-1.3B decode (outer); achieved HBM GB/s vs peak"
 PEAK_HBM_GBPS = 8000.0
-FPGA_OUTER_MS = 8.233  # U55C FPGA outer ms/token (architecture.md:1215)
+FPGA_OUTER_MS = 8.233  # U55C FPGA outer ms/token, the reference's published figure (architecture.md:1215)
 
 H, I, V, L = 2048, 5632, 32000, 24
 # Algorithmic bytes per token (the figures of the hot-path scope table):

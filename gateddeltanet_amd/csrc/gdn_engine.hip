@@ -933,14 +933,13 @@ __global__ __launch_bounds__(kT, gemv_min_waves(C, EPI)) void k_gemv(const void 
 //
 // One 1024-thread workgroup per CU (it claims all 512 VGPRs of every SIMD,
 // so no two share one) owns ROWS consecutive rows of the matrix, a
-// contiguous slice of the weight stream, and walks it in chunks of CR rows
-// held in registers (two chunk buffers when there are several chunks: the
-// loads of chunk c + 2 are issued as soon as chunk c has been multiplied).
-// The activation reads are issued, and a barrier passed, before any weight
-// read: the vector memory path of a CU serves requests in order, so an
-// activation read issued after a weight stream waits for all of it.  The
-// prologue (residual add, norms) then runs once per CU while the CU's
-// weights stream in.
+// contiguous slice of the weight stream, as 16-element items held in
+// registers (WStream).  Waves 0..3 read the activations and build the GEMV
+// input (residual add, norms) once per CU while the weights stream in.  The
+// vector memory path of a CU serves requests in order, so the activation
+// reads are issued before the weight loads: in the input-first kernels a
+// barrier orders them ahead of every weight load and only waves 4..15 carry
+// items; in gate/up and down all 16 waves stream.
 constexpr int kTB = 1024;  // threads per CU-resident workgroup
 // Rows per CU-resident workgroup (grids of 256 workgroups).
 constexpr int kCuQkvg = 32;   // 8192 / 256

@@ -326,8 +326,8 @@ double gdn_token_logprob(const float *logits, uint32_t vocab, int32_t target);
 uint32_t gdn_strict_argmax(const float *logits, uint32_t n);
 
 /* ===== multi-stream decode =====
- * No counterpart in the reference, which decodes one stream (README.md:75-77;
- * SURVEY config 5 asks for 64).  Up to GDN_MAX_STREAMS independent streams,
+ * No counterpart in the reference, which decodes one stream (README.md:75-77).
+ * Up to GDN_MAX_STREAMS (64) independent streams,
  * each with its own FP32 recurrent state and conv tails, advance one token
  * each per step.  Arithmetic is the BF16W_FP32S contract's except inside the
  * projections, which form exact products of the same BF16 operands and sum
