@@ -53,6 +53,7 @@ namespace bt {
 
 constexpr int kMaxB = GDN_MAX_STREAMS;  // streams = the 64 B-operand columns
 static_assert(kMaxB == 64, "four 16-stream groups per MFMA B operand");
+constexpr int kScanCols = 4;  // state columns per prefill-scan workgroup
 constexpr int kSplitO = 4;              // K splits of o_proj (16 k tiles each)
 constexpr int kSplitDown = 11;          // K splits of the down projection (16 k tiles each)
 constexpr int kKtH = kH / 32;           // k tiles of a K = 2048 projection
@@ -699,19 +700,20 @@ __global__ __launch_bounds__(kT) void k_pqk(const float *__restrict__ qkv, float
     if (t == 0) alpha_out[m * kNH + h] = (red2[0] + red2[1]) + (red2[2] + red2[3]);
 }
 
-// Sequential sum acc = acc + col[j * 64] over 256 rows of one LDS column in
-// row order; the reads run 16 rows ahead of the adds, a fence per block
-// bounding the registers they hold.
+// Sequential sum acc = acc + col[j * STRIDE] over 256 rows of one LDS
+// column in row order; the reads run 16 rows ahead of the adds, a fence per
+// block bounding the registers they hold.
+template <int STRIDE>
 __device__ __forceinline__ float column_chain(const float *col) {
     float acc = 0.0f;
     float cur[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) cur[j] = col[j * 64];
+    for (int j = 0; j < 16; ++j) cur[j] = col[j * STRIDE];
 #pragma unroll
     for (int b = 0; b < kHD / 16; ++b) {
         float nxt[16];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) nxt[j] = (b + 1 < kHD / 16) ? col[(16 * (b + 1) + j) * 64] : 0.0f;
+        for (int j = 0; j < 16; ++j) nxt[j] = (b + 1 < kHD / 16) ? col[(16 * (b + 1) + j) * STRIDE] : 0.0f;
 #pragma unroll
         for (int j = 0; j < 16; ++j) acc = acc + cur[j];
         asm volatile("" : "+v"(acc) : : "memory");
@@ -721,35 +723,43 @@ __device__ __forceinline__ float column_chain(const float *col) {
     return acc;
 }
 
-// The recurrence over a chunk's n tokens in order, for one head and 64 state
-// columns per workgroup (grid (4 column groups, heads)): columns are
-// independent, so four workgroups share a head.  Wave w owns rows 64 w ..
-// 64 w + 63 of column 64 blockIdx.x + lane, held in registers for the whole
-// chunk.  Per token: every wave forms its rows' products S[j][i] * kn[j] and
-// S[j][i] * qn[j] into LDS (row-major, a column per lane); wave 0 then sums
-// the r column chains and wave 1 the p chains, each in row order j = 0..255
-// (the reference's chain order, adds only), while waves 2-3 stage the next
-// token's k and q; every wave forms delta from the two sums and updates its
-// rows, and wave 0 writes o.
+// The recurrence over a chunk's n tokens in order, for one head and CB state
+// columns per workgroup (grid (256 / CB column groups, heads)): columns are
+// independent, so 256 / CB workgroups share a head.  Thread t holds column
+// t % CB of rows t / CB + (256 / CB) j, j < CB, in registers for the whole
+// chunk.  Per token: every thread forms its elements' products
+// S[j][i] * kn[j] and S[j][i] * qn[j] into LDS ([row][column]); lanes 0..CB-1
+// of wave 0 then sum the r column chains and lanes CB..2CB-1 the p chains,
+// each in row order j = 0..255 (the reference's chain order, adds only),
+// while waves 2-3 stage the next token's k and q; every thread forms delta
+// for its column from the two sums and updates its elements, and wave 0
+// writes o.  Narrow tiles keep the per-token products and update short, so
+// the serial chain dominates.
+template <int CB>
 __global__ __launch_bounds__(kT) void k_pscan(const float *__restrict__ qkv, const float *__restrict__ qn_all,
                                               const float *__restrict__ kn_all, const float *__restrict__ alpha_all,
                                               const float *__restrict__ bd, int n, float *__restrict__ state,
                                               float *__restrict__ attn) {
-    constexpr int RQ = kHD / 4;  // rows per wave
-    __shared__ float prod[2][kHD][64];                              // [k|q][row][column]
+    static_assert(2 * CB <= 64 && (kT % CB) == 0, "both chains of every column in wave 0");
+    constexpr int RS = kT / CB;  // row step between a thread's elements
+    constexpr int NE = kHD / RS; // elements per thread (= CB)
+    // [k|q][row][column]; the q tile starts 16 words on so the r and p chain
+    // lanes of wave 0 read distinct banks
+    constexpr int kQOff = kHD * CB + 16;
+    __shared__ float prod[kQOff + kHD * CB];
     __shared__ __attribute__((aligned(16))) float kq[2][2][kHD];    // [token parity][k|q][row]
-    __shared__ float rp[2][64];
-    __shared__ float vs[kMaxB][64];
+    __shared__ float rp[2][CB];
+    __shared__ float vs[kMaxB][CB];
     __shared__ float sc[kMaxB][3];  // beta, decay, alpha
     const int cg = blockIdx.x, h = blockIdx.y, t = threadIdx.x, w = t >> 6, lane = t & 63;
-    const int col = cg * 64 + lane, r0 = w * RQ;
+    const int c = t % CB, rsub = t / CB, col = cg * CB + c;
     float *S = state + (size_t)h * kHD * kHD + col;
-    float sv[RQ];
+    float sv[NE];
 #pragma unroll
-    for (int j = 0; j < RQ; ++j) sv[j] = S[(size_t)(r0 + j) * kHD];
-    for (int i = t; i < n * 64; i += kT) {
-        const int m = i >> 6, c = i & 63;
-        vs[m][c] = qkv[((size_t)m * 3 + 2) * kH + h * kHD + cg * 64 + c];
+    for (int j = 0; j < NE; ++j) sv[j] = S[(size_t)(rsub + RS * j) * kHD];
+    for (int i = t; i < n * CB; i += kT) {
+        const int m = i / CB, cc = i % CB;
+        vs[m][cc] = qkv[((size_t)m * 3 + 2) * kH + h * kHD + cg * CB + cc];
     }
     if (t < n) {
         sc[t][0] = bd[t * 16 + 2 * h];
@@ -761,16 +771,19 @@ __global__ __launch_bounds__(kT) void k_pscan(const float *__restrict__ qkv, con
     __syncthreads();
     for (int m = 0; m < n; ++m) {
         const float *kn = kq[m & 1][0], *qn = kq[m & 1][1];
-        // products of this wave's rows
 #pragma unroll
-        for (int j = 0; j < RQ; ++j) {
-            prod[0][r0 + j][lane] = sv[j] * kn[r0 + j];
-            prod[1][r0 + j][lane] = sv[j] * qn[r0 + j];
+        for (int j = 0; j < NE; ++j) {
+            const int row = rsub + RS * j;
+            prod[row * CB + c] = sv[j] * kn[row];
+            prod[kQOff + row * CB + c] = sv[j] * qn[row];
         }
         __syncthreads();
-        if (w < 2) {
-            rp[w][lane] = column_chain(&prod[w][0][lane]);
-        } else if (m + 1 < n) {
+        if (w == 0) {
+            if (lane < 2 * CB) {
+                const int which = lane / CB, cc = lane % CB;
+                rp[which][cc] = column_chain<CB>(prod + which * kQOff + cc);
+            }
+        } else if (w >= 2 && m + 1 < n) {
             const int i = t - 128;  // 128 threads stage 512 values
             const float *src = (i < 64 ? kn_all : qn_all) + (size_t)(m + 1) * kH + h * kHD;
             float *dst = kq[(m + 1) & 1][i < 64 ? 0 : 1];
@@ -780,20 +793,20 @@ __global__ __launch_bounds__(kT) void k_pscan(const float *__restrict__ qkv, con
         }
         __syncthreads();
         const float beta = sc[m][0], decay = sc[m][1];
-        const float r = rp[0][lane], p = rp[1][lane];
-        const float delta = beta * (vs[m][lane] - decay * r);
-        if (w == 0) {
+        const float r = rp[0][c], p = rp[1][c];
+        const float delta = beta * (vs[m][c] - decay * r);
+        if (t < CB) {
             const float o = 0.0625f * (decay * p + sc[m][2] * delta);
             attn[(size_t)m * kH + h * kHD + col] = rne_bf16(o);
         }
 #pragma unroll
-        for (int j = 0; j < RQ; ++j) sv[j] = decay * sv[j] + kn[r0 + j] * delta;
+        for (int j = 0; j < NE; ++j) sv[j] = decay * sv[j] + kn[rsub + RS * j] * delta;
     }
     // the store addresses are formed after the token loop, not kept across it
     float *Sw = S;
     asm volatile("" : "+v"(Sw));
 #pragma unroll
-    for (int j = 0; j < RQ; ++j) Sw[(size_t)(r0 + j) * kHD] = sv[j];
+    for (int j = 0; j < NE; ++j) Sw[(size_t)(rsub + RS * j) * kHD] = sv[j];
 }
 
 }  // namespace bt
@@ -1157,7 +1170,8 @@ void enqueue_prefill_chunk(GDNBatchEngine *e, int slot, int n, bool last, hipStr
         hipLaunchKernelGGL(k_pconv, dim3(4 * kH / 64), dim3(kT), 0, s, e->ypart, n, tl, b_aux(e, l) + kAuxConv,
                            e->qkv, e->gate, e->sgate);
         hipLaunchKernelGGL(k_pqk, dim3(kNH, n), dim3(kT), 0, s, e->qkv, e->p_qn, e->p_kn, e->p_alpha);
-        hipLaunchKernelGGL(k_pscan, dim3(kHD / 64, kNH), dim3(kT), 0, s, e->qkv, e->p_qn, e->p_kn, e->p_alpha,
+        hipLaunchKernelGGL(k_pscan<kScanCols>, dim3(kHD / kScanCols, kNH), dim3(kT), 0, s, e->qkv, e->p_qn, e->p_kn,
+                           e->p_alpha,
                            e->bd, n, st, e->attn);
         hipLaunchKernelGGL(k_bonorm, dim3(kNH, n), dim3(kT), 0, s, e->attn, e->gate, e->sgate,
                            b_aux(e, l) + kAuxONorm, e->eps, e->x_o);
