@@ -360,6 +360,8 @@ def main_prefill(args):
     pre_s = time.perf_counter() - t0
     bs.free()
     rs = g.RunState(model, g.CONTRACT_BF16W_FP32S)
+    if args.eager:
+        rs.set_graph(False)
     rs.teacher_forced(prompt[:16], 16, timing=False)
     rs.load_state(np.zeros(rs.n_state, np.float32), np.zeros(rs.n_conv, np.float32))
     sync()

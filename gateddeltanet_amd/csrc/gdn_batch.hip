@@ -639,9 +639,11 @@ __global__ __launch_bounds__(2 * kT) void k_brecur(const float *__restrict__ qkv
 // prefilled stream's for this layer, [q,k,v][3 oldest..newest][kH].  Token
 // m's window is (s[m], s[m+1], s[m+2]) and its input s[m+3] in the sequence
 // s = tails ++ R(raw[0..n)); the new tails are s[n], s[n+1], s[n+2].
-__global__ __launch_bounds__(kT) void k_pconv(const float *__restrict__ raw, int n, float *__restrict__ tails,
-                                              const float *__restrict__ conv_w, float *__restrict__ qkv,
-                                              float *__restrict__ gate, float *__restrict__ sgate) {
+constexpr int kConvT = 1024;  // threads per conv workgroup: 16 token lanes x 64 channels
+__global__ __launch_bounds__(kConvT) void k_pconv(const float *__restrict__ raw, int n, float *__restrict__ tails,
+                                                  const float *__restrict__ conv_w, float *__restrict__ qkv,
+                                                  float *__restrict__ gate, float *__restrict__ sgate) {
+    constexpr int MG = kConvT / 64;  // tokens in flight per channel
     __shared__ float xs[kMaxB + 3][64];
     const int row0 = blockIdx.x * 64, t = threadIdx.x, cl = t & 63, mg = t >> 6;
     const int row = row0 + cl, which = row0 / kH, c = row - which * kH;
@@ -652,10 +654,10 @@ __global__ __launch_bounds__(kT) void k_pconv(const float *__restrict__ raw, int
             xs[1][cl] = tl[kH];
             xs[2][cl] = tl[2 * kH];
         }
-        for (int m = mg; m < n; m += 4) xs[3 + m][cl] = rne_bf16(raw[(size_t)m * 4 * kH + row]);
+        for (int m = mg; m < n; m += MG) xs[3 + m][cl] = rne_bf16(raw[(size_t)m * 4 * kH + row]);
         __syncthreads();
         const f32x4 cw = *reinterpret_cast<const f32x4 *>(conv_w + ((size_t)which * kH + c) * 4);
-        for (int m = mg; m < n; m += 4) {
+        for (int m = mg; m < n; m += MG) {
             // gdn_depthwise_conv_silu_head_kind, gdn_model.cpp:1543-1667
             const float sum = xs[m][cl] * cw.x + xs[m + 1][cl] * cw.y + xs[m + 2][cl] * cw.z + xs[m + 3][cl] * cw.w;
             qkv[((size_t)m * 3 + which) * kH + c] = rne_bf16(silu_ref(sum));
@@ -666,7 +668,7 @@ __global__ __launch_bounds__(kT) void k_pconv(const float *__restrict__ raw, int
             tl[2 * kH] = xs[n + 2][cl];
         }
     } else {
-        for (int m = mg; m < n; m += 4) {
+        for (int m = mg; m < n; m += MG) {
             const float g = rne_bf16(raw[(size_t)m * 4 * kH + row]);
             gate[(size_t)m * kH + c] = g;
             sgate[(size_t)m * kH + c] = sigmoid_ref(g);
@@ -1167,7 +1169,7 @@ void enqueue_prefill_chunk(GDNBatchEngine *e, int slot, int n, bool last, hipStr
         raw.y = e->ypart;
         hipLaunchKernelGGL((k_bgemm<2, kKtH, 8, 1, EPI_RAW>), dim3(4 * kH / 32), dim3(8 * 64), 0, s, e->w_qkvg[l],
                            reinterpret_cast<const u32x4 *>(e->x_h), raw);
-        hipLaunchKernelGGL(k_pconv, dim3(4 * kH / 64), dim3(kT), 0, s, e->ypart, n, tl, b_aux(e, l) + kAuxConv,
+        hipLaunchKernelGGL(k_pconv, dim3(4 * kH / 64), dim3(kConvT), 0, s, e->ypart, n, tl, b_aux(e, l) + kAuxConv,
                            e->qkv, e->gate, e->sgate);
         hipLaunchKernelGGL(k_pqk, dim3(kNH, n), dim3(kT), 0, s, e->qkv, e->p_qn, e->p_kn, e->p_alpha);
         hipLaunchKernelGGL(k_pscan<kScanCols>, dim3(kHD / kScanCols, kNH), dim3(kT), 0, s, e->qkv, e->p_qn, e->p_kn,
