@@ -327,11 +327,11 @@ def stepped_reference(m, prompt):
         bs.free()
 
 
-@pytest.mark.parametrize("n", [1, 2, 150])
+@pytest.mark.parametrize("n", [1, 2, 64, 65, 128, 150])
 def test_prefill_equals_steps(model, n):
     """Prefill of n tokens (chunks of 64; n < 3 exercises the conv tails
-    alone) equals n single-stream steps bit for bit, and leaves the other
-    streams' states alone."""
+    alone, 64 / 65 / 128 the chunk edges) equals n single-stream steps bit
+    for bit, and leaves the other streams' states alone."""
     prompt = g.synth_tokens(n, 40 + n, 0)
     seed_ref, logits_ref, hidden_ref, (rec_ref, conv_ref) = stepped_reference(model, prompt)
     bs = g.BatchState(model, 3)
@@ -354,6 +354,25 @@ def test_prefill_equals_steps(model, n):
             assert same_bits(ref.logits(0), bs.logits(1))
         finally:
             ref.free()
+    finally:
+        bs.free()
+
+
+def test_prefill_continues_a_decoded_stream(model):
+    """A prefill on a stream that has already decoded tokens continues from
+    its state and conv tails: 5 steps then a 70-token prefill equal 75
+    steps bit for bit."""
+    head = g.synth_tokens(5, 47, 0)
+    prompt = g.synth_tokens(70, 48, 0)
+    seed_ref, logits_ref, hidden_ref, (rec_ref, conv_ref) = stepped_reference(model, np.concatenate([head, prompt]))
+    bs = g.BatchState(model, 2)
+    try:
+        for t in head:
+            bs.step([0, t])
+        assert bs.prefill(1, prompt) == seed_ref
+        assert same_bits(bs.logits(1), logits_ref) and same_bits(bs.final_hidden(1), hidden_ref)
+        rec, conv = bs.save_stream_state(1)
+        assert same_bits(rec, rec_ref) and same_bits(conv, conv_ref)
     finally:
         bs.free()
 
