@@ -56,6 +56,8 @@ static_assert(kMaxB == 64, "four 16-stream groups per MFMA B operand");
 constexpr int kScanCols = 4;  // state columns per prefill-scan workgroup
 constexpr int kSplitO = 4;              // K splits of o_proj (16 k tiles each)
 constexpr int kSplitDown = 11;          // K splits of the down projection (16 k tiles each)
+constexpr int kRtO = 2;                 // 16-row tiles per o_proj workgroup
+constexpr int kRtDown = 2;              // 16-row tiles per down workgroup
 constexpr int kKtH = kH / 32;           // k tiles of a K = 2048 projection
 constexpr int kKtI = kI / 32;           // k tiles of the down projection
 constexpr size_t kLayerState = (size_t)kNH * kHD * kHD;  // floats per (layer, stream)
@@ -906,7 +908,7 @@ int b_upload(GDNBatchEngine *e, const GDNModel *m) {
         }
         if (upload_tiled(rows, 4 * H, H, 2, p, e->w_qkvg[l])) return -1;
         to_bf16(w.o_proj, H * H, rows);
-        if (upload_tiled(rows, H, H, 2, p, e->w_o[l])) return -1;
+        if (upload_tiled(rows, H, H, kRtO, p, e->w_o[l])) return -1;
         // gate rows c..c+15 then up rows c..c+15: one SwiGLU row pair per
         // workgroup row block
         std::vector<uint16_t> g16, u16;
@@ -919,7 +921,7 @@ int b_upload(GDNBatchEngine *e, const GDNModel *m) {
         }
         if (upload_tiled(rows, 2 * I, H, 2, p, e->w_gu[l])) return -1;
         to_bf16(w.mlp_down_proj, H * I, rows);
-        if (upload_tiled(rows, H, I, 2, p, e->w_down[l])) return -1;
+        if (upload_tiled(rows, H, I, kRtDown, p, e->w_down[l])) return -1;
     }
     to_bf16(m->lm_head, V * H, rows);
     if (upload_tiled(rows, V, H, 2, p, e->w_lm)) return -1;
@@ -1050,8 +1052,8 @@ void launch_o(GDNBatchEngine *e, int l, hipStream_t s) {
     ep.n_streams = e->streams;
     ep.n_rows = kH;
     ep.y = e->ypart;
-    hipLaunchKernelGGL((k_bgemm<2, kKtH, 4, kSplitO, EPI_RAW>), dim3(kH / 32, kSplitO), dim3(kT), 0, s, e->w_o[l],
-                       reinterpret_cast<const u32x4 *>(e->x_o), ep);
+    hipLaunchKernelGGL((k_bgemm<kRtO, kKtH, 4, kSplitO, EPI_RAW>), dim3(kH / (16 * kRtO), kSplitO), dim3(kT), 0, s,
+                       e->w_o[l], reinterpret_cast<const u32x4 *>(e->x_o), ep);
 }
 void launch_mlp_norm(GDNBatchEngine *e, int l, hipStream_t s) {
     const BNorm p = bnorm(e, e->ypart, b_aux(e, l) + kAuxMlpNorm, e->x_h, -1);
@@ -1069,8 +1071,8 @@ void launch_down(GDNBatchEngine *e, int l, hipStream_t s) {
     ep.n_streams = e->streams;
     ep.n_rows = kH;
     ep.y = e->ypart;
-    hipLaunchKernelGGL((k_bgemm<2, kKtI, 4, kSplitDown, EPI_RAW>), dim3(kH / 32, kSplitDown), dim3(kT), 0, s,
-                       e->w_down[l], reinterpret_cast<const u32x4 *>(e->x_d), ep);
+    hipLaunchKernelGGL((k_bgemm<kRtDown, kKtI, 4, kSplitDown, EPI_RAW>), dim3(kH / (16 * kRtDown), kSplitDown),
+                       dim3(kT), 0, s, e->w_down[l], reinterpret_cast<const u32x4 *>(e->x_d), ep);
 }
 // After layer l's down projection: h = R(h + y), then the next layer's
 // attention norm with its a/b rows, or the final norm.
@@ -1181,8 +1183,8 @@ void enqueue_prefill_chunk(GDNBatchEngine *e, int slot, int n, bool last, hipStr
         eo.n_streams = n;
         eo.n_rows = kH;
         eo.y = e->ypart;
-        hipLaunchKernelGGL((k_bgemm<2, kKtH, 4, kSplitO, EPI_RAW>), dim3(kH / 32, kSplitO), dim3(kT), 0, s,
-                           e->w_o[l], reinterpret_cast<const u32x4 *>(e->x_o), eo);
+        hipLaunchKernelGGL((k_bgemm<kRtO, kKtH, 4, kSplitO, EPI_RAW>), dim3(kH / (16 * kRtO), kSplitO), dim3(kT), 0,
+                           s, e->w_o[l], reinterpret_cast<const u32x4 *>(e->x_o), eo);
         const BNorm pm = bnorm(e, e->ypart, b_aux(e, l) + kAuxMlpNorm, e->x_h, -1);
         hipLaunchKernelGGL((k_bnorm<kSplitO, false, false>), dim3(n), dim3(kT), 0, s, pm);
         BEpi eg{};
@@ -1194,8 +1196,8 @@ void enqueue_prefill_chunk(GDNBatchEngine *e, int slot, int n, bool last, hipStr
         ed.n_streams = n;
         ed.n_rows = kH;
         ed.y = e->ypart;
-        hipLaunchKernelGGL((k_bgemm<2, kKtI, 4, kSplitDown, EPI_RAW>), dim3(kH / 32, kSplitDown), dim3(kT), 0, s,
-                           e->w_down[l], reinterpret_cast<const u32x4 *>(e->x_d), ed);
+        hipLaunchKernelGGL((k_bgemm<kRtDown, kKtI, 4, kSplitDown, EPI_RAW>), dim3(kH / (16 * kRtDown), kSplitDown),
+                           dim3(kT), 0, s, e->w_down[l], reinterpret_cast<const u32x4 *>(e->x_d), ed);
         if (l + 1 < e->layers) {
             const BNorm pa = bnorm(e, e->ypart, b_aux(e, l + 1) + kAuxAttnNorm, e->x_h, l + 1);
             hipLaunchKernelGGL((k_bnorm<kSplitDown, false, true>), dim3(n), dim3(kT), 0, s, pa);
@@ -1450,15 +1452,16 @@ int gdn_batch_profile_kernels(GDNBatchState *state, uint32_t rounds, float *avg_
 
 int gdn_test_batch_gemm(const float *W, const float *X, uint32_t N, uint32_t K, float *Y) {
     const bool k_hidden = K == (uint32_t)kH;
-    if (!(k_hidden || K == (uint32_t)kI) || N == 0 || (N % 32u) != 0) {
-        gdn_error("gdn_test_batch_gemm: K must be 2048 or 5632 and N a multiple of 32");
+    const uint32_t rows = 16u * (uint32_t)(k_hidden ? kRtO : kRtDown);  // rows per workgroup
+    if (!(k_hidden || K == (uint32_t)kI) || N == 0 || (N % rows) != 0) {
+        gdn_error("gdn_test_batch_gemm: K must be 2048 or 5632 and N a multiple of the workgroup's rows");
         return -1;
     }
     // the production configurations: o_proj's for K = 2048, down's for 5632
     const int splits = k_hidden ? kSplitO : kSplitDown;
     std::vector<uint16_t> wb, wt((size_t)N * K), xb;
     to_bf16(W, (size_t)N * K, wb);
-    gdn_tile_bf16(wb.data(), N, K, 2, wt.data());
+    gdn_tile_bf16(wb.data(), N, K, k_hidden ? kRtO : kRtDown, wt.data());
     // X [64][K] in B-operand tiles: the A tiling of 64 rows in 4 row tiles
     to_bf16(X, (size_t)kMaxB * K, xb);
     std::vector<uint16_t> xt((size_t)kMaxB * K);
@@ -1475,11 +1478,11 @@ int gdn_test_batch_gemm(const float *W, const float *X, uint32_t N, uint32_t K, 
     ep.n_rows = (int)N;
     ep.y = dy;
     if (k_hidden)
-        hipLaunchKernelGGL((k_bgemm<2, kKtH, 4, kSplitO, EPI_RAW>), dim3(N / 32, kSplitO), dim3(kT), 0, 0,
+        hipLaunchKernelGGL((k_bgemm<kRtO, kKtH, 4, kSplitO, EPI_RAW>), dim3(N / rows, kSplitO), dim3(kT), 0, 0,
                            static_cast<const u32x4 *>(dw), static_cast<const u32x4 *>(dx), ep);
     else
-        hipLaunchKernelGGL((k_bgemm<2, kKtI, 4, kSplitDown, EPI_RAW>), dim3(N / 32, kSplitDown), dim3(kT), 0, 0,
-                           static_cast<const u32x4 *>(dw), static_cast<const u32x4 *>(dx), ep);
+        hipLaunchKernelGGL((k_bgemm<kRtDown, kKtI, 4, kSplitDown, EPI_RAW>), dim3(N / rows, kSplitDown), dim3(kT),
+                           0, 0, static_cast<const u32x4 *>(dw), static_cast<const u32x4 *>(dx), ep);
     GDN_HIP(hipGetLastError());
     std::vector<float> parts((size_t)splits * kMaxB * N);
     GDN_HIP(hipMemcpy(parts.data(), dy, parts.size() * 4, hipMemcpyDeviceToHost));
