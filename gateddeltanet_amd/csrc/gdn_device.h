@@ -103,11 +103,25 @@ __device__ __forceinline__ float tree16(const float *p) {
     return b0 + b1;
 }
 
-// XOR butterfly over a wave64: every lane ends with the balanced pairwise
-// sum of the 64 values (the lower six levels of gdn_tree_reduce_256).
+// Balanced pairwise sum of a wave64's 64 values (the lower six levels of
+// gdn_tree_reduce_256), left in every lane.  Level m adds the partial of the
+// partner block of m lanes.  After each level every lane of a block holds
+// the same value (FP32 addition is commutative), so any lane of the partner
+// block serves: quad permutes for m = 1, 2, the half-row and row mirrors for
+// m = 4, 8, and the gfx950 row swaps for m = 16, 32 -- no LDS round trip,
+// the same sums as an XOR butterfly.
 __device__ __forceinline__ float wave_tree64(float v) {
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) v = v + __shfl_xor(v, m);
+    v = v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false));   // [1,0,3,2]
+    v = v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, false));   // [2,3,0,1]
+    v = v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xf, 0xf, false));  // row_half_mirror
+    v = v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xf, 0xf, false));  // row_mirror
+    const int lane = threadIdx.x & 63;
+    // permlane16_swap(v, v) returns (rows 0,0,2,2 ; rows 1,1,3,3) of v
+    const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
+    v = v + __int_as_float(((lane >> 4) & 1) ? s16[0] : s16[1]);
+    // permlane32_swap(v, v) returns (low, low ; high, high) halves of v
+    const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+    v = v + __int_as_float((lane >> 5) ? s32[0] : s32[1]);
     return v;
 }
 
