@@ -430,7 +430,7 @@ __global__ __launch_bounds__(kT) void k_bnorm(BNorm p) {
     float part = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) part += hv[e] * hv[e];
-    const float lead = __shfl_xor(part, 1);
+    const float lead = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(part), 0xB1, 0xf, 0xf, false));
     if (t & 1) {
         float s = lead;
 #pragma unroll
@@ -484,8 +484,7 @@ __global__ __launch_bounds__(kT) void k_bnorm(BNorm p) {
             const f32x4 xq = *reinterpret_cast<const f32x4 *>(xs + 32 * (grp & 63) + 4 * sub);
             const f32x4 w = wq[i];
             float s = (xq.x * w.x + xq.y * w.y) + (xq.z * w.z + xq.w * w.w);
-            s = s + __shfl_xor(s, 1);
-            s = s + __shfl_xor(s, 2);
+            s = quad_sum(s);
             if ((sub & 3) == 0) tab[grp >> 6][grp & 63][sub >> 2] = s;
         }
         __syncthreads();

@@ -103,26 +103,40 @@ __device__ __forceinline__ float tree16(const float *p) {
     return b0 + b1;
 }
 
-// Balanced pairwise sum of a wave64's 64 values (the lower six levels of
-// gdn_tree_reduce_256), left in every lane.  Level m adds the partial of the
-// partner block of m lanes.  After each level every lane of a block holds
-// the same value (FP32 addition is commutative), so any lane of the partner
-// block serves: quad permutes for m = 1, 2, the half-row and row mirrors for
-// m = 4, 8, and the gfx950 row swaps for m = 16, 32 -- no LDS round trip,
-// the same sums as an XOR butterfly.
-__device__ __forceinline__ float wave_tree64(float v) {
-    v = v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false));   // [1,0,3,2]
-    v = v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, false));   // [2,3,0,1]
-    v = v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xf, 0xf, false));  // row_half_mirror
-    v = v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xf, 0xf, false));  // row_mirror
+// Reduction of a wave64's 64 values by a commutative operation, left in
+// every lane, in the pairing of an XOR butterfly: level m combines the
+// partials of partner blocks of m lanes.  After each level every lane of a
+// block holds the same value, so any lane of the partner block serves: quad
+// permutes for m = 1, 2, the half-row and row mirrors for m = 4, 8, and the
+// gfx950 row swaps for m = 16, 32 -- no LDS round trip.
+template <class Op>
+__device__ __forceinline__ uint32_t wave_reduce64(uint32_t v, Op op) {
+    v = op(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xf, 0xf, false));   // [1,0,3,2]
+    v = op(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xf, 0xf, false));   // [2,3,0,1]
+    v = op(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xf, 0xf, false));  // row_half_mirror
+    v = op(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xf, 0xf, false));  // row_mirror
     const int lane = threadIdx.x & 63;
     // permlane16_swap(v, v) returns (rows 0,0,2,2 ; rows 1,1,3,3) of v
-    const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
-    v = v + __int_as_float(((lane >> 4) & 1) ? s16[0] : s16[1]);
+    const auto s16 = __builtin_amdgcn_permlane16_swap((int)v, (int)v, false, false);
+    v = op(v, (uint32_t)(((lane >> 4) & 1) ? s16[0] : s16[1]));
     // permlane32_swap(v, v) returns (low, low ; high, high) halves of v
-    const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
-    v = v + __int_as_float((lane >> 5) ? s32[0] : s32[1]);
+    const auto s32 = __builtin_amdgcn_permlane32_swap((int)v, (int)v, false, false);
+    v = op(v, (uint32_t)((lane >> 5) ? s32[0] : s32[1]));
     return v;
+}
+
+// Balanced pairwise sum of the 64 values (the lower six levels of
+// gdn_tree_reduce_256); FP32 addition is commutative, so the sums equal an
+// XOR butterfly's.
+__device__ __forceinline__ float wave_tree64(float v) {
+    return u2f(wave_reduce64(f2u(v), [](uint32_t a, uint32_t b) { return f2u(u2f(a) + u2f(b)); }));
+}
+
+// Sum over lane quads (lanes 4i..4i+3) in XOR-butterfly pairing, in every
+// lane of the quad.
+__device__ __forceinline__ float quad_sum(float v) {
+    v = v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false));
+    return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, false));
 }
 
 // Two FP32 values to a BF16 pair (lo in bits 0..15), round to nearest even
@@ -240,7 +254,14 @@ __device__ __forceinline__ void recur_block(const float *__restrict__ qp, const 
             acc = acc + col_v[j4].z;
             acc = acc + col_v[j4].w;
         }
-        const float pv = __shfl(acc, (lane + CB) & 63);
+        // lane i takes p_i from lane CB + i
+        float pv;
+        if constexpr (CB == 16) {
+            pv = __int_as_float(__builtin_amdgcn_permlane16_swap(__float_as_int(acc), __float_as_int(acc), false,
+                                                                 false)[1]);
+        } else {
+            pv = __shfl(acc, (lane + CB) & 63);
+        }
         if (!is_p) {
             const float r = acc;
             const float delta = beta * (vi - decay * r);

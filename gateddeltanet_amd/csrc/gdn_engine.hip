@@ -305,8 +305,7 @@ __device__ __forceinline__ float gemv_chain(const float *part) {
 #pragma unroll 8
         for (int b = parity; b < NB; b += 2) acc = acc + pr[2 * b];
     }
-    const float s = acc + __shfl_xor(acc, 1);
-    return s + __shfl_xor(s, 2);
+    return quad_sum(acc);  // (lo + hi) per parity, then the two parities
 }
 
 // ---------------------------------------------------------------- prologues
@@ -377,11 +376,8 @@ struct Wave4Sync {
 __device__ __forceinline__ void publish_stats(PairStats st, uint32_t *red) {
     uint32_t mx = max(st.mx & 0xffffu, st.mx >> 16);
     uint32_t mn = min(st.mnm1 & 0xffffu, st.mnm1 >> 16);
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-        mx = max(mx, (uint32_t)__shfl_xor((int)mx, m));
-        mn = min(mn, (uint32_t)__shfl_xor((int)mn, m));
-    }
+    mx = wave_reduce64(mx, [](uint32_t a, uint32_t b) { return max(a, b); });
+    mn = wave_reduce64(mn, [](uint32_t a, uint32_t b) { return min(a, b); });
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     if (lane == 0 && w < 4) {
         red[w] = mx;
@@ -1078,8 +1074,7 @@ __device__ __forceinline__ float chain_rows(const float *part) {
             if (4 * i + 3 < BL::NB2) acc = acc + v[i].w;
         }
     }
-    const float s = acc + __shfl_xor(acc, 1);
-    return s + __shfl_xor(s, 2);
+    return quad_sum(acc);  // (lo + hi) per parity, then the two parities
 }
 
 template <int N>
