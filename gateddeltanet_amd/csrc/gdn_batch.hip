@@ -25,7 +25,7 @@
 // Per layer (8 launches):
 //   k_bgemm<QKVG>  q,k,v,g rows; epilogue: BF16 rounding, conv + SiLU with
 //                  each stream's tails, gate and sigmoid(gate)
-//   k_brecur       the recurrence per (head, stream), state in registers
+//   k_brecur       the recurrence per (head, stream, 128 columns), state in registers
 //   k_bonorm       per (head, stream) output RMSNorm * gate -> X
 //   k_bgemm<STORE> o_proj -> y (BF16)
 //   k_bnorm        h = R(h + y), MLP RMSNorm -> X
@@ -53,6 +53,7 @@ namespace bt {
 
 constexpr int kMaxB = GDN_MAX_STREAMS;  // streams = the 64 B-operand columns
 static_assert(kMaxB == 64, "four 16-stream groups per MFMA B operand");
+constexpr int kRecCols = 128;  // state columns per multi-stream recurrence workgroup
 constexpr int kScanCols = 4;  // state columns per prefill-scan workgroup
 constexpr int kSplitO = 4;              // K splits of o_proj (16 k tiles each)
 constexpr int kSplitDown = 11;          // K splits of the down projection (16 k tiles each)
@@ -551,22 +552,29 @@ __global__ __launch_bounds__(kT) void k_bonorm(const float *__restrict__ attn, c
     if (t < kHD / 8) store_x8(x_out, m, h * kHD + 8 * t, xs + 8 * t);
 }
 
-// The recurrence of one (head, stream) per workgroup of 512 threads, with
-// the batch-1 arithmetic (gdn_island_prep / read / update,
-// gdn_model.cpp:2376-2933).  Wave w owns state column 64 (w % 4) + lane and
-// rows 128 (w / 4) .. + 127, held in registers from load to store: waves 0-3
-// run the r and p chains over rows 0..127, hand the partial sums to waves
-// 4-7 through LDS, which continue over rows 128..255 (the chain order is
+// The recurrence of one (head, stream, CW-column group) per workgroup of
+// 2 CW threads, with the batch-1 arithmetic (gdn_island_prep / read /
+// update, gdn_model.cpp:2376-2933).  Wave w owns state column
+// c0 + 64 (w % (CW / 64)) + lane and rows 128 (w / (CW / 64)) .. + 127,
+// held in registers from load to store: the first half of the waves run
+// the r and p chains over rows 0..127, hand the partial sums to the second
+// half through LDS, which continue over rows 128..255 (the chain order is
 // j = 0..255 as in the reference) and form delta and o; every wave then
 // writes its rows of S' = decay * S + kn (x) delta.  The q/k norms and alpha
-// use the batch-1 tree order (four wave butterflies, (w0 + w1) + (w2 + w3)).
-__global__ __launch_bounds__(2 * kT) void k_brecur(const float *__restrict__ qkv, const float *__restrict__ bd,
+// use the batch-1 tree order; every column group of a head computes them.
+// 128-column groups (256 threads) leave room for three workgroups per CU,
+// so one group's stores overlap another's loads.
+template <int CW>
+__global__ __launch_bounds__(2 * CW) void k_brecur(const float *__restrict__ qkv, const float *__restrict__ bd,
                                                    float *__restrict__ state, float *__restrict__ attn) {
-    constexpr int RH = kHD / 2;  // rows per wave
-    __shared__ float qn[kHD], kn[kHD], rpart[kHD], ppart[kHD], dl[kHD];
+    static_assert(CW == 128 || CW == 256, "column groups of 128 or 256");
+    constexpr int RH = kHD / 2;   // rows per wave
+    constexpr int WPR = CW / 64;  // waves per 128-row half
+    __shared__ float qn[kHD], kn[kHD], rpart[CW], ppart[CW], dl[CW];
     __shared__ float red[8], red2[4];
-    const int h = blockIdx.x, m = blockIdx.y, t = threadIdx.x, w = t >> 6, lane = t & 63;
-    const int col = (w & 3) * 64 + lane, r0 = (w >> 2) * RH;
+    const int cg = blockIdx.x % (kHD / CW), h = blockIdx.x / (kHD / CW), m = blockIdx.y;
+    const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+    const int lc = (w % WPR) * 64 + lane, col = cg * CW + lc, r0 = (w / WPR) * RH;
     const float *qp = qkv + (size_t)m * 3 * kH + h * kHD;
     float *S = state + (size_t)m * kLayerState + (size_t)h * kHD * kHD + col;
     float sv[RH];
@@ -595,19 +603,19 @@ __global__ __launch_bounds__(2 * kT) void k_brecur(const float *__restrict__ qkv
         if (lane == 0) red2[w] = qk;
     }
     __syncthreads();
-    if (w < 4) {
+    if (w < WPR) {
         float r = 0.0f, p = 0.0f;
 #pragma unroll
         for (int j = 0; j < RH; ++j) {
             r = r + sv[j] * kn[j];
             p = p + sv[j] * qn[j];
         }
-        rpart[col] = r;
-        ppart[col] = p;
+        rpart[lc] = r;
+        ppart[lc] = p;
     }
     __syncthreads();
-    if (w >= 4) {
-        float r = rpart[col], p = ppart[col];
+    if (w >= WPR) {
+        float r = rpart[lc], p = ppart[lc];
 #pragma unroll
         for (int j = 0; j < RH; ++j) {
             r = r + sv[j] * kn[RH + j];
@@ -616,11 +624,11 @@ __global__ __launch_bounds__(2 * kT) void k_brecur(const float *__restrict__ qkv
         const float alpha = (red2[0] + red2[1]) + (red2[2] + red2[3]);
         const float delta = beta * (qp[2 * kH + col] - decay * r);
         const float o = 0.0625f * (decay * p + alpha * delta);
-        dl[col] = delta;
+        dl[lc] = delta;
         attn[(size_t)m * kH + h * kHD + col] = rne_bf16(o);
     }
     __syncthreads();
-    const float d = dl[col];
+    const float d = dl[lc];
 #pragma unroll
     for (int j = 0; j < RH; ++j) S[(size_t)(r0 + j) * kHD] = decay * sv[j] + kn[r0 + j] * d;
 }
@@ -1040,7 +1048,8 @@ void launch_qkvg(GDNBatchEngine *e, int l, hipStream_t s) {
                        reinterpret_cast<const u32x4 *>(e->x_h), ep);
 }
 void launch_recur(GDNBatchEngine *e, int l, hipStream_t s) {
-    hipLaunchKernelGGL(k_brecur, dim3(kNH, e->streams), dim3(2 * kT), 0, s, e->qkv, e->bd, b_state(e, l), e->attn);
+    hipLaunchKernelGGL((k_brecur<kRecCols>), dim3(kNH * (kHD / kRecCols), e->streams), dim3(2 * kRecCols), 0, s,
+                       e->qkv, e->bd, b_state(e, l), e->attn);
 }
 void launch_onorm(GDNBatchEngine *e, int l, hipStream_t s) {
     hipLaunchKernelGGL(k_bonorm, dim3(kNH, e->streams), dim3(kT), 0, s, e->attn, e->gate, e->sgate,
