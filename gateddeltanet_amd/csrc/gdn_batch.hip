@@ -56,7 +56,7 @@ static_assert(kMaxB == 64, "four 16-stream groups per MFMA B operand");
 constexpr int kRecCols = 128;  // state columns per multi-stream recurrence workgroup
 constexpr int kScanCols = 4;  // state columns per prefill-scan workgroup
 constexpr int kSplitO = 4;              // K splits of o_proj (16 k tiles each)
-constexpr int kSplitDown = 11;          // K splits of the down projection (16 k tiles each)
+constexpr int kSplitDown = 4;           // K splits of the down projection (44 k tiles each)
 constexpr int kRtO = 2;                 // 16-row tiles per o_proj workgroup
 constexpr int kRtDown = 2;              // 16-row tiles per down workgroup
 constexpr int kKtH = kH / 32;           // k tiles of a K = 2048 projection
