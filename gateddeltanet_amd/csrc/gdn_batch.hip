@@ -59,6 +59,7 @@ constexpr int kSplitO = 4;              // K splits of o_proj (16 k tiles each)
 constexpr int kSplitDown = 4;           // K splits of the down projection (44 k tiles each)
 constexpr int kRtO = 2;                 // 16-row tiles per o_proj workgroup
 constexpr int kRtDown = 2;              // 16-row tiles per down workgroup
+constexpr int kRtGu = 2;                // 16-row tiles per gate/up workgroup (gate/up pairs x 2)
 constexpr int kKtH = kH / 32;           // k tiles of a K = 2048 projection
 constexpr int kKtI = kI / 32;           // k tiles of the down projection
 constexpr size_t kLayerState = (size_t)kNH * kHD * kHD;  // floats per (layer, stream)
@@ -120,7 +121,7 @@ __global__ __launch_bounds__(NW * 64) void k_bgemm(const u32x4 *__restrict__ W, 
                                                    BEpi ep) {
     constexpr int KTS = KT / S, KTW = KTS / NW, GT = NW * 64;
     static_assert(KT % S == 0 && KTS % NW == 0, "whole k tiles per wave");
-    static_assert(EPI != EPI_SWIGLU || RT == 2, "SwiGLU pairs a gate and an up row tile");
+    static_assert(EPI != EPI_SWIGLU || (RT % 2) == 0, "SwiGLU pairs gate and up row tiles");
     static_assert(S == 1 || EPI == EPI_RAW, "split sums leave the GEMM unrounded");
     constexpr int D = KTW < 4 ? KTW : 4;
     constexpr size_t WSTEP = (size_t)NW * RT * 64, XSTEP = (size_t)NW * 4 * 64;
@@ -263,21 +264,24 @@ __global__ __launch_bounds__(NW * 64) void k_bgemm(const u32x4 *__restrict__ W, 
             }
         }
     } else {  // EPI_SWIGLU, gemv32_store SwiGLU branch, gdn_model.cpp:4751-4767
-        // one channel x stream per thread and pass, packed through LDS into
-        // 16-byte stores of eight channels
-        __shared__ __attribute__((aligned(16))) uint16_t hb[64][16];
+        // row tiles 2p and 2p + 1 are the gate and up rows of channels
+        // 16 (RT / 2) rb + 16 p ..; one channel x stream per thread and pass,
+        // packed through LDS into 16-byte stores of eight channels
+        constexpr int NP = RT / 2, CH = 16 * NP;  // pairs, channels per workgroup
+        __shared__ __attribute__((aligned(16))) uint16_t hb[64][CH];
 #pragma unroll
-        for (int q = t; q < 16 * 64; q += GT) {
-            const int cl = q & 15, m = q >> 4;
-            const float g = rne_bf16(reduced1(0, cl >> 2, m, cl & 3)), u = rne_bf16(reduced1(1, cl >> 2, m, cl & 3));
-            hb[m][cl] = (uint16_t)bf16_daz_bits(rne_bf16(silu_ref(g) * u));
+        for (int q = t; q < CH * 64; q += GT) {
+            const int cc = q % CH, m = q / CH, pr = cc >> 4, cl = cc & 15;
+            const float g = rne_bf16(reduced1(2 * pr, cl >> 2, m, cl & 3));
+            const float u = rne_bf16(reduced1(2 * pr + 1, cl >> 2, m, cl & 3));
+            hb[m][cc] = (uint16_t)bf16_daz_bits(rne_bf16(silu_ref(g) * u));
         }
         __syncthreads();
-        if (t < 128) {
-            const int mm = t >> 1, half = t & 1;
+        for (int q = t; q < 64 * (CH / 8); q += GT) {
+            const int mm = q / (CH / 8), g8 = q % (CH / 8);
             if (mm < ep.n_streams)
-                *reinterpret_cast<u32x4 *>(ep.x_next + xt_index(mm, rb * 16 + 8 * half)) =
-                    *reinterpret_cast<const u32x4 *>(&hb[mm][8 * half]);
+                *reinterpret_cast<u32x4 *>(ep.x_next + xt_index(mm, rb * CH + 8 * g8)) =
+                    *reinterpret_cast<const u32x4 *>(&hb[mm][8 * g8]);
         }
     }
     if constexpr (EPI == EPI_LM) {
@@ -926,7 +930,7 @@ int b_upload(GDNBatchEngine *e, const GDNModel *m) {
             std::memcpy(rows.data() + (2 * blk) * 16 * H, g16.data() + blk * 16 * H, 16 * H * 2);
             std::memcpy(rows.data() + (2 * blk + 1) * 16 * H, u16.data() + blk * 16 * H, 16 * H * 2);
         }
-        if (upload_tiled(rows, 2 * I, H, 2, p, e->w_gu[l])) return -1;
+        if (upload_tiled(rows, 2 * I, H, kRtGu, p, e->w_gu[l])) return -1;
         to_bf16(w.mlp_down_proj, H * I, rows);
         if (upload_tiled(rows, H, I, kRtDown, p, e->w_down[l])) return -1;
     }
@@ -1071,7 +1075,7 @@ void launch_gu(GDNBatchEngine *e, int l, hipStream_t s) {
     BEpi ep{};
     ep.n_streams = e->streams;
     ep.x_next = e->x_d;
-    hipLaunchKernelGGL((k_bgemm<2, kKtH, 4, 1, EPI_SWIGLU>), dim3(2 * kI / 32), dim3(kT), 0, s, e->w_gu[l],
+    hipLaunchKernelGGL((k_bgemm<kRtGu, kKtH, 4, 1, EPI_SWIGLU>), dim3(2 * kI / (16 * kRtGu)), dim3(kT), 0, s, e->w_gu[l],
                        reinterpret_cast<const u32x4 *>(e->x_h), ep);
 }
 void launch_down(GDNBatchEngine *e, int l, hipStream_t s) {
@@ -1198,7 +1202,7 @@ void enqueue_prefill_chunk(GDNBatchEngine *e, int slot, int n, bool last, hipStr
         BEpi eg{};
         eg.n_streams = n;
         eg.x_next = e->x_d;
-        hipLaunchKernelGGL((k_bgemm<2, kKtH, 4, 1, EPI_SWIGLU>), dim3(2 * kI / 32), dim3(kT), 0, s, e->w_gu[l],
+        hipLaunchKernelGGL((k_bgemm<kRtGu, kKtH, 4, 1, EPI_SWIGLU>), dim3(2 * kI / (16 * kRtGu)), dim3(kT), 0, s, e->w_gu[l],
                            reinterpret_cast<const u32x4 *>(e->x_h), eg);
         BEpi ed{};
         ed.n_streams = n;
