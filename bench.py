@@ -247,11 +247,11 @@ PER_STREAM = 102_565_120  # state read + write, conv tails, embedding row, logit
 STREAM_KERNEL_BYTES = {  # per launch, per stream where the traffic is per stream
     "recur": 8 * 256 * 256 * 4 * 2,
 }
-# DRAM bytes per recurrence launch at 64 streams (FETCH_SIZE 136.10 MB +
-# WRITE_SIZE 134.74 MB, scaled by a plain copy of known size) from the
-# counter passes summarised in profiles/k_bgemm_gdn13b_64stream_decode.md:
-# 1.009x the 268.4 MB of state it must read and write.
-MEASURED_RECUR_TRAFFIC_64 = 270_840_000
+# DRAM bytes per recurrence launch (k_brecur<128>) at 64 streams (FETCH_SIZE
+# 137.13 MB + WRITE_SIZE 134.74 MB, scaled by a plain copy of known size) from
+# the counter passes summarised in profiles/k_bgemm_gdn13b_64stream_decode.md:
+# 1.013x the 268.4 MB of state it must read and write.
+MEASURED_RECUR_TRAFFIC_64 = 271_876_000
 
 
 def main_streams(args):
