@@ -17,7 +17,7 @@
 // bit; outputs are rounded to BF16 at the same points.
 //
 // Layout.  A projection W [N][K] is stored as MFMA A-operand tiles (16 rows x
-// 32 columns, gdn_tile_bf16).  The activations of all streams enter as the B
+// 32 columns, gdn_tile_bf16; gate/up in k_bgu's 44-row blocks, tile_gu).  The activations of all streams enter as the B
 // operand: X [64 streams][K] BF16 in tiles of 32 columns x 16 streams, lane l
 // holding stream l % 16 and columns 8 (l / 16) .. + 7.  Stream s of a GEMM
 // output is column s of D = W X^T, so streams never mix.
@@ -27,12 +27,13 @@
 //                  each stream's tails, gate and sigmoid(gate)
 //   k_brecur       the recurrence per (head, stream, 128 columns), state in registers
 //   k_bonorm       per (head, stream) output RMSNorm * gate -> X
-//   k_bgemm<STORE> o_proj -> y (BF16)
-//   k_bnorm        h = R(h + y), MLP RMSNorm -> X
-//   k_bgemm<SWIGLU> gate/up row pairs, SwiGLU -> X (K = 5632)
-//   k_bgemm<STORE> down -> y
-//   k_bnorm        h = R(h + y), next attention RMSNorm (or the final norm)
-//                  -> X, with the next layer's a/b rows and beta/decay
+//   k_bgemm<RAW>   o_proj in 4 K splits -> split sums
+//   k_bnorm        h = R(h + R(y)), MLP RMSNorm -> X
+//   k_bgu          gate/up, 22 channels per workgroup, SwiGLU -> X (K = 5632)
+//   k_bgemm<RAW>   down in 4 K splits -> split sums
+//   k_bnorm        h = R(h + R(y)), next attention RMSNorm (or the final norm)
+//                  -> X; with the next layer's a/b rows and beta/decay it runs
+//                  four workgroups per stream, two heads' rows each
 // plus the embedding norm before layer 0, the LM head with a per-workgroup
 // argmax, and the per-stream argmax merge.
 #include <hip/hip_runtime.h>
@@ -59,7 +60,6 @@ constexpr int kSplitO = 4;              // K splits of o_proj (16 k tiles each)
 constexpr int kSplitDown = 4;           // K splits of the down projection (44 k tiles each)
 constexpr int kRtO = 2;                 // 16-row tiles per o_proj workgroup
 constexpr int kRtDown = 2;              // 16-row tiles per down workgroup
-constexpr int kRtGu = 2;                // 16-row tiles per gate/up workgroup (gate/up pairs x 2)
 constexpr int kKtH = kH / 32;           // k tiles of a K = 2048 projection
 constexpr int kKtI = kI / 32;           // k tiles of the down projection
 constexpr size_t kLayerState = (size_t)kNH * kHD * kHD;  // floats per (layer, stream)
@@ -67,7 +67,7 @@ constexpr size_t kStreamTails = (size_t)3 * 3 * kH;      // floats per (layer, s
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-enum { EPI_RAW = 0, EPI_STORE = 1, EPI_QKVG = 2, EPI_SWIGLU = 3, EPI_LM = 4 };
+enum { EPI_RAW = 0, EPI_STORE = 1, EPI_QKVG = 2, EPI_LM = 4 };
 
 // BF16 bits of a value already at a BF16 rounding point, subnormals flushed
 // to a signed zero (the reference's products treat them as zero).
@@ -103,7 +103,6 @@ struct BEpi {
     float *sgate;        // [64][kH] sigmoid(R(g))
     float *tails;        // this layer's [n_streams][3][3][kH]
     const float *conv_w; // [3][kH][4]
-    uint16_t *x_next;    // EPI_SWIGLU: X tiles of the down projection
     float *logits;       // EPI_LM: [64][N]
     float *part_val;     // [gridDim.x][64]
     int *part_idx;
@@ -121,7 +120,6 @@ __global__ __launch_bounds__(NW * 64) void k_bgemm(const u32x4 *__restrict__ W, 
                                                    BEpi ep) {
     constexpr int KTS = KT / S, KTW = KTS / NW, GT = NW * 64;
     static_assert(KT % S == 0 && KTS % NW == 0, "whole k tiles per wave");
-    static_assert(EPI != EPI_SWIGLU || (RT % 2) == 0, "SwiGLU pairs gate and up row tiles");
     static_assert(S == 1 || EPI == EPI_RAW, "split sums leave the GEMM unrounded");
     constexpr int D = KTW < 4 ? KTW : 4;
     constexpr size_t WSTEP = (size_t)NW * RT * 64, XSTEP = (size_t)NW * 4 * 64;
@@ -263,26 +261,6 @@ __global__ __launch_bounds__(NW * 64) void k_bgemm(const u32x4 *__restrict__ W, 
                 ep.sgate[(size_t)m * kH + c] = sigmoid_ref(raw);
             }
         }
-    } else {  // EPI_SWIGLU, gemv32_store SwiGLU branch, gdn_model.cpp:4751-4767
-        // row tiles 2p and 2p + 1 are the gate and up rows of channels
-        // 16 (RT / 2) rb + 16 p ..; one channel x stream per thread and pass,
-        // packed through LDS into 16-byte stores of eight channels
-        constexpr int NP = RT / 2, CH = 16 * NP;  // pairs, channels per workgroup
-        __shared__ __attribute__((aligned(16))) uint16_t hb[64][CH];
-#pragma unroll
-        for (int q = t; q < CH * 64; q += GT) {
-            const int cc = q % CH, m = q / CH, pr = cc >> 4, cl = cc & 15;
-            const float g = rne_bf16(reduced1(2 * pr, cl >> 2, m, cl & 3));
-            const float u = rne_bf16(reduced1(2 * pr + 1, cl >> 2, m, cl & 3));
-            hb[m][cc] = (uint16_t)bf16_daz_bits(rne_bf16(silu_ref(g) * u));
-        }
-        __syncthreads();
-        for (int q = t; q < 64 * (CH / 8); q += GT) {
-            const int mm = q / (CH / 8), g8 = q % (CH / 8);
-            if (mm < ep.n_streams)
-                *reinterpret_cast<u32x4 *>(ep.x_next + xt_index(mm, rb * CH + 8 * g8)) =
-                    *reinterpret_cast<const u32x4 *>(&hb[mm][8 * g8]);
-        }
     }
     if constexpr (EPI == EPI_LM) {
         __syncthreads();
@@ -300,6 +278,111 @@ __global__ __launch_bounds__(NW * 64) void k_bgemm(const u32x4 *__restrict__ W, 
             ep.part_val[(size_t)rb * 64 + t] = best;
             ep.part_idx[(size_t)rb * 64 + t] = idx;
         }
+    }
+}
+
+// ------------------------------------------------------------ gate/up
+//
+// 5632 channels over 256 workgroups, one per CU: workgroup b owns channels
+// 22 b .. 22 b + 21, i.e. 44 rows in three row tiles: the gate rows of its
+// first 16 channels, their up rows, and a 12-row tile with the gate then the
+// up rows of the last 6 (rows 12..15 of that tile stay zero).  Whole 16-row
+// pairs (32 rows per workgroup) give 352 workgroups, i.e. two on some CUs,
+// and every workgroup reads all 64 streams' activations beside its rows.
+constexpr int kGuCh = 22;                // channels per gate/up workgroup
+constexpr int kGuWgs = kI / kGuCh;       // 256
+constexpr int kGuTail2 = 2 * (kGuCh - 16);     // rows of the third tile (12)
+constexpr int kGuTileU4 = 128 + 4 * kGuTail2;  // 16-byte entries per k tile
+constexpr int kGuWaves = 4;                    // waves per gate/up workgroup
+static_assert(kGuWgs * kGuCh == kI && kGuCh > 16 && kGuCh <= 24 && (kGuCh % 2) == 0, "gate/up split");
+
+// One k tile of the layout: tile 0 lane l = (row l % 16, columns 8 (l / 16)..),
+// tile 1 likewise, the 12-row tile's entry (quarter kq, row r) at 128 + kq * 12 + r.
+// The NW waves split the 64 k tiles as k_bgemm's do (wave w: w, w + NW, ...)
+// and the per-wave sums are added in wave order, so each channel's sums are
+// those of k_bgemm's 16-channel pairing with the same NW.
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void k_bgu(const u32x4 *__restrict__ W, const u32x4 *__restrict__ X,
+                                                 uint16_t *__restrict__ x_next, int n_streams) {
+    constexpr int RT = 3, KT = kKtH, KTW = KT / NW, GT = NW * 64;
+    static_assert(KT % NW == 0, "whole k tiles per wave");
+    constexpr int D = KTW < 4 ? KTW : 4;
+    constexpr size_t WSTEP = (size_t)NW * kGuTileU4, XSTEP = (size_t)NW * 4 * 64;
+    __shared__ f32x4 red[NW * RT * 4 * 64];
+    const int t = threadIdx.x, w = t >> 6, l = t & 63, rb = blockIdx.x;
+    // the 12-row tile: lanes of rows 12..15 read entry 0 (in bounds) and
+    // zero it
+    const bool p2 = (l & 15) < kGuTail2;
+    const int o2 = 128 + (p2 ? (l >> 4) * kGuTail2 + (l & 15) : 0);
+    const u32x4 *wp = W + ((size_t)rb * KT + w) * kGuTileU4;
+    const u32x4 *xp = X + (size_t)w * (4 * 64) + l;
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+
+    f32x4 acc[RT][4];
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) acc[r][g] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    u32x4 a[D][RT], b[D][4];
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+        a[i][0] = wp[i * WSTEP + l];
+        a[i][1] = wp[i * WSTEP + 64 + l];
+        a[i][2] = wp[i * WSTEP + o2];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) b[i][g] = xp[i * XSTEP + g * 64];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < KTW; ++i) {
+        const int s = i % D;
+        if (!p2) a[s][2] = zero;
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                acc[r][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[s][r]),
+                                                                    __builtin_bit_cast(bf16x8, b[s][g]),
+                                                                    acc[r][g], 0, 0, 0);
+        if (i + D < KTW) {
+            a[s][0] = wp[(i + D) * WSTEP + l];
+            a[s][1] = wp[(i + D) * WSTEP + 64 + l];
+            a[s][2] = wp[(i + D) * WSTEP + o2];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) b[s][g] = xp[(i + D) * XSTEP + g * 64];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) red[((w * RT + r) * 4 + g) * 64 + l] = acc[r][g];
+    __syncthreads();
+
+    // row rr of tile r, stream m: lane (rr / 4) * 16 + m % 16 of stream
+    // group m / 16, component rr % 4; waves added in order
+    auto val = [&](int r, int rr, int m) {
+        const float *rf =
+            reinterpret_cast<const float *>(red) + 4 * ((r * 4 + (m >> 4)) * 64 + (rr >> 2) * 16 + (m & 15)) + (rr & 3);
+        float v = rf[0];
+#pragma unroll
+        for (int ww = 1; ww < NW; ++ww) v = v + rf[4 * ww * RT * 4 * 64];
+        return v;
+    };
+    // gemv32_store SwiGLU branch, gdn_model.cpp:4751-4767; two channels per
+    // thread and pass, one 4-byte store (22 b is even)
+    for (int q = t; q < 64 * (kGuCh / 2); q += GT) {
+        const int m = q / (kGuCh / 2), cp = q - m * (kGuCh / 2);
+        if (m >= n_streams) continue;
+        uint32_t packed = 0;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int cc = 2 * cp + e;
+            const float g = rne_bf16(cc < 16 ? val(0, cc, m) : val(2, cc - 16, m));
+            const float u = rne_bf16(cc < 16 ? val(1, cc, m) : val(2, cc - 16 + (kGuCh - 16), m));
+            packed |= bf16_daz_bits(rne_bf16(silu_ref(g) * u)) << (16 * e);
+        }
+        *reinterpret_cast<uint32_t *>(x_next + xt_index(m, rb * kGuCh + 2 * cp)) = packed;
     }
 }
 
@@ -348,7 +431,8 @@ __global__ __launch_bounds__(kT) void k_bargmax(const float *__restrict__ part_v
 // ------------------------------------------------------ per-stream kernels
 
 struct BNorm {
-    float *h;              // [64][kH] residual stream, updated in place
+    const float *h_in;     // [64][kH] residual stream
+    float *h_out;          // h_in, or (AB, several workgroups per stream) the other residual buffer
     const float *y;        // [splits][64][kH] partial sums: h = R(h + R(sum)) first
     const uint16_t *emb;   // embedding rows (BF16): h = R(emb[tok[m]]) (EMBED)
     const int *tok;
@@ -362,23 +446,32 @@ struct BNorm {
     float eps;
 };
 
-// One workgroup per stream: the residual add (or embedding import), the
-// RMSNorm in chunk order (gdn_rmsnorm_rows_bf16 / gdn_residual_rmsnorm_bf16,
+// Per stream: the residual add (or embedding import), the RMSNorm in chunk
+// order (gdn_rmsnorm_rows_bf16 / gdn_residual_rmsnorm_bf16,
 // gdn_model.cpp:1394-1474, :3351-3450) and, before an attention block, the
 // tiny a/b rows and beta/decay (gdn_gemv_tiny_ab :1501-1536, :2461-2465).
 // Thread t holds elements 8t..8t+7; a 16-element chunk is the sequential sum
 // of thread 2c's eight squares continued by thread 2c + 1.  SPLITS partial
 // sums of the preceding projection are added in split order (0: no residual
-// add; EMBED: the embedding row instead).  The a/b rows are requested
-// before the norm's first wait on memory.
+// add; EMBED: the embedding row instead).  Without AB one workgroup per
+// stream updates the residual in place.  With AB, grid (streams, kAbSplit):
+// workgroup j repeats the norm and runs the a/b rows of heads
+// kNH / kAbSplit * j .. (a 32 KB slice of the 128 KB of rows, requested
+// before the norm's first wait on memory); workgroup 0 alone writes the
+// residual, to h_out != h_in, and the X tiles.
+constexpr int kAbSplit = 4;
+constexpr int kAbHeads = kNH / kAbSplit;  // heads per a/b workgroup
 template <int SPLITS, bool EMBED, bool AB>
 __global__ __launch_bounds__(kT) void k_bnorm(BNorm p) {
+    constexpr int ABR = 2 * kAbHeads;  // a/b rows per workgroup: a rows, then b rows
     __shared__ __attribute__((aligned(16))) float xs[kH];
     __shared__ __attribute__((aligned(16))) float cs[kH / 16];
-    __shared__ __attribute__((aligned(16))) float tab[16][64][2];
-    __shared__ float abv[16];
+    __shared__ __attribute__((aligned(16))) float tab[ABR][64][2];
+    __shared__ float abv[ABR];
     __shared__ float scale_s;
     const int m = blockIdx.x, t = threadIdx.x, e0 = 8 * t;
+    const int j = AB ? (int)blockIdx.y : 0;
+    const bool writer = j == 0;
     const f32x4 *w4 = reinterpret_cast<const f32x4 *>(p.w + e0);
     const f32x4 wa = w4[0], wb = w4[1];
     float hv[8];
@@ -391,7 +484,7 @@ __global__ __launch_bounds__(kT) void k_bnorm(BNorm p) {
             hv[2 * j + 1] = rne_bf16(u2f(wv[j] & 0xffff0000u));
         }
     } else {
-        const f32x4 *h4 = reinterpret_cast<const f32x4 *>(p.h + (size_t)m * kH + e0);
+        const f32x4 *h4 = reinterpret_cast<const f32x4 *>(p.h_in + (size_t)m * kH + e0);
         const f32x4 a0 = h4[0], a1 = h4[1];
         hv[0] = a0.x; hv[1] = a0.y; hv[2] = a0.z; hv[3] = a0.w;
         hv[4] = a1.x; hv[5] = a1.y; hv[6] = a1.z; hv[7] = a1.w;
@@ -417,17 +510,21 @@ __global__ __launch_bounds__(kT) void k_bnorm(BNorm p) {
     }
     // the a/b rows are requested behind the operands of the norm (loads
     // return in order)
-    constexpr int ABN = AB ? 32 : 1;
+    // local row r: a row of head kAbHeads j + r (r < kAbHeads), else the b
+    // row of head kAbHeads j + r - kAbHeads
+    auto ab_row = [&](int r) { return r < kAbHeads ? kAbHeads * j + r : kNH + kAbHeads * j + r - kAbHeads; };
+    constexpr int ABN = AB ? ABR * kH / (4 * kT) : 1;
     f32x4 wq[ABN];
     if constexpr (AB) {
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
+        for (int i = 0; i < ABN; ++i) {
             const int q = t + kT * i, grp = q >> 3, sub = q & 7;
-            wq[i] = *reinterpret_cast<const f32x4 *>(p.ab_w + (size_t)(grp >> 6) * kH + 32 * (grp & 63) + 4 * sub);
+            wq[i] = *reinterpret_cast<const f32x4 *>(p.ab_w + (size_t)ab_row(grp >> 6) * kH + 32 * (grp & 63) +
+                                                     4 * sub);
         }
     }
-    if constexpr (EMBED || SPLITS > 0) {
-        f32x4 *d = reinterpret_cast<f32x4 *>(p.h + (size_t)m * kH + e0);
+    if ((EMBED || SPLITS > 0) && writer) {
+        f32x4 *d = reinterpret_cast<f32x4 *>(p.h_out + (size_t)m * kH + e0);
         d[0] = (f32x4){hv[0], hv[1], hv[2], hv[3]};
         d[1] = (f32x4){hv[4], hv[5], hv[6], hv[7]};
     }
@@ -465,8 +562,8 @@ __global__ __launch_bounds__(kT) void k_bnorm(BNorm p) {
     float xv[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) xv[e] = rne_bf16(hv[e] * sc * wv[e]);
-    store_x8(p.x_out, m, e0, xv);
-    if (p.xn_out) {
+    if (writer) store_x8(p.x_out, m, e0, xv);
+    if (p.xn_out && writer) {
         f32x4 *d = reinterpret_cast<f32x4 *>(p.xn_out + (size_t)m * kH + e0);
         d[0] = (f32x4){xv[0], xv[1], xv[2], xv[3]};
         d[1] = (f32x4){xv[4], xv[5], xv[6], xv[7]};
@@ -478,13 +575,12 @@ __global__ __launch_bounds__(kT) void k_bnorm(BNorm p) {
             d[1] = (f32x4){xv[4], xv[5], xv[6], xv[7]};
         }
         __syncthreads();
-        // rows 0..7 = a heads, 8..15 = b heads.  Eight lanes per (row,
-        // 32-column beat), four products each: lanes 0-3 form tree16 of the
-        // lower half, lanes 4-7 of the upper (pairs, then lane pairs, then
-        // lane quads), so a wave's loads cover eight consecutive beats of one
-        // row.
+        // Eight lanes per (local row, 32-column beat), four products each:
+        // lanes 0-3 form tree16 of the lower half, lanes 4-7 of the upper
+        // (pairs, then lane pairs, then lane quads), so a wave's loads cover
+        // eight consecutive beats of one row.
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
+        for (int i = 0; i < ABN; ++i) {
             const int q = t + kT * i, grp = q >> 3, sub = q & 7;
             const f32x4 xq = *reinterpret_cast<const f32x4 *>(xs + 32 * (grp & 63) + 4 * sub);
             const f32x4 w = wq[i];
@@ -493,7 +589,7 @@ __global__ __launch_bounds__(kT) void k_bnorm(BNorm p) {
             if ((sub & 3) == 0) tab[grp >> 6][grp & 63][sub >> 2] = s;
         }
         __syncthreads();
-        if (t < 16) {
+        if (t < ABR) {
             float v[128];
 #pragma unroll
             for (int i = 0; i < 32; ++i) {
@@ -509,11 +605,12 @@ __global__ __launch_bounds__(kT) void k_bnorm(BNorm p) {
             abv[t] = rne_bf16(acc);
         }
         __syncthreads();
-        if (t < kNH) {
+        if (t < kAbHeads) {
+            const int hd = kAbHeads * j + t;
             float beta, decay;
-            head_scalars(abv[t], abv[kNH + t], p.a_log[t], p.dt_bias[t], beta, decay);
-            p.bd[m * 16 + 2 * t] = beta;
-            p.bd[m * 16 + 2 * t + 1] = decay;
+            head_scalars(abv[t], abv[kAbHeads + t], p.a_log[hd], p.dt_bias[hd], beta, decay);
+            p.bd[m * 16 + 2 * hd] = beta;
+            p.bd[m * 16 + 2 * hd + 1] = decay;
         }
     }
 }
@@ -903,6 +1000,32 @@ int upload_tiled(const std::vector<uint16_t> &rows, size_t n_rows, size_t k, int
     return 0;
 }
 
+// Gate [kI][kH] and up [kI][kH] BF16 rows in k_bgu's layout: per workgroup b
+// and k tile, gate rows 22 b .. + 15 and up rows 22 b .. + 15 as A-operand
+// tiles, then the 12-row tile (gate rows 22 b + 16 .. + 21, up rows likewise)
+// as (quarter, row) entries.
+void tile_gu(const uint16_t *g, const uint16_t *u, uint16_t *dst) {
+    const size_t K = kH;
+#pragma omp parallel for schedule(static)
+    for (int b = 0; b < kGuWgs; ++b)
+        for (int kt = 0; kt < kKtH; ++kt) {
+            uint16_t *tile = dst + ((size_t)b * kKtH + kt) * kGuTileU4 * 8;
+            const size_t col = (size_t)kt * 32;
+            for (int l = 0; l < 64; ++l) {
+                const size_t ch = (size_t)b * kGuCh + l % 16, c8 = col + 8 * (l / 16);
+                std::memcpy(tile + l * 8, g + ch * K + c8, 16);
+                std::memcpy(tile + (64 + l) * 8, u + ch * K + c8, 16);
+            }
+            constexpr int kTail = kGuCh - 16;
+            for (int kq = 0; kq < 4; ++kq)
+                for (int r = 0; r < kGuTail2; ++r) {
+                    const size_t ch = (size_t)b * kGuCh + 16 + (r % kTail);
+                    std::memcpy(tile + (128 + kq * kGuTail2 + r) * 8, (r < kTail ? g : u) + ch * K + col + 8 * kq,
+                                16);
+                }
+        }
+}
+
 int b_upload(GDNBatchEngine *e, const GDNModel *m) {
     const size_t H = kH, I = kI, V = (size_t)e->vocab, L = (size_t)e->layers;
     const size_t per_layer = 4 * H * H + H * H + 2 * I * H + H * I;
@@ -920,17 +1043,14 @@ int b_upload(GDNBatchEngine *e, const GDNModel *m) {
         if (upload_tiled(rows, 4 * H, H, 2, p, e->w_qkvg[l])) return -1;
         to_bf16(w.o_proj, H * H, rows);
         if (upload_tiled(rows, H, H, kRtO, p, e->w_o[l])) return -1;
-        // gate rows c..c+15 then up rows c..c+15: one SwiGLU row pair per
-        // workgroup row block
         std::vector<uint16_t> g16, u16;
         to_bf16(w.mlp_gate_proj, I * H, g16);
         to_bf16(w.mlp_up_proj, I * H, u16);
         rows.resize(2 * I * H);
-        for (size_t blk = 0; blk < I / 16; ++blk) {
-            std::memcpy(rows.data() + (2 * blk) * 16 * H, g16.data() + blk * 16 * H, 16 * H * 2);
-            std::memcpy(rows.data() + (2 * blk + 1) * 16 * H, u16.data() + blk * 16 * H, 16 * H * 2);
-        }
-        if (upload_tiled(rows, 2 * I, H, kRtGu, p, e->w_gu[l])) return -1;
+        tile_gu(g16.data(), u16.data(), rows.data());
+        GDN_HIP(hipMemcpy(p, rows.data(), rows.size() * 2, hipMemcpyHostToDevice));
+        e->w_gu[l] = reinterpret_cast<const u32x4 *>(p);
+        p += rows.size() * 2;
         to_bf16(w.mlp_down_proj, H * I, rows);
         if (upload_tiled(rows, H, I, kRtDown, p, e->w_down[l])) return -1;
     }
@@ -974,11 +1094,11 @@ int b_alloc(GDNBatchEngine *e) {
     GDN_HIP(hipMalloc(&e->tails, L * B * kStreamTails * 4));
     GDN_HIP(hipMemset(e->tails, 0, L * B * kStreamTails * 4));
     const size_t G = (size_t)lm_wgs(e);
-    const size_t act = kMaxB * (kH + 3 * kH + kH + kH + 16 + kH + kSplitDown * kH + kH + V) + G * kMaxB;
+    const size_t act = kMaxB * (2 * kH + 3 * kH + kH + kH + 16 + kH + kSplitDown * kH + kH + V) + G * kMaxB;
     GDN_HIP(hipMalloc(&e->act, act * 4));
     GDN_HIP(hipMemset(e->act, 0, act * 4));
     float *p = e->act;
-    e->h = p; p += kMaxB * kH;
+    e->h = p; p += 2 * kMaxB * kH;  // residual ping-pong (layer parity)
     e->qkv = p; p += kMaxB * 3 * kH;
     e->gate = p; p += kMaxB * kH;
     e->sgate = p; p += kMaxB * kH;
@@ -1013,9 +1133,16 @@ int b_alloc(GDNBatchEngine *e) {
     return 0;
 }
 
-BNorm bnorm(GDNBatchEngine *e, const float *y, const float *w, uint16_t *x_out, int ab_layer) {
+// The residual entering layer l's attention block lives in buffer l & 1: the
+// MLP norm updates it in place and the split a/b norm after the down
+// projection writes the next layer's buffer.
+float *b_resid(GDNBatchEngine *e, int l) { return e->h + (size_t)(l & 1) * kMaxB * kH; }
+
+BNorm bnorm(GDNBatchEngine *e, const float *y, const float *w, uint16_t *x_out, int ab_layer, int l_in,
+            int l_out) {
     BNorm p{};
-    p.h = e->h;
+    p.h_in = b_resid(e, l_in);
+    p.h_out = b_resid(e, l_out);
     p.y = y;
     p.w = w;
     p.x_out = x_out;
@@ -1034,10 +1161,10 @@ BNorm bnorm(GDNBatchEngine *e, const float *y, const float *w, uint16_t *x_out, 
 enum { KB_EMBED, KB_QKVG, KB_RECUR, KB_ONORM, KB_O, KB_NORM, KB_GU, KB_DOWN, KB_LM, KB_ARGMAX, KB_KINDS };
 
 void launch_embed(GDNBatchEngine *e, hipStream_t s) {
-    BNorm p = bnorm(e, nullptr, b_aux(e, 0) + kAuxAttnNorm, e->x_h, 0);
+    BNorm p = bnorm(e, nullptr, b_aux(e, 0) + kAuxAttnNorm, e->x_h, 0, 0, 0);
     p.emb = e->emb;
     p.tok = e->tok_dev;
-    hipLaunchKernelGGL((k_bnorm<0, true, true>), dim3(e->streams), dim3(kT), 0, s, p);
+    hipLaunchKernelGGL((k_bnorm<0, true, true>), dim3(e->streams, kAbSplit), dim3(kT), 0, s, p);
 }
 void launch_qkvg(GDNBatchEngine *e, int l, hipStream_t s) {
     BEpi ep{};
@@ -1068,15 +1195,12 @@ void launch_o(GDNBatchEngine *e, int l, hipStream_t s) {
                        e->w_o[l], reinterpret_cast<const u32x4 *>(e->x_o), ep);
 }
 void launch_mlp_norm(GDNBatchEngine *e, int l, hipStream_t s) {
-    const BNorm p = bnorm(e, e->ypart, b_aux(e, l) + kAuxMlpNorm, e->x_h, -1);
+    const BNorm p = bnorm(e, e->ypart, b_aux(e, l) + kAuxMlpNorm, e->x_h, -1, l, l);
     hipLaunchKernelGGL((k_bnorm<kSplitO, false, false>), dim3(e->streams), dim3(kT), 0, s, p);
 }
 void launch_gu(GDNBatchEngine *e, int l, hipStream_t s) {
-    BEpi ep{};
-    ep.n_streams = e->streams;
-    ep.x_next = e->x_d;
-    hipLaunchKernelGGL((k_bgemm<kRtGu, kKtH, 4, 1, EPI_SWIGLU>), dim3(2 * kI / (16 * kRtGu)), dim3(kT), 0, s, e->w_gu[l],
-                       reinterpret_cast<const u32x4 *>(e->x_h), ep);
+    hipLaunchKernelGGL(k_bgu<kGuWaves>, dim3(kGuWgs), dim3(kGuWaves * 64), 0, s, e->w_gu[l],
+                       reinterpret_cast<const u32x4 *>(e->x_h), e->x_d, e->streams);
 }
 void launch_down(GDNBatchEngine *e, int l, hipStream_t s) {
     BEpi ep{};
@@ -1090,10 +1214,10 @@ void launch_down(GDNBatchEngine *e, int l, hipStream_t s) {
 // attention norm with its a/b rows, or the final norm.
 void launch_layer_norm(GDNBatchEngine *e, int l, hipStream_t s) {
     if (l + 1 < e->layers) {
-        const BNorm p = bnorm(e, e->ypart, b_aux(e, l + 1) + kAuxAttnNorm, e->x_h, l + 1);
-        hipLaunchKernelGGL((k_bnorm<kSplitDown, false, true>), dim3(e->streams), dim3(kT), 0, s, p);
+        const BNorm p = bnorm(e, e->ypart, b_aux(e, l + 1) + kAuxAttnNorm, e->x_h, l + 1, l, l + 1);
+        hipLaunchKernelGGL((k_bnorm<kSplitDown, false, true>), dim3(e->streams, kAbSplit), dim3(kT), 0, s, p);
     } else {
-        BNorm p = bnorm(e, e->ypart, e->aux + (size_t)e->layers * kAuxLayer, e->x_h, -1);
+        BNorm p = bnorm(e, e->ypart, e->aux + (size_t)e->layers * kAuxLayer, e->x_h, -1, l, l);
         p.xn_out = e->xn;
         hipLaunchKernelGGL((k_bnorm<kSplitDown, false, false>), dim3(e->streams), dim3(kT), 0, s, p);
     }
@@ -1170,10 +1294,10 @@ int b_run_step(GDNBatchEngine *e, const int32_t *tokens, int32_t *next, float *i
 // `slot`'s state: the step's kernels with the tokens as the streams, the
 // conv over the chunk (k_pconv) and the in-order recurrence (k_pqk, k_pscan).
 void enqueue_prefill_chunk(GDNBatchEngine *e, int slot, int n, bool last, hipStream_t s) {
-    BNorm p0 = bnorm(e, nullptr, b_aux(e, 0) + kAuxAttnNorm, e->x_h, 0);
+    BNorm p0 = bnorm(e, nullptr, b_aux(e, 0) + kAuxAttnNorm, e->x_h, 0, 0, 0);
     p0.emb = e->emb;
     p0.tok = e->tok_dev;
-    hipLaunchKernelGGL((k_bnorm<0, true, true>), dim3(n), dim3(kT), 0, s, p0);
+    hipLaunchKernelGGL((k_bnorm<0, true, true>), dim3(n, kAbSplit), dim3(kT), 0, s, p0);
     for (int l = 0; l < e->layers; ++l) {
         float *st = b_state(e, l) + (size_t)slot * kLayerState;
         float *tl = b_tails(e, l) + (size_t)slot * kStreamTails;
@@ -1197,13 +1321,10 @@ void enqueue_prefill_chunk(GDNBatchEngine *e, int slot, int n, bool last, hipStr
         eo.y = e->ypart;
         hipLaunchKernelGGL((k_bgemm<kRtO, kKtH, 4, kSplitO, EPI_RAW>), dim3(kH / (16 * kRtO), kSplitO), dim3(kT), 0,
                            s, e->w_o[l], reinterpret_cast<const u32x4 *>(e->x_o), eo);
-        const BNorm pm = bnorm(e, e->ypart, b_aux(e, l) + kAuxMlpNorm, e->x_h, -1);
+        const BNorm pm = bnorm(e, e->ypart, b_aux(e, l) + kAuxMlpNorm, e->x_h, -1, l, l);
         hipLaunchKernelGGL((k_bnorm<kSplitO, false, false>), dim3(n), dim3(kT), 0, s, pm);
-        BEpi eg{};
-        eg.n_streams = n;
-        eg.x_next = e->x_d;
-        hipLaunchKernelGGL((k_bgemm<kRtGu, kKtH, 4, 1, EPI_SWIGLU>), dim3(2 * kI / (16 * kRtGu)), dim3(kT), 0, s, e->w_gu[l],
-                           reinterpret_cast<const u32x4 *>(e->x_h), eg);
+        hipLaunchKernelGGL(k_bgu<kGuWaves>, dim3(kGuWgs), dim3(kGuWaves * 64), 0, s, e->w_gu[l],
+                           reinterpret_cast<const u32x4 *>(e->x_h), e->x_d, n);
         BEpi ed{};
         ed.n_streams = n;
         ed.n_rows = kH;
@@ -1211,10 +1332,10 @@ void enqueue_prefill_chunk(GDNBatchEngine *e, int slot, int n, bool last, hipStr
         hipLaunchKernelGGL((k_bgemm<kRtDown, kKtI, 4, kSplitDown, EPI_RAW>), dim3(kH / (16 * kRtDown), kSplitDown),
                            dim3(kT), 0, s, e->w_down[l], reinterpret_cast<const u32x4 *>(e->x_d), ed);
         if (l + 1 < e->layers) {
-            const BNorm pa = bnorm(e, e->ypart, b_aux(e, l + 1) + kAuxAttnNorm, e->x_h, l + 1);
-            hipLaunchKernelGGL((k_bnorm<kSplitDown, false, true>), dim3(n), dim3(kT), 0, s, pa);
+            const BNorm pa = bnorm(e, e->ypart, b_aux(e, l + 1) + kAuxAttnNorm, e->x_h, l + 1, l, l + 1);
+            hipLaunchKernelGGL((k_bnorm<kSplitDown, false, true>), dim3(n, kAbSplit), dim3(kT), 0, s, pa);
         } else {
-            BNorm pf = bnorm(e, e->ypart, e->aux + (size_t)e->layers * kAuxLayer, e->x_h, -1);
+            BNorm pf = bnorm(e, e->ypart, e->aux + (size_t)e->layers * kAuxLayer, e->x_h, -1, l, l);
             pf.xn_out = e->p_xn;
             hipLaunchKernelGGL((k_bnorm<kSplitDown, false, false>), dim3(n), dim3(kT), 0, s, pf);
         }
