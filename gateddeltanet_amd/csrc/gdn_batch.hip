@@ -55,7 +55,6 @@ namespace bt {
 constexpr int kMaxB = GDN_MAX_STREAMS;  // streams = the 64 B-operand columns
 static_assert(kMaxB == 64, "four 16-stream groups per MFMA B operand");
 constexpr int kRecCols = 128;  // state columns per multi-stream recurrence workgroup
-constexpr int kScanCols = 4;  // state columns per prefill-scan workgroup
 constexpr int kSplitO = 4;              // K splits of o_proj (16 k tiles each)
 constexpr int kSplitDown = 4;           // K splits of the down projection (44 k tiles each)
 constexpr int kRtO = 2;                 // 16-row tiles per o_proj workgroup
@@ -812,113 +811,120 @@ __global__ __launch_bounds__(kT) void k_pqk(const float *__restrict__ qkv, float
     if (t == 0) alpha_out[m * kNH + h] = (red2[0] + red2[1]) + (red2[2] + red2[3]);
 }
 
-// Sequential sum acc = acc + col[j * STRIDE] over 256 rows of one LDS
-// column in row order; the reads run 16 rows ahead of the adds, a fence per
-// block bounding the registers they hold.
-template <int STRIDE>
-__device__ __forceinline__ float column_chain(const float *col) {
-    float acc = 0.0f;
-    float cur[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) cur[j] = col[j * STRIDE];
-#pragma unroll
-    for (int b = 0; b < kHD / 16; ++b) {
-        float nxt[16];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) nxt[j] = (b + 1 < kHD / 16) ? col[(16 * (b + 1) + j) * STRIDE] : 0.0f;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) acc = acc + cur[j];
-        asm volatile("" : "+v"(acc) : : "memory");
-#pragma unroll
-        for (int j = 0; j < 16; ++j) cur[j] = nxt[j];
-    }
-    return acc;
-}
-
-// The recurrence over a chunk's n tokens in order, for one head and CB state
-// columns per workgroup (grid (256 / CB column groups, heads)): columns are
-// independent, so 256 / CB workgroups share a head.  Thread t holds column
-// t % CB of rows t / CB + (256 / CB) j, j < CB, in registers for the whole
-// chunk.  Per token: every thread forms its elements' products
-// S[j][i] * kn[j] and S[j][i] * qn[j] into LDS ([row][column]); lanes 0..CB-1
-// of wave 0 then sum the r column chains and lanes CB..2CB-1 the p chains,
-// each in row order j = 0..255 (the reference's chain order, adds only),
-// while waves 2-3 stage the next token's k and q; every thread forms delta
-// for its column from the two sums and updates its elements, and wave 0
-// writes o.  Narrow tiles keep the per-token products and update short, so
-// the serial chain dominates.
-template <int CB>
+// The recurrence over a chunk's n tokens in order, one wave per pair of
+// state columns and no workgroup barrier inside the token loop: grid
+// (kHD / kScanWgCols, kNH), four independent waves per workgroup (one per
+// SIMD, one workgroup per CU; a wave64 add holds its SIMD whatever its
+// active lanes, so two chain waves on one SIMD would take turns).  Lane l
+// holds rows l + 64 i (i < 4) of the wave's columns c0, c0 + 1 for the
+// whole chunk.  Per token: every lane writes its products S[j][c] * kn[j]
+// and S[j][c] * qn[j] to the wave's LDS rows; lanes 0..3 sum the chains (r
+// of c0, r of c0 + 1, p of c0, p of c0 + 1) in row order j = 0..255 (the
+// reference's chain order, adds only); the four sums and the token's v,
+// beta, decay, alpha (held in lane m) are read across the wave, and every
+// lane forms delta, o and its updated elements.  The chunk's normalised k
+// and q (2 x n x 256 FP32) are staged in LDS once.  Each value is formed
+// as the decode step's k_brecur forms it.
+constexpr int kScanWgCols = 8;  // 4 waves x 2 columns
 __global__ __launch_bounds__(kT) void k_pscan(const float *__restrict__ qkv, const float *__restrict__ qn_all,
-                                              const float *__restrict__ kn_all, const float *__restrict__ alpha_all,
-                                              const float *__restrict__ bd, int n, float *__restrict__ state,
-                                              float *__restrict__ attn) {
-    static_assert(2 * CB <= 64 && (kT % CB) == 0, "both chains of every column in wave 0");
-    constexpr int RS = kT / CB;  // row step between a thread's elements
-    constexpr int NE = kHD / RS; // elements per thread (= CB)
-    // [k|q][row][column]; the q tile starts 16 words on so the r and p chain
-    // lanes of wave 0 read distinct banks
-    constexpr int kQOff = kHD * CB + 16;
-    __shared__ float prod[kQOff + kHD * CB];
-    __shared__ __attribute__((aligned(16))) float kq[2][2][kHD];    // [token parity][k|q][row]
-    __shared__ float rp[2][CB];
-    __shared__ float vs[kMaxB][CB];
-    __shared__ float sc[kMaxB][3];  // beta, decay, alpha
-    const int cg = blockIdx.x, h = blockIdx.y, t = threadIdx.x, w = t >> 6, lane = t & 63;
-    const int c = t % CB, rsub = t / CB, col = cg * CB + c;
-    float *S = state + (size_t)h * kHD * kHD + col;
-    float sv[NE];
+                                               const float *__restrict__ kn_all, const float *__restrict__ alpha_all,
+                                               const float *__restrict__ bd, int n, float *__restrict__ state,
+                                               float *__restrict__ attn) {
+    constexpr int kPad = kHD + 4;  // chain rows 16 bytes apart in bank
+    __shared__ __attribute__((aligned(16))) float kqs[kMaxB][2][kHD];  // [token][k|q][row]
+    __shared__ __attribute__((aligned(16))) float prod[4][4 * kPad];   // [wave][chain][row]
+    const int h = blockIdx.y, t = threadIdx.x, w = t >> 6, lane = t & 63;
+    const int c0 = blockIdx.x * kScanWgCols + 2 * w;
+    for (int i = t; i < n * 2 * (kHD / 4); i += kT) {
+        const int m = i / (2 * (kHD / 4)), rest = i - m * 2 * (kHD / 4), kind = rest / (kHD / 4),
+                  r4 = rest - kind * (kHD / 4);
+        const float *src = (kind == 0 ? kn_all : qn_all) + (size_t)m * kH + h * kHD + 4 * r4;
+        *reinterpret_cast<f32x4 *>(&kqs[m][kind][4 * r4]) = *reinterpret_cast<const f32x4 *>(src);
+    }
+    // lane m < n: token m's v of both columns, beta, decay, alpha
+    float v0 = 0.0f, v1 = 0.0f, beta_l = 0.0f, decay_l = 0.0f, alpha_l = 0.0f;
+    if (lane < n) {
+        const float *vp = qkv + ((size_t)lane * 3 + 2) * kH + h * kHD + c0;
+        v0 = vp[0];
+        v1 = vp[1];
+        beta_l = bd[lane * 16 + 2 * h];
+        decay_l = bd[lane * 16 + 2 * h + 1];
+        alpha_l = alpha_all[lane * kNH + h];
+    }
+    float *S = state + (size_t)h * kHD * kHD + c0;
+    float sv[2][4];
 #pragma unroll
-    for (int j = 0; j < NE; ++j) sv[j] = S[(size_t)(rsub + RS * j) * kHD];
-    for (int i = t; i < n * CB; i += kT) {
-        const int m = i / CB, cc = i % CB;
-        vs[m][cc] = qkv[((size_t)m * 3 + 2) * kH + h * kHD + cg * CB + cc];
+    for (int i = 0; i < 4; ++i) {
+        const float2 s2 = *reinterpret_cast<const float2 *>(S + (size_t)(lane + 64 * i) * kHD);
+        sv[0][i] = s2.x;
+        sv[1][i] = s2.y;
     }
-    if (t < n) {
-        sc[t][0] = bd[t * 16 + 2 * h];
-        sc[t][1] = bd[t * 16 + 2 * h + 1];
-        sc[t][2] = alpha_all[t * kNH + h];
-    }
-    kq[0][0][t] = kn_all[h * kHD + t];
-    kq[0][1][t] = qn_all[h * kHD + t];
     __syncthreads();
+    float *pw = prod[w];
     for (int m = 0; m < n; ++m) {
-        const float *kn = kq[m & 1][0], *qn = kq[m & 1][1];
+        float kn[4], qn[4];
 #pragma unroll
-        for (int j = 0; j < NE; ++j) {
-            const int row = rsub + RS * j;
-            prod[row * CB + c] = sv[j] * kn[row];
-            prod[kQOff + row * CB + c] = sv[j] * qn[row];
+        for (int i = 0; i < 4; ++i) {
+            kn[i] = kqs[m][0][lane + 64 * i];
+            qn[i] = kqs[m][1][lane + 64 * i];
         }
-        __syncthreads();
-        if (w == 0) {
-            if (lane < 2 * CB) {
-                const int which = lane / CB, cc = lane % CB;
-                rp[which][cc] = column_chain<CB>(prod + which * kQOff + cc);
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                pw[e * kPad + lane + 64 * i] = sv[e][i] * kn[i];
+                pw[(2 + e) * kPad + lane + 64 * i] = sv[e][i] * qn[i];
             }
-        } else if (w >= 2 && m + 1 < n) {
-            const int i = t - 128;  // 128 threads stage 512 values
-            const float *src = (i < 64 ? kn_all : qn_all) + (size_t)(m + 1) * kH + h * kHD;
-            float *dst = kq[(m + 1) & 1][i < 64 ? 0 : 1];
-            const int b0 = (i & 63) * 4;
+        // the wave's own LDS writes, then its reads of other lanes' rows
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float acc = 0.0f;
+        if (lane < 4) {
+            const f32x4 *col = reinterpret_cast<const f32x4 *>(pw + lane * kPad);
+            f32x4 cur[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) dst[b0 + e] = src[b0 + e];
+            for (int j = 0; j < 4; ++j) cur[j] = col[j];
+#pragma unroll
+            for (int b = 0; b < kHD / 16; ++b) {
+                f32x4 nxt[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) nxt[j] = (b + 1 < kHD / 16) ? col[4 * (b + 1) + j] : cur[j];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc = (((acc + cur[j].x) + cur[j].y) + cur[j].z) + cur[j].w;
+                asm volatile("" : "+v"(acc) : : "memory");
+#pragma unroll
+                for (int j = 0; j < 4; ++j) cur[j] = nxt[j];
+            }
         }
-        __syncthreads();
-        const float beta = sc[m][0], decay = sc[m][1];
-        const float r = rp[0][c], p = rp[1][c];
-        const float delta = beta * (vs[m][c] - decay * r);
-        if (t < CB) {
-            const float o = 0.0625f * (decay * p + sc[m][2] * delta);
-            attn[(size_t)m * kH + h * kHD + col] = rne_bf16(o);
+        const float ra = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 0));
+        const float rb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 1));
+        const float pa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 2));
+        const float pb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 3));
+        const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_l), m));
+        const float decay = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(decay_l), m));
+        const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_l), m));
+        const float va = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v0), m));
+        const float vb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v1), m));
+        const float da = beta * (va - decay * ra);
+        const float db = beta * (vb - decay * rb);
+        if (lane < 2) {
+            const float o = lane == 0 ? 0.0625f * (decay * pa + alpha * da) : 0.0625f * (decay * pb + alpha * db);
+            attn[(size_t)m * kH + h * kHD + c0 + lane] = rne_bf16(o);
         }
 #pragma unroll
-        for (int j = 0; j < NE; ++j) sv[j] = decay * sv[j] + kn[rsub + RS * j] * delta;
+        for (int i = 0; i < 4; ++i) {
+            sv[0][i] = decay * sv[0][i] + kn[i] * da;
+            sv[1][i] = decay * sv[1][i] + kn[i] * db;
+        }
+        // the next token's products overwrite the rows the chains just read
+        __builtin_amdgcn_wave_barrier();
     }
-    // the store addresses are formed after the token loop, not kept across it
     float *Sw = S;
     asm volatile("" : "+v"(Sw));
 #pragma unroll
-    for (int j = 0; j < NE; ++j) Sw[(size_t)(rsub + RS * j) * kHD] = sv[j];
+    for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<float2 *>(Sw + (size_t)(lane + 64 * i) * kHD) = make_float2(sv[0][i], sv[1][i]);
 }
 
 }  // namespace bt
@@ -1310,9 +1316,8 @@ void enqueue_prefill_chunk(GDNBatchEngine *e, int slot, int n, bool last, hipStr
         hipLaunchKernelGGL(k_pconv, dim3(4 * kH / 64), dim3(kConvT), 0, s, e->ypart, n, tl, b_aux(e, l) + kAuxConv,
                            e->qkv, e->gate, e->sgate);
         hipLaunchKernelGGL(k_pqk, dim3(kNH, n), dim3(kT), 0, s, e->qkv, e->p_qn, e->p_kn, e->p_alpha);
-        hipLaunchKernelGGL(k_pscan<kScanCols>, dim3(kHD / kScanCols, kNH), dim3(kT), 0, s, e->qkv, e->p_qn, e->p_kn,
-                           e->p_alpha,
-                           e->bd, n, st, e->attn);
+        hipLaunchKernelGGL(k_pscan, dim3(kHD / kScanWgCols, kNH), dim3(kT), 0, s, e->qkv, e->p_qn, e->p_kn,
+                           e->p_alpha, e->bd, n, st, e->attn);
         hipLaunchKernelGGL(k_bonorm, dim3(kNH, n), dim3(kT), 0, s, e->attn, e->gate, e->sgate,
                            b_aux(e, l) + kAuxONorm, e->eps, e->x_o);
         BEpi eo{};
