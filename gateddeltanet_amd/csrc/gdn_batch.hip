@@ -816,8 +816,8 @@ __global__ __launch_bounds__(kT) void k_pqk(const float *__restrict__ qkv, float
 // (kHD / kScanWgCols, kNH), four independent waves per workgroup (one per
 // SIMD, one workgroup per CU; a wave64 add holds its SIMD whatever its
 // active lanes, so two chain waves on one SIMD would take turns).  Lane l
-// holds rows l + 64 i (i < 4) of the wave's columns c0, c0 + 1 for the
-// whole chunk.  Per token: every lane writes its products S[j][c] * kn[j]
+// holds rows 4 l .. 4 l + 3 of the wave's columns c0, c0 + 1 for the whole
+// chunk (one 16-byte LDS access per chain row piece).  Per token: every lane writes its products S[j][c] * kn[j]
 // and S[j][c] * qn[j] to the wave's LDS rows; lanes 0..3 sum the chains (r
 // of c0, r of c0 + 1, p of c0, p of c0 + 1) in row order j = 0..255 (the
 // reference's chain order, adds only); the four sums and the token's v,
@@ -855,26 +855,23 @@ __global__ __launch_bounds__(kT) void k_pscan(const float *__restrict__ qkv, con
     float sv[2][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const float2 s2 = *reinterpret_cast<const float2 *>(S + (size_t)(lane + 64 * i) * kHD);
+        const float2 s2 = *reinterpret_cast<const float2 *>(S + (size_t)(4 * lane + i) * kHD);
         sv[0][i] = s2.x;
         sv[1][i] = s2.y;
     }
     __syncthreads();
     float *pw = prod[w];
     for (int m = 0; m < n; ++m) {
-        float kn[4], qn[4];
+        const f32x4 k4 = *reinterpret_cast<const f32x4 *>(&kqs[m][0][4 * lane]);
+        const f32x4 q4 = *reinterpret_cast<const f32x4 *>(&kqs[m][1][4 * lane]);
+        const float kn[4] = {k4.x, k4.y, k4.z, k4.w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            kn[i] = kqs[m][0][lane + 64 * i];
-            qn[i] = kqs[m][1][lane + 64 * i];
+        for (int e = 0; e < 2; ++e) {
+            *reinterpret_cast<f32x4 *>(pw + e * kPad + 4 * lane) =
+                (f32x4){sv[e][0] * k4.x, sv[e][1] * k4.y, sv[e][2] * k4.z, sv[e][3] * k4.w};
+            *reinterpret_cast<f32x4 *>(pw + (2 + e) * kPad + 4 * lane) =
+                (f32x4){sv[e][0] * q4.x, sv[e][1] * q4.y, sv[e][2] * q4.z, sv[e][3] * q4.w};
         }
-#pragma unroll
-        for (int e = 0; e < 2; ++e)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                pw[e * kPad + lane + 64 * i] = sv[e][i] * kn[i];
-                pw[(2 + e) * kPad + lane + 64 * i] = sv[e][i] * qn[i];
-            }
         // the wave's own LDS writes, then its reads of other lanes' rows
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -924,7 +921,7 @@ __global__ __launch_bounds__(kT) void k_pscan(const float *__restrict__ qkv, con
     asm volatile("" : "+v"(Sw));
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<float2 *>(Sw + (size_t)(lane + 64 * i) * kHD) = make_float2(sv[0][i], sv[1][i]);
+        *reinterpret_cast<float2 *>(Sw + (size_t)(4 * lane + i) * kHD) = make_float2(sv[0][i], sv[1][i]);
 }
 
 }  // namespace bt
