@@ -861,9 +861,10 @@ __global__ __launch_bounds__(kT) void k_pscan(const float *__restrict__ qkv, con
     }
     __syncthreads();
     float *pw = prod[w];
+    f32x4 k4n = *reinterpret_cast<const f32x4 *>(&kqs[0][0][4 * lane]);
+    f32x4 q4n = *reinterpret_cast<const f32x4 *>(&kqs[0][1][4 * lane]);
     for (int m = 0; m < n; ++m) {
-        const f32x4 k4 = *reinterpret_cast<const f32x4 *>(&kqs[m][0][4 * lane]);
-        const f32x4 q4 = *reinterpret_cast<const f32x4 *>(&kqs[m][1][4 * lane]);
+        const f32x4 k4 = k4n, q4 = q4n;
         const float kn[4] = {k4.x, k4.y, k4.z, k4.w};
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
@@ -876,22 +877,28 @@ __global__ __launch_bounds__(kT) void k_pscan(const float *__restrict__ qkv, con
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        {
+            // the next token's k and q, read while the chains run
+            const int mn = m + 1 < n ? m + 1 : m;
+            k4n = *reinterpret_cast<const f32x4 *>(&kqs[mn][0][4 * lane]);
+            q4n = *reinterpret_cast<const f32x4 *>(&kqs[mn][1][4 * lane]);
+        }
         float acc = 0.0f;
         if (lane < 4) {
             const f32x4 *col = reinterpret_cast<const f32x4 *>(pw + lane * kPad);
-            f32x4 cur[4];
+            f32x4 cur[8];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) cur[j] = col[j];
+            for (int j = 0; j < 8; ++j) cur[j] = col[j];
 #pragma unroll
-            for (int b = 0; b < kHD / 16; ++b) {
-                f32x4 nxt[4];
+            for (int b = 0; b < kHD / 32; ++b) {
+                f32x4 nxt[8];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) nxt[j] = (b + 1 < kHD / 16) ? col[4 * (b + 1) + j] : cur[j];
+                for (int j = 0; j < 8; ++j) nxt[j] = (b + 1 < kHD / 32) ? col[8 * (b + 1) + j] : cur[j];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc = (((acc + cur[j].x) + cur[j].y) + cur[j].z) + cur[j].w;
+                for (int j = 0; j < 8; ++j) acc = (((acc + cur[j].x) + cur[j].y) + cur[j].z) + cur[j].w;
                 asm volatile("" : "+v"(acc) : : "memory");
 #pragma unroll
-                for (int j = 0; j < 4; ++j) cur[j] = nxt[j];
+                for (int j = 0; j < 8; ++j) cur[j] = nxt[j];
             }
         }
         const float ra = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 0));
