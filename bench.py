@@ -67,8 +67,8 @@ KERNEL_BYTES = {
 # recurrence moves 2.1 MB more than its state: each 16-column workgroup
 # writes half of every 128-byte line, which the L2 fills before merging.
 MEASURED_TRAFFIC = {
-    "qkvg": 34_441_000, "recur": 6_514_000, "o_proj": 8_705_000, "gate_up": 46_548_000,
-    "down": 23_362_000, "lm_head": 136_393_000, "argmax": 7_000,
+    "qkvg": 34_443_000, "recur": 6_528_000, "o_proj": 8_698_000, "gate_up": 46_667_000,
+    "down": 23_356_000, "lm_head": 136_507_000, "argmax": 7_000,
 }
 LAUNCHES_PER_TOKEN = {"qkvg": L, "recur": L, "o_proj": L, "gate_up": L, "down": L, "lm_head": 1, "argmax": 1}
 
