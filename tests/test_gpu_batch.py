@@ -161,6 +161,27 @@ def test_one_hot_model_bit_exact_to_batch1(onehot):
         bs.free()
 
 
+def test_one_hot_partial_stream_group(onehot):
+    """37 streams: the last 16-stream MFMA group is partly empty, the gate/up
+    epilogue and the split post-down norm see a stream count that is no
+    multiple of 16; every stream still equals its batch-1 run bit for bit."""
+    m, steps, nb = onehot, 2, 37
+    tokens = g.synth_tokens(steps * nb, 27, 0).reshape(steps, nb)
+    ref_logits, ref_toks, ref_states = batch1_reference(m, tokens)
+    bs = g.BatchState(m, nb)
+    try:
+        for i in range(steps):
+            got = bs.step(tokens[i])
+            assert (got == ref_toks[i]).all(), i
+            for s in range(nb):
+                assert equal_values(bs.logits(s), ref_logits[i, s]), (i, s)
+        for s in range(nb):
+            r, c = bs.save_stream_state(s)
+            assert equal_values(r, ref_states[s][0]) and equal_values(c, ref_states[s][1]), s
+    finally:
+        bs.free()
+
+
 def test_one_hot_model_bit_exact_to_oracle(orc, onehot):
     m = onehot
     hdr = orc.header_from(m.config)
