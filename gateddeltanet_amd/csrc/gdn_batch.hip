@@ -460,6 +460,8 @@ struct BNorm {
 // residual, to h_out != h_in, and the X tiles.
 constexpr int kAbSplit = 4;
 constexpr int kAbHeads = kNH / kAbSplit;  // heads per a/b workgroup
+static_assert(kNH % kAbSplit == 0 && (2 * kAbHeads * kH) % (4 * kT) == 0 && 2 * kAbHeads <= kT,
+              "whole heads per a/b workgroup, whole 16-byte row pieces per thread");
 template <int SPLITS, bool EMBED, bool AB>
 __global__ __launch_bounds__(kT) void k_bnorm(BNorm p) {
     constexpr int ABR = 2 * kAbHeads;  // a/b rows per workgroup: a rows, then b rows
