@@ -780,6 +780,7 @@ struct Epi {
     float *y2;         // QKVG: gate
     float *y3;         // QKVG: sigmoid(gate)
     const float *aux;  // QKVG: the layer's small weights
+    const uint16_t *ab16;  // QKVG (CU-resident): the layer's a/b rows [16][kH] as BF16 bits
     float *tails;      // QKVG: the layer's conv tails (3 stripes)
     float *ab;         // QKVG: a[8], b[8] (BF16-rounded)
     float *bd;         // QKVG: (beta, decay) per head
@@ -1133,12 +1134,15 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     // QKVG workgroup h < 8: head h's FP32 a and b rows (half-beat t & 127 of
     // row t >> 7), needed right after the input is built
     const bool ab_blk = (EPI == EPI_QKVG) && blockIdx.x < kNH;
-    u32x4 abw[4];
+    // (the BF16 copy: the BF16 contracts require BF16-exact weights, so its
+    // values are the FP32 rows' and the 8 workgroups stream 8 KB, not 16 KB,
+    // beyond their weight rows)
+    u32x4 abw[2];
     if (ab_blk && t < kT) {
         const int abrow = (t >> 7) * kNH + blockIdx.x, hb = t & 127;
-        const u32x4 *src4 = reinterpret_cast<const u32x4 *>(ep.aux + kAuxAB + (size_t)abrow * kH + hb * 16);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) abw[q] = src4[q];
+        const u32x4 *src4 = reinterpret_cast<const u32x4 *>(ep.ab16 + (size_t)abrow * kH + hb * 16);
+        abw[0] = src4[0];
+        abw[1] = src4[1];
     }
     if constexpr (kActFirst) __builtin_amdgcn_s_barrier();
 
@@ -1182,12 +1186,12 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
                 uint32_t xv[16];
                 lds_load16u(xs + hb * 16, xv);
                 float p[16];
+                const uint32_t wv[8] = {abw[0].x, abw[0].y, abw[0].z, abw[0].w,
+                                        abw[1].x, abw[1].y, abw[1].z, abw[1].w};
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    p[4 * q + 0] = lane_word_value(xv[4 * q + 0], 0) * u2f(abw[q].x);
-                    p[4 * q + 1] = lane_word_value(xv[4 * q + 1], 1) * u2f(abw[q].y);
-                    p[4 * q + 2] = lane_word_value(xv[4 * q + 2], 0) * u2f(abw[q].z);
-                    p[4 * q + 3] = lane_word_value(xv[4 * q + 3], 1) * u2f(abw[q].w);
+                for (int i = 0; i < 8; ++i) {
+                    p[2 * i] = lane_word_value(xv[2 * i], 0) * u2f(wv[i] << 16);
+                    p[2 * i + 1] = lane_word_value(xv[2 * i + 1], 1) * u2f(wv[i] & 0xffff0000u);
                 }
                 abpart[t] = tree16(p);
                 sync();
@@ -1394,6 +1398,7 @@ struct GDNEngine {
     WInfo i_qkvg[kMaxLayers] = {}, i_o[kMaxLayers] = {}, i_gu[kMaxLayers] = {},
           i_down[kMaxLayers] = {}, i_lm = {};
     float *aux = nullptr;  // [layers][kAuxLayer] + final_norm[kH]
+    uint16_t *ab16 = nullptr;  // [layers][16][kH]: the a/b rows' BF16 bits
     // workspace (GDN_WS_OFF_* layout) and activations
     float *ws = nullptr;
     float *act = nullptr;
@@ -1572,6 +1577,17 @@ int upload_weights(GDNEngine *e, const GDNModel *m) {
     std::memcpy(aux.data() + L * kAuxLayer, m->final_norm, H * 4);
     GDN_HIP(hipMalloc(&e->aux, aux.size() * 4));
     GDN_HIP(hipMemcpy(e->aux, aux.data(), aux.size() * 4, hipMemcpyHostToDevice));
+    // the a/b rows' top halves (the BF16 values under the BF16 contracts'
+    // BF16-exact weights; unused by the FP32 contract)
+    std::vector<uint16_t> ab16(L * 2 * kNH * H);
+    for (size_t l = 0; l < L; ++l)
+        for (size_t i = 0; i < 2 * kNH * H; ++i) {
+            uint32_t b;
+            std::memcpy(&b, aux.data() + l * kAuxLayer + kAuxAB + i, 4);
+            ab16[l * 2 * kNH * H + i] = (uint16_t)(b >> 16);
+        }
+    GDN_HIP(hipMalloc(&e->ab16, ab16.size() * 2));
+    GDN_HIP(hipMemcpy(e->ab16, ab16.data(), ab16.size() * 2, hipMemcpyHostToDevice));
     GDN_HIP(hipDeviceSynchronize());
     return 0;
 }
@@ -1634,6 +1650,7 @@ void launch_qkvg(GDNEngine *e, int l, const float *res_a, const float *res_b, hi
     q.y2 = e->gate;
     q.y3 = e->sgate;
     q.aux = aux;
+    q.ab16 = e->ab16 + (size_t)l * 2 * kNH * kH;
     q.tails = layer_tails(e, l);
     q.ab = e->ab;
     q.bd = e->bd;
@@ -1836,6 +1853,7 @@ void destroy_engine(GDNEngine *e) {
     if (e->stream) (void)hipStreamDestroy(e->stream);
     (void)hipFree(e->wmem);
     (void)hipFree(e->aux);
+    (void)hipFree(e->ab16);
     (void)hipFree(e->ws);
     (void)hipFree(e->act);
     (void)hipFree(e->lm_idx);
