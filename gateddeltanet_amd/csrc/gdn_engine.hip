@@ -1406,8 +1406,8 @@ struct GDNEngine {
           *gate = nullptr, *sgate = nullptr, *ab = nullptr, *bd = nullptr, *attn = nullptr,
           *ybuf_o = nullptr, *dbuf = nullptr, *hbuf = nullptr, *lm_val = nullptr;
     int *lm_idx = nullptr;
-    int *tok_dev = nullptr;   // [0] in, [1] out
-    int *tok_host = nullptr;  // pinned [0] in, [1] out
+    int *tok_host = nullptr;  // pinned, mapped, coherent: [0] in, [1] out
+    int *tok_map = nullptr;   // the device's address of tok_host
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     bool use_graph = true;
@@ -1614,10 +1614,11 @@ int alloc_buffers(GDNEngine *e) {
     e->hbuf = p; p += kI;
     e->lm_val = p; p += nblk_lm;
     GDN_HIP(hipMalloc(&e->lm_idx, nblk_lm * sizeof(int)));
-    GDN_HIP(hipMalloc(&e->tok_dev, 2 * sizeof(int)));
-    GDN_HIP(hipMemset(e->tok_dev, 0, 2 * sizeof(int)));
-    GDN_HIP(hipHostMalloc(&e->tok_host, 2 * sizeof(int), hipHostMallocDefault));
+    // the step reads its token from and writes its argmax to host memory
+    // directly: no copy kernels on a token's path
+    GDN_HIP(hipHostMalloc(&e->tok_host, 2 * sizeof(int), hipHostMallocMapped | hipHostMallocCoherent));
     e->tok_host[0] = e->tok_host[1] = 0;
+    GDN_HIP(hipHostGetDevicePointer(reinterpret_cast<void **>(&e->tok_map), e->tok_host, 0));
     GDN_HIP(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
     GDN_HIP(hipEventCreate(&e->ev0));
     GDN_HIP(hipEventCreate(&e->ev1));
@@ -1657,7 +1658,7 @@ void launch_qkvg(GDNEngine *e, int l, const float *res_a, const float *res_b, hi
     XSrc xq = xsrc(res_a, res_b, nullptr, aux + kAuxAttnNorm, e->resid, nullptr, e->eps);
     if constexpr (PRO0 == PRO_EMBED) {
         xq.emb = e->w_emb;
-        xq.tok = e->tok_dev;
+        xq.tok = e->tok_map;
         xq.vocab = e->vocab;
         xq.aux_out = e->ws + GDN_WS_OFF_X;
     }
@@ -1747,7 +1748,7 @@ void launch_lm(GDNEngine *e, hipStream_t s) {
 
 void launch_argmax(GDNEngine *e, hipStream_t s) {
     hipLaunchKernelGGL(k_argmax, dim3(1), dim3(kT), 0, s, e->lm_val, e->lm_idx, lm_blocks(e),
-                       e->tok_dev + 1, e->ws + GDN_WS_OFF_X_NORM);
+                       e->tok_map + 1, e->ws + GDN_WS_OFF_X_NORM);
 }
 
 template <int C, int PRO0>
@@ -1826,8 +1827,7 @@ int ensure_graph(GDNEngine *e) {
 // Token in (host) -> kernels -> token out (host).  Times when asked.
 int run_step(GDNEngine *e, int32_t token, int32_t *tok_out, float *inner_ms) {
     if (e->use_graph && ensure_graph(e) != 0) return -1;
-    e->tok_host[0] = token;
-    GDN_HIP(hipMemcpyAsync(e->tok_dev, e->tok_host, sizeof(int), hipMemcpyHostToDevice, e->stream));
+    e->tok_host[0] = token;  // read by layer 0's kernel through tok_map
     if (inner_ms) GDN_HIP(hipEventRecord(e->ev0, e->stream));
     if (e->use_graph) {
         GDN_HIP(hipGraphLaunch(e->exec, e->stream));
@@ -1836,9 +1836,7 @@ int run_step(GDNEngine *e, int32_t token, int32_t *tok_out, float *inner_ms) {
         GDN_HIP(hipGetLastError());
     }
     if (inner_ms) GDN_HIP(hipEventRecord(e->ev1, e->stream));
-    GDN_HIP(hipMemcpyAsync(e->tok_host + 1, e->tok_dev + 1, sizeof(int), hipMemcpyDeviceToHost,
-                           e->stream));
-    GDN_HIP(hipStreamSynchronize(e->stream));
+    GDN_HIP(hipStreamSynchronize(e->stream));  // k_argmax wrote tok_host[1]
     if (tok_out) *tok_out = e->tok_host[1];
     if (inner_ms) GDN_HIP(hipEventElapsedTime(inner_ms, e->ev0, e->ev1));
     return 0;
@@ -1857,7 +1855,6 @@ void destroy_engine(GDNEngine *e) {
     (void)hipFree(e->ws);
     (void)hipFree(e->act);
     (void)hipFree(e->lm_idx);
-    (void)hipFree(e->tok_dev);
     if (e->tok_host) (void)hipHostFree(e->tok_host);
     delete e;
 }
@@ -1939,7 +1936,8 @@ int gdn_decode_step_host(const GDNModel *model, GDNRunState *state, const int32_
 }
 
 int gdn_read_token(const GDNRunState *state, int32_t *token) {
-    GDN_HIP(hipMemcpy(token, state->engine->tok_dev + 1, sizeof(int32_t), hipMemcpyDeviceToHost));
+    GDN_HIP(hipStreamSynchronize(state->engine->stream));
+    *token = state->engine->tok_host[1];
     return 0;
 }
 
