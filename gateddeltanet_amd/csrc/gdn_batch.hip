@@ -958,8 +958,9 @@ struct GDNBatchEngine {
           *attn = nullptr, *ypart = nullptr, *xn = nullptr, *logits = nullptr, *part_val = nullptr;
     int *part_idx = nullptr;
     uint16_t *x_h = nullptr, *x_o = nullptr, *x_d = nullptr;  // X tiles, K = 2048 / 2048 / 5632
-    int *tok_dev = nullptr;   // [0..63] in, [64..127] out
-    int *tok_host = nullptr;  // pinned, same layout
+    int *tok_dev = nullptr;   // a prefill chunk's tokens [0..63]
+    int *tok_host = nullptr;  // pinned, mapped, coherent, same layout
+    int *tok_map = nullptr;   // the device's address of tok_host (the step's tokens)
     // prefill: the chunk's normalized q / k, alpha, its logits, final hidden
     // vectors and argmax tokens (per-token buffers of their own, so a
     // prefill leaves the other streams' last step readable)
@@ -1136,8 +1137,11 @@ int b_alloc(GDNBatchEngine *e) {
     GDN_HIP(hipMalloc(&e->p_tok, (size_t)kMaxB * sizeof(int)));
     GDN_HIP(hipMalloc(&e->tok_dev, 2 * kMaxB * sizeof(int)));
     GDN_HIP(hipMemset(e->tok_dev, 0, 2 * kMaxB * sizeof(int)));
-    GDN_HIP(hipHostMalloc(&e->tok_host, 2 * kMaxB * sizeof(int), hipHostMallocDefault));
+    // a step reads its tokens from and writes its argmaxes to host memory
+    // directly (prefill chunks still stage through tok_dev)
+    GDN_HIP(hipHostMalloc(&e->tok_host, 2 * kMaxB * sizeof(int), hipHostMallocMapped | hipHostMallocCoherent));
     std::memset(e->tok_host, 0, 2 * kMaxB * sizeof(int));
+    GDN_HIP(hipHostGetDevicePointer(reinterpret_cast<void **>(&e->tok_map), e->tok_host, 0));
     GDN_HIP(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
     GDN_HIP(hipEventCreate(&e->ev0));
     GDN_HIP(hipEventCreate(&e->ev1));
@@ -1175,7 +1179,7 @@ enum { KB_EMBED, KB_QKVG, KB_RECUR, KB_ONORM, KB_O, KB_NORM, KB_GU, KB_DOWN, KB_
 void launch_embed(GDNBatchEngine *e, hipStream_t s) {
     BNorm p = bnorm(e, nullptr, b_aux(e, 0) + kAuxAttnNorm, e->x_h, 0, 0, 0);
     p.emb = e->emb;
-    p.tok = e->tok_dev;
+    p.tok = e->tok_map;
     hipLaunchKernelGGL((k_bnorm<0, true, true>), dim3(e->streams, kAbSplit), dim3(kT), 0, s, p);
 }
 void launch_qkvg(GDNBatchEngine *e, int l, hipStream_t s) {
@@ -1246,7 +1250,7 @@ void launch_lm(GDNBatchEngine *e, hipStream_t s) {
 }
 void launch_argmax(GDNBatchEngine *e, hipStream_t s) {
     hipLaunchKernelGGL(k_bargmax, dim3(e->streams), dim3(kT), 0, s, e->part_val, e->part_idx, lm_wgs(e),
-                       e->tok_dev + kMaxB);
+                       e->tok_map + kMaxB);
 }
 
 void b_enqueue_step(GDNBatchEngine *e, hipStream_t s) {
@@ -1283,9 +1287,7 @@ int b_run_step(GDNBatchEngine *e, const int32_t *tokens, int32_t *next, float *i
         }
     }
     if (e->use_graph && b_ensure_graph(e) != 0) return -1;
-    std::memcpy(e->tok_host, tokens, (size_t)e->streams * sizeof(int));
-    GDN_HIP(hipMemcpyAsync(e->tok_dev, e->tok_host, (size_t)e->streams * sizeof(int), hipMemcpyHostToDevice,
-                           e->stream));
+    std::memcpy(e->tok_host, tokens, (size_t)e->streams * sizeof(int));  // read through tok_map
     if (inner_ms) GDN_HIP(hipEventRecord(e->ev0, e->stream));
     if (e->use_graph) {
         GDN_HIP(hipGraphLaunch(e->exec, e->stream));
@@ -1294,9 +1296,7 @@ int b_run_step(GDNBatchEngine *e, const int32_t *tokens, int32_t *next, float *i
         GDN_HIP(hipGetLastError());
     }
     if (inner_ms) GDN_HIP(hipEventRecord(e->ev1, e->stream));
-    GDN_HIP(hipMemcpyAsync(e->tok_host + kMaxB, e->tok_dev + kMaxB, (size_t)e->streams * sizeof(int),
-                           hipMemcpyDeviceToHost, e->stream));
-    GDN_HIP(hipStreamSynchronize(e->stream));
+    GDN_HIP(hipStreamSynchronize(e->stream));  // k_bargmax wrote tok_host[kMaxB..]
     if (next) std::memcpy(next, e->tok_host + kMaxB, (size_t)e->streams * sizeof(int));
     if (inner_ms) GDN_HIP(hipEventElapsedTime(inner_ms, e->ev0, e->ev1));
     return 0;
@@ -1387,8 +1387,6 @@ int b_prefill(GDNBatchEngine *e, int slot, const int32_t *prompt, uint32_t n_tok
                            (size_t)e->vocab * 4, hipMemcpyDeviceToDevice, e->stream));
     GDN_HIP(hipMemcpyAsync(e->xn + (size_t)slot * kH, e->p_xn + (size_t)(n - 1) * kH, (size_t)kH * 4,
                            hipMemcpyDeviceToDevice, e->stream));
-    GDN_HIP(hipMemcpyAsync(e->tok_dev + kMaxB + slot, e->p_tok + (n - 1), sizeof(int), hipMemcpyDeviceToDevice,
-                           e->stream));
     GDN_HIP(hipMemcpyAsync(e->tok_host + kMaxB + slot, e->p_tok + (n - 1), sizeof(int), hipMemcpyDeviceToHost,
                            e->stream));
     GDN_HIP(hipStreamSynchronize(e->stream));
@@ -1492,7 +1490,8 @@ int gdn_batch_decode_step(GDNBatchState *state, const int32_t *tokens, int32_t *
 int gdn_batch_read_tokens(const GDNBatchState *state, int32_t *tokens) {
     GDNBatchEngine *e = engine_of(state);
     if (!e) return -1;
-    GDN_HIP(hipMemcpy(tokens, e->tok_dev + kMaxB, (size_t)e->streams * sizeof(int), hipMemcpyDeviceToHost));
+    GDN_HIP(hipStreamSynchronize(e->stream));
+    std::memcpy(tokens, e->tok_host + kMaxB, (size_t)e->streams * sizeof(int));
     return 0;
 }
 
