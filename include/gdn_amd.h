@@ -208,9 +208,10 @@ int gdn_write_gdnstate(const GDNWeightHeader *config, const char *path, const fl
 
 /* Steady teacher-forced benchmark, host.cpp:2150-2256: tokens[i % n_tokens]
  * is fed at step i for n_steps steps.  Per step: outer = host token in ->
- * host token out (H2D of 4 bytes, graph launch, D2H of 4 bytes); inner =
- * HIP events around the graph on the engine stream.  Any output pointer
- * may be NULL. */
+ * host token out (the token is read and the argmax written through mapped
+ * pinned memory around one graph launch); inner = HIP events around the
+ * graph on the engine stream, recorded only when inner_ms is given.  Any
+ * output pointer may be NULL. */
 int gdn_run_teacher_forced(GDNRunState *state, const int32_t *tokens,
                            uint32_t n_tokens, uint32_t n_steps,
                            int32_t *argmax_out, float *inner_ms,
