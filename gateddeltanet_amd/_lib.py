@@ -82,13 +82,35 @@ class GDNModel(ctypes.Structure):
     ]
 
 
+GEMV_CHANNELS = 32
+RECURRENT_STATE_PORTS, RECURRENT_STATE_FIRST_PORT = 4, 28
+RECURRENT_STATE_STRIPE_BF16_BEATS = WSF_STATE // RECURRENT_STATE_PORTS // 32
+
+
+class Beat512(ctypes.Structure):
+    _fields_ = [("bytes", ctypes.c_ubyte * 64)]
+
+
 class GDNRunState(ctypes.Structure):
+    """gdn_model.h:153-160 field for field (host memory), engine appended."""
     _fields_ = [
-        ("workspace", c_void_p),
+        ("workspace", POINTER(Beat512)),
         ("x", POINTER(c_float)),
         ("recurrent_state", POINTER(c_float)),
         ("head_buffer", POINTER(c_float)),
+        ("weight_shards", POINTER(Beat512) * GEMV_CHANNELS),
+        ("aux_weights", POINTER(Beat512)),
         ("engine", c_void_p),
+    ]
+
+
+class GDNMixedMulStats(ctypes.Structure):
+    _fields_ = [
+        ("calls", c_uint64),
+        ("special_inputs", c_uint64),
+        ("flushed_inputs", c_uint64),
+        ("flushed_outputs", c_uint64),
+        ("overflows", c_uint64),
     ]
 
 
@@ -158,6 +180,20 @@ SIGNATURES = {
     "gdn_profile_kernels": (c_int, [POINTER(GDNRunState), c_uint32, FP, c_uint32]),
     "gdn_get_contract": (c_int, [POINTER(GDNRunState)]),
     "gdn_compute_logits": (None, [POINTER(GDNModel), FP, FP]),
+    "gdn_weight_shard_beats": (c_size_t, [POINTER(GDNWeightHeader)]),
+    "gdn_weight_shard_bytes": (c_size_t, [POINTER(GDNWeightHeader)]),
+    "gdn_validate_weight_shards": (c_int, [FP, POINTER(GDNWeightHeader), POINTER(POINTER(Beat512))]),
+    "gdn_scatter_recurrent_state": (c_int, [POINTER(POINTER(Beat512)), FP, c_size_t]),
+    "gdn_pack_conv_tails_bf16": (c_int, [POINTER(Beat512), FP, c_size_t]),
+    "gdn_set_native_debug_buffers": (None, [FP, FP]),
+    "gdn_reset_mixed_mul_stats": (None, []),
+    "gdn_get_mixed_mul_stats": (GDNMixedMulStats, []),
+    "gdn_stop_mixed_mul_stats": (None, []),
+    "gdn_sync_host_state": (c_int, [POINTER(GDNRunState)]),
+    "gdn_test_set_fp32_lane_bits": (None, [POINTER(Beat512), c_uint32, c_uint32]),
+    "gdn_test_get_fp32_lane_bits": (c_uint32, [POINTER(Beat512), c_uint32]),
+    "gdn_test_set_bf16_lane_bits": (None, [POINTER(Beat512), c_uint32, c_uint16]),
+    "gdn_test_get_bf16_lane_bits": (c_uint16, [POINTER(Beat512), c_uint32]),
     "gdn_native_bf16_mul_to_fp32": (c_float, [c_uint16, c_uint16]),
     "gdn_test_fp32_to_bf16_rne_bits": (c_uint16, [c_uint32]),
     "gdn_test_bf16_to_fp32_bits": (c_uint32, [c_uint16]),

@@ -33,6 +33,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <type_traits>
 #include <vector>
 
@@ -329,6 +330,8 @@ struct XSrc {
     const float *w;
     float *res_out;
     float *aux_out;
+    int *err;          // host-mapped error word: set when a bounded wait runs out
+    uint32_t *xdump;   // when set, workgroup 0 stores its GEMV input (K lane words) and fast-path verdict
     int vocab;
     float eps;
 };
@@ -340,30 +343,34 @@ struct XSrc {
 // only about one wave's worth of outstanding loads).  Each wave's lane 0
 // adds one to an LDS arrival counter; the waves spin (s_sleep) until it
 // reaches 4 x phase.  The spin is bounded so no wave can hang; the bound
-// (about a second) is never reached while the four waves run.
+// (about a second) is never reached while the four waves run; if it were,
+// the wave sets the error word, which the host turns into a failed step.
 struct BlockSync {
     __device__ __forceinline__ void operator()() { __syncthreads(); }
 };
 
 constexpr int kSpinMax = 1 << 24;
 
-__device__ __forceinline__ void wait_count(int *ctr, int target) {
+__device__ __forceinline__ void wait_count(int *ctr, int target, int *err) {
     int spins = 0;
     while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target &&
            ++spins < kSpinMax)
         __builtin_amdgcn_s_sleep(1);
+    if (spins >= kSpinMax && err != nullptr && (threadIdx.x & 63) == 0)
+        __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
 struct Wave4Sync {
     int *ctr;
+    int *err;
     int phase = 0;
     __device__ __forceinline__ void operator()() {
         ++phase;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         if ((threadIdx.x & 63) == 0)
             __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        wait_count(ctr, 4 * phase);
+        wait_count(ctr, 4 * phase, err);
     }
 };
 
@@ -1173,7 +1180,7 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     // loads are issued, wait for the prologue's last arrival
     bool fast;
     if (t < kT) {
-        Wave4Sync sync{&arrive};
+        Wave4Sync sync{&arrive, src.err};
         fast = pro.finish_bf16(src, wi, xs, scratch, bcast, red, sync);
         if constexpr (EPI == EPI_QKVG) {
             if (ab_blk) {
@@ -1217,8 +1224,14 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
             }
         }
     } else {
-        wait_count(&arrive, 4 * Prologue<C, K, PRO>::kSyncs);
+        wait_count(&arrive, 4 * Prologue<C, K, PRO>::kSyncs, src.err);
         fast = decide_fast(red, wi);
+    }
+    // the product-counter copy of the GEMV input (debug: off in the timed
+    // path, where xdump is null); xs is complete for every wave here
+    if (src.xdump != nullptr && blockIdx.x == 0) {
+        for (int i = t; i < K; i += kTB) src.xdump[i] = xs[i];
+        if (t == 0) src.xdump[K] = fast ? 1u : 0u;
     }
 
     // 4. products, barrier, bank chains and the row epilogue
@@ -1305,8 +1318,7 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
 // merge that keeps the larger value and, on ties, the lower index.
 __global__ __launch_bounds__(kT) void k_argmax(const float *__restrict__ part_val,
                                                const int *__restrict__ part_idx, int n,
-                                               int *__restrict__ tok_out,
-                                               float *__restrict__ ws_token) {
+                                               int *__restrict__ tok_out) {
     __shared__ float bv[4];
     __shared__ int bi[4];
     float best = -3.402823466e38f;
@@ -1340,8 +1352,7 @@ __global__ __launch_bounds__(kT) void k_argmax(const float *__restrict__ part_va
                 idx = bi[i];
             }
         }
-        tok_out[0] = idx;
-        ws_token[0] = (float)idx;
+        tok_out[0] = idx;  // host-mapped: the step's completion signal
     }
 }
 
@@ -1383,6 +1394,13 @@ __global__ __launch_bounds__(kT) void k_resadd(const float *__restrict__ a,
 
 using namespace gdn;
 
+// Per-matrix column counts of the native multiplier's special inputs, for
+// the product counters: colspec[k] = rows whose weight in column k has a zero
+// or all-ones exponent, colsub[k] = rows whose weight there is subnormal.
+struct ColCounts {
+    std::vector<uint32_t> spec, sub;
+};
+
 struct GDNEngine {
     int contract = 0;
     int layers = 0;
@@ -1399,18 +1417,35 @@ struct GDNEngine {
           i_down[kMaxLayers] = {}, i_lm = {};
     float *aux = nullptr;  // [layers][kAuxLayer] + final_norm[kH]
     uint16_t *ab16 = nullptr;  // [layers][16][kH]: the a/b rows' BF16 bits
-    // workspace (GDN_WS_OFF_* layout) and activations
-    float *ws = nullptr;
+    // persistent state: recurrent [L][8][256 K][256 V] (FP32, or BF16 for
+    // REF) and conv tails [L][q,k,v] stripes of kTailStripe floats (BF16
+    // payload in the first half for the BF16 contracts)
+    void *state = nullptr;
+    float *tails = nullptr;
+    // activations and step outputs
     float *act = nullptr;
     float *resid = nullptr, *resid_alt = nullptr, *fhid = nullptr, *qkv = nullptr,
           *gate = nullptr, *sgate = nullptr, *ab = nullptr, *bd = nullptr, *attn = nullptr,
-          *ybuf_o = nullptr, *dbuf = nullptr, *hbuf = nullptr, *lm_val = nullptr;
+          *ybuf_o = nullptr, *dbuf = nullptr, *hbuf = nullptr, *lm_val = nullptr,
+          *xrow = nullptr, *logits = nullptr;
     int *lm_idx = nullptr;
-    int *tok_host = nullptr;  // pinned, mapped, coherent: [0] in, [1] out
+    // pinned, mapped, coherent host words: [0] token in, [1] token out (-1
+    // until the step's argmax lands), [2] kernel error word
+    int *tok_host = nullptr;
     int *tok_map = nullptr;   // the device's address of tok_host
+    bool failed = false;      // a step timed out or reported an error
+    double timeout_ms = 10000.0;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     bool use_graph = true;
+    // product counters: GEMV inputs of one step (device, lane words + the
+    // fast-path verdict per launch) and the weights' column counts
+    uint32_t *xdump = nullptr;
+    bool counting = false;
+    bool trace_counts = false;    // GDN_COUNTER_TRACE=1: per-slot report on stderr
+    std::vector<ColCounts> cols;  // per layer: qkvg, o, gu, down; then the LM head
+    // host mirrors for the reference's run-state fields
+    GDNRunState *owner = nullptr;
 };
 
 namespace {
@@ -1419,20 +1454,32 @@ size_t welem(int contract) { return contract == kFp32 ? 4 : 2; }
 
 float *layer_aux(GDNEngine *e, int l) { return e->aux + (size_t)l * kAuxLayer; }
 float *final_norm(GDNEngine *e) { return e->aux + (size_t)e->layers * kAuxLayer; }
-float *layer_tails(GDNEngine *e, int l) {
-    return e->ws + GDN_WS_OFF_HEAD_BUF + (size_t)l * 3 * kTailStripe;
-}
+float *layer_tails(GDNEngine *e, int l) { return e->tails + (size_t)l * 3 * kTailStripe; }
 void *layer_state(GDNEngine *e, int l) {
     const size_t off = (size_t)l * kNH * kHD * kHD;
-    if (e->contract == kRef)
-        return reinterpret_cast<uint16_t *>(e->ws + GDN_WS_OFF_REC_STATE) + off;
-    return e->ws + GDN_WS_OFF_REC_STATE + off;
+    if (e->contract == kRef) return static_cast<uint16_t *>(e->state) + off;
+    return static_cast<float *>(e->state) + off;
+}
+size_t state_floats(const GDNEngine *e) { return (size_t)e->layers * kNH * kHD * kHD; }
+size_t state_bytes(const GDNEngine *e) { return state_floats(e) * (e->contract == kRef ? 2 : 4); }
+size_t tail_floats(const GDNEngine *e) { return (size_t)e->layers * 3 * kTailStripe; }
+
+// Product-counter slots: one per GEMV launch of a step (layer l: 4l QKVG,
+// 4l + 1 o_proj, 4l + 2 gate/up, 4l + 3 down; 4L the LM head), each K lane
+// words and the fast-path verdict.
+constexpr int kDumpStride = kI + 64;
+uint32_t *dump_slot(GDNEngine *e, int slot) {
+    return e->counting ? e->xdump + (size_t)slot * kDumpStride : nullptr;
 }
 
 // Pack rows of BF16-exact FP32 words into the device matrix at `dst`.
+// In verify mode upload() downloads the device copy instead and counts the
+// bytes that differ from the packing (gdn_validate_weight_shards).
 struct Packer {
     int contract;
     std::vector<unsigned char> staging;
+    bool verify = false;
+    size_t mismatches = 0;
     float min_abs = INFINITY;
     float max_abs = 0.0f;
     int nonfinite = 0;
@@ -1472,7 +1519,18 @@ struct Packer {
         filled += n;
     }
     int upload(void *dst) {
-        GDN_HIP(hipMemcpy(dst, staging.data(), filled * welem(contract), hipMemcpyHostToDevice));
+        return transfer(dst, staging.data(), filled * welem(contract));
+    }
+    // H2D of `bytes` at `src`, or in verify mode D2H and compare.
+    int transfer(void *dst, const void *src, size_t bytes) {
+        if (!verify) {
+            GDN_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+            return 0;
+        }
+        std::vector<unsigned char> back(bytes);
+        GDN_HIP(hipMemcpy(back.data(), dst, bytes, hipMemcpyDeviceToHost));
+        const unsigned char *a = back.data(), *b = static_cast<const unsigned char *>(src);
+        for (size_t i = 0; i < bytes; ++i) mismatches += a[i] != b[i];
         return 0;
     }
     WInfo info() const { return WInfo{min_abs, max_abs, nonfinite}; }
@@ -1482,29 +1540,34 @@ int check_shape(const GDNWeightHeader *c) {
     if (c->hidden_size != (uint32_t)kH || c->num_heads != (uint32_t)kNH ||
         c->num_v_heads != (uint32_t)kNH || c->head_dim != (uint32_t)kHD ||
         c->intermediate_size != (uint32_t)kI || c->conv_size != 4u) {
-        gdn_error("gdn: the engine is specialised for hidden 2048, 8x256 heads, "
-                  "intermediate 5632, conv 4");
+        gdn_error("gdn: the kernels are built for hidden 2048, 8 heads of 256, intermediate 5632 "
+                  "and conv width 4; the model header differs");
         return -1;
     }
     if (c->num_layers < 1 || c->num_layers > (uint32_t)kMaxLayers) {
-        gdn_error("gdn: num_layers must be 1..24");
+        std::fprintf(stderr, "gdn: %u layers; the engine takes 1..%d\n", c->num_layers, kMaxLayers);
         return -1;
     }
     if (c->vocab_size == 0 || (c->vocab_size % kRbLm) != 0) {
-        gdn_error("gdn: vocab_size must be a positive multiple of 8");
+        std::fprintf(stderr, "gdn: vocabulary %u is not a positive multiple of %d (the LM head's row block)\n",
+                     c->vocab_size, kRbLm);
         return -1;
     }
     return 0;
 }
 
-int upload_weights(GDNEngine *e, const GDNModel *m) {
+// Packs the model into the device layout and uploads it; with verify set
+// (gdn_validate_weight_shards) compares the device copy with the packing
+// instead and returns the number of differing bytes in *mismatches.
+int upload_weights(GDNEngine *e, const GDNModel *m, bool verify = false, size_t *mismatches = nullptr) {
     const size_t H = kH, I = kI, V = (size_t)e->vocab, L = (size_t)e->layers;
     const size_t per_layer = 4 * H * H + H * H + 2 * I * H + H * I;
     const size_t total = L * per_layer + 2 * V * H;
     const size_t es = welem(e->contract);
-    GDN_HIP(hipMalloc(&e->wmem, total * es));
+    if (!verify) GDN_HIP(hipMalloc(&e->wmem, total * es));
     char *p = static_cast<char *>(e->wmem);
     Packer pk{e->contract, {}};
+    pk.verify = verify;
     for (size_t l = 0; l < L; ++l) {
         const GDNLayerWeights &w = m->layers[l];
         pk.begin(4 * H * H);
@@ -1575,8 +1638,8 @@ int upload_weights(GDNEngine *e, const GDNModel *m) {
         std::memcpy(a + kAuxConv + 2 * H * 4, w.v_conv, H * 4 * 4);
     }
     std::memcpy(aux.data() + L * kAuxLayer, m->final_norm, H * 4);
-    GDN_HIP(hipMalloc(&e->aux, aux.size() * 4));
-    GDN_HIP(hipMemcpy(e->aux, aux.data(), aux.size() * 4, hipMemcpyHostToDevice));
+    if (!verify) GDN_HIP(hipMalloc(&e->aux, aux.size() * 4));
+    if (pk.transfer(e->aux, aux.data(), aux.size() * 4)) return -1;
     // the a/b rows' top halves (the BF16 values under the BF16 contracts'
     // BF16-exact weights; unused by the FP32 contract)
     std::vector<uint16_t> ab16(L * 2 * kNH * H);
@@ -1586,17 +1649,21 @@ int upload_weights(GDNEngine *e, const GDNModel *m) {
             std::memcpy(&b, aux.data() + l * kAuxLayer + kAuxAB + i, 4);
             ab16[l * 2 * kNH * H + i] = (uint16_t)(b >> 16);
         }
-    GDN_HIP(hipMalloc(&e->ab16, ab16.size() * 2));
-    GDN_HIP(hipMemcpy(e->ab16, ab16.data(), ab16.size() * 2, hipMemcpyHostToDevice));
+    if (!verify) GDN_HIP(hipMalloc(&e->ab16, ab16.size() * 2));
+    if (pk.transfer(e->ab16, ab16.data(), ab16.size() * 2)) return -1;
     GDN_HIP(hipDeviceSynchronize());
+    if (mismatches) *mismatches = pk.mismatches;
     return 0;
 }
 
 int alloc_buffers(GDNEngine *e) {
-    GDN_HIP(hipMalloc(&e->ws, (size_t)GDN_WS_FLOATS * 4));
-    GDN_HIP(hipMemset(e->ws, 0, (size_t)GDN_WS_FLOATS * 4));
+    GDN_HIP(hipMalloc(&e->state, state_bytes(e)));
+    GDN_HIP(hipMemset(e->state, 0, state_bytes(e)));
+    GDN_HIP(hipMalloc(&e->tails, tail_floats(e) * 4));
+    GDN_HIP(hipMemset(e->tails, 0, tail_floats(e) * 4));
     const size_t nblk_lm = (size_t)e->vocab / kRbLm;
-    const size_t act_floats = 3 * kH + 3 * kH + 2 * kH + 16 + 2 * kNH + 3 * kH + kI + nblk_lm;
+    const size_t act_floats =
+        3 * kH + 3 * kH + 2 * kH + 16 + 2 * kNH + 3 * kH + kI + nblk_lm + kH + (size_t)e->vocab;
     GDN_HIP(hipMalloc(&e->act, act_floats * 4));
     GDN_HIP(hipMemset(e->act, 0, act_floats * 4));
     float *p = e->act;
@@ -1613,20 +1680,27 @@ int alloc_buffers(GDNEngine *e) {
     e->dbuf = p; p += kH;
     e->hbuf = p; p += kI;
     e->lm_val = p; p += nblk_lm;
+    e->xrow = p; p += kH;
+    e->logits = p; p += e->vocab;
     GDN_HIP(hipMalloc(&e->lm_idx, nblk_lm * sizeof(int)));
     // the step reads its token from and writes its argmax to host memory
     // directly: no copy kernels on a token's path
-    GDN_HIP(hipHostMalloc(&e->tok_host, 2 * sizeof(int), hipHostMallocMapped | hipHostMallocCoherent));
-    e->tok_host[0] = e->tok_host[1] = 0;
+    GDN_HIP(hipHostMalloc(&e->tok_host, 4 * sizeof(int), hipHostMallocMapped | hipHostMallocCoherent));
+    e->tok_host[0] = e->tok_host[1] = e->tok_host[2] = e->tok_host[3] = 0;
     GDN_HIP(hipHostGetDevicePointer(reinterpret_cast<void **>(&e->tok_map), e->tok_host, 0));
     GDN_HIP(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
     GDN_HIP(hipEventCreate(&e->ev0));
     GDN_HIP(hipEventCreate(&e->ev1));
+    if (const char *env = std::getenv("GDN_COUNTER_TRACE")) e->trace_counts = env[0] == '1';
+    if (const char *env = std::getenv("GDN_KERNEL_WAIT_TIMEOUT_MS")) {
+        const double v = std::atof(env);
+        if (v > 0.0) e->timeout_ms = v;
+    }
     return 0;
 }
 
-XSrc xsrc(const float *a, const float *b, const float *c, const float *w, float *res_out,
-          float *aux_out, float eps) {
+XSrc xsrc(GDNEngine *e, const float *a, const float *b, const float *c, const float *w, float *res_out,
+          float *aux_out, uint32_t *xdump) {
     XSrc x{};
     x.a = a;
     x.b = b;
@@ -1634,7 +1708,9 @@ XSrc xsrc(const float *a, const float *b, const float *c, const float *w, float 
     x.w = w;
     x.res_out = res_out;
     x.aux_out = aux_out;
-    x.eps = eps;
+    x.err = e->tok_map + 2;
+    x.xdump = xdump;
+    x.eps = e->eps;
     return x;
 }
 
@@ -1655,12 +1731,12 @@ void launch_qkvg(GDNEngine *e, int l, const float *res_a, const float *res_b, hi
     q.tails = layer_tails(e, l);
     q.ab = e->ab;
     q.bd = e->bd;
-    XSrc xq = xsrc(res_a, res_b, nullptr, aux + kAuxAttnNorm, e->resid, nullptr, e->eps);
+    XSrc xq = xsrc(e, res_a, res_b, nullptr, aux + kAuxAttnNorm, e->resid, nullptr, dump_slot(e, 4 * l));
     if constexpr (PRO0 == PRO_EMBED) {
         xq.emb = e->w_emb;
         xq.tok = e->tok_map;
         xq.vocab = e->vocab;
-        xq.aux_out = e->ws + GDN_WS_OFF_X;
+        xq.aux_out = e->xrow;
     }
     if constexpr (C == kFp32) {
         hipLaunchKernelGGL((k_gemv<C, kH, kRbQkvg, PRO0, EPI_QKVG>), dim3(4 * kH / kRbQkvg + kAbBlocks),
@@ -1681,7 +1757,8 @@ template <int C>
 void launch_o(GDNEngine *e, int l, hipStream_t s) {
     Epi st{};
     st.y = e->ybuf_o;
-    const XSrc xo = xsrc(e->attn, e->gate, e->sgate, layer_aux(e, l) + kAuxONorm, nullptr, nullptr, e->eps);
+    const XSrc xo = xsrc(e, e->attn, e->gate, e->sgate, layer_aux(e, l) + kAuxONorm, nullptr, nullptr,
+                         dump_slot(e, 4 * l + 1));
     if constexpr (C == kFp32) {
         hipLaunchKernelGGL((k_gemv<C, kH, kRbO, PRO_ONORM, EPI_STORE>), dim3(kH / kRbO), dim3(kT), 0, s,
                            e->w_o[l], e->i_o[l], xo, st);
@@ -1695,8 +1772,8 @@ template <int C>
 void launch_gu(GDNEngine *e, int l, hipStream_t s) {
     Epi sw{};
     sw.y = e->hbuf;
-    const XSrc xg = xsrc(e->resid, e->ybuf_o, nullptr, layer_aux(e, l) + kAuxMlpNorm, e->resid_alt,
-                         nullptr, e->eps);
+    const XSrc xg = xsrc(e, e->resid, e->ybuf_o, nullptr, layer_aux(e, l) + kAuxMlpNorm, e->resid_alt,
+                         nullptr, dump_slot(e, 4 * l + 2));
     if constexpr (C == kFp32) {
         hipLaunchKernelGGL((k_gemv<C, kH, kRbGu, PRO_RESNORM, EPI_SWIGLU>), dim3(2 * kI / kRbGu), dim3(kT),
                            0, s, e->w_gu[l], e->i_gu[l], xg, sw);
@@ -1710,7 +1787,7 @@ template <int C>
 void launch_down(GDNEngine *e, int l, hipStream_t s) {
     Epi dn{};
     dn.y = e->dbuf;
-    const XSrc xd = xsrc(e->hbuf, nullptr, nullptr, nullptr, nullptr, nullptr, e->eps);
+    const XSrc xd = xsrc(e, e->hbuf, nullptr, nullptr, nullptr, nullptr, nullptr, dump_slot(e, 4 * l + 3));
     if constexpr (C == kFp32) {
         hipLaunchKernelGGL((k_gemv<C, kI, kRbDown, PRO_PLAIN, EPI_STORE>), dim3(kH / kRbDown), dim3(kT), 0,
                            s, e->w_down[l], e->i_down[l], xd, dn);
@@ -1729,10 +1806,11 @@ int lm_blocks(const GDNEngine *e) {
 template <int C>
 void launch_lm(GDNEngine *e, hipStream_t s) {
     Epi lm{};
-    lm.y = e->ws + GDN_WS_OFF_LOGITS;
+    lm.y = e->logits;
     lm.part_val = e->lm_val;
     lm.part_idx = e->lm_idx;
-    const XSrc xl = xsrc(e->resid_alt, e->dbuf, nullptr, final_norm(e), e->resid, e->fhid, e->eps);
+    const XSrc xl = xsrc(e, e->resid_alt, e->dbuf, nullptr, final_norm(e), e->resid, e->fhid,
+                         dump_slot(e, 4 * e->layers));
     const dim3 grid(lm_blocks(e));
     if constexpr (C == kFp32) {
         hipLaunchKernelGGL((k_gemv<C, kH, kRbLm, PRO_RESNORM, EPI_LM>), grid, dim3(kT), 0, s, e->w_lm,
@@ -1747,8 +1825,7 @@ void launch_lm(GDNEngine *e, hipStream_t s) {
 }
 
 void launch_argmax(GDNEngine *e, hipStream_t s) {
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(kT), 0, s, e->lm_val, e->lm_idx, lm_blocks(e),
-                       e->tok_map + 1, e->ws + GDN_WS_OFF_X_NORM);
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(kT), 0, s, e->lm_val, e->lm_idx, lm_blocks(e), e->tok_map + 1);
 }
 
 template <int C, int PRO0>
@@ -1824,10 +1901,45 @@ int ensure_graph(GDNEngine *e) {
     return 0;
 }
 
+void drop_graph(GDNEngine *e) {
+    if (e->exec) (void)hipGraphExecDestroy(e->exec);
+    if (e->graph) (void)hipGraphDestroy(e->graph);
+    e->exec = nullptr;
+    e->graph = nullptr;
+}
+
+// Waits for the step's argmax to land in host memory (the last kernel
+// writes it), with a deadline, then checks the kernels' error word.
+int wait_step(GDNEngine *e) {
+    const auto t0 = std::chrono::steady_clock::now();
+    const auto limit = std::chrono::duration<double, std::milli>(e->timeout_ms);
+    unsigned polls = 0;
+    while (__atomic_load_n(&e->tok_host[1], __ATOMIC_ACQUIRE) < 0) {
+        if ((++polls & 15u) == 0 && std::chrono::steady_clock::now() - t0 > limit) {
+            std::fprintf(stderr, "gdn: decode step did not finish within %.0f ms (GDN_KERNEL_WAIT_TIMEOUT_MS)\n",
+                         e->timeout_ms);
+            e->failed = true;
+            return -1;
+        }
+        __builtin_ia32_pause();
+    }
+    if (__atomic_load_n(&e->tok_host[2], __ATOMIC_ACQUIRE) != 0) {
+        gdn_error("gdn: a kernel's bounded wait ran out; the step's results are not valid");
+        e->failed = true;
+        return -1;
+    }
+    return 0;
+}
+
 // Token in (host) -> kernels -> token out (host).  Times when asked.
 int run_step(GDNEngine *e, int32_t token, int32_t *tok_out, float *inner_ms) {
+    if (e->failed) {
+        gdn_error("gdn: this run state failed an earlier step");
+        return -1;
+    }
     if (e->use_graph && ensure_graph(e) != 0) return -1;
     e->tok_host[0] = token;  // read by layer 0's kernel through tok_map
+    __atomic_store_n(&e->tok_host[1], -1, __ATOMIC_RELEASE);
     if (inner_ms) GDN_HIP(hipEventRecord(e->ev0, e->stream));
     if (e->use_graph) {
         GDN_HIP(hipGraphLaunch(e->exec, e->stream));
@@ -1836,207 +1948,167 @@ int run_step(GDNEngine *e, int32_t token, int32_t *tok_out, float *inner_ms) {
         GDN_HIP(hipGetLastError());
     }
     if (inner_ms) GDN_HIP(hipEventRecord(e->ev1, e->stream));
-    GDN_HIP(hipStreamSynchronize(e->stream));  // k_argmax wrote tok_host[1]
+    if (wait_step(e) != 0) return -1;
     if (tok_out) *tok_out = e->tok_host[1];
-    if (inner_ms) GDN_HIP(hipEventElapsedTime(inner_ms, e->ev0, e->ev1));
+    if (inner_ms) {
+        GDN_HIP(hipEventSynchronize(e->ev1));
+        GDN_HIP(hipEventElapsedTime(inner_ms, e->ev0, e->ev1));
+    }
     return 0;
 }
 
+// Device -> host copy ordered after the engine's work.
+int d2h(GDNEngine *e, void *dst, const void *src, size_t bytes) {
+    GDN_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, e->stream));
+    GDN_HIP(hipStreamSynchronize(e->stream));
+    return 0;
+}
+
+int h2d(GDNEngine *e, void *dst, const void *src, size_t bytes) {
+    GDN_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, e->stream));
+    GDN_HIP(hipStreamSynchronize(e->stream));
+    return 0;
+}
+
+// Host buffers behind the reference's run-state fields.
+struct HostMirror {
+    GDNEngine *engine = nullptr;
+    float *workspace = nullptr;          // GDN_WS_FLOATS floats
+    Beat512 *stripes[GDN_RECURRENT_STATE_PORTS] = {};
+};
+
+// The host buffers of every live run state: the reference's state packers
+// receive only a stripe array or a head_buffer pointer, which identify
+// their run state here.
+std::mutex g_mirrors_mu;
+std::vector<HostMirror> g_mirrors;
+
 void destroy_engine(GDNEngine *e) {
     if (!e) return;
-    if (e->exec) (void)hipGraphExecDestroy(e->exec);
-    if (e->graph) (void)hipGraphDestroy(e->graph);
+    // a step that missed its deadline may still be running: let it finish
+    // before its buffers go
+    if (e->stream) (void)hipStreamSynchronize(e->stream);
+    {
+        std::lock_guard<std::mutex> lock(g_mirrors_mu);
+        for (size_t i = 0; i < g_mirrors.size(); ++i) {
+            if (g_mirrors[i].engine != e) continue;
+            std::free(g_mirrors[i].workspace);
+            for (Beat512 *st : g_mirrors[i].stripes) std::free(st);
+            g_mirrors.erase(g_mirrors.begin() + (long)i);
+            break;
+        }
+    }
+    drop_graph(e);
     if (e->ev0) (void)hipEventDestroy(e->ev0);
     if (e->ev1) (void)hipEventDestroy(e->ev1);
     if (e->stream) (void)hipStreamDestroy(e->stream);
     (void)hipFree(e->wmem);
     (void)hipFree(e->aux);
     (void)hipFree(e->ab16);
-    (void)hipFree(e->ws);
+    (void)hipFree(e->state);
+    (void)hipFree(e->tails);
     (void)hipFree(e->act);
     (void)hipFree(e->lm_idx);
+    (void)hipFree(e->xdump);
     if (e->tok_host) (void)hipHostFree(e->tok_host);
     delete e;
 }
 
-bool bf16_exact(float v) {
-    uint32_t b;
-    std::memcpy(&b, &v, 4);
-    return (b & 0xffffu) == 0;
-}
-
-}  // namespace
-
-// ================================================================== C ABI
-
-extern "C" {
-
-int gdn_run_state_init_contract(GDNRunState *state, const GDNModel *model, uint32_t max_tokens,
-                                int contract) {
-    std::memset(state, 0, sizeof(*state));
-    if (max_tokens == 0 || max_tokens > model->config.max_seq_len) {
-        gdn_error("invalid max_tokens for run state");
-        return -1;
+GDNEngine *engine_of(const GDNRunState *state) {
+    if (state == nullptr || state->engine == nullptr) {
+        gdn_error("gdn: the run state is not initialised");
+        return nullptr;
     }
-    if (contract < kRef || contract > kFp32) {
-        gdn_error("gdn: unknown contract");
-        return -1;
-    }
-    if (check_shape(&model->config) != 0) return -1;
-    if (contract != kFp32 && gdn_validate_bf16_exact_weights(model->weight_data, &model->config) != 0) {
-        gdn_error("gdn: BF16 contracts need a BF16-exact checkpoint");
-        return -1;
-    }
-    GDNEngine *e = new GDNEngine();
-    e->contract = contract;
-    e->layers = (int)model->config.num_layers;
-    e->vocab = (int)model->config.vocab_size;
-    e->eps = model->config.norm_eps;
-    if (alloc_buffers(e) != 0 || upload_weights(e, model) != 0) {
-        destroy_engine(e);
-        return -1;
-    }
-    state->engine = e;
-    state->workspace = e->ws;
-    state->x = e->ws + GDN_WS_OFF_X;
-    state->recurrent_state = e->ws + GDN_WS_OFF_REC_STATE;
-    state->head_buffer = e->ws + GDN_WS_OFF_HEAD_BUF;
-    return 0;
+    return state->engine;
 }
 
-int gdn_run_state_init(GDNRunState *state, const GDNModel *model, uint32_t max_tokens) {
-    return gdn_run_state_init_contract(state, model, max_tokens, kRef);
-}
-
-void gdn_run_state_free(GDNRunState *state) {
-    destroy_engine(state->engine);
-    std::memset(state, 0, sizeof(*state));
-}
-
-int gdn_get_contract(const GDNRunState *state) {
-    return state->engine ? state->engine->contract : -1;
-}
-
-int gdn_set_graph_mode(GDNRunState *state, int use_graph) {
-    if (!state->engine) return -1;
-    state->engine->use_graph = use_graph != 0;
-    return 0;
-}
-
-int gdn_decode_step_host(const GDNModel *model, GDNRunState *state, const int32_t *token) {
-    if (*token < 0 || (uint32_t)*token >= model->config.vocab_size) {
-        gdn_error("token id out of range");
-        return -1;
-    }
-    if (!state->engine) {
-        gdn_error("gdn: run state not initialised");
-        return -1;
-    }
-    return run_step(state->engine, *token, nullptr, nullptr);
-}
-
-int gdn_read_token(const GDNRunState *state, int32_t *token) {
-    GDN_HIP(hipStreamSynchronize(state->engine->stream));
-    *token = state->engine->tok_host[1];
-    return 0;
-}
-
-int gdn_read_logits(const GDNRunState *state, float *logits, size_t count) {
-    if (count > (size_t)state->engine->vocab) return -1;
-    GDN_HIP(hipMemcpy(logits, state->engine->ws + GDN_WS_OFF_LOGITS, count * 4, hipMemcpyDeviceToHost));
-    return 0;
-}
-
-int gdn_read_final_hidden(const GDNRunState *state, float *hidden, size_t count) {
-    if (count > (size_t)kH) return -1;
-    GDN_HIP(hipMemcpy(hidden, state->engine->fhid, count * 4, hipMemcpyDeviceToHost));
-    return 0;
-}
-
-int gdn_load_recurrent_state(GDNRunState *state, const float *rec, size_t floats) {
-    GDNEngine *e = state->engine;
-    const size_t n = (size_t)e->layers * kNH * kHD * kHD;
+// Recurrent state [L][8][256][256] FP32 words <-> the device (BF16 bits for
+// REF, whose values must then be BF16-exact).
+int load_state(GDNEngine *e, const float *rec, size_t floats) {
+    const size_t n = state_floats(e);
     if (floats != n) {
-        gdn_error("recurrent state size does not match the model");
+        std::fprintf(stderr, "gdn: recurrent state of %zu values given; the model's is %zu\n", floats, n);
         return -1;
     }
     if (e->contract == kRef) {
+        const size_t bad = gdn_first_non_bf16(rec, n);
+        if (bad != n) {
+            gdn_report_non_bf16("REF-contract recurrent state", rec, bad);
+            return -1;
+        }
         std::vector<uint16_t> b(n);
         for (size_t i = 0; i < n; ++i) {
-            if (!bf16_exact(rec[i])) {
-                std::fprintf(stderr, "gdn: recurrent state %zu is not BF16-exact\n", i);
-                return -1;
-            }
             uint32_t u;
             std::memcpy(&u, rec + i, 4);
             b[i] = (uint16_t)(u >> 16);
         }
-        GDN_HIP(hipMemcpy(layer_state(e, 0), b.data(), n * 2, hipMemcpyHostToDevice));
-    } else {
-        GDN_HIP(hipMemcpy(layer_state(e, 0), rec, n * 4, hipMemcpyHostToDevice));
+        return h2d(e, e->state, b.data(), n * 2);
     }
-    GDN_HIP(hipDeviceSynchronize());
-    return 0;
+    return h2d(e, e->state, rec, n * 4);
 }
 
-int gdn_save_recurrent_state(const GDNRunState *state, float *rec, size_t floats) {
-    GDNEngine *e = state->engine;
-    const size_t n = (size_t)e->layers * kNH * kHD * kHD;
-    if (floats != n) return -1;
+int save_state(GDNEngine *e, float *rec, size_t floats) {
+    const size_t n = state_floats(e);
+    if (floats != n) {
+        std::fprintf(stderr, "gdn: recurrent state buffer of %zu values; the model's is %zu\n", floats, n);
+        return -1;
+    }
     if (e->contract == kRef) {
         std::vector<uint16_t> b(n);
-        GDN_HIP(hipMemcpy(b.data(), layer_state(e, 0), n * 2, hipMemcpyDeviceToHost));
+        if (d2h(e, b.data(), e->state, n * 2)) return -1;
         for (size_t i = 0; i < n; ++i) {
             const uint32_t u = (uint32_t)b[i] << 16;
             std::memcpy(rec + i, &u, 4);
         }
-    } else {
-        GDN_HIP(hipMemcpy(rec, layer_state(e, 0), n * 4, hipMemcpyDeviceToHost));
+        return 0;
     }
-    return 0;
+    return d2h(e, rec, e->state, n * 4);
 }
 
-// .gdnstate conv section [L][q,k,v][W-1][H] <-> per-stripe device tails.
-int gdn_load_conv_tails(GDNRunState *state, const float *conv, size_t floats) {
-    GDNEngine *e = state->engine;
+// .gdnstate conv section [L][q,k,v][W-1][H] <-> the device's tail stripes.
+int load_tails(GDNEngine *e, const float *conv, size_t floats) {
     const size_t stripes = (size_t)e->layers * 3, per = 3 * (size_t)kH;
     if (floats != stripes * per) {
-        gdn_error("convolution-tail size does not match the model");
+        std::fprintf(stderr, "gdn: conv tails of %zu values given; the model's are %zu\n", floats, stripes * per);
         return -1;
     }
+    if (e->contract != kFp32) {
+        const size_t bad = gdn_first_non_bf16(conv, floats);
+        if (bad != floats) {
+            gdn_report_non_bf16("BF16-contract conv tail", conv, bad);
+            return -1;
+        }
+    }
     std::vector<float> img(stripes * kTailStripe, 0.0f);
-    for (size_t s = 0; s < stripes; ++s) {
-        float *dst = img.data() + s * kTailStripe;
-        const float *src = conv + s * per;
+    for (size_t st = 0; st < stripes; ++st) {
+        float *dst = img.data() + st * kTailStripe;
+        const float *src = conv + st * per;
         if (e->contract == kFp32) {
             std::memcpy(dst, src, per * 4);
         } else {
             uint16_t *d16 = reinterpret_cast<uint16_t *>(dst);
             for (size_t i = 0; i < per; ++i) {
-                if (!bf16_exact(src[i])) {
-                    std::fprintf(stderr, "gdn: convolution tail %zu is not BF16-exact\n", s * per + i);
-                    return -1;
-                }
                 uint32_t u;
                 std::memcpy(&u, src + i, 4);
                 d16[i] = (uint16_t)(u >> 16);
             }
         }
     }
-    GDN_HIP(hipMemcpy(e->ws + GDN_WS_OFF_HEAD_BUF, img.data(), img.size() * 4, hipMemcpyHostToDevice));
-    GDN_HIP(hipDeviceSynchronize());
-    return 0;
+    return h2d(e, e->tails, img.data(), img.size() * 4);
 }
 
-int gdn_save_conv_tails(const GDNRunState *state, float *conv, size_t floats) {
-    GDNEngine *e = state->engine;
+int save_tails(GDNEngine *e, float *conv, size_t floats) {
     const size_t stripes = (size_t)e->layers * 3, per = 3 * (size_t)kH;
-    if (floats != stripes * per) return -1;
+    if (floats != stripes * per) {
+        std::fprintf(stderr, "gdn: conv-tail buffer of %zu values; the model's tails are %zu\n", floats,
+                     stripes * per);
+        return -1;
+    }
     std::vector<float> img(stripes * kTailStripe);
-    GDN_HIP(hipMemcpy(img.data(), e->ws + GDN_WS_OFF_HEAD_BUF, img.size() * 4, hipMemcpyDeviceToHost));
-    for (size_t s = 0; s < stripes; ++s) {
-        const float *src = img.data() + s * kTailStripe;
-        float *dst = conv + s * per;
+    if (d2h(e, img.data(), e->tails, img.size() * 4)) return -1;
+    for (size_t st = 0; st < stripes; ++st) {
+        const float *src = img.data() + st * kTailStripe;
+        float *dst = conv + st * per;
         if (e->contract == kFp32) {
             std::memcpy(dst, src, per * 4);
         } else {
@@ -2050,17 +2122,391 @@ int gdn_save_conv_tails(const GDNRunState *state, float *conv, size_t floats) {
     return 0;
 }
 
-int gdn_run_teacher_forced(GDNRunState *state, const int32_t *tokens, uint32_t n_tokens,
-                           uint32_t n_steps, int32_t *argmax_out, float *inner_ms,
-                           float *outer_ms) {
-    GDNEngine *e = state->engine;
-    if (!e || n_tokens == 0) return -1;
-    for (uint32_t i = 0; i < n_tokens; ++i) {
-        if (tokens[i] < 0 || tokens[i] >= e->vocab) {
-            gdn_error("token id out of range");
+// ---- native-product counters of a decode step (counting mode) ----
+
+// The weight matrices of one counter slot, as row blocks of the host model.
+struct SlotRows {
+    const float *w[4];
+    size_t rows[4];
+    int n;
+    int K;
+};
+
+SlotRows slot_rows(const GDNModel *m, int layers, int slot) {
+    SlotRows r{};
+    if (slot == 4 * layers) {
+        r.w[0] = m->lm_head;
+        r.rows[0] = m->config.vocab_size;
+        r.n = 1;
+        r.K = kH;
+        return r;
+    }
+    const GDNLayerWeights &lw = m->layers[slot / 4];
+    switch (slot % 4) {
+    case 0:
+        r.w[0] = lw.q_proj; r.w[1] = lw.k_proj; r.w[2] = lw.v_proj; r.w[3] = lw.g_proj;
+        r.rows[0] = r.rows[1] = r.rows[2] = r.rows[3] = kH;
+        r.n = 4;
+        r.K = kH;
+        break;
+    case 1:
+        r.w[0] = lw.o_proj; r.rows[0] = kH; r.n = 1; r.K = kH;
+        break;
+    case 2:
+        r.w[0] = lw.mlp_gate_proj; r.w[1] = lw.mlp_up_proj;
+        r.rows[0] = r.rows[1] = kI; r.n = 2; r.K = kH;
+        break;
+    default:
+        r.w[0] = lw.mlp_down_proj; r.rows[0] = kH; r.n = 1; r.K = kI;
+        break;
+    }
+    return r;
+}
+
+int count_step_products(GDNEngine *e, const GDNModel *m) {
+    if (e->contract == kFp32) return 0;  // FP32 products: no native multiplier
+    const int slots = 4 * e->layers + 1;
+    if (e->cols.empty()) {
+        e->cols.resize((size_t)slots);
+        for (int sl = 0; sl < slots; ++sl) {
+            const SlotRows r = slot_rows(m, e->layers, sl);
+            ColCounts &c = e->cols[(size_t)sl];
+            c.spec.assign((size_t)r.K, 0u);
+            c.sub.assign((size_t)r.K, 0u);
+            for (int i = 0; i < r.n; ++i)
+                gdn_weight_column_counts(r.w[i], r.rows[i], (size_t)r.K, c.spec.data(), c.sub.data());
+        }
+    }
+    std::vector<uint32_t> dump((size_t)slots * kDumpStride);
+    if (d2h(e, dump.data(), e->xdump, dump.size() * 4)) return -1;
+    uint64_t calls = 0, special = 0, flushed_in = 0, flushed_out = 0, overflow = 0;
+    std::vector<uint16_t> xb(kI);
+    for (int sl = 0; sl < slots; ++sl) {
+        const SlotRows r = slot_rows(m, e->layers, sl);
+        const uint32_t *words = dump.data() + (size_t)sl * kDumpStride;
+        const ColCounts &c = e->cols[(size_t)sl];
+        size_t M = 0;
+        for (int i = 0; i < r.n; ++i) M += r.rows[i];
+        uint64_t x_special = 0, w_special = 0;
+        for (int k = 0; k < r.K; ++k) {
+            const uint16_t b = (uint16_t)((k & 1) ? words[k] >> 16 : words[k] & 0xffffu);
+            xb[(size_t)k] = b;
+            const uint32_t ex = (b >> 7) & 0xffu;
+            const bool spec = ex == 0 || ex == 0xffu, sub = ex == 0 && (b & 0x7fu) != 0;
+            calls += M;
+            special += spec ? M : c.spec[(size_t)k];
+            flushed_in += sub ? M : c.sub[(size_t)k];
+            x_special += spec;
+            w_special += spec ? 0 : c.spec[(size_t)k];
+        }
+        if (e->trace_counts && (x_special || w_special))
+            std::fprintf(stderr, "gdn counters: slot %d (K %d, M %zu): %llu special inputs, %llu special weights "
+                         "met by normal inputs, fast path %u\n", sl, r.K, M, (unsigned long long)x_special,
+                         (unsigned long long)w_special, words[r.K]);
+        if (words[r.K] == 0) {
+            // the kernel ran its exact per-product path: count each product's
+            // outcome (the fast-path verdict excludes flushes and overflows)
+            for (int i = 0; i < r.n; ++i)
+                gdn_count_native_outcomes(r.w[i], r.rows[i], (size_t)r.K, xb.data(), &flushed_out, &overflow);
+        }
+    }
+    gdn_stats_add(calls, special, flushed_in, flushed_out, overflow);
+    return 0;
+}
+
+// Turns the engine's per-step counting on or off to match the process-wide
+// switch; the captured graph carries the dump pointers, so it is rebuilt.
+int sync_counting(GDNEngine *e) {
+    const bool want = gdn_stats_counting() != 0 && e->contract != kFp32;
+    if (want == e->counting) return 0;
+    if (want && !e->xdump)
+        GDN_HIP(hipMalloc(&e->xdump, (size_t)(4 * e->layers + 1) * kDumpStride * 4));
+    e->counting = want;
+    drop_graph(e);
+    return 0;
+}
+
+float *g_debug_hidden = nullptr;
+float *g_debug_logits = nullptr;
+
+}  // namespace
+
+// ================================================================== C ABI
+
+extern "C" {
+
+int gdn_run_state_init_contract(GDNRunState *state, const GDNModel *model, uint32_t max_tokens,
+                                int contract) {
+    std::memset(state, 0, sizeof(*state));
+    if (max_tokens == 0 || max_tokens > model->config.max_seq_len) {
+        std::fprintf(stderr, "gdn_run_state_init: max_tokens %u is outside 1..max_seq_len (%u)\n", max_tokens,
+                     model->config.max_seq_len);
+        return -1;
+    }
+    if (contract < kRef || contract > kFp32) {
+        std::fprintf(stderr, "gdn_run_state_init: unknown contract %d\n", contract);
+        return -1;
+    }
+    if (check_shape(&model->config) != 0) return -1;
+    if (contract != kFp32 && gdn_validate_bf16_exact_weights(model->weight_data, &model->config) != 0) {
+        gdn_error("gdn: the BF16 contracts take a BF16-valued checkpoint");
+        return -1;
+    }
+    HostMirror hm;
+    hm.workspace = static_cast<float *>(std::aligned_alloc(64, (size_t)GDN_WS_FLOATS * 4));
+    bool ok = hm.workspace != nullptr;
+    for (int p = 0; ok && p < GDN_RECURRENT_STATE_PORTS; ++p) {
+        hm.stripes[p] = static_cast<Beat512 *>(
+            std::aligned_alloc(64, (size_t)GDN_RECURRENT_STATE_STRIPE_BF16_BEATS * sizeof(Beat512)));
+        ok = hm.stripes[p] != nullptr;
+    }
+    if (!ok) {
+        gdn_error("gdn_run_state_init: host allocation failed");
+        std::free(hm.workspace);
+        for (Beat512 *st : hm.stripes) std::free(st);
+        return -1;
+    }
+    std::memset(hm.workspace, 0, (size_t)GDN_WS_FLOATS * 4);
+    for (Beat512 *st : hm.stripes) std::memset(st, 0, (size_t)GDN_RECURRENT_STATE_STRIPE_BF16_BEATS * 64);
+    GDNEngine *e = new GDNEngine();
+    e->contract = contract;
+    e->layers = (int)model->config.num_layers;
+    e->vocab = (int)model->config.vocab_size;
+    e->eps = model->config.norm_eps;
+    hm.engine = e;
+    {
+        std::lock_guard<std::mutex> lock(g_mirrors_mu);
+        g_mirrors.push_back(hm);
+    }
+    if (alloc_buffers(e) != 0 || upload_weights(e, model) != 0) {
+        destroy_engine(e);
+        return -1;
+    }
+    state->engine = e;
+    state->workspace = reinterpret_cast<Beat512 *>(hm.workspace);
+    state->x = hm.workspace + GDN_WS_OFF_X;
+    state->recurrent_state = hm.workspace + GDN_WS_OFF_REC_STATE;
+    state->head_buffer = hm.workspace + GDN_WS_OFF_HEAD_BUF;
+    for (int p = 0; p < GDN_RECURRENT_STATE_PORTS; ++p)
+        state->weight_shards[GDN_RECURRENT_STATE_FIRST_PORT + p] = hm.stripes[p];
+    return 0;
+}
+
+int gdn_run_state_init(GDNRunState *state, const GDNModel *model, uint32_t max_tokens) {
+    return gdn_run_state_init_contract(state, model, max_tokens, kRef);
+}
+
+void gdn_run_state_free(GDNRunState *state) {
+    destroy_engine(state->engine);
+    std::memset(state, 0, sizeof(*state));
+}
+
+int gdn_get_contract(const GDNRunState *state) {
+    return state && state->engine ? state->engine->contract : -1;
+}
+
+int gdn_set_graph_mode(GDNRunState *state, int use_graph) {
+    GDNEngine *e = engine_of(state);
+    if (!e) return -1;
+    e->use_graph = use_graph != 0;
+    return 0;
+}
+
+int gdn_decode_step_host(const GDNModel *model, GDNRunState *state, const int32_t *token) {
+    if (*token < 0 || (uint32_t)*token >= model->config.vocab_size) {
+        std::fprintf(stderr, "gdn: token %d is outside the vocabulary [0, %u)\n", *token,
+                     model->config.vocab_size);
+        return -1;
+    }
+    GDNEngine *e = engine_of(state);
+    if (!e || sync_counting(e) != 0) return -1;
+    // the reference's host stages the FP32 embedding row in workspace X
+    std::memcpy(state->x, model->embeddings + (size_t)*token * kH, (size_t)kH * 4);
+    int32_t out = 0;
+    if (run_step(e, *token, &out, nullptr) != 0) return -1;
+    reinterpret_cast<float *>(state->workspace)[GDN_WS_OFF_X_NORM] = (float)out;  // the token line
+    if (g_debug_hidden && d2h(e, g_debug_hidden, e->fhid, (size_t)kH * 4)) return -1;
+    if (g_debug_logits && d2h(e, g_debug_logits, e->logits, (size_t)e->vocab * 4)) return -1;
+    if (e->counting && count_step_products(e, model) != 0) return -1;
+    return 0;
+}
+
+int gdn_read_token(const GDNRunState *state, int32_t *token) {
+    GDNEngine *e = engine_of(state);
+    if (!e) return -1;
+    GDN_HIP(hipStreamSynchronize(e->stream));
+    *token = e->tok_host[1];
+    return 0;
+}
+
+int gdn_read_logits(const GDNRunState *state, float *logits, size_t count) {
+    GDNEngine *e = engine_of(state);
+    if (!e) return -1;
+    if (count > (size_t)e->vocab) {
+        std::fprintf(stderr, "gdn_read_logits: %zu values asked, the vocabulary has %d\n", count, e->vocab);
+        return -1;
+    }
+    return d2h(e, logits, e->logits, count * 4);
+}
+
+int gdn_read_final_hidden(const GDNRunState *state, float *hidden, size_t count) {
+    GDNEngine *e = engine_of(state);
+    if (!e) return -1;
+    if (count > (size_t)kH) {
+        std::fprintf(stderr, "gdn_read_final_hidden: %zu values asked, the hidden size is %d\n", count, kH);
+        return -1;
+    }
+    return d2h(e, hidden, e->fhid, count * 4);
+}
+
+int gdn_load_recurrent_state(GDNRunState *state, const float *rec, size_t floats) {
+    GDNEngine *e = engine_of(state);
+    return e ? load_state(e, rec, floats) : -1;
+}
+
+int gdn_save_recurrent_state(const GDNRunState *state, float *rec, size_t floats) {
+    GDNEngine *e = engine_of(state);
+    return e ? save_state(e, rec, floats) : -1;
+}
+
+int gdn_load_conv_tails(GDNRunState *state, const float *conv, size_t floats) {
+    GDNEngine *e = engine_of(state);
+    return e ? load_tails(e, conv, floats) : -1;
+}
+
+int gdn_save_conv_tails(const GDNRunState *state, float *conv, size_t floats) {
+    GDNEngine *e = engine_of(state);
+    return e ? save_tails(e, conv, floats) : -1;
+}
+
+// ---- the reference's remaining run-state calls (gdn_model.h:170-210, :274) ----
+
+size_t gdn_weight_shard_beats(const GDNWeightHeader *config) {
+    (void)config;
+    return 0;
+}
+
+size_t gdn_weight_shard_bytes(const GDNWeightHeader *config) {
+    (void)config;
+    return 0;
+}
+
+int gdn_validate_weight_shards(const float *weight_data, const GDNWeightHeader *config, Beat512 *const shards[]) {
+    GDNEngine *e = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_mirrors_mu);
+        for (auto &m : g_mirrors)
+            if (shards != nullptr && m.stripes[0] == shards[GDN_RECURRENT_STATE_FIRST_PORT]) e = m.engine;
+    }
+    if (!e) {
+        gdn_error("gdn_validate_weight_shards: the shard array belongs to no live run state");
+        return -1;
+    }
+    if (config->vocab_size != (uint32_t)e->vocab || config->num_layers != (uint32_t)e->layers) {
+        gdn_error("gdn_validate_weight_shards: the header does not describe this run state's model");
+        return -1;
+    }
+    GDNModel view;
+    if (gdn_model_wrap(&view, config, weight_data) != 0) return -1;
+    size_t bad = 0;
+    const int rc = upload_weights(e, &view, /*verify=*/true, &bad);
+    std::free(view.layers);
+    if (rc != 0) return -1;
+    if (bad != 0) {
+        std::fprintf(stderr, "gdn_validate_weight_shards: %zu device bytes differ from the packed weights\n", bad);
+        return -1;
+    }
+    return 0;
+}
+
+int gdn_scatter_recurrent_state(Beat512 *const state_stripes[], const float *rec, size_t floats) {
+    if (state_stripes == nullptr || floats % kHD != 0) {
+        gdn_error("gdn_scatter_recurrent_state: no stripes, or the state is not whole 256-value rows");
+        return -1;
+    }
+    GDNEngine *e = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_mirrors_mu);
+        for (auto &m : g_mirrors)
+            if (m.stripes[0] == state_stripes[0]) e = m.engine;
+    }
+    // stripes of a run state: the values go to its engine (which checks
+    // them for its contract); other stripes are packed only, BF16-exact
+    // values required, as the reference's packer does
+    if (e != nullptr) {
+        if (load_state(e, rec, floats) != 0) return -1;
+    } else {
+        const size_t bad = gdn_first_non_bf16(rec, floats);
+        if (bad != floats) {
+            gdn_report_non_bf16("recurrent state", rec, bad);
             return -1;
         }
     }
+    gdn_pack_state_stripes(rec, floats / kHD, state_stripes);
+    return 0;
+}
+
+int gdn_pack_conv_tails_bf16(Beat512 *head_buffer, const float *conv, size_t floats) {
+    if (head_buffer == nullptr) {
+        gdn_error("gdn_pack_conv_tails_bf16: no head buffer");
+        return -1;
+    }
+    GDNEngine *e = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_mirrors_mu);
+        for (auto &m : g_mirrors)
+            if (reinterpret_cast<float *>(head_buffer) == m.workspace + GDN_WS_OFF_HEAD_BUF) e = m.engine;
+    }
+    if (e != nullptr) {
+        if (load_tails(e, conv, floats) != 0) return -1;
+    } else {
+        if (floats != GDN_WSF_HEADBUF) {
+            std::fprintf(stderr, "gdn_pack_conv_tails_bf16: %zu values; the workspace holds %u\n", floats,
+                         GDN_WSF_HEADBUF);
+            return -1;
+        }
+        const size_t bad = gdn_first_non_bf16(conv, floats);
+        if (bad != floats) {
+            gdn_report_non_bf16("conv tail", conv, bad);
+            return -1;
+        }
+    }
+    gdn_pack_tail_stripes(conv, floats / (3 * (size_t)kH), reinterpret_cast<float *>(head_buffer));
+    return 0;
+}
+
+int gdn_sync_host_state(GDNRunState *state) {
+    GDNEngine *e = engine_of(state);
+    if (!e) return -1;
+    std::vector<float> rec(state_floats(e)), conv((size_t)e->layers * 9 * kH);
+    if (save_state(e, rec.data(), rec.size()) != 0 || save_tails(e, conv.data(), conv.size()) != 0) return -1;
+    gdn_pack_state_stripes(rec.data(), rec.size() / kHD, state->weight_shards + GDN_RECURRENT_STATE_FIRST_PORT);
+    gdn_pack_tail_stripes(conv.data(), (size_t)e->layers * 3, state->head_buffer);
+    return 0;
+}
+
+void gdn_set_native_debug_buffers(float *final_hidden, float *logits) {
+    g_debug_hidden = final_hidden;
+    g_debug_logits = logits;
+}
+
+int gdn_run_teacher_forced(GDNRunState *state, const int32_t *tokens, uint32_t n_tokens,
+                           uint32_t n_steps, int32_t *argmax_out, float *inner_ms,
+                           float *outer_ms) {
+    GDNEngine *e = engine_of(state);
+    if (!e) return -1;
+    if (n_tokens == 0) {
+        gdn_error("gdn_run_teacher_forced: no tokens");
+        return -1;
+    }
+    for (uint32_t i = 0; i < n_tokens; ++i) {
+        if (tokens[i] < 0 || tokens[i] >= e->vocab) {
+            std::fprintf(stderr, "gdn: token %d (position %u) is outside the vocabulary [0, %d)\n", tokens[i], i,
+                         e->vocab);
+            return -1;
+        }
+    }
+    if (sync_counting(e) != 0) return -1;
     if (e->use_graph && ensure_graph(e) != 0) return -1;
     for (uint32_t s = 0; s < n_steps; ++s) {
         const auto t0 = std::chrono::steady_clock::now();
@@ -2076,7 +2522,7 @@ int gdn_run_teacher_forced(GDNRunState *state, const int32_t *tokens, uint32_t n
 }
 
 int gdn_profile_kernels(GDNRunState *state, uint32_t rounds, float *avg_us, uint32_t n_kinds) {
-    GDNEngine *e = state->engine;
+    GDNEngine *e = engine_of(state);
     if (!e || rounds == 0) return -1;
     switch (e->contract) {
     case kRef: return profile_t<kRef>(e, rounds, avg_us, n_kinds);

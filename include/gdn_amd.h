@@ -43,7 +43,7 @@ typedef struct {
 } GDNWeightHeader;
 
 /* ---- workspace layout in FLOATS: identical values to gdn_model.h:54-75.
- *      The engine keeps this layout in device memory. ---- */
+ *      GDNRunState.workspace is a host buffer of this layout. ---- */
 #define GDN_WSF_HID     2048u
 #define GDN_WSF_HEAD    16u
 #define GDN_WSF_MLP     5632u
@@ -109,20 +109,68 @@ typedef struct {
     const float *lm_head;
 } GDNModel;
 
+/* ---- device-format geometry the reference's drivers compute with
+ *      (gdn_model.h:22, :84-90, :115-121).  The values are the reference's;
+ *      on this engine the 32 weight shards hold no weights (see
+ *      gdn_weight_shard_beats) and shards 28..31 are host mirrors of the
+ *      BF16 recurrent-state stripes. ---- */
+#define GEMV_CHANNELS 32
+#define GDN_RECURRENT_STATE_PORTS       4
+#define GDN_RECURRENT_STATE_FIRST_PORT 28
+#define GDN_RECURRENT_STATE_STRIPE_FLOATS (GDN_WSF_STATE / GDN_RECURRENT_STATE_PORTS)
+#define GDN_RECURRENT_STATE_STRIPE_BF16_BEATS (GDN_RECURRENT_STATE_STRIPE_FLOATS / 32u)
+#define GDN_CONV_TAIL_STRIPES (24u * 3u)
+#define GDN_CONV_TAIL_FLOATS_PER_STRIPE (GDN_WSF_HEADBUF / GDN_CONV_TAIL_STRIPES)
+#define GDN_CONV_TAIL_RESERVED_BEATS_PER_STRIPE (GDN_CONV_TAIL_FLOATS_PER_STRIPE / 16u)
+#define GDN_CONV_TAIL_BF16_BEATS_PER_STRIPE (GDN_CONV_TAIL_FLOATS_PER_STRIPE / 32u)
+
+/* One 512-bit beat, the reference's Beat512 (ap_uint<512>, gdn_model.h:10-14):
+ * 64 bytes, FP32 lane i at bytes 4i..4i+3, BF16 lane i at bytes 2i..2i+1,
+ * little-endian. */
+typedef struct GDNBeat512 {
+    unsigned char bytes[64];
+} Beat512;
+
 struct GDNEngine;
 
-/* Run state (gdn_model.h:153-160).  The reference's 32 FPGA weight shards
- * and aux image are replaced by `engine` (device weights, activations,
- * stream, captured step graph).  workspace, x, recurrent_state and
- * head_buffer keep their meaning and GDN_WS_OFF_* offsets but point to
- * DEVICE memory. */
+/* Run state: the reference's GDNRunState (gdn_model.h:153-160) field for
+ * field, with the device engine appended.  Every reference field is HOST
+ * memory, so a caller written against gdn_model.cpp reads and writes it as
+ * before:
+ *   workspace        GDN_WS_FLOATS floats, 64-byte aligned.  After each
+ *                    gdn_decode_step_host: X holds the token's FP32
+ *                    embedding row and lane 0 of X_NORM the argmax token as
+ *                    a float (the reference's token line).  The other slots
+ *                    are not refreshed per step (the debug buffers and
+ *                    gdn_read_* return device results).
+ *   x, recurrent_state, head_buffer   views at GDN_WS_OFF_X / _REC_STATE /
+ *                    _HEAD_BUF (the .gdnstate loader reads into
+ *                    recurrent_state, as gdn_eval.cpp does)
+ *   weight_shards    [0..27] NULL; [28..31] host buffers of
+ *                    GDN_RECURRENT_STATE_STRIPE_BF16_BEATS beats holding the
+ *                    recurrent state in the reference's BF16 stripe layout,
+ *                    written by gdn_scatter_recurrent_state and refreshed
+ *                    from the device by gdn_sync_host_state
+ *   aux_weights      NULL (the small weights live on the device)
+ *   engine           device weights, state, activations, stream and graph */
 typedef struct {
-    void *workspace;            /* device, GDN_WS_FLOATS floats */
-    float *x;                   /* device view at GDN_WS_OFF_X */
-    float *recurrent_state;     /* device view at GDN_WS_OFF_REC_STATE */
-    float *head_buffer;         /* device view at GDN_WS_OFF_HEAD_BUF */
+    Beat512 *workspace;
+    float *x;
+    float *recurrent_state;
+    float *head_buffer;
+    Beat512 *weight_shards[GEMV_CHANNELS];
+    Beat512 *aux_weights;
     struct GDNEngine *engine;
 } GDNRunState;
+
+/* Product counters of the native BF16 multiplier (gdn_model.h:162-168). */
+typedef struct {
+    uint64_t calls;
+    uint64_t special_inputs;
+    uint64_t flushed_inputs;
+    uint64_t flushed_outputs;
+    uint64_t overflows;
+} GDNMixedMulStats;
 
 /* ===== model (host) ===== */
 
@@ -153,9 +201,12 @@ void gdn_default_config(GDNWeightHeader *config, uint32_t num_layers);
 
 /* ===== run state (device) ===== */
 
-/* gdn_model.h:216 -- allocate the device workspace, upload the weights in
- * the engine's layout and zero the recurrent/conv state, for the REF
- * contract.  Fails on max_tokens == 0 or > max_seq_len. */
+/* gdn_model.h:216 -- allocate the host workspace and state mirrors, upload
+ * the weights to the device in the engine's layout and zero the
+ * recurrent/conv state, for the REF contract.  Fails on max_tokens == 0 or
+ * > max_seq_len, and on a model shape the kernels are not built for
+ * (hidden 2048, 8 x 256 heads, intermediate 5632, conv 4, 1..24 layers,
+ * vocab a positive multiple of 8). */
 int gdn_run_state_init(GDNRunState *state, const GDNModel *model,
                        uint32_t max_tokens);
 /* Same with an explicit contract (GDN_CONTRACT_*). */
@@ -164,12 +215,77 @@ int gdn_run_state_init_contract(GDNRunState *state, const GDNModel *model,
 /* gdn_model.h:217 */
 void gdn_run_state_free(GDNRunState *state);
 
-/* gdn_model.h:264 -- one teacher-forced decode step: embedding row of
- * *token into workspace X, 24 layers against the persistent state, LM head
- * into workspace LOGITS, argmax (as a float) into lane 0 of workspace
- * X_NORM.  Returns -1 for a token outside [0, vocab). */
+/* gdn_model.h:264 -- one teacher-forced decode step: the embedding row of
+ * *token (host workspace X gets its FP32 copy), every layer against the
+ * persistent device state, the LM head and the argmax, which lands as a
+ * float in lane 0 of the host workspace's X_NORM.  Returns -1 for a token
+ * outside [0, vocab), for a run state that was never initialised, and when
+ * the step does not finish within GDN_KERNEL_WAIT_TIMEOUT_MS milliseconds
+ * (environment; default 10000) or a kernel's bounded internal wait ran out
+ * (the run state then refuses further steps). */
 int gdn_decode_step_host(const GDNModel *model, GDNRunState *state,
                          const int32_t *token);
+/* ---- the remaining gdn_model.h calls of the reference's gdn_eval.cpp ---- */
+
+/* gdn_model.h:172-173: beats per packed weight shard.  This engine keeps its
+ * weights on the device in its own layout, so the shards hold no weight
+ * beats: 0 (and 0 bytes), which makes a caller's
+ * weight_shards[GDN_RECURRENT_STATE_FIRST_PORT + p] + gdn_weight_shard_beats()
+ * the state stripe itself. */
+size_t gdn_weight_shard_beats(const GDNWeightHeader *config);
+size_t gdn_weight_shard_bytes(const GDNWeightHeader *config);
+/* gdn_model.h:176-178: checks the device copy of every weight against the
+ * FP32-word blob, value for value in the engine's packing (download and
+ * compare; about 3 GB of reads).  `shards` identifies the run state (its
+ * weight_shards array).  0 when every value matches. */
+int gdn_validate_weight_shards(const float *weight_data, const GDNWeightHeader *config,
+                               Beat512 *const shards[]);
+/* gdn_model.h:190-192: the recurrent state [L][H][K][V] (FP32 words)
+ * written into `state_stripes` in the reference's BF16 stripe layout.  When
+ * the stripes are a run state's (weight_shards + GDN_RECURRENT_STATE_FIRST_PORT)
+ * the values also go to its engine: under the REF contract they must be
+ * BF16-exact, as in the reference, while the FP32-state contracts keep the
+ * FP32 values on the device and mirror their BF16 rounding in the stripes.
+ * Other stripes are only packed, from BF16-exact values. */
+int gdn_scatter_recurrent_state(Beat512 *const state_stripes[], const float *recurrent_state,
+                                size_t recurrent_state_floats);
+/* gdn_model.h:193-195: the conv tails [L][q,k,v][W-1][hidden] written into
+ * `workspace_head_buffer` as BF16 payloads in the first half of each stripe
+ * reservation, the rest zeroed.  When it is a run state's head_buffer the
+ * values also go to its engine (BF16-exact except under the FP32 contract);
+ * any other buffer is only packed, from GDN_WSF_HEADBUF BF16-exact values. */
+int gdn_pack_conv_tails_bf16(Beat512 *workspace_head_buffer, const float *conv_tails,
+                             size_t conv_tail_floats);
+/* gdn_model.h:274: after every gdn_decode_step_host the final normalised
+ * hidden vector (hidden_size floats) and the FP32 logits (vocab_size floats)
+ * are copied into these caller buffers; NULL stops the copies.  Process-wide,
+ * like the reference. */
+void gdn_set_native_debug_buffers(float *final_hidden, float *logits);
+/* gdn_model.h:203-204: counters of the native BF16 products, process-wide.
+ * Host products (gdn_compute_logits, gdn_native_bf16_mul_to_fp32) are
+ * counted as they run.  Device products are counted per decode step while
+ * counting is on: calls exactly; special and flushed inputs exactly, from
+ * each GEMV's input vector and per-column tables of the weights; flushed
+ * outputs and overflows exactly, and only where the kernel's fast-path
+ * verdict does not already exclude them.  gdn_reset_mixed_mul_stats zeroes
+ * the counters and turns device counting on (each counted step also copies
+ * the step's GEMV inputs to the host); gdn_get_mixed_mul_stats reads them. */
+void gdn_reset_mixed_mul_stats(void);
+GDNMixedMulStats gdn_get_mixed_mul_stats(void);
+/* Turns device counting off again (no reference counterpart). */
+void gdn_stop_mixed_mul_stats(void);
+/* Refresh the host mirrors of the run state from the device: the BF16 state
+ * stripes in weight_shards[28..31] and the packed conv tails in head_buffer,
+ * in the layouts gdn_scatter_recurrent_state / gdn_pack_conv_tails_bf16
+ * write.  Call before reading them (e.g. a GDNSDMP1 state dump).  No
+ * reference counterpart: the reference's stripes are the device memory. */
+int gdn_sync_host_state(GDNRunState *state);
+/* gdn_model.h:207-210: lane accessors of a Beat512. */
+void gdn_test_set_fp32_lane_bits(Beat512 *beat, uint32_t lane, uint32_t bits);
+uint32_t gdn_test_get_fp32_lane_bits(const Beat512 *beat, uint32_t lane);
+void gdn_test_set_bf16_lane_bits(Beat512 *beat, uint32_t lane, uint16_t bits);
+uint16_t gdn_test_get_bf16_lane_bits(const Beat512 *beat, uint32_t lane);
+
 /* Device results of the last step, copied to host memory. */
 int gdn_read_token(const GDNRunState *state, int32_t *token);
 int gdn_read_logits(const GDNRunState *state, float *logits, size_t count);

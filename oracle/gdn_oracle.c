@@ -3,8 +3,9 @@
  * arithmetic (YAMWD/GatedDeltaNet, c_impl/gdn_model.cpp).
  *
  * TEST INFRASTRUCTURE: the checker for the HIP engine, never the product.
- * Built with -O2 -ffp-contract=off (the reference Makefile:27-34 flag) and
- * without -ffast-math, so every expression rounds where the C source does.
+ * Built with -O3 -ffp-contract=off (the reference Makefile:27-34 flag) and
+ * without -ffast-math, so every expression rounds where the C source does
+ * (vectorised loops perform the same IEEE operations in the same order).
  *
  * What pins each function (tests named after tests/):
  *   orc_rne_bits / orc_widen_bits   the 20 RNE boundary cases and the
@@ -12,20 +13,32 @@
  *       an exhaustive 2^32 sweep against an independent integer model
  *       (test_oracle_bf16.py).
  *   orc_native_product_bits         the rule text of the reference
- *       (architecture.md:867-878): exhaustive over all 2^32 BF16 pairs
- *       against an independent double-precision model (test_oracle_bf16.py).
+ *       (architecture.md:867-878): an independent double-precision model on
+ *       every BF16 weight x 64 structured activations and 2^20 random pairs,
+ *       the flush tie 0x007fc000 and the special classes
+ *       (test_oracle_bf16.py).
  *   orc_tree16 / orc_tree256        closed forms: powers of two, integer
  *       inputs, and order-sensitive inputs whose result differs under any
- *       other association (test_oracle_ops.py).
+ *       other association (test_oracle_ops.py: test_tree16_association,
+ *       test_tree256_association).
  *   orc_gemv / orc_gemv_tiny        one-hot activations select the rounded
  *       weight column; integer inputs give exact sums; cancellation vectors
- *       distinguish the bank order; brute force against a literal loop over
- *       the stated formula in Python on tiny shapes (test_oracle_ops.py).
+ *       distinguish the bank order (test_gemv_bank_order, test_gemv_tiny_
+ *       order); a brute force against a literal Python loop over the stated
+ *       formula on random operands with zeros and subnormals
+ *       (test_gemv_brute_force_literal_loop).  The rows' branch-free native
+ *       product equals orc_native_product_bits on every weight x structured
+ *       activations and 2^22 random pairs (test_native_product_select_form).
  *   orc_rmsnorm / residual / output_norm_gate   constant vectors give exact
- *       results; scale invariance; the 16-lane/halves association is pinned
- *       by order-sensitive inputs (test_oracle_ops.py).
+ *       results; scale invariance; the 16-value chunk / sequential chunk-sum
+ *       association is pinned by inputs where a flat sequential sum or a
+ *       tree over the chunk sums gives a different result
+ *       (test_rmsnorm_sum_is_chunked_then_sequential,
+ *       test_output_norm_sum_is_chunked_per_head).
  *   orc_conv_silu                   tap one-hots give silu(x) / silu(t0);
- *       zero tails propagate; tail shift (test_oracle_ops.py).
+ *       zero tails propagate; tail shift; the left association
+ *       ((t0w0 + t1w1) + t2w2) + xw3 by inputs where any other pairing
+ *       differs (test_conv_taps_and_shift, test_conv_sum_is_left_associated).
  *   orc_recurrence_head             beta=0, decay=1/beta=1/k=e_j special
  *       cases; plain-IEEE case decay=1 beta=0.5; fp64 textbook recurrence
  *       (chunk.py:688-718 restated) within tolerance (test_oracle_ops.py).
@@ -109,11 +122,6 @@ uint16_t orc_native_product_bits(uint16_t w, uint16_t x) {
     return r;
 }
 
-static inline float native_mul(float w, float x) {
-    return u2f(orc_widen_bits(orc_native_product_bits(
-        (uint16_t)(f2u(w) >> 16), (uint16_t)(f2u(x) >> 16))));
-}
-
 /* ---- transcendentals: gdn_sigmoid / gdn_silu / gdn_softplus,
  *      gdn_model.cpp:1307-1330 ---- */
 float orc_expf(float x, int tmode) {
@@ -165,33 +173,101 @@ float orc_tree256(const float *a) {
     return buf[0];
 }
 
+/* The native product of two BF16-exact FP32 words as integer selects: the
+ * same IEEE multiply and the same cases as orc_native_product_bits, with
+ * its special cases applied last in reverse order of precedence (the last
+ * select wins), so that the row loop below vectorises.  Returns the widened
+ * product's bits.  tests/test_oracle_bf16.py compares the two forms. */
+static inline uint32_t native_bits_sel(uint32_t wb, uint32_t xb) {
+    const uint32_t w = wb >> 16, x = xb >> 16;
+    const uint32_t ew = (w >> 7) & 0xffu, fw = w & 0x7fu;
+    const uint32_t ex = (x >> 7) & 0xffu, fx = x & 0x7fu;
+    const uint32_t sign = (w ^ x) & 0x8000u;
+    const uint32_t pb = f2u(u2f(w << 16) * u2f(x << 16));
+    const uint32_t mag = pb & 0x7fffffffu;
+    const uint32_t r = (pb + 0x7fffu + ((pb >> 16) & 1u)) >> 16;
+    uint32_t res = (r & 0x7f80u) == 0 ? (r & 0x8000u) : r;
+    res = mag < 0x007fc000u ? ((pb >> 16) & 0x8000u) : res;
+    res = mag == 0x7f800000u ? (pb >> 16) : res;
+    const int w_zero = ew == 0, x_zero = ex == 0;
+    const int w_inf = ew == 0xffu && fw == 0, x_inf = ex == 0xffu && fx == 0;
+    const int w_nan = ew == 0xffu && fw != 0, x_nan = ex == 0xffu && fx != 0;
+    res = (w_zero | x_zero) ? sign : res;
+    res = (w_inf | x_inf) ? (sign | 0x7f80u) : res;
+    res = (w_nan | x_nan | (w_inf & x_zero) | (x_inf & w_zero)) ? 0x7fc0u : res;
+    return res << 16;
+}
+
+/* p[i] = the contract's product of w[i] and x[i]: native BF16 (ORC_REF,
+ * ORC_BF16W_FP32S) or plain FP32 (ORC_FP32, ORC_BF16X). */
+static inline void row_products(int contract, const float *w, const float *x,
+                                int n, float *p) {
+    if (contract == ORC_FP32 || contract == ORC_BF16X) {
+        for (int i = 0; i < n; ++i) p[i] = w[i] * x[i];
+        return;
+    }
+    for (int i = 0; i < n; ++i) {
+        uint32_t wb, xb;
+        memcpy(&wb, w + i, 4);
+        memcpy(&xb, x + i, 4);
+        const uint32_t pb = native_bits_sel(wb, xb);
+        memcpy(p + i, &pb, 4);
+    }
+}
+
+#define ORC_KMAX 8192
+
 /* One dense GEMV row, gemv32_cluster2 + gemv32_pair_dot16 +
  * gemv32_reduce_parts (gdn_model.cpp:4037-4059, :4444-4586, :4115-4127).
  * For every 32-column beat b the lower and upper 16 products are each
  * reduced with tree16; four banks (lower/upper x even/odd beat) accumulate
  * those sums in beat order starting from +0.0f; the row result is
- * (even_lo + even_hi) + (odd_lo + odd_hi).  Products are native BF16
- * (ORC_REF, ORC_BF16W_FP32S) or plain FP32 (ORC_FP32, ORC_BF16X). */
+ * (even_lo + even_hi) + (odd_lo + odd_hi).  The four tree16 levels run over
+ * the whole row at once (level m adds neighbouring pairs of level m - 1),
+ * which is tree16 on every 16-product half-beat.  Products are native BF16
+ * (ORC_REF, ORC_BF16W_FP32S) or plain FP32 (ORC_FP32, ORC_BF16X).  The row
+ * functions are compiled for AVX-512, AVX2 and baseline x86-64 and chosen
+ * at load time; every clone performs the same IEEE operations. */
+#if defined(__x86_64__) && defined(__GNUC__) && !defined(__clang__)
+#define ORC_CLONES __attribute__((target_clones("avx512f", "avx2", "default")))
+#else
+#define ORC_CLONES
+#endif
+
+ORC_CLONES
 static float gemv_row(int contract, const float *w, const float *x, int K) {
+    float p[ORC_KMAX], s1[ORC_KMAX / 2], s2[ORC_KMAX / 4], s3[ORC_KMAX / 8];
+    float t[ORC_KMAX / 16];
+    row_products(contract, w, x, K, p);
+    for (int i = 0; i < K / 2; ++i) s1[i] = p[2 * i] + p[2 * i + 1];
+    for (int i = 0; i < K / 4; ++i) s2[i] = s1[2 * i] + s1[2 * i + 1];
+    for (int i = 0; i < K / 8; ++i) s3[i] = s2[2 * i] + s2[2 * i + 1];
+    for (int i = 0; i < K / 16; ++i) t[i] = s3[2 * i] + s3[2 * i + 1];
     float bank[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    float p[32];
     for (int b = 0; b < K / 32; ++b) {
-        for (int l = 0; l < 32; ++l) {
-            const float wv = w[32 * b + l], xv = x[32 * b + l];
-            p[l] = (contract == ORC_FP32 || contract == ORC_BF16X) ? wv * xv : native_mul(wv, xv);
-        }
-        const float lo = orc_tree16(p), hi = orc_tree16(p + 16);
         const int e = (b & 1) * 2;
-        bank[e] = bank[e] + lo;
-        bank[e + 1] = bank[e + 1] + hi;
+        bank[e] = bank[e] + t[2 * b];
+        bank[e + 1] = bank[e + 1] + t[2 * b + 1];
     }
     const float s0 = bank[0] + bank[1];
-    const float s1 = bank[2] + bank[3];
-    return s0 + s1;
+    const float s1v = bank[2] + bank[3];
+    return s0 + s1v;
+}
+
+/* gdn_compute_logits' row: the same native products, summed sequentially
+ * from +0.0f. */
+ORC_CLONES
+static float seq_native_row(const float *w, const float *x, int K) {
+    float p[ORC_KMAX];
+    row_products(ORC_REF, w, x, K, p);
+    float sum = 0.0f;
+    for (int i = 0; i < K; ++i) sum += p[i];
+    return sum;
 }
 
 void orc_gemv(int contract, const float *W, const float *x, int M, int K,
               float *y) {
+    if (K > ORC_KMAX || K % 32 != 0) abort();  /* whole beats, row buffers */
 #pragma omp parallel for schedule(static) if (M >= 64)
     for (int r = 0; r < M; ++r)
         y[r] = gemv_row(contract, W + (size_t)r * K, x, K);
@@ -199,6 +275,7 @@ void orc_gemv(int contract, const float *W, const float *x, int M, int K,
 
 void orc_gemv_rows(int contract, const float *W, const float *x, int M, int K,
                    float *y) {
+    if (K > ORC_KMAX || K % 32 != 0) abort();
     for (int r = 0; r < M; ++r)
         y[r] = gemv_row(contract, W + (size_t)r * K, x, K);
 }
@@ -462,9 +539,24 @@ static void round_vec(int contract, float *x, int n) {
 /* gdn_forward's per-layer sequence, gdn_model.cpp:3741-3843 (the attention
  * norm is evaluated at the layer start; the reference fuses it into the
  * previous layer's residual add, which is the same arithmetic). */
+/* gemv_in (optional) receives the layer's four dense-GEMV input vectors in
+ * order: the QKVG input [H], the o_proj input [H], the gate/up input [H]
+ * and the down input [I] (the native multiplier's activations). */
+static void layer_forward_impl(int contract, int tmode, const orc_header *h,
+                               const float *blob, int layer, float *x,
+                               float *state, float *conv, float *attn_out,
+                               float *gemv_in);
+
 void orc_layer_forward(int contract, int tmode, const orc_header *h,
                        const float *blob, int layer, float *x, float *state,
                        float *conv, float *attn_out) {
+    layer_forward_impl(contract, tmode, h, blob, layer, x, state, conv, attn_out, NULL);
+}
+
+static void layer_forward_impl(int contract, int tmode, const orc_header *h,
+                               const float *blob, int layer, float *x,
+                               float *state, float *conv, float *attn_out,
+                               float *gemv_in) {
     const int H = (int)h->hidden_size, nh = (int)h->num_heads;
     const int hd = (int)h->head_dim, I = (int)h->intermediate_size;
     const float eps = h->norm_eps;
@@ -482,6 +574,7 @@ void orc_layer_forward(int contract, int tmode, const orc_header *h,
     float a[64], b[64];
 
     orc_rmsnorm(contract, x, w.attn_norm, H, eps, xn);
+    if (gemv_in) memcpy(gemv_in, xn, sizeof(float) * (size_t)H);
     orc_gemv_tiny(w.a_proj, xn, nh, H, a);
     orc_gemv_tiny(w.b_proj, xn, nh, H, b);
     round_vec(contract, a, nh);
@@ -508,14 +601,17 @@ void orc_layer_forward(int contract, int tmode, const orc_header *h,
     if (attn_out) memcpy(attn_out, o, sizeof(float) * (size_t)H);
     orc_output_norm_gate(contract, tmode, o, q + 3 * H, w.o_norm, nh, hd, eps,
                          og);
+    if (gemv_in) memcpy(gemv_in + H, og, sizeof(float) * (size_t)H);
     orc_gemv(contract, w.o_proj, og, H, H, y);
     round_vec(contract, y, H);
     orc_residual_rmsnorm(contract, x, y, w.mlp_norm, H, eps, xalt, xn);
+    if (gemv_in) memcpy(gemv_in + 2 * H, xn, sizeof(float) * (size_t)H);
     orc_gemv(contract, w.gate, xn, I, H, gt);
     orc_gemv(contract, w.up, xn, I, H, ut);
     round_vec(contract, gt, I);
     round_vec(contract, ut, I);
     orc_swiglu(contract, tmode, gt, ut, I, hh);
+    if (gemv_in) memcpy(gemv_in + 3 * H, hh, sizeof(float) * (size_t)I);
     orc_gemv(contract, w.down, hh, H, I, y);
     round_vec(contract, y, H);
     for (int i = 0; i < H; ++i) x[i] = R(contract, xalt[i] + y[i]);
@@ -528,9 +624,31 @@ void orc_layer_forward(int contract, int tmode, const orc_header *h,
  * the FP32 embedding row is rounded to the contract, run through the
  * layers, normalised with final_norm and multiplied by lm_head into FP32
  * logits (not rounded); the argmax is the returned token. */
+static int decode_step_impl(int contract, int tmode, const orc_header *h,
+                            const float *blob, float *state, float *conv,
+                            int token, float *logits, float *final_hidden,
+                            float *gemv_in);
+
 int orc_decode_step(int contract, int tmode, const orc_header *h,
                     const float *blob, float *state, float *conv, int token,
                     float *logits, float *final_hidden) {
+    return decode_step_impl(contract, tmode, h, blob, state, conv, token, logits, final_hidden, NULL);
+}
+
+/* As orc_decode_step, also writing every dense GEMV's input vector of the
+ * step to gemv_in: per layer [H] QKVG, [H] o_proj, [H] gate/up, [I] down,
+ * then the LM head's [H] (the final hidden vector). */
+int orc_decode_step_trace(int contract, int tmode, const orc_header *h,
+                          const float *blob, float *state, float *conv,
+                          int token, float *logits, float *final_hidden,
+                          float *gemv_in) {
+    return decode_step_impl(contract, tmode, h, blob, state, conv, token, logits, final_hidden, gemv_in);
+}
+
+static int decode_step_impl(int contract, int tmode, const orc_header *h,
+                            const float *blob, float *state, float *conv,
+                            int token, float *logits, float *final_hidden,
+                            float *gemv_in) {
     const int H = (int)h->hidden_size, L = (int)h->num_layers;
     const size_t layer_state = (size_t)h->num_heads * h->head_dim * h->head_dim;
     const size_t layer_conv = (size_t)3 * (h->conv_size - 1) * H;
@@ -539,14 +657,17 @@ int orc_decode_step(int contract, int tmode, const orc_header *h,
     float *xn = (float *)malloc(sizeof(float) * (size_t)H);
     const float *emb = blob + (size_t)token * H;
     for (int i = 0; i < H; ++i) x[i] = R(contract, emb[i]);
+    const size_t per_layer_in = 3 * (size_t)H + h->intermediate_size;
     for (int l = 0; l < L; ++l)
-        orc_layer_forward(contract, tmode, h, blob, l, x,
-                          state + (size_t)l * layer_state,
-                          conv + (size_t)l * layer_conv, NULL);
+        layer_forward_impl(contract, tmode, h, blob, l, x,
+                           state + (size_t)l * layer_state,
+                           conv + (size_t)l * layer_conv, NULL,
+                           gemv_in ? gemv_in + (size_t)l * per_layer_in : NULL);
     const float *final_norm = blob + orc_layer_offset(h, L);
     const float *lm_head = final_norm + H;
     orc_rmsnorm(contract, x, final_norm, H, h->norm_eps, xn);
     if (final_hidden) memcpy(final_hidden, xn, sizeof(float) * (size_t)H);
+    if (gemv_in) memcpy(gemv_in + (size_t)L * per_layer_in, xn, sizeof(float) * (size_t)H);
     orc_gemv(contract, lm_head, xn, (int)h->vocab_size, H, logits);
     free(x);
     free(xn);
@@ -564,10 +685,7 @@ void orc_compute_logits(const orc_header *h, const float *blob,
     for (int i = 0; i < H; ++i) rounded[i] = orc_bf16_round(hidden[i]);
 #pragma omp parallel for schedule(static)
     for (int v = 0; v < (int)h->vocab_size; ++v) {
-        const float *row = lm_head + (size_t)v * H;
-        float sum = 0.0f;
-        for (int i = 0; i < H; ++i) sum += native_mul(row[i], rounded[i]);
-        logits[v] = sum;
+        logits[v] = seq_native_row(lm_head + (size_t)v * H, rounded, H);
     }
     free(rounded);
 }
@@ -582,6 +700,14 @@ void orc_native_product_array(const uint16_t *w, const uint16_t *x, uint16_t *ou
 #pragma omp parallel for schedule(static)
     for (long long i = 0; i < (long long)n; ++i)
         out[i] = orc_native_product_bits(w[i], x[i]);
+}
+
+/* The select form used by the GEMV rows, for the test that compares it with
+ * orc_native_product_bits. */
+void orc_native_product_sel_array(const uint16_t *w, const uint16_t *x, uint16_t *out, size_t n) {
+#pragma omp parallel for schedule(static)
+    for (long long i = 0; i < (long long)n; ++i)
+        out[i] = (uint16_t)(native_bits_sel((uint32_t)w[i] << 16, (uint32_t)x[i] << 16) >> 16);
 }
 
 void orc_transcendental_array(int which, int tmode, const float *in, float *out, size_t n) {

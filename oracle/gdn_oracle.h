@@ -123,6 +123,10 @@ void orc_layer_forward(int contract, int tmode, const orc_header *h,
 int orc_decode_step(int contract, int tmode, const orc_header *h,
                     const float *blob, float *state, float *conv, int token,
                     float *logits, float *final_hidden);
+int orc_decode_step_trace(int contract, int tmode, const orc_header *h,
+                          const float *blob, float *state, float *conv,
+                          int token, float *logits, float *final_hidden,
+                          float *gemv_in);
 
 /* Reference-style independent scalar LM head (gdn_compute_logits). */
 void orc_compute_logits(const orc_header *h, const float *blob,
@@ -134,6 +138,7 @@ void orc_set_threads(int n);
  * 1 log1pf, 2 sigmoid, 3 silu, 4 softplus. */
 void orc_rne_array(const uint32_t *in, uint16_t *out, size_t n);
 void orc_native_product_array(const uint16_t *w, const uint16_t *x, uint16_t *out, size_t n);
+void orc_native_product_sel_array(const uint16_t *w, const uint16_t *x, uint16_t *out, size_t n);
 void orc_transcendental_array(int which, int tmode, const float *in, float *out, size_t n);
 
 #ifdef __cplusplus

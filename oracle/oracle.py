@@ -62,9 +62,11 @@ _SIG = {
     "orc_layer_forward": (None, [c_int, c_int, POINTER(Header), FP, c_int, FP, FP, FP, FP]),
     "orc_decode_step": (c_int, [c_int, c_int, POINTER(Header), FP, FP, FP, c_int, FP, FP]),
     "orc_compute_logits": (None, [POINTER(Header), FP, FP, FP]),
+    "orc_decode_step_trace": (c_int, [c_int, c_int, POINTER(Header), FP, FP, FP, c_int, FP, FP, FP]),
     "orc_set_threads": (None, [c_int]),
     "orc_rne_array": (None, [POINTER(c_uint32), POINTER(c_uint16), c_size_t]),
     "orc_native_product_array": (None, [POINTER(c_uint16), POINTER(c_uint16), POINTER(c_uint16), c_size_t]),
+    "orc_native_product_sel_array": (None, [POINTER(c_uint16), POINTER(c_uint16), POINTER(c_uint16), c_size_t]),
     "orc_transcendental_array": (None, [c_int, c_int, FP, FP, c_size_t]),
 }
 
@@ -123,6 +125,16 @@ def native_product_array(w: np.ndarray, x: np.ndarray) -> np.ndarray:
     out = np.empty(w.size, np.uint16)
     lib().orc_native_product_array(w.ctypes.data_as(POINTER(c_uint16)), x.ctypes.data_as(POINTER(c_uint16)),
                                    out.ctypes.data_as(POINTER(c_uint16)), w.size)
+    return out
+
+
+def native_product_sel_array(w: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """The branch-free form of the native product used inside the GEMV rows."""
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    out = np.empty(w.size, np.uint16)
+    lib().orc_native_product_sel_array(w.ctypes.data_as(POINTER(c_uint16)), x.ctypes.data_as(POINTER(c_uint16)),
+                                       out.ctypes.data_as(POINTER(c_uint16)), w.size)
     return out
 
 
@@ -250,6 +262,26 @@ def decode_step(contract: int, hdr: Header, blob: np.ndarray, state: np.ndarray,
     tok = lib().orc_decode_step(contract, tmode, ctypes.byref(hdr), _p(blob), _p(state), _p(conv), token,
                                 _p(logits), _p(fh))
     return int(tok), logits, fh
+
+
+def decode_step_trace(contract: int, hdr: Header, blob: np.ndarray, state: np.ndarray, conv: np.ndarray,
+                      token: int, tmode: int = LIBM):
+    """decode_step that also returns the step's dense-GEMV input vectors:
+    a list of (layer, kind, vector) with kind in qkvg, o, gu, down, then
+    (None, "lm", final hidden)."""
+    H, I, L = hdr.hidden_size, hdr.intermediate_size, hdr.num_layers
+    per = 3 * H + I
+    gin = np.empty(L * per + H, np.float32)
+    logits = np.empty(hdr.vocab_size, np.float32)
+    fh = np.empty(H, np.float32)
+    tok = lib().orc_decode_step_trace(contract, tmode, ctypes.byref(hdr), _p(blob), _p(state), _p(conv), token,
+                                      _p(logits), _p(fh), _p(gin))
+    ins = []
+    for l in range(L):
+        b = gin[l * per:(l + 1) * per]
+        ins += [(l, "qkvg", b[:H]), (l, "o", b[H:2 * H]), (l, "gu", b[2 * H:3 * H]), (l, "down", b[3 * H:])]
+    ins.append((None, "lm", gin[L * per:]))
+    return int(tok), logits, fh, ins
 
 
 def compute_logits(hdr: Header, blob: np.ndarray, hidden) -> np.ndarray:

@@ -138,6 +138,26 @@ def test_native_product_random_pairs(orc):
     assert (orc.native_product_array(w, x) == text_model(w, x)).all()
 
 
+def test_native_product_select_form(orc):
+    """The branch-free form the GEMV rows use (integer selects, special cases
+    applied last) equals the pinned scalar form: every weight against the
+    structured activations, plus 2^22 random pairs; all 2^32 pairs with
+    GDN_EXHAUSTIVE=1."""
+    w = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    for a in _structured_activations():
+        x = np.full(w.size, a, np.uint16)
+        assert (orc.native_product_sel_array(w, x) == orc.native_product_array(w, x)).all(), hex(int(a))
+    rng = np.random.default_rng(7)
+    w = rng.integers(0, 1 << 16, 1 << 22, dtype=np.uint32).astype(np.uint16)
+    x = rng.integers(0, 1 << 16, 1 << 22, dtype=np.uint32).astype(np.uint16)
+    assert (orc.native_product_sel_array(w, x) == orc.native_product_array(w, x)).all()
+    if os.environ.get("GDN_EXHAUSTIVE") == "1":
+        w = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+        for a in range(1 << 16):
+            x = np.full(w.size, a, np.uint16)
+            assert (orc.native_product_sel_array(w, x) == orc.native_product_array(w, x)).all(), hex(a)
+
+
 def test_native_product_flush_boundary(orc):
     """146/128 * 224/128 = 2 - 2^-8: with exponents summing to -127 the exact
     product is 0x007fc000 = 2^-126 - 2^-135, a tie that rounds up into the

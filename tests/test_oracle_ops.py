@@ -97,6 +97,54 @@ def test_gemv_native_rounding_point(orc):
     assert y_f32 != y_ref
 
 
+def _literal_gemv_row(products):
+    """The GEMV contract written out as plain loops over float32 values:
+    tree16 = balanced pairs over each 16-product half-beat, four banks
+    (lower/upper x even/odd beat) accumulated in beat order from +0.0, then
+    (even_lo + even_hi) + (odd_lo + odd_hi)."""
+    def tree16(v):
+        v = list(v)
+        while len(v) > 1:
+            v = [F(v[2 * i] + v[2 * i + 1]) for i in range(len(v) // 2)]
+        return v[0]
+    banks = [F(0.0)] * 4
+    for b in range(len(products) // 32):
+        lo = tree16(products[32 * b:32 * b + 16])
+        hi = tree16(products[32 * b + 16:32 * b + 32])
+        e = 2 * (b & 1)
+        banks[e] = F(banks[e] + lo)
+        banks[e + 1] = F(banks[e + 1] + hi)
+    return F(F(banks[0] + banks[1]) + F(banks[2] + banks[3]))
+
+
+@pytest.mark.parametrize("K", [64, 128, 2048])
+def test_gemv_brute_force_literal_loop(orc, K):
+    """orc_gemv against the literal loop above on random BF16 operands with
+    zeros, subnormals and a wide exponent range; the native products come
+    from orc_native_product_bits (exhaustively pinned in
+    test_oracle_bf16.py), the FP32 arm's from float32 multiplication."""
+    rng = np.random.default_rng(K)
+    M = 6
+    W = bf(rng.normal(0, 1, (M, K)).astype(F) * np.exp2(rng.integers(-20, 20, (M, K))).astype(F))
+    x = bf(rng.normal(0, 1, K).astype(F) * np.exp2(rng.integers(-20, 20, K)).astype(F))
+    W[0, ::7] = 0.0
+    x[::11] = 0.0
+    W[1, 3] = np.uint32(0x00010000).view(F)   # a subnormal weight (DAZ)
+    x[5] = np.uint32(0x80020000).view(F)      # a subnormal activation
+    wb = (W.view(np.uint32) >> 16).astype(np.uint16)
+    xb = (x.view(np.uint32) >> 16).astype(np.uint16)
+    for contract in (0, 2):
+        got = orc.gemv(contract, W, x, threads=False)
+        for r in range(M):
+            if contract == 0:
+                p = orc.native_product_array(wb[r], xb).astype(np.uint32) << 16
+                prod = p.view(F)
+            else:
+                prod = (W[r] * x).astype(F)
+            want = _literal_gemv_row(prod)
+            assert got[r].view(np.uint32) == want.view(np.uint32), (contract, r)
+
+
 def test_gemv_tiny_order(orc):
     # acc = (acc + lo) + hi per beat: (0 + 2^24) + 1 -> 2^24; then
     # (2^24 + -2^24) + 0 = 0.  Separate lo/hi banks would give 1.
@@ -153,6 +201,56 @@ def test_output_norm_gate(orc):
     np.testing.assert_allclose(out, np.full(2048, s, F), rtol=2e-6)
 
 
+def _rms_scale(total, n):
+    # 1 / sqrtf(total / n + 1e-6f) in float32
+    return F(1.0) / np.sqrt(F(total) / F(n) + F(1e-6))
+
+
+def test_rmsnorm_sum_is_chunked_then_sequential(orc):
+    # gdn_model.cpp:1432-1450: sixteen-value chunks summed in lane order from
+    # 0, the 128 chunk sums then added in order.  x^2 values:
+    #  (a) chunk 0 = [2^24, 1 x 15], chunk 1 = sixteen 1s: the chunk sums are
+    #      2^24 (each +1 is a tie that rounds back to 2^24) and 16, total
+    #      2^24 + 16 exactly; one flat sequential sum over all 2048 squares
+    #      stays at 2^24.
+    #  (b) chunk 0 = [2^24], chunks 1..127 = [1]: chunk sums added in order
+    #      stay at 2^24; a balanced tree over the chunk sums (127 first) gives
+    #      2^24 + 128.
+    # Expected outputs from the closed-form totals (FP32 arm: no rounding).
+    x = np.zeros(2048, F)
+    x[0] = 4096.0
+    x[1:32] = 1.0
+    w = np.ones(2048, F)
+    out = orc.rmsnorm(2, x, w)
+    want = x * _rms_scale(2.0 ** 24 + 16, 2048)
+    assert (out.view(np.uint32) == want.view(np.uint32)).all()
+    assert not (out == x * _rms_scale(2.0 ** 24, 2048)).all()
+    x = np.zeros(2048, F)
+    x[0] = 4096.0
+    x[16::16] = 1.0
+    out = orc.rmsnorm(2, x, w)
+    want = x * _rms_scale(2.0 ** 24, 2048)
+    assert (out.view(np.uint32) == want.view(np.uint32)).all()
+    assert not (out == x * _rms_scale(2.0 ** 24 + 128, 2048)).all()
+
+
+def test_output_norm_sum_is_chunked_per_head(orc):
+    # The same association per 256-value head (16 chunks of 16): head 0 holds
+    # [4096, 1 x 31] (chunk sums 2^24 and 16 -> 2^24 + 16), head 1 holds 4096
+    # then a 1 in each later chunk (sums in order stay 2^24).  Gate g = 2^7
+    # with sigmoid(2^7) = 1 in float32, so out = x * scale * 128.
+    o = np.zeros(2048, F)
+    o[0], o[1:32] = 4096.0, 1.0
+    o[256], o[256 + 16:512:16] = 4096.0, 1.0
+    g = np.full(2048, 128.0, F)
+    out = orc.output_norm_gate(2, o, g, np.ones(256, F), 8, 256)
+    s0 = _rms_scale(2.0 ** 24 + 16, 256)
+    s1 = _rms_scale(2.0 ** 24, 256)
+    assert (out[:256] == o[:256] * s0 * F(128)).all()
+    assert (out[256:512] == o[256:512] * s1 * F(128)).all()
+    assert s0 != s1
+
+
 # ----------------------------------------------------------------- conv
 
 def test_conv_taps_and_shift(orc):
@@ -177,6 +275,27 @@ def test_conv_taps_and_shift(orc):
     # zero tails and zero weights give silu(0) = 0
     out, _ = orc.conv_silu(0, raw, np.zeros((C, 4), F), np.zeros((3, C), F))
     assert (out == 0).all()
+
+
+def test_conv_sum_is_left_associated(orc):
+    # s = ((t0 w0 + t1 w1) + t2 w2) + x w3 (gdn_model.cpp:1646-1650) with
+    # products 2^24, 1, 1, 1: every +1 onto 2^24 is a tie that rounds back,
+    # so s = 2^24 and silu(s) = 2^24.  Any pairing of the last three terms
+    # first (1 + 1 = 2, or 1 + 1 + 1 = 3 -> 2^24 + 2 or + 4) differs.
+    C = 2048
+    tails = np.ones((3, C), F)
+    tails[0] = 4096.0
+    w = np.zeros((C, 4), F)
+    w[:, 0] = 4096.0
+    w[:, 1:] = 1.0
+    out, _ = orc.conv_silu(2, np.ones(C, F), w, tails, orc.CR)
+    assert (out == TWO24).all()
+    # the newest term alone large: ((1 + 1) + 1) + 2^24 = 2^24 + 3 -> 2^24 + 4
+    tails = np.ones((3, C), F)
+    w = np.ones((C, 4), F)
+    w[:, 3] = TWO24
+    out, _ = orc.conv_silu(2, np.ones(C, F), w, tails, orc.CR)
+    assert (out == F(2.0 ** 24 + 4)).all()
 
 
 # ----------------------------------------------------------------- recurrence
