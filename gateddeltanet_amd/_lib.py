@@ -203,6 +203,8 @@ SIGNATURES = {
     "gdn_test_gemv": (c_int, [c_int, FP, FP, c_uint32, c_uint32, FP]),
     "gdn_test_recurrence": (c_int, [c_int, c_uint32, c_uint32, FP, FP, FP, FP, FP, FP, FP, FP, FP]),
     "gdn_test_layer": (c_int, [POINTER(GDNRunState), c_uint32, c_uint32, FP, FP]),
+    "gdn_recurrence_noalloc": (c_int, [c_int, c_uint32, c_uint32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                       c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "gdn_logits_parity_init": (None, [LP]),
     "gdn_logits_parity_step": (None, [LP, FP, FP, c_uint32, c_uint32, c_int]),
     "gdn_logits_parity_nrmse": (ctypes.c_double, [LP]),

@@ -385,6 +385,20 @@ int gdn_test_recurrence(int contract, uint32_t n_heads, uint32_t n_steps,
                         const float *q, const float *k, const float *v,
                         const float *a, const float *b, const float *a_log,
                         const float *dt_bias, float *S, float *o);
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops that forbid it): the
+ * steps of gdn_test_recurrence on caller-owned DEVICE buffers, allocating
+ * nothing.  Arguments and layouts as gdn_test_recurrence, all device
+ * pointers, except S, which is in the engine's device format: [heads][256][256]
+ * BF16 bits (uint16) for GDN_CONTRACT_REF, FP32 otherwise.  The per-step
+ * (beta, decay) pairs live in a fixed 128 KiB device array of 16384 pairs that
+ * every call on a GPU shares (steps run in chunks that fit it); n_heads above
+ * 16384 is rejected.  Work is enqueued on `stream` (a hipStream_t; NULL = the
+ * null stream) and not waited for.  Calls that overlap on one GPU race on the
+ * shared array. */
+int gdn_recurrence_noalloc(int contract, uint32_t n_heads, uint32_t n_steps, const float *q,
+                           const float *k, const float *v, const float *a, const float *b,
+                           const float *a_log, const float *dt_bias, void *S, float *o, void *stream);
 /* Layer `layer` of the run state's model for n_steps teacher-forced residual
  * inputs x_in[step][H] (BF16-exact for the BF16 contracts): the same kernels
  * a decode step runs for that layer, against the run state's persistent
