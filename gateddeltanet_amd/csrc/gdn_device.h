@@ -132,6 +132,22 @@ __device__ __forceinline__ float wave_tree64(float v) {
     return u2f(wave_reduce64(f2u(v), [](uint32_t a, uint32_t b) { return f2u(u2f(a) + u2f(b)); }));
 }
 
+// Balanced pairwise sum of each 32-lane half's values (the lower five levels
+// of gdn_tree_reduce_256 over 32 consecutive values), left in every lane of
+// the half.
+__device__ __forceinline__ float wave_tree32(float v) {
+    auto add = [](uint32_t a, uint32_t b) { return f2u(u2f(a) + u2f(b)); };
+    uint32_t u = f2u(v);
+    u = add(u, (uint32_t)__builtin_amdgcn_mov_dpp((int)u, 0xB1, 0xf, 0xf, false));
+    u = add(u, (uint32_t)__builtin_amdgcn_mov_dpp((int)u, 0x4E, 0xf, 0xf, false));
+    u = add(u, (uint32_t)__builtin_amdgcn_mov_dpp((int)u, 0x141, 0xf, 0xf, false));
+    u = add(u, (uint32_t)__builtin_amdgcn_mov_dpp((int)u, 0x140, 0xf, 0xf, false));
+    const int lane = threadIdx.x & 63;
+    const auto s16 = __builtin_amdgcn_permlane16_swap((int)u, (int)u, false, false);
+    u = add(u, (uint32_t)(((lane >> 4) & 1) ? s16[0] : s16[1]));
+    return u2f(u);
+}
+
 // Sum over lane quads (lanes 4i..4i+3) in XOR-butterfly pairing, in every
 // lane of the quad.
 __device__ __forceinline__ float quad_sum(float v) {
@@ -155,38 +171,54 @@ __device__ __forceinline__ void head_scalars(float a, float b, float a_log, floa
     decay = exp_cr(decay_val);
 }
 
+// Recurrent-state layouts.  Row-major: head h, key row j, value column i
+// at h*65536 + j*256 + i (the .gdnstate order).  Tiled: the 256 x CB tile
+// of columns [c0, c0 + CB) is contiguous, rows in order, so a workgroup
+// owning one tile reads and writes whole cache lines:
+// h*65536 + (c0/CB)*256*CB + j*CB + (i - c0).
+template <bool TILED, int CB>
+__device__ __forceinline__ size_t state_index(int h, int j, int c0) {
+    if constexpr (TILED) return (size_t)h * kHD * kHD + (size_t)(c0 / CB) * kHD * CB + (size_t)j * CB;
+    else return (size_t)h * kHD * kHD + (size_t)j * kHD + c0;
+}
+
 // Gated delta rule for one head and CB state columns (beta/decay per head
-// come from the QKVG kernel), run by one workgroup of 256 threads.
-//   q/k L2 norms in gdn_tree_reduce_256 order (four wave butterflies, then
-//   (w0 + w1) + (w2 + w3)), alpha = tree256(qn * kn);
+// come from the QKVG kernel), run by one workgroup of 256 threads; thread t
+// holds key row t of the tile (CB columns) in registers.
+//   q/k L2 norms in gdn_tree_reduce_256 order: with PRE the QKVG kernel
+//   has already reduced each 16-row block (the tree's lower four levels;
+//   qk_part[h*16 + b], k at offset 128) and the top four levels run here,
+//   otherwise four wave butterflies then (w0 + w1) + (w2 + w3);
+//   alpha = tree256(qn * kn) (only o needs it, after the chains);
 //   every product S[j][i] * kn[j] and S[j][i] * qn[j] is formed in parallel
 //   into column-major LDS tiles, then lane i runs the r_i chain and lane
 //   CB + i the p_i chain over j = 0..255 in order (only the dependent adds
 //   are serial); delta and o; the update S' = decay * S + kn (x) delta is
 //   applied to the tile still held in registers.
-template <int C, int CB>
+//   With OSUM (CB = 16: one tile is one 16-value chunk of the output norm)
+//   the workgroup also writes sum_i R(o_i)^2 in order, the chunk's sum of
+//   squares, to o_sum[h*16 + c0/16].
+template <int C, int CB, bool TILED, bool PRE, bool OSUM>
 __device__ __forceinline__ void recur_block(const float *__restrict__ qp, const float *__restrict__ kp,
                                             const float *__restrict__ vp, const float *__restrict__ bd,
-                                            void *__restrict__ state, float *__restrict__ attn, const int h,
+                                            const float *__restrict__ qk_part, void *__restrict__ state,
+                                            float *__restrict__ attn, float *__restrict__ o_sum, const int h,
                                             const int c0) {
-    static_assert(2 * CB <= 64 && (CB % 8) == 0, "one wave runs both chains of every column");
-    constexpr int EPT = kHD * CB / kT;                  // state elements per thread
-    constexpr int PER_ROW = CB / EPT;                   // threads per tile row
+    static_assert(CB == 16 || CB == 32, "one wave runs both chains of every column; a thread holds one row");
+    static_assert(!OSUM || CB == 16, "an output-norm chunk is 16 columns");
+    constexpr int EPT = CB;                             // state elements per thread (its row)
     constexpr int LDT = kHD + 4;                        // padded column stride of the product tiles
-    static_assert(EPT % 8 == 0 && PER_ROW * EPT == CB, "whole 16-byte pieces per thread");
-    __shared__ float qn[kHD], kn[kHD];
     __shared__ __attribute__((aligned(16))) float pk_t[CB * LDT];  // S[j][i] * kn[j] at [i][j]
     __shared__ __attribute__((aligned(16))) float pq_t[CB * LDT];  // S[j][i] * qn[j] at [i][j]
     __shared__ float dl[CB];
     __shared__ float red[8], red2[4];
     const int t = threadIdx.x;
     const int lane = t & 63, w = t >> 6;
-    const int row = t / PER_ROW, col = (t - row * PER_ROW) * EPT;  // this thread's tile piece
-    const size_t sidx = (size_t)h * kHD * kHD + (size_t)row * kHD + c0 + col;
+    const size_t sidx = state_index<TILED, CB>(h, t, c0);
 
     const float q = qp[h * kHD + t], k = kp[h * kHD + t];
     const float vi = (t < CB) ? vp[h * kHD + c0 + t] : 0.0f;
-    float sv[EPT];  // S[row][c0 + col + e]
+    float sv[EPT];  // S[t][c0 + e]
     {
         constexpr int NV = (C == kRef) ? EPT / 8 : EPT / 4;
         u32x4 tr[NV];
@@ -213,28 +245,38 @@ __device__ __forceinline__ void recur_block(const float *__restrict__ qp, const 
     }
     const float beta = bd[2 * h], decay = bd[2 * h + 1];
 
-    const float qs = wave_tree64(q * q), ks = wave_tree64(k * k);
-    if (lane == 0) {
-        red[w] = qs;
-        red[4 + w] = ks;
+    float q_sq, k_sq;
+    if constexpr (PRE) {
+        const f32x4 *qp4 = reinterpret_cast<const f32x4 *>(qk_part + h * 16);
+        const f32x4 *kp4 = reinterpret_cast<const f32x4 *>(qk_part + 128 + h * 16);
+        float qv[16], kv[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const f32x4 a = qp4[i], b = kp4[i];
+            qv[4 * i] = a.x; qv[4 * i + 1] = a.y; qv[4 * i + 2] = a.z; qv[4 * i + 3] = a.w;
+            kv[4 * i] = b.x; kv[4 * i + 1] = b.y; kv[4 * i + 2] = b.z; kv[4 * i + 3] = b.w;
+        }
+        q_sq = tree16(qv);
+        k_sq = tree16(kv);
+    } else {
+        const float qs = wave_tree64(q * q), ks = wave_tree64(k * k);
+        if (lane == 0) {
+            red[w] = qs;
+            red[4 + w] = ks;
+        }
+        __syncthreads();
+        q_sq = (red[0] + red[1]) + (red[2] + red[3]);
+        k_sq = (red[4] + red[5]) + (red[6] + red[7]);
     }
-    __syncthreads();
-    const float q_sq = (red[0] + red[1]) + (red[2] + red[3]);
-    const float k_sq = (red[4] + red[5]) + (red[6] + red[7]);
     const float q_inv = 1.0f / __builtin_sqrtf(q_sq + 1e-6f);
     const float k_inv = 1.0f / __builtin_sqrtf(k_sq + 1e-6f);
-    const float qv = q * q_inv, kv = k * k_inv;
-    qn[t] = qv;
-    kn[t] = kv;
-    const float qk = wave_tree64(qv * kv);
+    const float qj = q * q_inv, kj = k * k_inv;  // row t's normalised q and k
+    const float qk = wave_tree64(qj * kj);
     if (lane == 0) red2[w] = qk;
-    __syncthreads();
-    const float alpha = (red2[0] + red2[1]) + (red2[2] + red2[3]);
-    const float kj = kn[row], qj = qn[row];
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
-        pk_t[(col + e) * LDT + row] = sv[e] * kj;
-        pq_t[(col + e) * LDT + row] = sv[e] * qj;
+        pk_t[e * LDT + t] = sv[e] * kj;
+        pq_t[e * LDT + t] = sv[e] * qj;
     }
     __syncthreads();
 
@@ -262,19 +304,31 @@ __device__ __forceinline__ void recur_block(const float *__restrict__ qp, const 
         } else {
             pv = __shfl(acc, (lane + CB) & 63);
         }
+        float o = 0.0f;
         if (!is_p) {
+            const float alpha = (red2[0] + red2[1]) + (red2[2] + red2[3]);
             const float r = acc;
             const float delta = beta * (vi - decay * r);
-            const float o = 0.0625f * (decay * pv + alpha * delta);
+            o = R<C>(0.0625f * (decay * pv + alpha * delta));
             dl[t] = delta;
-            attn[h * kHD + c0 + t] = R<C>(o);
+            attn[h * kHD + c0 + t] = o;
+        }
+        if constexpr (OSUM) {
+            // the chunk's sum of squares, lanes 0..15 in order from 0.  The
+            // lane reads run in every chain lane (not under t == 0), so each
+            // lane's square is computed where it is read.
+            const uint32_t sq = f2u(o * o);
+            float sum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sum += u2f((uint32_t)__builtin_amdgcn_readlane((int)sq, i));
+            if (t == 0) o_sum[h * (kHD / 16) + c0 / 16] = sum;
         }
     }
     __syncthreads();
 
     float nv[EPT];
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) nv[e] = decay * sv[e] + kj * dl[col + e];
+    for (int e = 0; e < EPT; ++e) nv[e] = decay * sv[e] + kj * dl[e];
     if constexpr (C == kRef) {
 #pragma unroll
         for (int i = 0; i < EPT / 8; ++i) {

@@ -330,6 +330,7 @@ struct XSrc {
     const float *w;
     float *res_out;
     float *aux_out;
+    const float *osum; // PRO_ONORM (BF16): the output norm's 16-value chunk sums [8 heads][16]
     int *err;          // host-mapped error word: set when a bounded wait runs out
     uint32_t *xdump;   // when set, workgroup 0 stores its GEMV input (K lane words) and fast-path verdict
     int vocab;
@@ -559,7 +560,7 @@ struct Prologue {
     }
 
     // barriers finish_bf16 passes through
-    static constexpr int kSyncs = (PRO == PRO_PLAIN) ? 1 : 3;
+    static constexpr int kSyncs = (PRO == PRO_PLAIN || PRO == PRO_ONORM) ? 1 : 3;
 
     // BF16 contracts: called by threads 0..255 (the element owners); every
     // barrier is sync(), kSyncs of them.
@@ -666,32 +667,32 @@ struct Prologue {
                 }
             }
         } else {
-            // per-head sums of squares: 16-value chunks (thread pairs), then
-            // each head's 16 chunk sums in order (one lane of wave 0 per head)
-            float a[8], g[8], s[8], w[8];
+            // per-head sums of squares: the recurrence wrote each 16-value
+            // chunk's sum (one chunk per recurrence workgroup); every thread
+            // adds its head's 16 chunk sums in order itself
             if (act) {
+                float a[8], g[8], sg[8], w[8];
                 unpack8(a4, a);
                 unpack8(b4, g);
-                unpack8(c4, s);
+                unpack8(c4, sg);
                 unpack8(w4, w);
-                const float cs = chunk_sumsq8(a);
-                if (t & 1) scratch[t >> 1] = cs;
-            }
-            sync();
-            if (t < kNH) {
+                const int h = t >> 5;  // elements 8t.. belong to head t / 32
+                const f32x4 *cs4 = reinterpret_cast<const f32x4 *>(src.osum + h * (kHD / 16));
                 float sum = 0.0f;
 #pragma unroll
-                for (int ch = 0; ch < kHD / 16; ++ch) sum += scratch[t * (kHD / 16) + ch];
-                bcast[t] = 1.0f / __builtin_sqrtf(sum / (float)kHD + src.eps);
-            }
-            sync();
-            if (act) {
-                const float sc = bcast[t >> 5];  // elements 8t.. belong to head t / 32
+                for (int i = 0; i < 4; ++i) {
+                    const f32x4 c = cs4[i];
+                    sum += c.x;
+                    sum += c.y;
+                    sum += c.z;
+                    sum += c.w;
+                }
+                const float sc = 1.0f / __builtin_sqrtf(sum / (float)kHD + src.eps);
                 uint32_t pairs[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const float x0 = a[2 * j] * sc * w[2 * j] * g[2 * j] * s[2 * j];
-                    const float x1 = a[2 * j + 1] * sc * w[2 * j + 1] * g[2 * j + 1] * s[2 * j + 1];
+                    const float x0 = a[2 * j] * sc * w[2 * j] * g[2 * j] * sg[2 * j];
+                    const float x1 = a[2 * j + 1] * sc * w[2 * j + 1] * g[2 * j + 1] * sg[2 * j + 1];
                     pairs[j] = cvt_pk(x0, x1);
                 }
                 store_pairs8(xs, pairs, st);
@@ -791,6 +792,7 @@ struct Epi {
     float *tails;      // QKVG: the layer's conv tails (3 stripes)
     float *ab;         // QKVG: a[8], b[8] (BF16-rounded)
     float *bd;         // QKVG: (beta, decay) per head
+    float *qk_part;    // QKVG: q and k sums of squares per 16-row block, [2][8 heads][16]
     float *part_val;   // LM: per-block argmax
     int *part_idx;
 };
@@ -1242,6 +1244,7 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     __syncthreads();
     if (wave < CHW) {
         const float y = chain_rows<K, CR>(part);
+        float conv_out = 0.0f;  // QKVG: the row's conv + SiLU output (owner lanes)
         if (owner) {
             const int rr = t >> 2;  // row within the workgroup
             const int r = row0 + rr;
@@ -1261,7 +1264,8 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
                     tl[kH + ch] = tail_b[2];
                     tl[2 * kH + ch] = (uint16_t)(f2u(yv) >> 16);
                     const float s = t0 * taps.x + t1 * taps.y + t2 * taps.z + yv * taps.w;
-                    ep.y[r] = R<C>(silu_ref(s));
+                    conv_out = R<C>(silu_ref(s));
+                    ep.y[r] = conv_out;
                 } else {
                     ep.y2[r - 3 * kH] = yv;
                     ep.y3[r - 3 * kH] = sigmoid_ref(yv);
@@ -1271,6 +1275,27 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
             } else {
                 ep.y[r] = y;  // LM: FP32 logits (no rounding point)
                 ybuf[rr] = y;
+            }
+        }
+        if constexpr (EPI == EPI_QKVG) {
+            // q and k rows: each wave's 16 rows reduced in the tree order of
+            // gdn_tree_reduce_256 (its lower four levels) for the recurrence's
+            // L2 norms.  Row r sits in the lanes of quad r % 16; the owner's
+            // square goes to its quad, then the half-row and row mirrors and
+            // the 16- and 32-lane swaps pair rows (2i, 2i+1), then pairs of
+            // pairs, and so on (the sums of an XOR butterfly).
+            if (row0 < 2 * kH) {
+                const auto add = [](uint32_t a, uint32_t b) { return f2u(u2f(a) + u2f(b)); };
+                uint32_t v = f2u(conv_out * conv_out);
+                v = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x00, 0xf, 0xf, false);  // quad lane 0
+                v = add(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xf, 0xf, false));
+                v = add(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xf, 0xf, false));
+                const int lane = t & 63;
+                const auto s16 = __builtin_amdgcn_permlane16_swap((int)v, (int)v, false, false);
+                v = add(v, (uint32_t)(((lane >> 4) & 1) ? s16[0] : s16[1]));
+                const auto s32 = __builtin_amdgcn_permlane32_swap((int)v, (int)v, false, false);
+                v = add(v, (uint32_t)((lane >> 5) ? s32[0] : s32[1]));
+                if (lane == 0) ep.qk_part[2 * blockIdx.x + wave] = u2f(v);
             }
         }
     }
@@ -1356,14 +1381,18 @@ __global__ __launch_bounds__(kT) void k_argmax(const float *__restrict__ part_va
     }
 }
 
-// One workgroup per (16 state columns, head): grid (kHD / CB, kNH).
-template <int C, int CB>
+// One workgroup per (16 state columns, head): grid (kHD / CB, kNH), state
+// in the tiled layout.  PRE: the q/k sums of squares come from the QKVG
+// kernel and the output norm's chunk sums go to o_sum (BF16 contracts).
+template <int C, int CB, bool PRE>
 __global__ __launch_bounds__(kT) void k_recur(const float *__restrict__ qp,
                                               const float *__restrict__ kp,
                                               const float *__restrict__ vp,
                                               const float *__restrict__ bd,
-                                              void *__restrict__ state, float *__restrict__ attn) {
-    recur_block<C, CB>(qp, kp, vp, bd, state, attn, blockIdx.y, blockIdx.x * CB);
+                                              const float *__restrict__ qk_part,
+                                              void *__restrict__ state, float *__restrict__ attn,
+                                              float *__restrict__ o_sum) {
+    recur_block<C, CB, true, PRE, PRE>(qp, kp, vp, bd, qk_part, state, attn, o_sum, blockIdx.y, blockIdx.x * CB);
 }
 
 // beta/decay for n heads from raw (a, b, a_log, dt_bias) (recurrence hook).
@@ -1427,7 +1456,7 @@ struct GDNEngine {
     float *resid = nullptr, *resid_alt = nullptr, *fhid = nullptr, *qkv = nullptr,
           *gate = nullptr, *sgate = nullptr, *ab = nullptr, *bd = nullptr, *attn = nullptr,
           *ybuf_o = nullptr, *dbuf = nullptr, *hbuf = nullptr, *lm_val = nullptr,
-          *xrow = nullptr, *logits = nullptr;
+          *xrow = nullptr, *logits = nullptr, *qkpart = nullptr, *osum = nullptr;
     int *lm_idx = nullptr;
     // pinned, mapped, coherent host words: [0] token in, [1] token out (-1
     // until the step's argmax lands), [2] kernel error word
@@ -1463,6 +1492,21 @@ void *layer_state(GDNEngine *e, int l) {
 size_t state_floats(const GDNEngine *e) { return (size_t)e->layers * kNH * kHD * kHD; }
 size_t state_bytes(const GDNEngine *e) { return state_floats(e) * (e->contract == kRef ? 2 : 4); }
 size_t tail_floats(const GDNEngine *e) { return (size_t)e->layers * 3 * kTailStripe; }
+
+// The recurrent state's row-major order [heads][256 K][256 V] (.gdnstate)
+// <-> the device's tiled order, in which each recurrence workgroup's 256 x
+// kCB tile is contiguous (state_index<true, kCB>).
+template <class T>
+void tile_state(const T *src, T *dst, size_t heads, bool to_tiles) {
+    for (size_t h = 0; h < heads; ++h)
+        for (int j = 0; j < kHD; ++j)
+            for (int c = 0; c < kHD; ++c) {
+                const size_t rm = h * kHD * kHD + (size_t)j * kHD + c;
+                const size_t tl = h * kHD * kHD + (size_t)(c / kCB) * kHD * kCB + (size_t)j * kCB + (c % kCB);
+                if (to_tiles) dst[tl] = src[rm];
+                else dst[rm] = src[tl];
+            }
+}
 
 // Product-counter slots: one per GEMV launch of a step (layer l: 4l QKVG,
 // 4l + 1 o_proj, 4l + 2 gate/up, 4l + 3 down; 4L the LM head), each K lane
@@ -1662,8 +1706,9 @@ int alloc_buffers(GDNEngine *e) {
     GDN_HIP(hipMalloc(&e->tails, tail_floats(e) * 4));
     GDN_HIP(hipMemset(e->tails, 0, tail_floats(e) * 4));
     const size_t nblk_lm = (size_t)e->vocab / kRbLm;
-    const size_t act_floats =
-        3 * kH + 3 * kH + 2 * kH + 16 + 2 * kNH + 3 * kH + kI + nblk_lm + kH + (size_t)e->vocab;
+    auto up64 = [](size_t n) { return (n + 63) & ~(size_t)63; };  // 256-byte aligned pieces
+    const size_t act_floats = 3 * kH + 3 * kH + 2 * kH + 64 + 64 + 3 * kH + kI + up64(nblk_lm) + kH +
+                              up64((size_t)e->vocab) + 2 * kNH * 16 + kNH * (kHD / 16);
     GDN_HIP(hipMalloc(&e->act, act_floats * 4));
     GDN_HIP(hipMemset(e->act, 0, act_floats * 4));
     float *p = e->act;
@@ -1673,15 +1718,17 @@ int alloc_buffers(GDNEngine *e) {
     e->qkv = p; p += 3 * kH;
     e->gate = p; p += kH;
     e->sgate = p; p += kH;
-    e->ab = p; p += 16;
-    e->bd = p; p += 2 * kNH;
+    e->ab = p; p += 64;
+    e->bd = p; p += 64;
     e->attn = p; p += kH;
     e->ybuf_o = p; p += kH;
     e->dbuf = p; p += kH;
     e->hbuf = p; p += kI;
-    e->lm_val = p; p += nblk_lm;
+    e->lm_val = p; p += up64(nblk_lm);
     e->xrow = p; p += kH;
-    e->logits = p; p += e->vocab;
+    e->logits = p; p += up64((size_t)e->vocab);
+    e->qkpart = p; p += 2 * kNH * 16;
+    e->osum = p; p += kNH * (kHD / 16);
     GDN_HIP(hipMalloc(&e->lm_idx, nblk_lm * sizeof(int)));
     // the step reads its token from and writes its argmax to host memory
     // directly: no copy kernels on a token's path
@@ -1731,6 +1778,7 @@ void launch_qkvg(GDNEngine *e, int l, const float *res_a, const float *res_b, hi
     q.tails = layer_tails(e, l);
     q.ab = e->ab;
     q.bd = e->bd;
+    q.qk_part = e->qkpart;
     XSrc xq = xsrc(e, res_a, res_b, nullptr, aux + kAuxAttnNorm, e->resid, nullptr, dump_slot(e, 4 * l));
     if constexpr (PRO0 == PRO_EMBED) {
         xq.emb = e->w_emb;
@@ -1749,16 +1797,17 @@ void launch_qkvg(GDNEngine *e, int l, const float *res_a, const float *res_b, hi
 
 template <int C>
 void launch_recur(GDNEngine *e, int l, hipStream_t s) {
-    hipLaunchKernelGGL((k_recur<C, kCB>), dim3(kHD / kCB, kNH), dim3(kT), 0, s, e->qkv,
-                       e->qkv + kH, e->qkv + 2 * kH, e->bd, layer_state(e, l), e->attn);
+    hipLaunchKernelGGL((k_recur<C, kCB, C != kFp32>), dim3(kHD / kCB, kNH), dim3(kT), 0, s, e->qkv,
+                       e->qkv + kH, e->qkv + 2 * kH, e->bd, e->qkpart, layer_state(e, l), e->attn, e->osum);
 }
 
 template <int C>
 void launch_o(GDNEngine *e, int l, hipStream_t s) {
     Epi st{};
     st.y = e->ybuf_o;
-    const XSrc xo = xsrc(e, e->attn, e->gate, e->sgate, layer_aux(e, l) + kAuxONorm, nullptr, nullptr,
-                         dump_slot(e, 4 * l + 1));
+    XSrc xo = xsrc(e, e->attn, e->gate, e->sgate, layer_aux(e, l) + kAuxONorm, nullptr, nullptr,
+                   dump_slot(e, 4 * l + 1));
+    xo.osum = e->osum;
     if constexpr (C == kFp32) {
         hipLaunchKernelGGL((k_gemv<C, kH, kRbO, PRO_ONORM, EPI_STORE>), dim3(kH / kRbO), dim3(kT), 0, s,
                            e->w_o[l], e->i_o[l], xo, st);
@@ -2036,15 +2085,18 @@ int load_state(GDNEngine *e, const float *rec, size_t floats) {
             gdn_report_non_bf16("REF-contract recurrent state", rec, bad);
             return -1;
         }
-        std::vector<uint16_t> b(n);
+        std::vector<uint16_t> b(n), tiles(n);
         for (size_t i = 0; i < n; ++i) {
             uint32_t u;
             std::memcpy(&u, rec + i, 4);
             b[i] = (uint16_t)(u >> 16);
         }
-        return h2d(e, e->state, b.data(), n * 2);
+        tile_state(b.data(), tiles.data(), n / (kHD * kHD), true);
+        return h2d(e, e->state, tiles.data(), n * 2);
     }
-    return h2d(e, e->state, rec, n * 4);
+    std::vector<float> tiles(n);
+    tile_state(rec, tiles.data(), n / (kHD * kHD), true);
+    return h2d(e, e->state, tiles.data(), n * 4);
 }
 
 int save_state(GDNEngine *e, float *rec, size_t floats) {
@@ -2054,15 +2106,19 @@ int save_state(GDNEngine *e, float *rec, size_t floats) {
         return -1;
     }
     if (e->contract == kRef) {
-        std::vector<uint16_t> b(n);
-        if (d2h(e, b.data(), e->state, n * 2)) return -1;
+        std::vector<uint16_t> tiles(n), b(n);
+        if (d2h(e, tiles.data(), e->state, n * 2)) return -1;
+        tile_state(tiles.data(), b.data(), n / (kHD * kHD), false);
         for (size_t i = 0; i < n; ++i) {
             const uint32_t u = (uint32_t)b[i] << 16;
             std::memcpy(rec + i, &u, 4);
         }
         return 0;
     }
-    return d2h(e, rec, e->state, n * 4);
+    std::vector<float> tiles(n);
+    if (d2h(e, tiles.data(), e->state, n * 4)) return -1;
+    tile_state(tiles.data(), rec, n / (kHD * kHD), false);
+    return 0;
 }
 
 // .gdnstate conv section [L][q,k,v][W-1][H] <-> the device's tail stripes.
@@ -2601,15 +2657,18 @@ int gdn_test_recurrence(int contract, uint32_t n_heads, uint32_t n_steps, const 
     GDN_HIP(hipMemcpy(dal, a_log, ns * 4, hipMemcpyHostToDevice));
     GDN_HIP(hipMemcpy(ddt, dt_bias, ns * 4, hipMemcpyHostToDevice));
     if (contract == kRef) {
-        std::vector<uint16_t> sb(nstate);
+        std::vector<uint16_t> sb(nstate), tiles(nstate);
         for (size_t i = 0; i < nstate; ++i) {
             uint32_t u;
             std::memcpy(&u, S + i, 4);
             sb[i] = (uint16_t)(u >> 16);
         }
-        GDN_HIP(hipMemcpy(dS, sb.data(), nstate * 2, hipMemcpyHostToDevice));
+        tile_state(sb.data(), tiles.data(), n_heads, true);
+        GDN_HIP(hipMemcpy(dS, tiles.data(), nstate * 2, hipMemcpyHostToDevice));
     } else {
-        GDN_HIP(hipMemcpy(dS, S, nstate * 4, hipMemcpyHostToDevice));
+        std::vector<float> tiles(nstate);
+        tile_state(S, tiles.data(), n_heads, true);
+        GDN_HIP(hipMemcpy(dS, tiles.data(), nstate * 4, hipMemcpyHostToDevice));
     }
     float *dbd;
     GDN_HIP(hipMalloc(&dbd, 2 * ns * 4));
@@ -2619,8 +2678,8 @@ int gdn_test_recurrence(int contract, uint32_t n_heads, uint32_t n_steps, const 
     for (uint32_t s = 0; s < n_steps; ++s) {
         const size_t ov = (size_t)s * n_heads * kHD, os = (size_t)s * n_heads;
 #define GDN_REC(CC)                                                                             \
-    hipLaunchKernelGGL((k_recur<CC, kCB>), grid, block, 0, 0, dq + ov, dk + ov, dv + ov, dbd + 2 * os, \
-                       dS, dout + ov)
+    hipLaunchKernelGGL((k_recur<CC, kCB, false>), grid, block, 0, 0, dq + ov, dk + ov, dv + ov, dbd + 2 * os, \
+                       nullptr, dS, dout + ov, nullptr)
         if (contract == kRef) GDN_REC(kRef);
         else if (contract == kBf16w) GDN_REC(kBf16w);
         else GDN_REC(kFp32);
@@ -2630,14 +2689,17 @@ int gdn_test_recurrence(int contract, uint32_t n_heads, uint32_t n_steps, const 
     GDN_HIP(hipDeviceSynchronize());
     GDN_HIP(hipMemcpy(o, dout, nv * 4, hipMemcpyDeviceToHost));
     if (contract == kRef) {
-        std::vector<uint16_t> sb(nstate);
-        GDN_HIP(hipMemcpy(sb.data(), dS, nstate * 2, hipMemcpyDeviceToHost));
+        std::vector<uint16_t> sb(nstate), tiles(nstate);
+        GDN_HIP(hipMemcpy(tiles.data(), dS, nstate * 2, hipMemcpyDeviceToHost));
+        tile_state(tiles.data(), sb.data(), n_heads, false);
         for (size_t i = 0; i < nstate; ++i) {
             const uint32_t u = (uint32_t)sb[i] << 16;
             std::memcpy(S + i, &u, 4);
         }
     } else {
-        GDN_HIP(hipMemcpy(S, dS, nstate * 4, hipMemcpyDeviceToHost));
+        std::vector<float> tiles(nstate);
+        GDN_HIP(hipMemcpy(tiles.data(), dS, nstate * 4, hipMemcpyDeviceToHost));
+        tile_state(tiles.data(), S, n_heads, false);
     }
     float *bufs[] = {dq, dk, dv, da, db, dal, ddt, dout, dbd};
     for (float *p : bufs) GDN_HIP(hipFree(p));
