@@ -203,6 +203,7 @@ SIGNATURES = {
     "gdn_test_gemv": (c_int, [c_int, FP, FP, c_uint32, c_uint32, FP]),
     "gdn_test_recurrence": (c_int, [c_int, c_uint32, c_uint32, FP, FP, FP, FP, FP, FP, FP, FP, FP]),
     "gdn_test_layer": (c_int, [POINTER(GDNRunState), c_uint32, c_uint32, FP, FP]),
+    "gdn_test_libm_array": (None, [c_int, FP, FP, c_size_t]),
     "gdn_recurrence_noalloc": (c_int, [c_int, c_uint32, c_uint32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "gdn_logits_parity_init": (None, [LP]),

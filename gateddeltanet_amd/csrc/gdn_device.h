@@ -10,6 +10,7 @@
 #include <cstdio>
 
 #include "gdn_amd.h"
+#include "gdn_libm.h"
 
 // Host side: return -1 from the enclosing function when a HIP call fails.
 #define GDN_HIP(call)                                                              \
@@ -74,24 +75,25 @@ __device__ __forceinline__ float R(float x) {
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b16) { return u2f(b16 << 16); }
 
-// exp and log1p through double: correctly rounded float results.
-__device__ __forceinline__ float exp_cr(float x) { return (float)exp((double)x); }
-__device__ __forceinline__ float log1p_cr(float x) { return (float)log1p((double)x); }
+// expf and log1pf as the reference's C library evaluates them (glibc 2.35,
+// gdn_libm.h): the engine's transcendentals equal the reference's bit for bit.
+__device__ __forceinline__ float exp_ref(float x) { return gdn_libm::gdn_expf(x); }
+__device__ __forceinline__ float log1p_ref(float x) { return gdn_libm::gdn_log1pf(x); }
 
 // gdn_sigmoid / gdn_silu / gdn_softplus, gdn_model.cpp:1307-1330.
 __device__ __forceinline__ float sigmoid_ref(float x) {
     if (x >= 0.0f) {
-        const float z = exp_cr(-x);
+        const float z = exp_ref(-x);
         return 1.0f / (1.0f + z);
     }
-    const float z = exp_cr(x);
+    const float z = exp_ref(x);
     return z / (1.0f + z);
 }
 __device__ __forceinline__ float silu_ref(float x) { return x * sigmoid_ref(x); }
 __device__ __forceinline__ float softplus_ref(float x) {
     if (x > 20.0f) return x;
-    if (x < -20.0f) return exp_cr(x);
-    return log1p_cr(exp_cr(x));
+    if (x < -20.0f) return exp_ref(x);
+    return log1p_ref(exp_ref(x));
 }
 
 // Balanced pairwise sum of 16 contiguous values (gemv32_tree16).
@@ -167,8 +169,8 @@ __device__ __forceinline__ void head_scalars(float a, float b, float a_log, floa
                                              float &beta, float &decay) {
     beta = sigmoid_ref(b);
     const float decay_in = a + dt_bias;
-    const float decay_val = -exp_cr(a_log) * softplus_ref(decay_in);
-    decay = exp_cr(decay_val);
+    const float decay_val = -exp_ref(a_log) * softplus_ref(decay_in);
+    decay = exp_ref(decay_val);
 }
 
 // Recurrent-state layouts.  Row-major: head h, key row j, value column i

@@ -11,6 +11,7 @@
 //   export_gdn_state.py:340-362  .gdnstate writer
 #include "gdn_amd.h"
 #include "gdn_internal.h"
+#include "gdn_libm.h"
 
 #include <algorithm>
 #include <cmath>
@@ -561,6 +562,12 @@ int gdn_model_wrap(GDNModel *m, const GDNWeightHeader *c, const float *data) {
     }
     assign_views(m);
     return 0;
+}
+
+void gdn_test_libm_array(int which, const float *in, float *out, size_t n) {
+#pragma omp parallel for schedule(static)
+    for (long long i = 0; i < (long long)n; ++i)
+        out[i] = which == 0 ? gdn_libm::gdn_expf(in[i]) : gdn_libm::gdn_log1pf(in[i]);
 }
 
 // ---- Beat512 lane accessors, gdn_model.h:207-210 ----

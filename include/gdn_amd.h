@@ -399,6 +399,10 @@ int gdn_test_recurrence(int contract, uint32_t n_heads, uint32_t n_steps,
 int gdn_recurrence_noalloc(int contract, uint32_t n_heads, uint32_t n_steps, const float *q,
                            const float *k, const float *v, const float *a, const float *b,
                            const float *a_log, const float *dt_bias, void *S, float *o, void *stream);
+/* The engine's expf (which = 0) or log1pf (which = 1) evaluated on the host
+ * over n inputs: the same code the kernels run, a restatement of the methods
+ * of the reference's C library (glibc 2.35) that equals it on every input. */
+void gdn_test_libm_array(int which, const float *in, float *out, size_t n);
 /* Layer `layer` of the run state's model for n_steps teacher-forced residual
  * inputs x_in[step][H] (BF16-exact for the BF16 contracts): the same kernels
  * a decode step runs for that layer, against the run state's persistent

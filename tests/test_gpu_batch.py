@@ -10,7 +10,7 @@ Bit-exact checks:
   * a 24-layer model whose projection rows each hold a single power of two
     (every projection sum then has one nonzero term, so summation order and
     product rounding cannot matter): the multi-stream engine equals the
-    batch-1 engine and the oracle (BF16W_FP32S, CR) bit for bit -- tokens,
+    batch-1 engine and the oracle (BF16W_FP32S, glibc transcendentals) bit for bit -- tokens,
     logits and every stream's state -- which pins the whole composition
     (norms, a/b rows, conv tails, recurrence, output norm, SwiGLU, residual
     adds, LM head and the argmax tie rule);
@@ -194,7 +194,7 @@ def test_one_hot_model_bit_exact_to_oracle(orc, onehot):
         for i in range(steps):
             got = bs.step(tokens[i])
             for s in range(nb):
-                ot, ol, oh = orc.decode_step(1, hdr, m.blob, st[s], cv[s], int(tokens[i, s]), orc.CR)
+                ot, ol, oh = orc.decode_step(1, hdr, m.blob, st[s], cv[s], int(tokens[i, s]), orc.LIBM)
                 assert got[s] == ot
                 assert equal_values(bs.logits(s), ol) and equal_values(bs.final_hidden(s), oh)
         for s in range(nb):
@@ -308,7 +308,7 @@ def test_batch_graph_eager_and_teacher_forced(model):
 
 
 def test_random_one_layer_against_exact_product_oracle(orc):
-    """One layer, four streams, three steps against ORC_BF16X (CR): the
+    """One layer, four streams, three steps against ORC_BF16X (LIBM): the
     remaining difference is the summation order of the projections."""
     m = g.Model.synth(num_layers=1, seed=3, std=0.02, bf16=True)
     hdr = orc.header_from(m.config)
@@ -321,7 +321,7 @@ def test_random_one_layer_against_exact_product_oracle(orc):
         for i in range(steps):
             got = bs.step(tokens[i])
             for s in range(nb):
-                ot, ol, _ = orc.decode_step(orc.BF16X, hdr, m.blob, st[s], cv[s], int(tokens[i, s]), orc.CR)
+                ot, ol, _ = orc.decode_step(orc.BF16X, hdr, m.blob, st[s], cv[s], int(tokens[i, s]), orc.LIBM)
                 lg = bs.logits(s)
                 err = np.abs(lg - ol).max()
                 assert err <= LOGIT_TOL, (i, s, err)

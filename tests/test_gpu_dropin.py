@@ -164,12 +164,12 @@ def test_reference_driver_call_sequence(orc, tmp_path):
     # the pairs with a special or subnormal operand: the planted weights
     # against every normal activation, plus whole rows against the exact
     # zeros BF16 residual adds produce (R(a + b) = 0 when a = -b), taken from
-    # the correctly rounded oracle's GEMV inputs along the same trajectory
+    # the oracle's GEMV inputs along the same trajectory
     hdr = orc.header_from(c)
     ost, ocv = rec.copy(), conv.copy()
     traces = []
     for s_ in range(steps):
-        tok, _, _, ins = orc.decode_step_trace(0, hdr, m.blob, ost, ocv, traj[s_], orc.CR)
+        tok, _, _, ins = orc.decode_step_trace(0, hdr, m.blob, ost, ocv, traj[s_], orc.LIBM)
         assert tok == traj[s_ + 1]
         traces.append(ins)
     want_special, want_flushed = expected_input_counts(m, traces, host_lm_head=True)
@@ -214,7 +214,7 @@ def test_product_counters_exact_path(orc):
         lib.gdn_reset_mixed_mul_stats()
         for tok in (3, 400, 17):
             rs.decode_step(tok)
-            _, logits, fh, ins = orc.decode_step_trace(1, hdr, m.blob, st, cv, tok, orc.CR)
+            _, logits, fh, ins = orc.decode_step_trace(1, hdr, m.blob, st, cv, tok, orc.LIBM)
             traces.append(ins)
             assert same_bits(rs.logits(), logits)
             xb = (fh.view(np.uint32) >> 16).astype(np.uint16)
@@ -244,7 +244,7 @@ def test_vocab_not_multiple_of_125(orc):
     try:
         for tok in (32007, 5):
             got = rs.decode_step(tok)
-            want, logits, _ = orc.decode_step(1, hdr, m.blob, st, cv, tok, orc.CR)
+            want, logits, _ = orc.decode_step(1, hdr, m.blob, st, cv, tok, orc.LIBM)
             assert got == want
             assert same_bits(rs.logits(), logits)
     finally:
