@@ -4,8 +4,8 @@
 // include/gdn_amd.h.
 //
 // One decode step (token id -> argmax token id) is one captured hipGraph of
-// 122 launches.  Per layer l (BF16 contracts; the FP32 control arm runs the
-// same steps with the row-block k_gemv):
+// 122 launches.  Per layer l (every contract; the FP32 control arm streams
+// FP32 weights through the same kernels):
 //   QKVG    k_gemv_cu: residual add + attention RMSNorm prologue (the
 //           embedding import in layer 0), BF16 GEMV [4H x H] (q,k,v,g),
 //           per-channel causal conv/SiLU with the conv-tail shift, gate and
@@ -23,9 +23,8 @@
 //
 // Arithmetic follows the reference's all-BF16 contract bit for bit (products
 // rounded to BF16 with DAZ/FTZ, tree16 + four-bank reduction, every operator
-// output rounded to BF16); exp/log1p are evaluated through double precision
-// (correctly rounded float results), the only place the reference's glibc
-// calls can differ.
+// output rounded to BF16); expf/log1pf are glibc's methods restated
+// (gdn_libm.h), so they match the reference's C library bit for bit too.
 #include <hip/hip_runtime.h>
 
 #include <chrono>
@@ -43,13 +42,6 @@
 
 namespace gdn {
 
-// Row blocking per GEMV (rows per workgroup).
-constexpr int kRbQkvg = 8;
-constexpr int kRbO = 4;
-constexpr int kRbGu = 8;   // 4 gate rows + the 4 matching up rows
-constexpr int kRbDown = 4;
-constexpr int kRbLm = 8;
-constexpr int kRbTest = 8;
 constexpr int kCB = 16;    // state columns per recurrence workgroup
 
 // Smallest nonzero and largest |w| of a matrix (after DAZ) and whether any
@@ -187,126 +179,8 @@ struct Hb {
     static constexpr int NB = K / 32;     // 32-column beats per row
 };
 
-// The row-block QKVG kernel's first kAbBlocks workgroups compute head h's
-// tiny a and b rows (workgroup h) instead of projection rows.
-constexpr int kAbBlocks = kNH;
-constexpr int kAbRows = 2;
-
 __device__ __forceinline__ float lane_word_value(uint32_t w, int k) {
     return (k & 1) ? u2f(w) : u2f(w << 16);
-}
-
-template <int K, int RB, int C>
-struct WRegs {
-    static constexpr int HB = Hb<K>::HB, HBP = Hb<K>::HBP;
-    static constexpr int ITEMS = RB * HB;
-    static constexpr int NIT = (ITEMS + kT - 1) / kT;
-    static constexpr bool kFull = (ITEMS % kT) == 0;
-    static constexpr bool kSameHb = (kT % HB) == 0;  // every item of a thread has one half-beat
-    static constexpr int WPI = (C == kFp32) ? 4 : 2;  // 16-byte loads per item
-    u32x4 v[NIT][WPI];
-
-    __device__ __forceinline__ void load(const void *__restrict__ W, int rb) {
-        constexpr size_t esz = (C == kFp32) ? 4 : 2;
-        const u32x4 *wb = reinterpret_cast<const u32x4 *>(reinterpret_cast<const char *>(W) +
-                                                           (size_t)rb * RB * K * esz);
-#pragma unroll
-        for (int i = 0; i < NIT; ++i) {
-            const int f = threadIdx.x + kT * i;
-            if (kFull || f < ITEMS) {
-#pragma unroll
-                for (int q = 0; q < WPI; ++q) v[i][q] = __builtin_nontemporal_load(wb + WPI * f + q);
-            }
-        }
-    }
-
-    // a/b workgroup h: rows a_h (item t < 128) and b_h (item t >= 128) of
-    // the FP32 a/b block, half-beat t % 128.
-    __device__ __forceinline__ void load_ab(const float *__restrict__ abw, int h) {
-        static_assert(K == kH && kAbRows == 2 && NIT * WPI >= 4, "a/b rows fit the weight registers");
-        const int t = threadIdx.x;
-        const int row = (t >> 7) * kNH + h, hb = t & 127;
-        const u32x4 *src = reinterpret_cast<const u32x4 *>(abw + (size_t)row * kH + hb * 16);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) v[q / WPI][q % WPI] = src[q];
-    }
-
-    template <bool FAST>
-    __device__ __forceinline__ void compute(const uint32_t *xs, float *part) const {
-        uint32_t xv[16];
-        if constexpr (kSameHb) lds_load16u(xs + (threadIdx.x % HB) * 16, xv);
-#pragma unroll
-        for (int i = 0; i < NIT; ++i) {
-            const int f = threadIdx.x + kT * i;
-            if (kFull || f < ITEMS) {
-                const int row = f / HB, hb = f - row * HB;
-                if constexpr (!kSameHb) lds_load16u(xs + hb * 16, xv);
-                float p[16];
-                if constexpr (C == kFp32) {
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        p[4 * q + 0] = u2f(v[i][q].x) * u2f(xv[4 * q + 0]);
-                        p[4 * q + 1] = u2f(v[i][q].y) * u2f(xv[4 * q + 1]);
-                        p[4 * q + 2] = u2f(v[i][q].z) * u2f(xv[4 * q + 2]);
-                        p[4 * q + 3] = u2f(v[i][q].w) * u2f(xv[4 * q + 3]);
-                    }
-                } else {
-                    const uint32_t w8[8] = {v[i][0].x, v[i][0].y, v[i][0].z, v[i][0].w,
-                                            v[i][1].x, v[i][1].y, v[i][1].z, v[i][1].w};
-                    if constexpr (FAST) {
-                        uint32_t rbits[8];
-                        dot8_bf16(w8, xv, rbits);
-                        dot8_bf16(w8 + 4, xv + 8, rbits + 4);
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) {
-                            p[2 * e] = u2f(rbits[e] << 16);
-                            p[2 * e + 1] = u2f(rbits[e] & 0xffff0000u);
-                        }
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) {
-                            p[2 * e] = native_exact(w8[e] & 0xffffu, u2f(xv[2 * e] << 16));
-                            p[2 * e + 1] = native_exact(w8[e] >> 16, u2f(xv[2 * e + 1]));
-                        }
-                    }
-                }
-                part[row * HBP + hb] = tree16(p);
-            }
-        }
-    }
-
-    // a/b rows: FP32 products x * w, tree16 per half-beat (gdn_gemv_tiny_ab).
-    __device__ __forceinline__ void compute_ab(const uint32_t *xs, float *part) const {
-        const int t = threadIdx.x, hb = t & 127;
-        uint32_t xv[16];
-        lds_load16u(xs + hb * 16, xv);
-        float p[16];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const u32x4 wq = v[q / WPI][q % WPI];
-            p[4 * q + 0] = u2f(xv[4 * q + 0]) * u2f(wq.x);
-            p[4 * q + 1] = u2f(xv[4 * q + 1]) * u2f(wq.y);
-            p[4 * q + 2] = u2f(xv[4 * q + 2]) * u2f(wq.z);
-            p[4 * q + 3] = u2f(xv[4 * q + 3]) * u2f(wq.w);
-        }
-        part[(t >> 7) * HBP + hb] = tree16(p);
-    }
-};
-
-// Wave 0 only.  Lane 4r ends with row r's result.
-template <int K, int RB>
-__device__ __forceinline__ float gemv_chain(const float *part) {
-    constexpr int HBP = Hb<K>::HBP, NB = Hb<K>::NB;
-    static_assert(RB * 4 <= 64, "one wave runs every bank chain");
-    const int lane = threadIdx.x;
-    float acc = 0.0f;
-    if (lane < RB * 4) {
-        const int row = lane >> 2, parity = (lane >> 1) & 1, half = lane & 1;
-        const float *pr = part + row * HBP + half;
-#pragma unroll 8
-        for (int b = parity; b < NB; b += 2) acc = acc + pr[2 * b];
-    }
-    return quad_sum(acc);  // (lo + hi) per parity, then the two parities
 }
 
 // ---------------------------------------------------------------- prologues
@@ -482,6 +356,7 @@ struct Prologue {
     static constexpr bool BF = C != kFp32;
     static_assert(!BF || PRO == PRO_PLAIN || PER == 8, "normalised inputs: 8 per thread");
     f32x4 a4[2], b4[2], c4[2], w4[2];
+    f32x4 os4[4];  // PRO_ONORM (BF16): the thread's head's 16 output-norm chunk sums
     f32x2 p2[PER / 2];
     u32x4 e4;
     float va[PER], vb[PER], vc[PER], vw[PER];
@@ -521,6 +396,9 @@ struct Prologue {
                 const f32x4 *g = reinterpret_cast<const f32x4 *>(src.b) + 2 * t;
                 const f32x4 *s = reinterpret_cast<const f32x4 *>(src.c) + 2 * t;
                 const f32x4 *w = reinterpret_cast<const f32x4 *>(src.w) + 2 * (t & 31);
+                // elements 8t.. belong to head t / 32; its 16 chunk sums are
+                // read here, ahead of the weight stream
+                const f32x4 *cs4 = reinterpret_cast<const f32x4 *>(src.osum + (t >> 5) * (kHD / 16));
                 a4[0] = a[0];
                 a4[1] = a[1];
                 b4[0] = g[0];
@@ -529,6 +407,8 @@ struct Prologue {
                 c4[1] = s[1];
                 w4[0] = w[0];
                 w4[1] = w[1];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) os4[i] = cs4[i];
             }
         } else {
             if constexpr (PRO == PRO_PLAIN) {
@@ -676,12 +556,10 @@ struct Prologue {
                 unpack8(b4, g);
                 unpack8(c4, sg);
                 unpack8(w4, w);
-                const int h = t >> 5;  // elements 8t.. belong to head t / 32
-                const f32x4 *cs4 = reinterpret_cast<const f32x4 *>(src.osum + h * (kHD / 16));
                 float sum = 0.0f;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const f32x4 c = cs4[i];
+                    const f32x4 c = os4[i];
                     sum += c.x;
                     sum += c.y;
                     sum += c.z;
@@ -704,11 +582,14 @@ struct Prologue {
     }
 
     // FP32 contract: the same operators with every rounding point the
-    // identity; products are plain FP32 (no fast path needed).
+    // identity; products are plain FP32 (no fast path needed).  Called by
+    // threads 0..255; every barrier is sync(), kSyncsFp32 of them.
+    static constexpr int kSyncsFp32 = (PRO == PRO_PLAIN) ? 1 : 4;
+
+    template <class Sync>
     __device__ __forceinline__ bool finish_fp32(const XSrc &src, float *xs, float *scratch,
-                                                float *bcast) {
+                                                float *bcast, Sync &sync) {
         const int t = threadIdx.x;
-        BlockSync sync;
         if constexpr (PRO == PRO_PLAIN) {
 #pragma unroll
             for (int m = 0; m < PER; ++m) xs[t + kT * m] = va[m];
@@ -727,7 +608,7 @@ struct Prologue {
                 xs[t + kT * m] = r;
                 if (blk0 && src.res_out) src.res_out[t + kT * m] = r;
             }
-            __syncthreads();
+            sync();
             if (t < kH / 16) {
                 float s = 0.0f;
 #pragma unroll
@@ -750,7 +631,7 @@ struct Prologue {
         } else {
 #pragma unroll
             for (int m = 0; m < PER; ++m) xs[t + kT * m] = va[m];
-            __syncthreads();
+            sync();
             if (t < kNH * (kHD / 16)) {
                 float s = 0.0f;
 #pragma unroll
@@ -760,21 +641,21 @@ struct Prologue {
                 }
                 scratch[t] = s;
             }
-            __syncthreads();
+            sync();
             if (t < kNH) {
                 float sum = 0.0f;
 #pragma unroll
                 for (int ch = 0; ch < kHD / 16; ++ch) sum += scratch[t * (kHD / 16) + ch];
                 bcast[t] = 1.0f / __builtin_sqrtf(sum / (float)kHD + src.eps);
             }
-            __syncthreads();
+            sync();
 #pragma unroll
             for (int m = 0; m < PER; ++m) {  // element t + 256 m belongs to head m
                 const float normalized = va[m] * bcast[m] * vw[0];
                 xs[t + kT * m] = normalized * vb[m] * vc[m];
             }
         }
-        __syncthreads();
+        sync();
         return false;
     }
 };
@@ -797,145 +678,7 @@ struct Epi {
     int *part_idx;
 };
 
-// ------------------------------------------------------------ the GEMV kernel
-
-// Waves per SIMD each GEMV instantiation must fit (caps its VGPRs): the
-// whole grid is then resident at once (QKVG 1028 blocks <= 5 x 256 CUs,
-// gate/up 1408 <= 6 x 256) and no straggler block runs in a second round.
-constexpr int gemv_min_waves(int C, int EPI) {
-    return C == kFp32 ? 4 : (EPI == EPI_SWIGLU || EPI == EPI_LM) ? 6 : 5;
-}
-
-template <int C, int K, int RB, int PRO, int EPI>
-__global__ __launch_bounds__(kT, gemv_min_waves(C, EPI)) void k_gemv(const void *__restrict__ W, WInfo wi, XSrc src,
-                                             Epi ep) {
-    constexpr int HBP = Hb<K>::HBP;
-    static_assert(K % kT == 0, "K splits evenly over the workgroup");
-    static_assert(PRO == PRO_PLAIN || K == kH, "normalised inputs are hidden-sized");
-    static_assert(EPI != EPI_QKVG || RB >= kAbRows, "a/b rows fit the partial-sum buffer");
-    __shared__ __attribute__((aligned(16))) uint32_t xs[K];
-    __shared__ __attribute__((aligned(16))) float part[RB * HBP];
-    __shared__ __attribute__((aligned(16))) float scratch[kH / 16];
-    __shared__ float bcast[kNH];
-    const int t = threadIdx.x;
-    // QKVG: blocks 0..kAbBlocks-1 are the a/b blocks, the rest own the
-    // projection rows.
-    const bool ab_blk = (EPI == EPI_QKVG) && blockIdx.x < kAbBlocks;
-    const int rb = (EPI == EPI_QKVG) ? (int)blockIdx.x - kAbBlocks : (int)blockIdx.x;
-
-    // 1. activation loads, 2. the weight stream, 3. the prologue proper
-    Prologue<C, K, PRO> pro;
-    pro.load(src);
-    WRegs<K, RB, C> w;
-    if constexpr (EPI == EPI_QKVG) {
-        if (ab_blk) w.load_ab(ep.aux + kAuxAB, blockIdx.x);
-        else w.load(W, rb);
-    } else {
-        w.load(W, rb);
-    }
-    static_assert(C == kFp32, "BF16 contracts use k_gemv_cu");
-    const bool fast = pro.finish_fp32(src, reinterpret_cast<float *>(xs), scratch, bcast);
-
-    // 4. products and reduction
-    if constexpr (EPI == EPI_QKVG) {
-        if (ab_blk) {
-            // acc = (acc + tree16(lo)) + tree16(hi) per beat, rounded; then
-            // beta_h and decay_h
-            w.compute_ab(xs, part);
-            __syncthreads();
-            if (t >= 64) return;
-            float acc = 0.0f;
-            if (t < kAbRows) {
-                const float *pr = part + t * HBP;
-                for (int j = 0; j < Hb<kH>::NB; ++j) acc = (acc + pr[2 * j]) + pr[2 * j + 1];
-            }
-            const float a = R<C>(acc);
-            const float b = R<C>(__shfl(acc, 1));
-            if (t == 0) {
-                float beta, decay;
-                head_scalars(a, b, ep.aux[kAuxALog + blockIdx.x], ep.aux[kAuxDtBias + blockIdx.x], beta, decay);
-                ep.ab[blockIdx.x] = a;
-                ep.ab[kNH + blockIdx.x] = b;
-                ep.bd[2 * blockIdx.x] = beta;
-                ep.bd[2 * blockIdx.x + 1] = decay;
-            }
-            return;
-        }
-    }
-    if (fast) w.template compute<true>(xs, part);
-    else w.template compute<false>(xs, part);
-    __syncthreads();
-    if (t >= 64) return;
-    const float y = gemv_chain<K, RB>(part);
-
-    // 5. epilogue (wave 0; lane 4r holds row r)
-    const int lane = t;
-    const bool owner = (lane & 3) == 0 && (lane >> 2) < RB;
-    const int r = rb * RB + (lane >> 2);
-    if constexpr (EPI == EPI_RAW) {
-        if (owner) ep.y[r] = y;
-    } else if constexpr (EPI == EPI_STORE) {
-        if (owner) ep.y[r] = R<C>(y);
-    } else if constexpr (EPI == EPI_QKVG) {
-        if (!owner) return;
-        const float yv = R<C>(y);
-        if (r < 3 * kH) {
-            // causal conv over [t0, t1, t2, x] + SiLU; tails shift to [t1, t2, x]
-            const int kind = r / kH, c = r - kind * kH;
-            const float *cw = ep.aux + kAuxConv + ((size_t)kind * kH + c) * 4;
-            float t0, t1, t2;
-            if constexpr (C == kFp32) {
-                float *tl = ep.tails + (size_t)kind * kTailStripe;
-                t0 = tl[c];
-                t1 = tl[kH + c];
-                t2 = tl[2 * kH + c];
-                tl[c] = t1;
-                tl[kH + c] = t2;
-                tl[2 * kH + c] = yv;
-            } else {
-                uint16_t *tl = reinterpret_cast<uint16_t *>(ep.tails + (size_t)kind * kTailStripe);
-                const uint16_t b0 = tl[c], b1 = tl[kH + c], b2 = tl[2 * kH + c];
-                t0 = bf16_bits_to_f32(b0);
-                t1 = bf16_bits_to_f32(b1);
-                t2 = bf16_bits_to_f32(b2);
-                tl[c] = b1;
-                tl[kH + c] = b2;
-                tl[2 * kH + c] = (uint16_t)(f2u(yv) >> 16);
-            }
-            const float s = t0 * cw[0] + t1 * cw[1] + t2 * cw[2] + yv * cw[3];
-            ep.y[r] = R<C>(silu_ref(s));
-        } else {
-            ep.y2[r - 3 * kH] = yv;
-            ep.y3[r - 3 * kH] = sigmoid_ref(yv);
-        }
-    } else if constexpr (EPI == EPI_SWIGLU) {
-        // rows 0..RB/2-1 are gate rows, RB/2..RB-1 the matching up rows
-        const float yu = __shfl_down(y, 4 * (RB / 2));
-        if ((lane & 3) == 0 && (lane >> 2) < RB / 2) {
-            const float g = R<C>(y), u = R<C>(yu);
-            ep.y[rb * (RB / 2) + (lane >> 2)] = R<C>(silu_ref(g) * u);
-        }
-    } else {
-        // LM head: FP32 logits (no rounding point) and the block's argmax
-        if (owner) ep.y[r] = y;
-        float best = -3.402823466e38f;
-        int idx = 0;
-#pragma unroll
-        for (int rr = 0; rr < RB; ++rr) {
-            const float v = __shfl(y, 4 * rr);
-            if (v > best) {
-                best = v;
-                idx = rb * RB + rr;
-            }
-        }
-        if (lane == 0) {
-            ep.part_val[blockIdx.x] = best;
-            ep.part_idx[blockIdx.x] = idx;
-        }
-    }
-}
-
-// ------------------------------------------------ CU-resident GEMV (BF16)
+// ------------------------------------------------ CU-resident GEMV
 //
 // One 1024-thread workgroup per CU (it claims all 512 VGPRs of every SIMD,
 // so no two share one) owns ROWS consecutive rows of the matrix, a
@@ -964,6 +707,18 @@ constexpr int kDepthQkvg = 4;
 constexpr int kDepthGu = 3;
 constexpr int kDepthDown = 2;
 constexpr int kDepthLm = 2;  // of 21 items per stream thread (3: 0.7 us per token slower)
+// Per contract: an FP32 item is 64 bytes (16 VGPRs), so the FP32 control
+// arm keeps fewer in flight within the same 128-VGPR budget.
+template <int C>
+struct Depth {
+    static constexpr bool F = C == kFp32;
+    static constexpr int qkvg = F ? 3 : kDepthQkvg;
+    static constexpr int o = F ? 2 : kDepthAll;
+    static constexpr int gu = F ? 3 : kDepthGu;
+    static constexpr int down = F ? 2 : kDepthDown;
+    static constexpr int lm = F ? 2 : kDepthLm;
+    static constexpr int lm_small = F ? 2 : kDepthAll;
+};
 
 // Partial sums of the CU-resident GEMV, bank-contiguous: row r, bank
 // (beat parity, half) = 2 * (beat & 1) + half, position beat / 2.  A bank
@@ -997,16 +752,16 @@ struct WStream {
     static constexpr int DEPTH = D < NIT ? D : NIT;
     static constexpr bool kFull = (ITEMS % NT) == 0;
     static constexpr bool kSameHb = (NT % HB) == 0;
-    static_assert(C != kFp32, "BF16 weights");
+    static constexpr int WPI = (C == kFp32) ? 4 : 2;  // 16-byte loads per item
     const u32x4 *wb;
-    u32x4 v[NIT][2];
+    u32x4 v[NIT][WPI];
 
     template <int I>
     __device__ __forceinline__ void load() {
         const int f = (int)threadIdx.x - T0 + NT * I;
         if (kFull || f < ITEMS) {
-            v[I][0] = __builtin_nontemporal_load(wb + 2 * f);
-            v[I][1] = __builtin_nontemporal_load(wb + 2 * f + 1);
+#pragma unroll
+            for (int q = 0; q < WPI; ++q) v[I][q] = __builtin_nontemporal_load(wb + WPI * f + q);
         }
     }
 
@@ -1018,7 +773,7 @@ struct WStream {
         }
     }
 
-    __device__ __forceinline__ void prime(const uint16_t *__restrict__ slice) {
+    __device__ __forceinline__ void prime(const void *__restrict__ slice) {
         wb = reinterpret_cast<const u32x4 *>(slice);
         prime_from<0>();
     }
@@ -1033,10 +788,18 @@ struct WStream {
             if (kFull || f < ITEMS) {
                 const int row = f / HB, hb = f - row * HB;
                 if constexpr (!kSameHb) lds_load16u(xs + hb * 16, xv);
-                const uint32_t w8[8] = {v[I][0].x, v[I][0].y, v[I][0].z, v[I][0].w,
-                                        v[I][1].x, v[I][1].y, v[I][1].z, v[I][1].w};
                 float p[16];
-                if constexpr (FAST) {
+                if constexpr (C == kFp32) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        p[4 * q + 0] = u2f(v[I][q].x) * u2f(xv[4 * q + 0]);
+                        p[4 * q + 1] = u2f(v[I][q].y) * u2f(xv[4 * q + 1]);
+                        p[4 * q + 2] = u2f(v[I][q].z) * u2f(xv[4 * q + 2]);
+                        p[4 * q + 3] = u2f(v[I][q].w) * u2f(xv[4 * q + 3]);
+                    }
+                } else if constexpr (FAST) {
+                    const uint32_t w8[8] = {v[I][0].x, v[I][0].y, v[I][0].z, v[I][0].w,
+                                            v[I][1].x, v[I][1].y, v[I][1].z, v[I][1].w};
                     uint32_t rbits[8];
                     dot8_bf16(w8, xv, rbits);
                     dot8_bf16(w8 + 4, xv + 8, rbits + 4);
@@ -1046,6 +809,8 @@ struct WStream {
                         p[2 * e + 1] = u2f(rbits[e] & 0xffff0000u);
                     }
                 } else {
+                    const uint32_t w8[8] = {v[I][0].x, v[I][0].y, v[I][0].z, v[I][0].w,
+                                            v[I][1].x, v[I][1].y, v[I][1].z, v[I][1].w};
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         p[2 * e] = native_exact(w8[e] & 0xffffu, u2f(xv[2 * e] << 16));
@@ -1121,8 +886,9 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     // claim the whole register file (128 VGPRs x 16 waves): one workgroup per CU
     asm volatile("" ::: "v127");
     const int t = threadIdx.x, wave = t >> 6;
+    constexpr bool BF = C != kFp32;
     const int row0 = blockIdx.x * ROWS;
-    const uint16_t *wblk = static_cast<const uint16_t *>(W) + (size_t)row0 * K;
+    const char *wblk = static_cast<const char *>(W) + (size_t)row0 * K * (BF ? 2 : 4);
     __shared__ int arrive;  // Wave4Sync arrivals of the prologue waves
     if (t == 0) arrive = 0;
     __syncthreads();  // before any load: the waves are just starting
@@ -1143,15 +909,17 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     // QKVG workgroup h < 8: head h's FP32 a and b rows (half-beat t & 127 of
     // row t >> 7), needed right after the input is built
     const bool ab_blk = (EPI == EPI_QKVG) && blockIdx.x < kNH;
-    // (the BF16 copy: the BF16 contracts require BF16-exact weights, so its
-    // values are the FP32 rows' and the 8 workgroups stream 8 KB, not 16 KB,
-    // beyond their weight rows)
-    u32x4 abw[2];
+    // (BF16 contracts read the BF16 copy: they require BF16-exact weights,
+    // so its values are the FP32 rows' and the 8 workgroups stream 8 KB, not
+    // 16 KB, beyond their weight rows)
+    constexpr int ABW = BF ? 2 : 4;
+    u32x4 abw[ABW];
     if (ab_blk && t < kT) {
         const int abrow = (t >> 7) * kNH + blockIdx.x, hb = t & 127;
-        const u32x4 *src4 = reinterpret_cast<const u32x4 *>(ep.ab16 + (size_t)abrow * kH + hb * 16);
-        abw[0] = src4[0];
-        abw[1] = src4[1];
+        const u32x4 *src4 = BF ? reinterpret_cast<const u32x4 *>(ep.ab16 + (size_t)abrow * kH + hb * 16)
+                               : reinterpret_cast<const u32x4 *>(ep.aux + kAuxAB + (size_t)abrow * kH + hb * 16);
+#pragma unroll
+        for (int q = 0; q < ABW; ++q) abw[q] = src4[q];
     }
     if constexpr (kActFirst) __builtin_amdgcn_s_barrier();
 
@@ -1163,16 +931,24 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     // slot ahead of the stream: the conv tails and taps of each q/k/v row
     // (its owner lane)
     const bool owner = wave < CHW && (t & 3) == 0 && (t >> 2) < CR;
-    uint16_t tail_b[3] = {0, 0, 0};
+    uint16_t tail_b[3] = {0, 0, 0};        // BF16 contracts: the tails' BF16 bits
+    float tail_f[3] = {0.0f, 0.0f, 0.0f};  // FP32 contract: FP32 tails
     f32x4 taps = {0.0f, 0.0f, 0.0f, 0.0f};
     if constexpr (EPI == EPI_QKVG) {
         const int r = row0 + (t >> 2);
         if (owner && r < 3 * kH) {
             const int kind = r / kH, ch = r - kind * kH;
-            const uint16_t *tl = reinterpret_cast<const uint16_t *>(ep.tails + (size_t)kind * kTailStripe);
-            tail_b[0] = tl[ch];
-            tail_b[1] = tl[kH + ch];
-            tail_b[2] = tl[2 * kH + ch];
+            if constexpr (BF) {
+                const uint16_t *tl = reinterpret_cast<const uint16_t *>(ep.tails + (size_t)kind * kTailStripe);
+                tail_b[0] = tl[ch];
+                tail_b[1] = tl[kH + ch];
+                tail_b[2] = tl[2 * kH + ch];
+            } else {
+                const float *tl = ep.tails + (size_t)kind * kTailStripe;
+                tail_f[0] = tl[ch];
+                tail_f[1] = tl[kH + ch];
+                tail_f[2] = tl[2 * kH + ch];
+            }
             taps = *reinterpret_cast<const f32x4 *>(ep.aux + kAuxConv + ((size_t)kind * kH + ch) * 4);
         }
     }
@@ -1183,7 +959,8 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     bool fast;
     if (t < kT) {
         Wave4Sync sync{&arrive, src.err};
-        fast = pro.finish_bf16(src, wi, xs, scratch, bcast, red, sync);
+        if constexpr (BF) fast = pro.finish_bf16(src, wi, xs, scratch, bcast, red, sync);
+        else fast = pro.finish_fp32(src, reinterpret_cast<float *>(xs), scratch, bcast, sync);
         if constexpr (EPI == EPI_QKVG) {
             if (ab_blk) {
                 // a_h and b_h while the weights stream (gdn_gemv_tiny_ab):
@@ -1195,12 +972,22 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
                 uint32_t xv[16];
                 lds_load16u(xs + hb * 16, xv);
                 float p[16];
-                const uint32_t wv[8] = {abw[0].x, abw[0].y, abw[0].z, abw[0].w,
-                                        abw[1].x, abw[1].y, abw[1].z, abw[1].w};
+                if constexpr (BF) {
+                    const uint32_t wv[8] = {abw[0].x, abw[0].y, abw[0].z, abw[0].w,
+                                            abw[1].x, abw[1].y, abw[1].z, abw[1].w};
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    p[2 * i] = lane_word_value(xv[2 * i], 0) * u2f(wv[i] << 16);
-                    p[2 * i + 1] = lane_word_value(xv[2 * i + 1], 1) * u2f(wv[i] & 0xffff0000u);
+                    for (int i = 0; i < 8; ++i) {
+                        p[2 * i] = lane_word_value(xv[2 * i], 0) * u2f(wv[i] << 16);
+                        p[2 * i + 1] = lane_word_value(xv[2 * i + 1], 1) * u2f(wv[i] & 0xffff0000u);
+                    }
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        p[4 * q + 0] = u2f(xv[4 * q + 0]) * u2f(abw[q].x);
+                        p[4 * q + 1] = u2f(xv[4 * q + 1]) * u2f(abw[q].y);
+                        p[4 * q + 2] = u2f(xv[4 * q + 2]) * u2f(abw[q].z);
+                        p[4 * q + 3] = u2f(xv[4 * q + 3]) * u2f(abw[q].w);
+                    }
                 }
                 abpart[t] = tree16(p);
                 sync();
@@ -1226,8 +1013,13 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
             }
         }
     } else {
-        wait_count(&arrive, 4 * Prologue<C, K, PRO>::kSyncs, src.err);
-        fast = decide_fast(red, wi);
+        if constexpr (BF) {
+            wait_count(&arrive, 4 * Prologue<C, K, PRO>::kSyncs, src.err);
+            fast = decide_fast(red, wi);
+        } else {
+            wait_count(&arrive, 4 * Prologue<C, K, PRO>::kSyncsFp32, src.err);
+            fast = false;
+        }
     }
     // the product-counter copy of the GEMV input (debug: off in the timed
     // path, where xdump is null); xs is complete for every wave here
@@ -1257,12 +1049,24 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
                 if (r < 3 * kH) {
                     // causal conv over [t0, t1, t2, x] + SiLU; tails shift to [t1, t2, x]
                     const int kind = r / kH, ch = r - kind * kH;
-                    uint16_t *tl = reinterpret_cast<uint16_t *>(ep.tails + (size_t)kind * kTailStripe);
-                    const float t0 = bf16_bits_to_f32(tail_b[0]), t1 = bf16_bits_to_f32(tail_b[1]),
-                                t2 = bf16_bits_to_f32(tail_b[2]);
-                    tl[ch] = tail_b[1];
-                    tl[kH + ch] = tail_b[2];
-                    tl[2 * kH + ch] = (uint16_t)(f2u(yv) >> 16);
+                    float t0, t1, t2;
+                    if constexpr (BF) {
+                        uint16_t *tl = reinterpret_cast<uint16_t *>(ep.tails + (size_t)kind * kTailStripe);
+                        t0 = bf16_bits_to_f32(tail_b[0]);
+                        t1 = bf16_bits_to_f32(tail_b[1]);
+                        t2 = bf16_bits_to_f32(tail_b[2]);
+                        tl[ch] = tail_b[1];
+                        tl[kH + ch] = tail_b[2];
+                        tl[2 * kH + ch] = (uint16_t)(f2u(yv) >> 16);
+                    } else {
+                        float *tl = ep.tails + (size_t)kind * kTailStripe;
+                        t0 = tail_f[0];
+                        t1 = tail_f[1];
+                        t2 = tail_f[2];
+                        tl[ch] = t1;
+                        tl[kH + ch] = t2;
+                        tl[2 * kH + ch] = yv;
+                    }
                     const float s = t0 * taps.x + t1 * taps.y + t2 * taps.z + yv * taps.w;
                     conv_out = R<C>(silu_ref(s));
                     ep.y[r] = conv_out;
@@ -1277,7 +1081,7 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
                 ybuf[rr] = y;
             }
         }
-        if constexpr (EPI == EPI_QKVG) {
+        if constexpr (EPI == EPI_QKVG && BF) {
             // q and k rows: each wave's 16 rows reduced in the tree order of
             // gdn_tree_reduce_256 (its lower four levels) for the recurrence's
             // L2 norms.  Row r sits in the lanes of quad r % 16; the owner's
@@ -1592,9 +1396,9 @@ int check_shape(const GDNWeightHeader *c) {
         std::fprintf(stderr, "gdn: %u layers; the engine takes 1..%d\n", c->num_layers, kMaxLayers);
         return -1;
     }
-    if (c->vocab_size == 0 || (c->vocab_size % kRbLm) != 0) {
-        std::fprintf(stderr, "gdn: vocabulary %u is not a positive multiple of %d (the LM head's row block)\n",
-                     c->vocab_size, kRbLm);
+    if (c->vocab_size == 0 || (c->vocab_size % kCuLmSmall) != 0) {
+        std::fprintf(stderr, "gdn: vocabulary %u is not a positive multiple of %d (the LM head's rows per workgroup)\n",
+                     c->vocab_size, kCuLmSmall);
         return -1;
     }
     return 0;
@@ -1634,7 +1438,7 @@ int upload_weights(GDNEngine *e, const GDNModel *m, bool verify = false, size_t 
         // gate/up rows interleaved per workgroup: G gate rows, then the
         // matching G up rows
         pk.begin(2 * I * H);
-        const size_t G = (e->contract == kFp32) ? kRbGu / 2 : kCuGu / 2;
+        const size_t G = kCuGu / 2;
         for (size_t blk = 0; blk < I / G; ++blk) {
             pk.rows(w.mlp_gate_proj + blk * G * H, G * H);
             pk.rows(w.mlp_up_proj + blk * G * H, G * H);
@@ -1705,7 +1509,7 @@ int alloc_buffers(GDNEngine *e) {
     GDN_HIP(hipMemset(e->state, 0, state_bytes(e)));
     GDN_HIP(hipMalloc(&e->tails, tail_floats(e) * 4));
     GDN_HIP(hipMemset(e->tails, 0, tail_floats(e) * 4));
-    const size_t nblk_lm = (size_t)e->vocab / kRbLm;
+    const size_t nblk_lm = (size_t)e->vocab / kCuLmSmall;  // the most LM-head workgroups
     auto up64 = [](size_t n) { return (n + 63) & ~(size_t)63; };  // 256-byte aligned pieces
     const size_t act_floats = 3 * kH + 3 * kH + 2 * kH + 64 + 64 + 3 * kH + kI + up64(nblk_lm) + kH +
                               up64((size_t)e->vocab) + 2 * kNH * 16 + kNH * (kHD / 16);
@@ -1763,9 +1567,8 @@ XSrc xsrc(GDNEngine *e, const float *a, const float *b, const float *c, const fl
 
 // Per-kernel launches.  The QKVG prologue (PRO0) takes the embedding row
 // (first layer of a step), the previous layer's residual (res_b = its down
-// output), or a caller-given residual (res_b = nullptr).  BF16 contracts use
-// the CU-resident kernels (grids of 256), the FP32 control arm the
-// row-block kernels.
+// output), or a caller-given residual (res_b = nullptr).  Every contract uses
+// the CU-resident kernels (grids of 256 one-per-CU workgroups).
 template <int C, int PRO0>
 void launch_qkvg(GDNEngine *e, int l, const float *res_a, const float *res_b, hipStream_t s) {
     float *aux = layer_aux(e, l);
@@ -1786,13 +1589,8 @@ void launch_qkvg(GDNEngine *e, int l, const float *res_a, const float *res_b, hi
         xq.vocab = e->vocab;
         xq.aux_out = e->xrow;
     }
-    if constexpr (C == kFp32) {
-        hipLaunchKernelGGL((k_gemv<C, kH, kRbQkvg, PRO0, EPI_QKVG>), dim3(4 * kH / kRbQkvg + kAbBlocks),
-                           dim3(kT), 0, s, e->w_qkvg[l], e->i_qkvg[l], xq, q);
-    } else {
-        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuQkvg, kDepthQkvg, PRO0, EPI_QKVG>), dim3(4 * kH / kCuQkvg),
-                           dim3(kTB), 0, s, e->w_qkvg[l], e->i_qkvg[l], xq, q);
-    }
+    hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuQkvg, Depth<C>::qkvg, PRO0, EPI_QKVG>), dim3(4 * kH / kCuQkvg),
+                       dim3(kTB), 0, s, e->w_qkvg[l], e->i_qkvg[l], xq, q);
 }
 
 template <int C>
@@ -1808,13 +1606,8 @@ void launch_o(GDNEngine *e, int l, hipStream_t s) {
     XSrc xo = xsrc(e, e->attn, e->gate, e->sgate, layer_aux(e, l) + kAuxONorm, nullptr, nullptr,
                    dump_slot(e, 4 * l + 1));
     xo.osum = e->osum;
-    if constexpr (C == kFp32) {
-        hipLaunchKernelGGL((k_gemv<C, kH, kRbO, PRO_ONORM, EPI_STORE>), dim3(kH / kRbO), dim3(kT), 0, s,
-                           e->w_o[l], e->i_o[l], xo, st);
-    } else {
-        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuO, kDepthAll, PRO_ONORM, EPI_STORE>), dim3(kH / kCuO), dim3(kTB),
-                           0, s, e->w_o[l], e->i_o[l], xo, st);
-    }
+    hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuO, Depth<C>::o, PRO_ONORM, EPI_STORE>), dim3(kH / kCuO), dim3(kTB), 0,
+                       s, e->w_o[l], e->i_o[l], xo, st);
 }
 
 template <int C>
@@ -1823,13 +1616,8 @@ void launch_gu(GDNEngine *e, int l, hipStream_t s) {
     sw.y = e->hbuf;
     const XSrc xg = xsrc(e, e->resid, e->ybuf_o, nullptr, layer_aux(e, l) + kAuxMlpNorm, e->resid_alt,
                          nullptr, dump_slot(e, 4 * l + 2));
-    if constexpr (C == kFp32) {
-        hipLaunchKernelGGL((k_gemv<C, kH, kRbGu, PRO_RESNORM, EPI_SWIGLU>), dim3(2 * kI / kRbGu), dim3(kT),
-                           0, s, e->w_gu[l], e->i_gu[l], xg, sw);
-    } else {
-        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuGu, kDepthGu, PRO_RESNORM, EPI_SWIGLU>), dim3(2 * kI / kCuGu),
-                           dim3(kTB), 0, s, e->w_gu[l], e->i_gu[l], xg, sw);
-    }
+    hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuGu, Depth<C>::gu, PRO_RESNORM, EPI_SWIGLU>), dim3(2 * kI / kCuGu),
+                       dim3(kTB), 0, s, e->w_gu[l], e->i_gu[l], xg, sw);
 }
 
 template <int C>
@@ -1837,18 +1625,12 @@ void launch_down(GDNEngine *e, int l, hipStream_t s) {
     Epi dn{};
     dn.y = e->dbuf;
     const XSrc xd = xsrc(e, e->hbuf, nullptr, nullptr, nullptr, nullptr, nullptr, dump_slot(e, 4 * l + 3));
-    if constexpr (C == kFp32) {
-        hipLaunchKernelGGL((k_gemv<C, kI, kRbDown, PRO_PLAIN, EPI_STORE>), dim3(kH / kRbDown), dim3(kT), 0,
-                           s, e->w_down[l], e->i_down[l], xd, dn);
-    } else {
-        hipLaunchKernelGGL((k_gemv_cu<C, kI, kCuDown, kDepthDown, PRO_PLAIN, EPI_STORE>), dim3(kH / kCuDown),
-                           dim3(kTB), 0, s, e->w_down[l], e->i_down[l], xd, dn);
-    }
+    hipLaunchKernelGGL((k_gemv_cu<C, kI, kCuDown, Depth<C>::down, PRO_PLAIN, EPI_STORE>), dim3(kH / kCuDown),
+                       dim3(kTB), 0, s, e->w_down[l], e->i_down[l], xd, dn);
 }
 
 // LM-head workgroups (= first-stage argmax results) of a contract/vocabulary.
 int lm_blocks(const GDNEngine *e) {
-    if (e->contract == kFp32) return e->vocab / kRbLm;
     return (e->vocab % kCuLm) == 0 ? e->vocab / kCuLm : e->vocab / kCuLmSmall;
 }
 
@@ -1861,15 +1643,12 @@ void launch_lm(GDNEngine *e, hipStream_t s) {
     const XSrc xl = xsrc(e, e->resid_alt, e->dbuf, nullptr, final_norm(e), e->resid, e->fhid,
                          dump_slot(e, 4 * e->layers));
     const dim3 grid(lm_blocks(e));
-    if constexpr (C == kFp32) {
-        hipLaunchKernelGGL((k_gemv<C, kH, kRbLm, PRO_RESNORM, EPI_LM>), grid, dim3(kT), 0, s, e->w_lm,
-                           e->i_lm, xl, lm);
-    } else if ((e->vocab % kCuLm) == 0) {
-        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuLm, kDepthLm, PRO_RESNORM, EPI_LM>), grid, dim3(kTB), 0, s,
+    if ((e->vocab % kCuLm) == 0) {
+        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuLm, Depth<C>::lm, PRO_RESNORM, EPI_LM>), grid, dim3(kTB), 0, s,
                            e->w_lm, e->i_lm, xl, lm);
     } else {
-        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuLmSmall, kDepthAll, PRO_RESNORM, EPI_LM>), grid, dim3(kTB),
-                           0, s, e->w_lm, e->i_lm, xl, lm);
+        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuLmSmall, Depth<C>::lm_small, PRO_RESNORM, EPI_LM>), grid,
+                           dim3(kTB), 0, s, e->w_lm, e->i_lm, xl, lm);
     }
 }
 
@@ -2590,7 +2369,8 @@ int gdn_profile_kernels(GDNRunState *state, uint32_t rounds, float *avg_us, uint
 // ---------------------------------------------------------------- test hooks
 
 int gdn_test_gemv(int contract, const float *W, const float *x, uint32_t M, uint32_t K, float *y) {
-    if ((K != (uint32_t)kH && K != (uint32_t)kI) || M == 0 || (M % kRbTest) != 0) {
+    constexpr int kRows = 8;  // rows per workgroup
+    if ((K != (uint32_t)kH && K != (uint32_t)kI) || M == 0 || (M % kRows) != 0) {
         gdn_error("gdn_test_gemv: K must be 2048 or 5632 and M a multiple of 8");
         return -1;
     }
@@ -2605,25 +2385,22 @@ int gdn_test_gemv(int contract, const float *W, const float *x, uint32_t M, uint
     if (pk.upload(dW)) return -1;
     GDN_HIP(hipMemcpy(dx, x, (size_t)K * 4, hipMemcpyHostToDevice));
     const WInfo wi = pk.info();
-    const dim3 grid(M / kRbTest), block(kT);
-#define GDN_PLAIN(CC, KK)                                                                     \
-    hipLaunchKernelGGL((k_gemv<CC, KK, kRbTest, PRO_PLAIN, EPI_RAW>), grid, block, 0, 0, dW, wi, xs, ep)
-#define GDN_PLAIN_CU(KK)                                                                      \
-    hipLaunchKernelGGL((k_gemv_cu<kRef, KK, kRbTest, kDepthAll, PRO_PLAIN, EPI_RAW>), grid, dim3(kTB), 0, 0, \
-                       dW, wi, xs, ep)
+    const dim3 grid(M / kRows);
+#define GDN_PLAIN(CC, KK)                                                                                  \
+    hipLaunchKernelGGL((k_gemv_cu<CC, KK, kRows, Depth<CC>::o, PRO_PLAIN, EPI_RAW>), grid, dim3(kTB), 0, 0, dW, wi, \
+                       xs, ep)
     XSrc xs{};
     xs.a = dx;
     Epi ep{};
     ep.y = dy;
     if (K == (uint32_t)kH) {
         if (contract == kFp32) GDN_PLAIN(kFp32, kH);
-        else GDN_PLAIN_CU(kH);
+        else GDN_PLAIN(kRef, kH);  // the two BF16 contracts share their products
     } else {
         if (contract == kFp32) GDN_PLAIN(kFp32, kI);
-        else GDN_PLAIN_CU(kI);
+        else GDN_PLAIN(kRef, kI);
     }
 #undef GDN_PLAIN
-#undef GDN_PLAIN_CU
     GDN_HIP(hipGetLastError());
     GDN_HIP(hipMemcpy(y, dy, (size_t)M * 4, hipMemcpyDeviceToHost));
     GDN_HIP(hipFree(dW));
