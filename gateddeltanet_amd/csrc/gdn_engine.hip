@@ -734,9 +734,28 @@ struct BankLayout {
     }
 };
 
-// A workgroup's weight rows as a stream of 16-element items: item f (row
-// f / (K/16), half-beat f % (K/16)) sits at element 16 f of the workgroup's
-// slice and stream thread u = threadIdx.x - T0 takes items u + (kTB - T0) i
+// Input-first GEMVs (QKVG, o_proj, LM head): waves 0..3 build the input and
+// own no weight items, so kTB - kT threads stream; the others stream on all
+// kTB threads.
+constexpr bool act_first(int pro, int epi) { return epi == EPI_QKVG || pro == PRO_ONORM || epi == EPI_LM; }
+constexpr int stream_threads(int pro, int epi) { return act_first(pro, epi) ? kTB - kT : kTB; }
+
+// Device order of a workgroup's weight slice.  Item f (16 elements: row
+// f / (K/16), half-beat f % (K/16)) is held by stream thread u = f % NT as its
+// item I = f / NT and arrives in WPI 16-byte pieces (2 for BF16, 4 for FP32).
+// Piece q of every item of group I of the NT threads is stored contiguously,
+// so each load instruction of a wave reads 1 KB of consecutive bytes: piece
+// (f, q) sits at 16-byte position NT WPI I + q span + u, span = NT (or the
+// item count of the last group when NT does not divide the items).
+__host__ __device__ constexpr size_t stream_piece(int f, int q, int items, int nt, int wpi) {
+    const int I = f / nt, u = f - I * nt;
+    const int full = items / nt;  // complete groups
+    const int span = I < full ? nt : items - full * nt;
+    return (size_t)nt * wpi * I + (size_t)q * span + u;
+}
+
+// A workgroup's weight rows as a stream of 16-element items (stream_piece
+// order); stream thread u = threadIdx.x - T0 takes items u + (kTB - T0) i
 // (T0 = 256 when waves 0..3 build the input and own no items).  prime()
 // issues the loads of the first DEPTH items; run() walks the items in order,
 // issuing item i + DEPTH before multiplying item i, so a wave never has more
@@ -758,10 +777,12 @@ struct WStream {
 
     template <int I>
     __device__ __forceinline__ void load() {
-        const int f = (int)threadIdx.x - T0 + NT * I;
-        if (kFull || f < ITEMS) {
+        const int u = (int)threadIdx.x - T0;
+        if (kFull || u + NT * I < ITEMS) {
+            constexpr int span = (kFull || I < NIT - 1) ? NT : ITEMS - NT * (NIT - 1);
 #pragma unroll
-            for (int q = 0; q < WPI; ++q) v[I][q] = __builtin_nontemporal_load(wb + WPI * f + q);
+            for (int q = 0; q < WPI; ++q)
+                v[I][q] = __builtin_nontemporal_load(wb + (size_t)NT * WPI * I + q * span + u);
         }
     }
 
@@ -902,8 +923,8 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     // queue is full, which would hold the prologue back).  gate/up and down
     // (measured faster so) let all 16 waves issue weights at once, the input
     // waves after their activation reads.
-    constexpr bool kActFirst = EPI == EPI_QKVG || PRO == PRO_ONORM || EPI == EPI_LM;
-    constexpr int T0 = kActFirst ? kT : 0;
+    constexpr bool kActFirst = act_first(PRO, EPI);
+    constexpr int T0 = kTB - stream_threads(PRO, EPI);
     Prologue<C, K, PRO> pro;
     if (t < kT) pro.load(src);
     // QKVG workgroup h < 8: head h's FP32 a and b rows (half-beat t & 127 of
@@ -1366,6 +1387,21 @@ struct Packer {
         nonfinite |= bad;
         filled += n;
     }
+    // Reorders the staged matrix into the CU-resident GEMV's stream order
+    // (stream_piece), one workgroup slice of `rows` rows at a time.
+    void stream_order(size_t rows, size_t K, int pro, int epi) {
+        const size_t es = welem(contract), wpi = es;  // 16-byte pieces per 16-element item
+        const size_t slice = rows * K * es, nslices = filled * es / slice;
+        const int items = (int)(rows * K / 16), nt = stream_threads(pro, epi);
+        std::vector<unsigned char> tmp(slice);
+        for (size_t b = 0; b < nslices; ++b) {
+            unsigned char *sl = staging.data() + b * slice;
+            std::memcpy(tmp.data(), sl, slice);
+            for (int f = 0; f < items; ++f)
+                for (int q = 0; q < (int)wpi; ++q)
+                    std::memcpy(sl + 16 * stream_piece(f, q, items, nt, (int)wpi), tmp.data() + 16 * (f * wpi + q), 16);
+        }
+    }
     int upload(void *dst) {
         return transfer(dst, staging.data(), filled * welem(contract));
     }
@@ -1423,6 +1459,7 @@ int upload_weights(GDNEngine *e, const GDNModel *m, bool verify = false, size_t 
         pk.rows(w.k_proj, H * H);
         pk.rows(w.v_proj, H * H);
         pk.rows(w.g_proj, H * H);
+        pk.stream_order(kCuQkvg, H, PRO_RESNORM, EPI_QKVG);
         e->w_qkvg[l] = p;
         e->i_qkvg[l] = pk.info();
         if (pk.upload(p)) return -1;
@@ -1430,6 +1467,7 @@ int upload_weights(GDNEngine *e, const GDNModel *m, bool verify = false, size_t 
 
         pk.begin(H * H);
         pk.rows(w.o_proj, H * H);
+        pk.stream_order(kCuO, H, PRO_ONORM, EPI_STORE);
         e->w_o[l] = p;
         e->i_o[l] = pk.info();
         if (pk.upload(p)) return -1;
@@ -1443,6 +1481,7 @@ int upload_weights(GDNEngine *e, const GDNModel *m, bool verify = false, size_t 
             pk.rows(w.mlp_gate_proj + blk * G * H, G * H);
             pk.rows(w.mlp_up_proj + blk * G * H, G * H);
         }
+        pk.stream_order(kCuGu, H, PRO_RESNORM, EPI_SWIGLU);
         e->w_gu[l] = p;
         e->i_gu[l] = pk.info();
         if (pk.upload(p)) return -1;
@@ -1450,6 +1489,7 @@ int upload_weights(GDNEngine *e, const GDNModel *m, bool verify = false, size_t 
 
         pk.begin(H * I);
         pk.rows(w.mlp_down_proj, H * I);
+        pk.stream_order(kCuDown, I, PRO_PLAIN, EPI_STORE);
         e->w_down[l] = p;
         e->i_down[l] = pk.info();
         if (pk.upload(p)) return -1;
@@ -1457,6 +1497,7 @@ int upload_weights(GDNEngine *e, const GDNModel *m, bool verify = false, size_t 
     }
     pk.begin(V * H);
     pk.rows(m->lm_head, V * H);
+    pk.stream_order((V % kCuLm) == 0 ? kCuLm : kCuLmSmall, H, PRO_RESNORM, EPI_LM);
     e->w_lm = p;
     e->i_lm = pk.info();
     if (pk.upload(p)) return -1;
@@ -2377,6 +2418,7 @@ int gdn_test_gemv(int contract, const float *W, const float *x, uint32_t M, uint
     Packer pk{contract, {}};
     pk.begin((size_t)M * K);
     pk.rows(W, (size_t)M * K);
+    pk.stream_order(kRows, K, PRO_PLAIN, EPI_RAW);
     void *dW = nullptr;
     float *dx = nullptr, *dy = nullptr;
     GDN_HIP(hipMalloc(&dW, (size_t)M * K * welem(contract)));
