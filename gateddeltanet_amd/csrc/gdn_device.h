@@ -77,23 +77,46 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b16) { return u2f(b16
 
 // expf and log1pf as the reference's C library evaluates them (glibc 2.35,
 // gdn_libm.h): the engine's transcendentals equal the reference's bit for bit.
-__device__ __forceinline__ float exp_ref(float x) { return gdn_libm::gdn_expf(x); }
+// Tab: where expf's 32-entry table is read (gdn_libm::Exp2Const, or Exp2Lds:
+// a workgroup's copy in LDS, filled by fill_exp2_lds).
+using Exp2Const = gdn_libm::Exp2Const;
+struct Exp2Lds {
+    const uint64_t *t;
+    __device__ __forceinline__ uint64_t operator()(int i) const { return t[i]; }
+};
+// Threads 0..31: entry t of the table.  Load early (load()), store late
+// (store(), before a barrier that precedes the first use).
+struct Exp2Fill {
+    uint64_t v = 0;
+    __device__ __forceinline__ void load() {
+        if (threadIdx.x < 32) v = gdn_libm::exp2_table((int)threadIdx.x);
+    }
+    __device__ __forceinline__ void store(uint64_t *lds) const {
+        if (threadIdx.x < 32) lds[threadIdx.x] = v;
+    }
+};
+
+template <class Tab = Exp2Const>
+__device__ __forceinline__ float exp_ref(float x, const Tab &tab = Tab()) { return gdn_libm::gdn_expf_t(x, tab); }
 __device__ __forceinline__ float log1p_ref(float x) { return gdn_libm::gdn_log1pf(x); }
 
 // gdn_sigmoid / gdn_silu / gdn_softplus, gdn_model.cpp:1307-1330.
-__device__ __forceinline__ float sigmoid_ref(float x) {
+template <class Tab = Exp2Const>
+__device__ __forceinline__ float sigmoid_ref(float x, const Tab &tab = Tab()) {
     if (x >= 0.0f) {
-        const float z = exp_ref(-x);
+        const float z = exp_ref(-x, tab);
         return 1.0f / (1.0f + z);
     }
-    const float z = exp_ref(x);
+    const float z = exp_ref(x, tab);
     return z / (1.0f + z);
 }
-__device__ __forceinline__ float silu_ref(float x) { return x * sigmoid_ref(x); }
-__device__ __forceinline__ float softplus_ref(float x) {
+template <class Tab = Exp2Const>
+__device__ __forceinline__ float silu_ref(float x, const Tab &tab = Tab()) { return x * sigmoid_ref(x, tab); }
+template <class Tab = Exp2Const>
+__device__ __forceinline__ float softplus_ref(float x, const Tab &tab = Tab()) {
     if (x > 20.0f) return x;
-    if (x < -20.0f) return exp_ref(x);
-    return log1p_ref(exp_ref(x));
+    if (x < -20.0f) return exp_ref(x, tab);
+    return log1p_ref(exp_ref(x, tab));
 }
 
 // Balanced pairwise sum of 16 contiguous values (gemv32_tree16).
@@ -165,12 +188,13 @@ __device__ __forceinline__ uint32_t cvt_pk(float lo, float hi) {
 
 // beta = sigmoid(b); decay = expf(-expf(a_log) * softplus(a + dt_bias))
 // (gdn_island_prep, gdn_model.cpp:2461-2465).
+template <class Tab = Exp2Const>
 __device__ __forceinline__ void head_scalars(float a, float b, float a_log, float dt_bias,
-                                             float &beta, float &decay) {
-    beta = sigmoid_ref(b);
+                                             float &beta, float &decay, const Tab &tab = Tab()) {
+    beta = sigmoid_ref(b, tab);
     const float decay_in = a + dt_bias;
-    const float decay_val = -exp_ref(a_log) * softplus_ref(decay_in);
-    decay = exp_ref(decay_val);
+    const float decay_val = -exp_ref(a_log, tab) * softplus_ref(decay_in, tab);
+    decay = exp_ref(decay_val, tab);
 }
 
 // Recurrent-state layouts.  Row-major: head h, key row j, value column i
@@ -184,9 +208,50 @@ __device__ __forceinline__ size_t state_index(int h, int j, int c0) {
     else return (size_t)h * kHD * kHD + (size_t)j * kHD + c0;
 }
 
-// Gated delta rule for one head and CB state columns (beta/decay per head
-// come from the QKVG kernel), run by one workgroup of 256 threads; thread t
-// holds key row t of the tile (CB columns) in registers.
+// A load of one float through a vector memory instruction: the address is
+// moved into VGPRs first, so a uniform address does not become a scalar load
+// (whose wait, lgkmcnt, would also hold back unrelated scalar loads).
+__device__ __forceinline__ float vector_load(const float *p) {
+    asm volatile("" : "+v"(p));
+    return *(const __attribute__((address_space(1))) float *)p;
+}
+
+// Per-head (beta, decay) for recur_block: read from precomputed pairs, or
+// computed from the raw a_h and b_h (head_scalars).  read() issues the loads
+// (after the state loads), get() returns the pair; recur_block evaluates it
+// on wave 3 while wave 0 runs the column chains.
+struct ScalarsFromPairs {
+    const float *bd;
+    float v[2];
+    __device__ __forceinline__ void read(int h) {
+        v[0] = vector_load(bd + 2 * h);
+        v[1] = vector_load(bd + 2 * h + 1);
+    }
+    template <class Tab>
+    __device__ __forceinline__ void get(float &beta, float &decay, const Tab &) const {
+        beta = v[0];
+        decay = v[1];
+    }
+};
+struct ScalarsFromAB {
+    const float *a, *b, *a_log, *dt_bias;
+    float v[4];
+    __device__ __forceinline__ void read(int h) {
+        v[0] = vector_load(a + h);
+        v[1] = vector_load(b + h);
+        v[2] = vector_load(a_log + h);
+        v[3] = vector_load(dt_bias + h);
+    }
+    template <class Tab>
+    __device__ __forceinline__ void get(float &beta, float &decay, const Tab &tab) const {
+        head_scalars(v[0], v[1], v[2], v[3], beta, decay, tab);
+    }
+};
+
+// Gated delta rule for one head and CB state columns, run by one workgroup
+// of 256 threads; thread t holds key row t of the tile (CB columns) in
+// registers.  beta/decay come from scal, evaluated while the state loads
+// are in flight.
 //   q/k L2 norms in gdn_tree_reduce_256 order: with PRE the QKVG kernel
 //   has already reduced each 16-row block (the tree's lower four levels;
 //   qk_part[h*16 + b], k at offset 128) and the top four levels run here,
@@ -200,9 +265,9 @@ __device__ __forceinline__ size_t state_index(int h, int j, int c0) {
 //   With OSUM (CB = 16: one tile is one 16-value chunk of the output norm)
 //   the workgroup also writes sum_i R(o_i)^2 in order, the chunk's sum of
 //   squares, to o_sum[h*16 + c0/16].
-template <int C, int CB, bool TILED, bool PRE, bool OSUM>
+template <int C, int CB, bool TILED, bool PRE, bool OSUM, class Scal>
 __device__ __forceinline__ void recur_block(const float *__restrict__ qp, const float *__restrict__ kp,
-                                            const float *__restrict__ vp, const float *__restrict__ bd,
+                                            const float *__restrict__ vp, Scal scal,
                                             const float *__restrict__ qk_part, void *__restrict__ state,
                                             float *__restrict__ attn, float *__restrict__ o_sum, const int h,
                                             const int c0) {
@@ -213,10 +278,12 @@ __device__ __forceinline__ void recur_block(const float *__restrict__ qp, const 
     __shared__ __attribute__((aligned(16))) float pk_t[CB * LDT];  // S[j][i] * kn[j] at [i][j]
     __shared__ __attribute__((aligned(16))) float pq_t[CB * LDT];  // S[j][i] * qn[j] at [i][j]
     __shared__ float dl[CB];
-    __shared__ float red[8], red2[4];
+    __shared__ float red[8], red2[4], bdsh[2];
+    __shared__ uint64_t exp2_lds[32];
     const int t = threadIdx.x;
     const int lane = t & 63, w = t >> 6;
     const size_t sidx = state_index<TILED, CB>(h, t, c0);
+    Exp2Fill e2;
 
     const float q = qp[h * kHD + t], k = kp[h * kHD + t];
     const float vi = (t < CB) ? vp[h * kHD + c0 + t] : 0.0f;
@@ -231,6 +298,8 @@ __device__ __forceinline__ void recur_block(const float *__restrict__ qp, const 
             else
                 tr[i] = reinterpret_cast<const u32x4 *>(reinterpret_cast<const float *>(state) + sidx)[i];
         }
+        scal.read(h);
+        e2.load();
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const uint32_t wv[4] = {tr[i].x, tr[i].y, tr[i].z, tr[i].w};
@@ -245,7 +314,6 @@ __device__ __forceinline__ void recur_block(const float *__restrict__ qp, const 
             }
         }
     }
-    const float beta = bd[2 * h], decay = bd[2 * h + 1];
 
     float q_sq, k_sq;
     if constexpr (PRE) {
@@ -280,8 +348,11 @@ __device__ __forceinline__ void recur_block(const float *__restrict__ qp, const 
         pk_t[e * LDT + t] = sv[e] * kj;
         pq_t[e * LDT + t] = sv[e] * qj;
     }
+    e2.store(exp2_lds);
     __syncthreads();
 
+    // wave 0: the column chains; meanwhile wave 3 evaluates beta and decay
+    float acc = 0.0f, pv = 0.0f;
     if (t < 2 * CB) {
         // lane i: r_i = sum_j S[j][i] kn[j]; lane CB + i: p_i (same order)
         const bool is_p = t >= CB;
@@ -290,7 +361,6 @@ __device__ __forceinline__ void recur_block(const float *__restrict__ qp, const 
         f32x4 col_v[kHD / 4];  // the whole column, read ahead of the serial adds
 #pragma unroll
         for (int j4 = 0; j4 < kHD / 4; ++j4) col_v[j4] = src[j4];
-        float acc = 0.0f;
 #pragma unroll
         for (int j4 = 0; j4 < kHD / 4; ++j4) {
             acc = acc + col_v[j4].x;
@@ -299,13 +369,25 @@ __device__ __forceinline__ void recur_block(const float *__restrict__ qp, const 
             acc = acc + col_v[j4].w;
         }
         // lane i takes p_i from lane CB + i
-        float pv;
         if constexpr (CB == 16) {
             pv = __int_as_float(__builtin_amdgcn_permlane16_swap(__float_as_int(acc), __float_as_int(acc), false,
                                                                  false)[1]);
         } else {
             pv = __shfl(acc, (lane + CB) & 63);
         }
+    } else if (w == 3) {
+        float b_, d_;
+        scal.get(b_, d_, Exp2Lds{exp2_lds});
+        if (lane == 0) {
+            bdsh[0] = b_;
+            bdsh[1] = d_;
+        }
+    }
+    __syncthreads();
+    const float beta = bdsh[0], decay = bdsh[1];
+
+    if (t < 2 * CB) {
+        const bool is_p = t >= CB;
         float o = 0.0f;
         if (!is_p) {
             const float alpha = (red2[0] + red2[1]) + (red2[2] + red2[3]);

@@ -671,8 +671,7 @@ struct Epi {
     const float *aux;  // QKVG: the layer's small weights
     const uint16_t *ab16;  // QKVG (CU-resident): the layer's a/b rows [16][kH] as BF16 bits
     float *tails;      // QKVG: the layer's conv tails (3 stripes)
-    float *ab;         // QKVG: a[8], b[8] (BF16-rounded)
-    float *bd;         // QKVG: (beta, decay) per head
+    float *ab;         // QKVG: a[8], b[8] (rounded)
     float *qk_part;    // QKVG: q and k sums of squares per 16-row block, [2][8 heads][16]
     float *part_val;   // LM: per-block argmax
     int *part_idx;
@@ -885,7 +884,8 @@ using IC = std::integral_constant<int, N>;
 
 // ROWS rows per workgroup (grid = M / ROWS), at most D items in flight per
 // thread.
-//   EPI_QKVG    rows are q|k|v|g; workgroups 0..7 also run head h's a/b rows
+//   EPI_QKVG    rows are q|k|v|g; workgroups 0..15 also run one row of the
+//               tiny a|b projection
 //   EPI_SWIGLU  a workgroup's rows are ROWS/2 gate rows then the matching
 //               ROWS/2 up rows
 //   EPI_LM      FP32 logits and the workgroup's argmax
@@ -903,7 +903,7 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     __shared__ float bcast[kNH];
     __shared__ uint32_t red[8];
     __shared__ float ybuf[ROWS];
-    __shared__ float abpart[2 * Hb<kH>::HB];
+    __shared__ float abpart[Hb<kH>::HB];
     // claim the whole register file (128 VGPRs x 16 waves): one workgroup per CU
     asm volatile("" ::: "v127");
     const int t = threadIdx.x, wave = t >> 6;
@@ -927,18 +927,17 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     constexpr int T0 = kTB - stream_threads(PRO, EPI);
     Prologue<C, K, PRO> pro;
     if (t < kT) pro.load(src);
-    // QKVG workgroup h < 8: head h's FP32 a and b rows (half-beat t & 127 of
-    // row t >> 7), needed right after the input is built
-    const bool ab_blk = (EPI == EPI_QKVG) && blockIdx.x < kNH;
-    // (BF16 contracts read the BF16 copy: they require BF16-exact weights,
-    // so its values are the FP32 rows' and the 8 workgroups stream 8 KB, not
-    // 16 KB, beyond their weight rows)
+    // QKVG workgroup j < 16: row j of the tiny a|b projection (a_h for
+    // j = h, b_h for j = 8 + h), half-beat t of it on threads t < 128,
+    // needed right after the input is built.  (BF16 contracts read the BF16
+    // copy: they require BF16-exact weights, so its values are the FP32
+    // row's and the workgroup streams 4 KB, not 8 KB, beyond its weight rows.)
+    const bool ab_blk = (EPI == EPI_QKVG) && blockIdx.x < 2 * kNH;
     constexpr int ABW = BF ? 2 : 4;
     u32x4 abw[ABW];
-    if (ab_blk && t < kT) {
-        const int abrow = (t >> 7) * kNH + blockIdx.x, hb = t & 127;
-        const u32x4 *src4 = BF ? reinterpret_cast<const u32x4 *>(ep.ab16 + (size_t)abrow * kH + hb * 16)
-                               : reinterpret_cast<const u32x4 *>(ep.aux + kAuxAB + (size_t)abrow * kH + hb * 16);
+    if (ab_blk && t < Hb<kH>::HB) {
+        const u32x4 *src4 = BF ? reinterpret_cast<const u32x4 *>(ep.ab16 + (size_t)blockIdx.x * kH + t * 16)
+                               : reinterpret_cast<const u32x4 *>(ep.aux + kAuxAB + (size_t)blockIdx.x * kH + t * 16);
 #pragma unroll
         for (int q = 0; q < ABW; ++q) abw[q] = src4[q];
     }
@@ -984,52 +983,38 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
         else fast = pro.finish_fp32(src, reinterpret_cast<float *>(xs), scratch, bcast, sync);
         if constexpr (EPI == EPI_QKVG) {
             if (ab_blk) {
-                // a_h and b_h while the weights stream (gdn_gemv_tiny_ab):
+                // a_h or b_h while the weights stream (gdn_gemv_tiny_ab):
                 // FP32 products x * w, tree16 per half-beat; then wave 3 runs
-                // acc = (acc + tree16(lo)) + tree16(hi) per beat, rounded,
-                // and beta_h, decay_h (its double-precision exp/log1p would
-                // otherwise trail the workgroup's epilogue)
-                const int hb = t & 127;
-                uint32_t xv[16];
-                lds_load16u(xs + hb * 16, xv);
-                float p[16];
-                if constexpr (BF) {
-                    const uint32_t wv[8] = {abw[0].x, abw[0].y, abw[0].z, abw[0].w,
-                                            abw[1].x, abw[1].y, abw[1].z, abw[1].w};
+                // acc = (acc + tree16(lo)) + tree16(hi) per beat and rounds
+                // it (the recurrence turns a_h, b_h into beta_h, decay_h)
+                if (t < Hb<kH>::HB) {
+                    uint32_t xv[16];
+                    lds_load16u(xs + t * 16, xv);
+                    float p[16];
+                    if constexpr (BF) {
+                        const uint32_t wv[8] = {abw[0].x, abw[0].y, abw[0].z, abw[0].w,
+                                                abw[1].x, abw[1].y, abw[1].z, abw[1].w};
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        p[2 * i] = lane_word_value(xv[2 * i], 0) * u2f(wv[i] << 16);
-                        p[2 * i + 1] = lane_word_value(xv[2 * i + 1], 1) * u2f(wv[i] & 0xffff0000u);
-                    }
-                } else {
+                        for (int i = 0; i < 8; ++i) {
+                            p[2 * i] = lane_word_value(xv[2 * i], 0) * u2f(wv[i] << 16);
+                            p[2 * i + 1] = lane_word_value(xv[2 * i + 1], 1) * u2f(wv[i] & 0xffff0000u);
+                        }
+                    } else {
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        p[4 * q + 0] = u2f(xv[4 * q + 0]) * u2f(abw[q].x);
-                        p[4 * q + 1] = u2f(xv[4 * q + 1]) * u2f(abw[q].y);
-                        p[4 * q + 2] = u2f(xv[4 * q + 2]) * u2f(abw[q].z);
-                        p[4 * q + 3] = u2f(xv[4 * q + 3]) * u2f(abw[q].w);
+                        for (int q = 0; q < 4; ++q) {
+                            p[4 * q + 0] = u2f(xv[4 * q + 0]) * u2f(abw[q].x);
+                            p[4 * q + 1] = u2f(xv[4 * q + 1]) * u2f(abw[q].y);
+                            p[4 * q + 2] = u2f(xv[4 * q + 2]) * u2f(abw[q].z);
+                            p[4 * q + 3] = u2f(xv[4 * q + 3]) * u2f(abw[q].w);
+                        }
                     }
+                    abpart[t] = tree16(p);
                 }
-                abpart[t] = tree16(p);
                 sync();
-                if (wave == 3) {
-                    const int lane = t & 63;
+                if (t == 3 * 64) {
                     float acc = 0.0f;
-                    if (lane < 2) {
-                        const float *pr = abpart + lane * Hb<kH>::HB;
-                        for (int j = 0; j < Hb<kH>::NB; ++j) acc = (acc + pr[2 * j]) + pr[2 * j + 1];
-                    }
-                    const float a = R<C>(acc);
-                    const float b = R<C>(__shfl(acc, 1));
-                    if (lane == 0) {
-                        float beta, decay;
-                        head_scalars(a, b, ep.aux[kAuxALog + blockIdx.x], ep.aux[kAuxDtBias + blockIdx.x], beta,
-                                     decay);
-                        ep.ab[blockIdx.x] = a;
-                        ep.ab[kNH + blockIdx.x] = b;
-                        ep.bd[2 * blockIdx.x] = beta;
-                        ep.bd[2 * blockIdx.x + 1] = decay;
-                    }
+                    for (int j = 0; j < Hb<kH>::NB; ++j) acc = (acc + abpart[2 * j]) + abpart[2 * j + 1];
+                    ep.ab[blockIdx.x] = R<C>(acc);
                 }
             }
         }
@@ -1207,31 +1192,17 @@ __global__ __launch_bounds__(kT) void k_argmax(const float *__restrict__ part_va
 }
 
 // One workgroup per (16 state columns, head): grid (kHD / CB, kNH), state
-// in the tiled layout.  PRE: the q/k sums of squares come from the QKVG
+// in the tiled layout.  beta_h and decay_h are evaluated from the QKVG
+// kernel's a_h and b_h in every workgroup of head h.  PRE: the q/k sums of squares come from the QKVG
 // kernel and the output norm's chunk sums go to o_sum (BF16 contracts).
 template <int C, int CB, bool PRE>
 __global__ __launch_bounds__(kT) void k_recur(const float *__restrict__ qp,
                                               const float *__restrict__ kp,
-                                              const float *__restrict__ vp,
-                                              const float *__restrict__ bd,
+                                              const float *__restrict__ vp, ScalarsFromAB scal,
                                               const float *__restrict__ qk_part,
                                               void *__restrict__ state, float *__restrict__ attn,
                                               float *__restrict__ o_sum) {
-    recur_block<C, CB, true, PRE, PRE>(qp, kp, vp, bd, qk_part, state, attn, o_sum, blockIdx.y, blockIdx.x * CB);
-}
-
-// beta/decay for n heads from raw (a, b, a_log, dt_bias) (recurrence hook).
-__global__ __launch_bounds__(kT) void k_head_scalars(const float *__restrict__ a,
-                                                     const float *__restrict__ b,
-                                                     const float *__restrict__ a_log,
-                                                     const float *__restrict__ dt_bias, int n,
-                                                     float *__restrict__ bd) {
-    const int i = blockIdx.x * kT + threadIdx.x;
-    if (i >= n) return;
-    float beta, decay;
-    head_scalars(a[i], b[i], a_log[i], dt_bias[i], beta, decay);
-    bd[2 * i] = beta;
-    bd[2 * i + 1] = decay;
+    recur_block<C, CB, true, PRE, PRE>(qp, kp, vp, scal, qk_part, state, attn, o_sum, blockIdx.y, blockIdx.x * CB);
 }
 
 // out = R(a + b) over the hidden vector (layer output for the layer hook).
@@ -1279,7 +1250,7 @@ struct GDNEngine {
     // activations and step outputs
     float *act = nullptr;
     float *resid = nullptr, *resid_alt = nullptr, *fhid = nullptr, *qkv = nullptr,
-          *gate = nullptr, *sgate = nullptr, *ab = nullptr, *bd = nullptr, *attn = nullptr,
+          *gate = nullptr, *sgate = nullptr, *ab = nullptr, *attn = nullptr,
           *ybuf_o = nullptr, *dbuf = nullptr, *hbuf = nullptr, *lm_val = nullptr,
           *xrow = nullptr, *logits = nullptr, *qkpart = nullptr, *osum = nullptr;
     int *lm_idx = nullptr;
@@ -1552,7 +1523,7 @@ int alloc_buffers(GDNEngine *e) {
     GDN_HIP(hipMemset(e->tails, 0, tail_floats(e) * 4));
     const size_t nblk_lm = (size_t)e->vocab / kCuLmSmall;  // the most LM-head workgroups
     auto up64 = [](size_t n) { return (n + 63) & ~(size_t)63; };  // 256-byte aligned pieces
-    const size_t act_floats = 3 * kH + 3 * kH + 2 * kH + 64 + 64 + 3 * kH + kI + up64(nblk_lm) + kH +
+    const size_t act_floats = 3 * kH + 3 * kH + 2 * kH + 64 + 3 * kH + kI + up64(nblk_lm) + kH +
                               up64((size_t)e->vocab) + 2 * kNH * 16 + kNH * (kHD / 16);
     GDN_HIP(hipMalloc(&e->act, act_floats * 4));
     GDN_HIP(hipMemset(e->act, 0, act_floats * 4));
@@ -1564,7 +1535,6 @@ int alloc_buffers(GDNEngine *e) {
     e->gate = p; p += kH;
     e->sgate = p; p += kH;
     e->ab = p; p += 64;
-    e->bd = p; p += 64;
     e->attn = p; p += kH;
     e->ybuf_o = p; p += kH;
     e->dbuf = p; p += kH;
@@ -1621,7 +1591,6 @@ void launch_qkvg(GDNEngine *e, int l, const float *res_a, const float *res_b, hi
     q.ab16 = e->ab16 + (size_t)l * 2 * kNH * kH;
     q.tails = layer_tails(e, l);
     q.ab = e->ab;
-    q.bd = e->bd;
     q.qk_part = e->qkpart;
     XSrc xq = xsrc(e, res_a, res_b, nullptr, aux + kAuxAttnNorm, e->resid, nullptr, dump_slot(e, 4 * l));
     if constexpr (PRO0 == PRO_EMBED) {
@@ -1636,8 +1605,10 @@ void launch_qkvg(GDNEngine *e, int l, const float *res_a, const float *res_b, hi
 
 template <int C>
 void launch_recur(GDNEngine *e, int l, hipStream_t s) {
+    const float *aux = layer_aux(e, l);
+    const ScalarsFromAB scal{e->ab, e->ab + kNH, aux + kAuxALog, aux + kAuxDtBias};
     hipLaunchKernelGGL((k_recur<C, kCB, C != kFp32>), dim3(kHD / kCB, kNH), dim3(kT), 0, s, e->qkv,
-                       e->qkv + kH, e->qkv + 2 * kH, e->bd, e->qkpart, layer_state(e, l), e->attn, e->osum);
+                       e->qkv + kH, e->qkv + 2 * kH, scal, e->qkpart, layer_state(e, l), e->attn, e->osum);
 }
 
 template <int C>
@@ -2489,16 +2460,13 @@ int gdn_test_recurrence(int contract, uint32_t n_heads, uint32_t n_steps, const 
         tile_state(S, tiles.data(), n_heads, true);
         GDN_HIP(hipMemcpy(dS, tiles.data(), nstate * 4, hipMemcpyHostToDevice));
     }
-    float *dbd;
-    GDN_HIP(hipMalloc(&dbd, 2 * ns * 4));
-    hipLaunchKernelGGL(k_head_scalars, dim3((unsigned)((ns + kT - 1) / kT)), dim3(kT), 0, 0, da, db, dal,
-                       ddt, (int)ns, dbd);
     const dim3 grid(kHD / kCB, n_heads), block(kT);
     for (uint32_t s = 0; s < n_steps; ++s) {
         const size_t ov = (size_t)s * n_heads * kHD, os = (size_t)s * n_heads;
-#define GDN_REC(CC)                                                                             \
-    hipLaunchKernelGGL((k_recur<CC, kCB, false>), grid, block, 0, 0, dq + ov, dk + ov, dv + ov, dbd + 2 * os, \
-                       nullptr, dS, dout + ov, nullptr)
+        const ScalarsFromAB scal{da + os, db + os, dal + os, ddt + os};
+#define GDN_REC(CC)                                                                                       \
+    hipLaunchKernelGGL((k_recur<CC, kCB, false>), grid, block, 0, 0, dq + ov, dk + ov, dv + ov, scal, nullptr, \
+                       dS, dout + ov, nullptr)
         if (contract == kRef) GDN_REC(kRef);
         else if (contract == kBf16w) GDN_REC(kBf16w);
         else GDN_REC(kFp32);
@@ -2520,7 +2488,7 @@ int gdn_test_recurrence(int contract, uint32_t n_heads, uint32_t n_steps, const 
         GDN_HIP(hipMemcpy(tiles.data(), dS, nstate * 4, hipMemcpyDeviceToHost));
         tile_state(tiles.data(), S, n_heads, false);
     }
-    float *bufs[] = {dq, dk, dv, da, db, dal, ddt, dout, dbd};
+    float *bufs[] = {dq, dk, dv, da, db, dal, ddt, dout};
     for (float *p : bufs) GDN_HIP(hipFree(p));
     GDN_HIP(hipFree(dS));
     return 0;

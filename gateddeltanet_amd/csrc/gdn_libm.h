@@ -76,7 +76,15 @@ GDN_HD inline uint64_t exp2_table(int i) {
     return T[i];
 }
 
-GDN_HD inline float gdn_expf(float x) {
+// The table as a function of i, for gdn_expf_t: the constant array, or a
+// caller's copy (the kernels keep one in LDS, since a lookup in global memory
+// costs a memory round trip on a kernel's serial tail).
+struct Exp2Const {
+    GDN_HD uint64_t operator()(int i) const { return exp2_table(i); }
+};
+
+template <class Tab>
+GDN_HD inline float gdn_expf_t(float x, const Tab &tab) {
     constexpr double kN = 32.0;
     constexpr double kInvLn2N = 0x1.71547652b82fep+0 * kN;  // 32 / ln 2
     constexpr double kShift = 0x1.8p+52;
@@ -97,7 +105,7 @@ GDN_HD inline float gdn_expf(float x) {
     const uint64_t ki = bits_d(kd);
     kd -= kShift;
     const double r = fused(kInvLn2N, xd, -kd);
-    const double s = from_bits_d(exp2_table((int)(ki % 32u)) + (ki << 47));
+    const double s = from_bits_d(tab((int)(ki % 32u)) + (ki << 47));
     const double z = fused(kC0, r, kC1);
     const double r2 = r * r;
     double y = fused(kC2, r, 1.0);
@@ -105,6 +113,8 @@ GDN_HD inline float gdn_expf(float x) {
     y = y * s;
     return (float)y;
 }
+
+GDN_HD inline float gdn_expf(float x) { return gdn_expf_t(x, Exp2Const{}); }
 
 GDN_HD inline float gdn_log1pf(float x) {
     constexpr float ln2_hi = 6.9313812256e-01f;  // 0x3f317180

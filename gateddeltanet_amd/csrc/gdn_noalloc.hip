@@ -73,8 +73,9 @@ template <int C>
 __global__ __launch_bounds__(gdn::kT) void k_step(const float *__restrict__ q, const float *__restrict__ k,
                                                   const float *__restrict__ v, const float2 *__restrict__ bd,
                                                   void *__restrict__ S, float *__restrict__ o) {
-    gdn::recur_block<C, kCols, false, false, false>(q, k, v, reinterpret_cast<const float *>(bd), nullptr, S, o,
-                                                     nullptr, blockIdx.y, blockIdx.x * kCols);
+    const gdn::ScalarsFromPairs scal{reinterpret_cast<const float *>(bd)};
+    gdn::recur_block<C, kCols, false, false, false>(q, k, v, scal, nullptr, S, o, nullptr, blockIdx.y,
+                                                     blockIdx.x * kCols);
 }
 
 }  // namespace
