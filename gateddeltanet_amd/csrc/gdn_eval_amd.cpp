@@ -10,7 +10,10 @@
 //       [--logits-dump F] [--logits-reference F] [--hidden-dump F]
 //       [--dump-state F] [--no-host-check]
 //   gdn_eval_amd <weights.gdnw> [output.json] --decode-from-state <state>
-//       --benchmark-tokens <tokens.txt> [--benchmark-steps N]
+//       --benchmark-tokens <tokens.txt> [--benchmark-idle-seconds N]
+//       [--benchmark-warmup-seconds N] [--benchmark-interval-seconds N]
+//       [--benchmark-intervals N]   (the reference's timed protocol, its
+//       defaults 60 / 30 / 60 / 3), or a fixed count: [--benchmark-steps N]
 //       [--benchmark-warmup N]
 //   gdn_eval_amd <weights.gdnw> <rolling.gdnreq> [output.json] --score
 //       [--score-doc-limit N]
@@ -45,6 +48,7 @@
 #include <cstring>
 #include <fstream>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "gdn_amd.h"
@@ -65,6 +69,8 @@ struct Options {
     std::string weights, fixture, output, state, logits_dump, logits_ref, hidden_dump, dump_state,
         bench_tokens, prefill;
     uint32_t decode_len = 0, bench_steps = 0, bench_warmup = 64, score_limit = 0, synth_layers = 0;
+    // the timed benchmark protocol, with the reference's defaults (host.cpp:208-211)
+    uint32_t bench_idle_s = 60, bench_warmup_s = 30, bench_interval_s = 60, bench_intervals = 3;
     uint32_t example = 0;
     bool synth = false, host_check = true, score = false, round_bf16 = false;
     int contract = GDN_CONTRACT_REF;
@@ -97,6 +103,14 @@ Options parse(int argc, char **argv) {
         else if (a == "--benchmark-tokens") o.bench_tokens = next("--benchmark-tokens");
         else if (a == "--benchmark-steps") o.bench_steps = parse_u32(next("--benchmark-steps"), "--benchmark-steps");
         else if (a == "--benchmark-warmup") o.bench_warmup = parse_u32(next("--benchmark-warmup"), "--benchmark-warmup");
+        else if (a == "--benchmark-idle-seconds")
+            o.bench_idle_s = parse_u32(next("--benchmark-idle-seconds"), "--benchmark-idle-seconds");
+        else if (a == "--benchmark-warmup-seconds")
+            o.bench_warmup_s = parse_u32(next("--benchmark-warmup-seconds"), "--benchmark-warmup-seconds");
+        else if (a == "--benchmark-interval-seconds")
+            o.bench_interval_s = parse_u32(next("--benchmark-interval-seconds"), "--benchmark-interval-seconds");
+        else if (a == "--benchmark-intervals")
+            o.bench_intervals = parse_u32(next("--benchmark-intervals"), "--benchmark-intervals");
         else if (a == "--score") o.score = true;
         else if (a == "--prefill") o.prefill = next("--prefill");
         else if (a == "--example") o.example = parse_u32(next("--example"), "--example");
@@ -118,7 +132,8 @@ Options parse(int argc, char **argv) {
                 "--decode-from-state S [--decode-len N] [--logits-dump F] [--logits-reference F] "
                 "[--hidden-dump F] [--dump-state F] [--no-host-check]\n"
                 "  gdn_eval_amd <weights|--synth[=L]> [out.json] --decode-from-state S --benchmark-tokens T "
-                "[--benchmark-steps N] [--benchmark-warmup N]\n"
+                "[--benchmark-idle-seconds N] [--benchmark-warmup-seconds N] [--benchmark-interval-seconds N] "
+                "[--benchmark-intervals N]   (or a fixed count: [--benchmark-steps N] [--benchmark-warmup N])\n"
                 "  gdn_eval_amd <weights|--synth[=L]> <rolling.gdnreq> [out.json] --score [--score-doc-limit N]\n"
                 "  gdn_eval_amd <weights|--synth[=L]> [out.json] --prefill <prompt.txt|ll.gdnreq> [--example N] "
                 "--dump-state S [--round-bf16]\n"
@@ -153,6 +168,8 @@ Options parse(int argc, char **argv) {
     if (!o.score && o.state.empty() && o.prefill.empty())
         die("a mode is required: --decode-from-state S, --score or --prefill P; see --help");
     if (!o.bench_tokens.empty() && o.state.empty()) die("--benchmark-tokens requires --decode-from-state");
+    if (!o.bench_tokens.empty() && !o.bench_steps && (o.bench_interval_s == 0 || o.bench_intervals == 0))
+        die("--benchmark-interval-seconds and --benchmark-intervals must be positive");
     return o;
 }
 
@@ -411,36 +428,109 @@ std::vector<int32_t> load_token_file(const std::string &path, uint32_t V, const 
     return tokens;
 }
 
+double unix_now() {
+    return std::chrono::duration<double>(std::chrono::system_clock::now().time_since_epoch()).count();
+}
+
+void write_bench_header(FILE *out, const Options &o, size_t stream_len) {
+    std::fprintf(out,
+                 "{\n  \"schema\": \"gdn-steady-tpot-v1\",\n  \"weights\": \"%s\",\n  \"state\": \"%s\",\n"
+                 "  \"token_file\": \"%s\",\n  \"token_stream_length\": %zu,\n  \"teacher_forced\": true,\n"
+                 "  \"full_lm_head\": true,\n  \"onchip_argmax\": true,\n  \"full_logits_readback\": false,\n"
+                 "  \"contract\": \"%s\",\n",
+                 o.synth ? "synthetic" : o.weights.c_str(), o.state.c_str(), o.bench_tokens.c_str(), stream_len,
+                 contract_name(o.contract));
+}
+
+// One measured interval: its wall-clock bounds and every step's token-in ->
+// token-out time (production_tpot) and graph time between HIP events
+// (kernel).
+struct Interval {
+    double start_unix = 0, end_unix = 0;
+    std::vector<double> outer, inner;
+};
+
+void write_interval(FILE *out, size_t index, const Interval &iv, bool first) {
+    std::fprintf(out, "%s\n    {\"index\": %zu, \"start_unix\": %.6f, \"end_unix\": %.6f, \"steps\": %zu, "
+                 "\"tokens_per_second\": %.3f, \"production_tpot\": ",
+                 first ? "" : ",", index, iv.start_unix, iv.end_unix, iv.outer.size(),
+                 (double)iv.outer.size() / (iv.end_unix - iv.start_unix));
+    write_summary(out, summarize(iv.outer));
+    std::fprintf(out, ", \"kernel\": ");
+    write_summary(out, summarize(iv.inner));
+    std::fprintf(out, "}");
+}
+
+// The steady teacher-forced benchmark (host.cpp:2150-2256): a loaded-idle
+// window, a timed warmup, then timed intervals over the cyclic token
+// stream, each summarised.  With --benchmark-steps: a fixed warmup count and
+// one interval of a fixed step count instead.  The reference's embedding
+// write / H2D / launch / token D2H phases have no counterpart: the embedding
+// import runs on the device and the token crosses through mapped memory.
 int run_benchmark(const Options &o, const GDNModel &model, GDNRunState &rs) {
     const std::vector<int32_t> tokens = load_token_file(o.bench_tokens, model.config.vocab_size, "benchmark");
     uint32_t prompt_len = 0;
     int32_t seed = 0;
     if (gdn_load_gdnstate(&rs, &model, o.state.c_str(), &prompt_len, &seed) != 0) die("cannot load " + o.state);
-    const uint32_t steps = o.bench_steps ? o.bench_steps : (uint32_t)tokens.size();
-    if (o.bench_warmup && gdn_run_teacher_forced(&rs, tokens.data(), (uint32_t)tokens.size(), o.bench_warmup,
-                                                 nullptr, nullptr, nullptr) != 0)
-        die("benchmark warmup failed");
-    std::vector<float> inner(steps), outer(steps);
-    const double t0 = now_ms();
-    if (gdn_run_teacher_forced(&rs, tokens.data(), (uint32_t)tokens.size(), steps, nullptr, inner.data(),
-                               outer.data()) != 0)
-        die("benchmark failed");
-    const double wall = now_ms() - t0;
-    const Summary so = summarize(std::vector<double>(outer.begin(), outer.end()));
-    const Summary si = summarize(std::vector<double>(inner.begin(), inner.end()));
+    if (o.bench_steps) {
+        const uint32_t steps = o.bench_steps;
+        if (o.bench_warmup && gdn_run_teacher_forced(&rs, tokens.data(), (uint32_t)tokens.size(), o.bench_warmup,
+                                                     nullptr, nullptr, nullptr) != 0)
+            die("benchmark warmup failed");
+        std::vector<float> inner(steps), outer(steps);
+        Interval iv;
+        iv.start_unix = unix_now();
+        if (gdn_run_teacher_forced(&rs, tokens.data(), (uint32_t)tokens.size(), steps, nullptr, inner.data(),
+                                   outer.data()) != 0)
+            die("benchmark failed");
+        iv.end_unix = unix_now();
+        iv.outer.assign(outer.begin(), outer.end());
+        iv.inner.assign(inner.begin(), inner.end());
+        FILE *out = open_output(o.output);
+        write_bench_header(out, o, tokens.size());
+        std::fprintf(out, "  \"warmup_steps\": %u,\n  \"intervals\": [", o.bench_warmup);
+        write_interval(out, 0, iv, true);
+        std::fprintf(out, "\n  ]\n}\n");
+        if (out != stdout) std::fclose(out);
+        return 0;
+    }
+    size_t next = 0;
+    auto one = [&](float *inner, float *outer) {
+        const int32_t tok = tokens[next];
+        next = (next + 1) % tokens.size();
+        if (gdn_run_teacher_forced(&rs, &tok, 1, 1, nullptr, inner, outer) != 0) die("benchmark step failed");
+    };
+    using clock = std::chrono::steady_clock;
+    const double idle_start = unix_now();
+    std::fprintf(stderr, "[benchmark] loaded-idle window %us\n", o.bench_idle_s);
+    std::this_thread::sleep_for(std::chrono::seconds(o.bench_idle_s));
+    const double warmup_start = unix_now();
+    uint64_t warmup_steps = 0;
+    for (const auto end = clock::now() + std::chrono::seconds(o.bench_warmup_s); clock::now() < end; ++warmup_steps)
+        one(nullptr, nullptr);
+    const double warmup_end = unix_now();
+    std::fprintf(stderr, "[benchmark] warmup complete steps=%llu\n", (unsigned long long)warmup_steps);
+    std::vector<Interval> intervals(o.bench_intervals);
+    for (uint32_t i = 0; i < o.bench_intervals; ++i) {
+        Interval &iv = intervals[i];
+        iv.start_unix = unix_now();
+        for (const auto end = clock::now() + std::chrono::seconds(o.bench_interval_s); clock::now() < end;) {
+            float inner = 0.0f, outer = 0.0f;
+            one(&inner, &outer);
+            iv.inner.push_back(inner);
+            iv.outer.push_back(outer);
+        }
+        iv.end_unix = unix_now();
+        std::fprintf(stderr, "[benchmark] interval %u/%u steps=%zu\n", i + 1, o.bench_intervals, iv.outer.size());
+    }
     FILE *out = open_output(o.output);
+    write_bench_header(out, o, tokens.size());
     std::fprintf(out,
-                 "{\n  \"schema\": \"gdn-steady-tpot-v1\",\n  \"weights\": \"%s\",\n  \"state\": \"%s\",\n"
-                 "  \"token_file\": \"%s\",\n  \"token_stream_length\": %zu,\n  \"teacher_forced\": true,\n"
-                 "  \"full_lm_head\": true,\n  \"onchip_argmax\": true,\n  \"full_logits_readback\": false,\n"
-                 "  \"contract\": \"%s\",\n  \"warmup_steps\": %u,\n  \"intervals\": [\n    {\"index\": 0, "
-                 "\"steps\": %u, \"tokens_per_second\": %.3f, \"production_tpot\": ",
-                 o.synth ? "synthetic" : o.weights.c_str(), o.state.c_str(), o.bench_tokens.c_str(), tokens.size(),
-                 contract_name(o.contract), o.bench_warmup, steps, 1000.0 * steps / wall);
-    write_summary(out, so);
-    std::fprintf(out, ", \"kernel\": ");
-    write_summary(out, si);
-    std::fprintf(out, "}\n  ]\n}\n");
+                 "  \"idle_start_unix\": %.6f,\n  \"warmup_start_unix\": %.6f,\n  \"warmup_end_unix\": %.6f,\n"
+                 "  \"warmup_steps\": %llu,\n  \"intervals\": [",
+                 idle_start, warmup_start, warmup_end, (unsigned long long)warmup_steps);
+    for (size_t i = 0; i < intervals.size(); ++i) write_interval(out, i, intervals[i], i == 0);
+    std::fprintf(out, "\n  ]\n}\n");
     if (out != stdout) std::fclose(out);
     return 0;
 }

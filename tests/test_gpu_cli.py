@@ -7,7 +7,8 @@ the same model stepped through the library in this process.
   against the first run's logits dump reports no exact mismatch and passes
   the vector gate.
 * the steady teacher-forced benchmark (host.cpp:2150-2256) reports every
-  step it was asked for.
+  step it was asked for; its timed protocol (idle window, timed warmup,
+  timed intervals) reports ordered windows and consistent rates.
 * rolling scoring (host.cpp:1943-2070) over a kind-3 fixture, with the model
   read from a .gdnw file, gives the log-likelihood of a blank-state
   teacher-forced run scored with float64 log-softmax in numpy.
@@ -151,6 +152,35 @@ def test_benchmark_mode(decoded):
         s = iv[k]
         assert 0 < s["min_ms"] <= s["median_ms"] <= s["p95_ms"] <= s["max_ms"]
     assert iv["kernel"]["median_ms"] <= iv["production_tpot"]["median_ms"]
+
+
+def test_benchmark_timed_protocol(decoded):
+    """The reference's timed protocol (host.cpp:2150-2256): a loaded-idle
+    window, a timed warmup, then timed intervals, each with its wall-clock
+    bounds and step summaries."""
+    d = decoded["dir"]
+    toks = d / "tokens_timed.txt"
+    toks.write_text(" ".join(str(t) for t in PROMPT) + "\n")
+    out = str(d / "bench_timed.json")
+    r = run_cli("--synth=1", out, "--decode-from-state", decoded["state"], "--benchmark-tokens", str(toks),
+                "--benchmark-idle-seconds", "1", "--benchmark-warmup-seconds", "1",
+                "--benchmark-interval-seconds", "1", "--benchmark-intervals", "2")
+    assert r.returncode == 0, r.stderr
+    res = json.load(open(out))
+    assert res["schema"] == "gdn-steady-tpot-v1" and res["warmup_steps"] > 0
+    assert res["warmup_start_unix"] - res["idle_start_unix"] >= 0.99
+    assert res["warmup_end_unix"] - res["warmup_start_unix"] >= 0.99
+    ivs = res["intervals"]
+    assert [iv["index"] for iv in ivs] == [0, 1]
+    prev_end = res["warmup_end_unix"]
+    for iv in ivs:
+        assert iv["start_unix"] >= prev_end and iv["end_unix"] - iv["start_unix"] >= 0.99
+        prev_end = iv["end_unix"]
+        assert iv["steps"] > 0
+        assert abs(iv["tokens_per_second"] - iv["steps"] / (iv["end_unix"] - iv["start_unix"])) < 1e-2 * iv["tokens_per_second"]
+        for k in ("production_tpot", "kernel"):
+            s = iv[k]
+            assert 0 < s["min_ms"] <= s["median_ms"] <= s["p95_ms"] <= s["max_ms"]
 
 
 def test_rolling_score_matches_library(model, tmp_path):
