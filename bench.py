@@ -6,7 +6,9 @@ vocab 32000, untied LM head), random-init BF16 weights N(0, 0.02) with norm
 weights = 1 (seed 0), in the bf16 arm (BF16 weights and operator boundaries,
 FP32 recurrent state).  A uniform-random prompt of --warmup tokens builds the
 state step by step (untimed); then --steps teacher-forced steps run over a
-fixed uniform-random 4096-token stream consumed cyclically.
+fixed uniform-random 4096-token stream consumed cyclically.  --contract fp32
+runs BASELINE config 4 (FP32 weights, activations and state) the same way,
+its GB/s taken at the FP32 byte count.
 
 One step = token id in on the host -> one captured hipGraph of 122 kernels
 -> argmax token id back on the host (the reference's "outer" boundary,
@@ -54,7 +56,7 @@ BYTES_PER_TOKEN = {
 # Algorithmic bytes per launch of each kernel kind (bf16 arm): weights at
 # BF16 plus the state / conv-tail traffic the kernel must move.
 KERNEL_BYTES = {
-    "qkvg": 4 * H * H * 2 + 2 * 8 * H * 4 + 3 * H * 4 * 4 + 3 * 3 * H * 2 * 2 + 2 * H * 2,
+    "qkvg": 4 * H * H * 2 + 2 * 8 * H * 2 + 3 * H * 4 * 4 + 3 * 3 * H * 2 * 2 + 2 * H * 2,
     "recur": 8 * 256 * 256 * 4 * 2,
     "o_proj": H * H * 2 + 256 * 2,
     "gate_up": 2 * I * H * 2 + H * 2,
@@ -64,13 +66,15 @@ KERNEL_BYTES = {
 }
 # DRAM bytes per launch (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy of
 # known size) from the counter passes summarised in
-# profiles/k_gemv_cu_gdn13b_bf16w_decode.md (bf16w_fp32s arm).  The
-# recurrence moves 2.1 MB more than its state: each 16-column workgroup
-# writes half of every 128-byte line, which the L2 fills before merging.
+# profiles/k_gemv_cu_gdn13b_bf16w_decode.md (bf16w_fp32s arm).  These are
+# constants from that profile, not measured by this run (the bench line says
+# so in roofline.traffic_source).
 MEASURED_TRAFFIC = {
-    "qkvg": 34_443_000, "recur": 6_528_000, "o_proj": 8_698_000, "gate_up": 46_667_000,
-    "down": 23_356_000, "lm_head": 136_507_000, "argmax": 7_000,
+    "qkvg": 34_361_000, "recur": 4_519_000, "o_proj": 8_708_000, "gate_up": 46_589_000,
+    "down": 23_379_000, "lm_head": 131_758_000, "argmax": 7_000,
 }
+TRAFFIC_SOURCE = ("rocprofv3 FETCH_SIZE + WRITE_SIZE passes, copy-calibrated "
+                  "(profiles/k_gemv_cu_gdn13b_bf16w_decode.md); a profile constant, not measured in this run")
 LAUNCHES_PER_TOKEN = {"qkvg": L, "recur": L, "o_proj": L, "gate_up": L, "down": L, "lm_head": 1, "argmax": 1}
 
 
@@ -208,8 +212,11 @@ def main():
         "dtype": "bf16" if contract != g.CONTRACT_FP32 else "fp32",
         "data": "synthetic (seeded random-init weights, uniform random token streams)",
         "config": {
-            "workload": "BASELINE config 3: GatedDeltaNet-1.3B decode, 24 layers, batch 1, "
-                        f"{args.warmup}-token uniform prompt then {args.steps} teacher-forced steps over a "
+            "workload": ("BASELINE config 4: GatedDeltaNet-1.3B decode with FP32 weights, activations and "
+                         "state (precision control arm; GB/s at double the weight bytes), 24 layers, batch 1, "
+                         if contract == g.CONTRACT_FP32 else
+                         "BASELINE config 3: GatedDeltaNet-1.3B decode, 24 layers, batch 1, ")
+                        + f"{args.warmup}-token uniform prompt then {args.steps} teacher-forced steps over a "
                         "fixed 4096-token uniform stream (cyclic), greedy argmax",
             "contract": args.contract,
             "state_dtype": "bf16" if contract == g.CONTRACT_REF else "fp32",
@@ -233,6 +240,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved_k / PEAK_HBM_GBPS, 4),
             "traffic": MEASURED_TRAFFIC[dom] if contract == g.CONTRACT_BF16W_FP32S else None,
+            "traffic_source": TRAFFIC_SOURCE if contract == g.CONTRACT_BF16W_FP32S else None,
             "algorithmic_bytes_per_launch": kb,
             "avg_launch_us": round(prof[dom], 3),
         },
