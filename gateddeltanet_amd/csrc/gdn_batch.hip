@@ -100,7 +100,7 @@ struct BEpi {
     float *qkv;          // EPI_QKVG: [64][3][kH] after conv + SiLU
     float *gate;         // [64][kH] R(g)
     float *sgate;        // [64][kH] sigmoid(R(g))
-    float *tails;        // this layer's [n_streams][3][3][kH]
+    uint16_t *tails;     // this layer's [n_streams][3][3][kH], BF16 bits (the values are BF16)
     const float *conv_w; // [3][kH][4]
     float *logits;       // EPI_LM: [64][N]
     float *part_val;     // [gridDim.x][64]
@@ -125,7 +125,13 @@ __global__ __launch_bounds__(NW * 64) void k_bgemm(const u32x4 *__restrict__ W, 
     __shared__ f32x4 red[NW * RT * 4 * 64];
     __shared__ float lm_v[RT * 4][64];
     __shared__ int lm_i[RT * 4][64];
-    const int t = threadIdx.x, w = t >> 6, l = t & 63, rb = blockIdx.x, sp = blockIdx.y;
+    // QKVG: consecutive row blocks on one XCD (workgroups are dealt to the 8
+    // XCDs round-robin), so the two 64-byte halves of a conv-tail line are
+    // fetched into one XCD's L2 once instead of into two
+    const int rb = (EPI == EPI_QKVG && (gridDim.x & 7) == 0)
+                       ? (int)((blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3))
+                       : (int)blockIdx.x;
+    const int t = threadIdx.x, w = t >> 6, l = t & 63, sp = blockIdx.y;
     const int kt0 = sp * KTS + w;
     const u32x4 *wp = W + ((size_t)rb * KT + kt0) * (RT * 64) + l;
     const u32x4 *xp = X + (size_t)kt0 * (4 * 64) + l;
@@ -142,8 +148,9 @@ __global__ __launch_bounds__(NW * 64) void k_bgemm(const u32x4 *__restrict__ W, 
             qtl[j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
             qcw[j] = qtl[j];
             if (which < 3 && m < ep.n_streams) {
-                const float *tl = ep.tails + ((size_t)m * 3 + which) * 3 * kH + c;
-                qtl[j] = (f32x4){tl[0], tl[kH], tl[2 * kH], 0.0f};
+                const uint16_t *tl = ep.tails + ((size_t)m * 3 + which) * 3 * kH + c;
+                qtl[j] = (f32x4){bf16_bits_to_f32(tl[0]), bf16_bits_to_f32(tl[kH]), bf16_bits_to_f32(tl[2 * kH]),
+                                 0.0f};
                 qcw[j] = *reinterpret_cast<const f32x4 *>(ep.conv_w + ((size_t)which * kH + c) * 4);
             }
         }
@@ -248,12 +255,12 @@ __global__ __launch_bounds__(NW * 64) void k_bgemm(const u32x4 *__restrict__ W, 
             const float raw = rne_bf16(reduced1(cl >> 4, (cl >> 2) & 3, m, cl & 3));
             if (which < 3) {
                 // gdn_depthwise_conv_silu_head_kind, gdn_model.cpp:1543-1667
-                float *tl = ep.tails + ((size_t)m * 3 + which) * 3 * kH + c;
+                uint16_t *tl = ep.tails + ((size_t)m * 3 + which) * 3 * kH + c;
                 const f32x4 tv = qtl[j], cw = qcw[j];
                 const float sum = tv.x * cw.x + tv.y * cw.y + tv.z * cw.z + raw * cw.w;
-                tl[0] = tv.y;
-                tl[kH] = tv.z;
-                tl[2 * kH] = raw;
+                tl[0] = bf16_hi(tv.y);
+                tl[kH] = bf16_hi(tv.z);
+                tl[2 * kH] = bf16_hi(raw);
                 ep.qkv[((size_t)m * 3 + which) * kH + c] = rne_bf16(silu_ref(sum));
             } else {
                 ep.gate[(size_t)m * kH + c] = raw;
@@ -751,7 +758,7 @@ __global__ __launch_bounds__(2 * CW) void k_brecur(const float *__restrict__ qkv
 // m's window is (s[m], s[m+1], s[m+2]) and its input s[m+3] in the sequence
 // s = tails ++ R(raw[0..n)); the new tails are s[n], s[n+1], s[n+2].
 constexpr int kConvT = 1024;  // threads per conv workgroup: 16 token lanes x 64 channels
-__global__ __launch_bounds__(kConvT) void k_pconv(const float *__restrict__ raw, int n, float *__restrict__ tails,
+__global__ __launch_bounds__(kConvT) void k_pconv(const float *__restrict__ raw, int n, uint16_t *__restrict__ tails,
                                                   const float *__restrict__ conv_w, float *__restrict__ qkv,
                                                   float *__restrict__ gate, float *__restrict__ sgate) {
     constexpr int MG = kConvT / 64;  // tokens in flight per channel
@@ -759,11 +766,11 @@ __global__ __launch_bounds__(kConvT) void k_pconv(const float *__restrict__ raw,
     const int row0 = blockIdx.x * 64, t = threadIdx.x, cl = t & 63, mg = t >> 6;
     const int row = row0 + cl, which = row0 / kH, c = row - which * kH;
     if (which < 3) {
-        float *tl = tails + (size_t)which * 3 * kH + c;
+        uint16_t *tl = tails + (size_t)which * 3 * kH + c;
         if (t < 64) {
-            xs[0][cl] = tl[0];
-            xs[1][cl] = tl[kH];
-            xs[2][cl] = tl[2 * kH];
+            xs[0][cl] = bf16_bits_to_f32(tl[0]);
+            xs[1][cl] = bf16_bits_to_f32(tl[kH]);
+            xs[2][cl] = bf16_bits_to_f32(tl[2 * kH]);
         }
         for (int m = mg; m < n; m += MG) xs[3 + m][cl] = rne_bf16(raw[(size_t)m * 4 * kH + row]);
         __syncthreads();
@@ -774,9 +781,9 @@ __global__ __launch_bounds__(kConvT) void k_pconv(const float *__restrict__ raw,
             qkv[((size_t)m * 3 + which) * kH + c] = rne_bf16(silu_ref(sum));
         }
         if (t < 64) {
-            tl[0] = xs[n][cl];
-            tl[kH] = xs[n + 1][cl];
-            tl[2 * kH] = xs[n + 2][cl];
+            tl[0] = bf16_hi(xs[n][cl]);
+            tl[kH] = bf16_hi(xs[n + 1][cl]);
+            tl[2 * kH] = bf16_hi(xs[n + 2][cl]);
         }
     } else {
         for (int m = mg; m < n; m += MG) {
@@ -952,7 +959,7 @@ struct GDNBatchEngine {
     uint16_t *emb = nullptr;
     float *aux = nullptr;      // [layers][kAuxLayer] + final_norm[kH]
     float *state = nullptr;    // [layers][streams][kNH][kHD][kHD]
-    float *tails = nullptr;    // [layers][streams][3][3][kH]
+    uint16_t *tails = nullptr; // [layers][streams][3][3][kH], BF16 bits
     float *act = nullptr;
     float *h = nullptr, *qkv = nullptr, *gate = nullptr, *sgate = nullptr, *bd = nullptr,
           *attn = nullptr, *ypart = nullptr, *xn = nullptr, *logits = nullptr, *part_val = nullptr;
@@ -974,7 +981,7 @@ struct GDNBatchEngine {
 namespace {
 
 float *b_aux(GDNBatchEngine *e, int l) { return e->aux + (size_t)l * kAuxLayer; }
-float *b_tails(GDNBatchEngine *e, int l) { return e->tails + (size_t)l * e->streams * kStreamTails; }
+uint16_t *b_tails(GDNBatchEngine *e, int l) { return e->tails + (size_t)l * e->streams * kStreamTails; }
 float *b_state(GDNBatchEngine *e, int l) { return e->state + (size_t)l * e->streams * kLayerState; }
 int lm_wgs(const GDNBatchEngine *e) { return e->vocab / 32; }
 
@@ -1104,8 +1111,8 @@ int b_alloc(GDNBatchEngine *e) {
     const size_t L = (size_t)e->layers, B = (size_t)e->streams, V = (size_t)e->vocab;
     GDN_HIP(hipMalloc(&e->state, L * B * kLayerState * 4));
     GDN_HIP(hipMemset(e->state, 0, L * B * kLayerState * 4));
-    GDN_HIP(hipMalloc(&e->tails, L * B * kStreamTails * 4));
-    GDN_HIP(hipMemset(e->tails, 0, L * B * kStreamTails * 4));
+    GDN_HIP(hipMalloc(&e->tails, L * B * kStreamTails * 2));
+    GDN_HIP(hipMemset(e->tails, 0, L * B * kStreamTails * 2));
     const size_t G = (size_t)lm_wgs(e);
     const size_t act = kMaxB * (2 * kH + 3 * kH + kH + kH + 16 + kH + kSplitDown * kH + kH + V) + G * kMaxB;
     GDN_HIP(hipMalloc(&e->act, act * 4));
@@ -1312,7 +1319,7 @@ void enqueue_prefill_chunk(GDNBatchEngine *e, int slot, int n, bool last, hipStr
     hipLaunchKernelGGL((k_bnorm<0, true, true>), dim3(n, kAbSplit), dim3(kT), 0, s, p0);
     for (int l = 0; l < e->layers; ++l) {
         float *st = b_state(e, l) + (size_t)slot * kLayerState;
-        float *tl = b_tails(e, l) + (size_t)slot * kStreamTails;
+        uint16_t *tl = b_tails(e, l) + (size_t)slot * kStreamTails;
         BEpi raw{};
         raw.n_streams = n;
         raw.n_rows = 4 * kH;
@@ -1438,6 +1445,36 @@ int stream_copy(float *dev, size_t per, int streams, int layers, uint32_t stream
     return 0;
 }
 
+// The conv tails of one stream: FP32 words on the host (the .gdnstate
+// section layout), BF16 bits on the device.  Loading requires BF16-exact
+// values, as the reference's head buffer does.
+int tails_copy(uint16_t *dev, int streams, int layers, uint32_t stream, float *host, bool to_dev) {
+    const size_t n = (size_t)layers * kStreamTails;
+    std::vector<uint16_t> bits(n);
+    const size_t width = kStreamTails * 2, dpitch = (size_t)streams * kStreamTails * 2;
+    uint16_t *d = dev + (size_t)stream * kStreamTails;
+    if (to_dev) {
+        const size_t bad = gdn_first_non_bf16(host, n);
+        if (bad != n) {
+            gdn_report_non_bf16("multi-stream conv tail", host, bad);
+            return -1;
+        }
+        for (size_t i = 0; i < n; ++i) {
+            uint32_t u;
+            std::memcpy(&u, host + i, 4);
+            bits[i] = (uint16_t)(u >> 16);
+        }
+        GDN_HIP(hipMemcpy2D(d, dpitch, bits.data(), width, width, (size_t)layers, hipMemcpyHostToDevice));
+    } else {
+        GDN_HIP(hipMemcpy2D(bits.data(), width, d, dpitch, width, (size_t)layers, hipMemcpyDeviceToHost));
+        for (size_t i = 0; i < n; ++i) {
+            const uint32_t u = (uint32_t)bits[i] << 16;
+            std::memcpy(host + i, &u, 4);
+        }
+    }
+    return 0;
+}
+
 }  // namespace
 
 // ================================================================== C ABI
@@ -1515,11 +1552,11 @@ int gdn_batch_load_stream_state(GDNBatchState *state, uint32_t stream, const flo
     if (!e || stream >= (uint32_t)e->streams) return -1;
     if (recurrent && recurrent_floats != (size_t)e->layers * kLayerState) return -1;
     if (conv_tails && conv_floats != (size_t)e->layers * kStreamTails) return -1;
+    // the tails first: they are checked (BF16-exact) before anything is written
+    if (conv_tails && tails_copy(e->tails, e->streams, e->layers, stream, const_cast<float *>(conv_tails), true))
+        return -1;
     if (recurrent && stream_copy(e->state, kLayerState, e->streams, e->layers, stream,
                                  const_cast<float *>(recurrent), true))
-        return -1;
-    if (conv_tails && stream_copy(e->tails, kStreamTails, e->streams, e->layers, stream,
-                                  const_cast<float *>(conv_tails), true))
         return -1;
     return 0;
 }
@@ -1531,8 +1568,7 @@ int gdn_batch_save_stream_state(const GDNBatchState *state, uint32_t stream, flo
     if (recurrent && recurrent_floats != (size_t)e->layers * kLayerState) return -1;
     if (conv_tails && conv_floats != (size_t)e->layers * kStreamTails) return -1;
     if (recurrent && stream_copy(e->state, kLayerState, e->streams, e->layers, stream, recurrent, false)) return -1;
-    if (conv_tails && stream_copy(e->tails, kStreamTails, e->streams, e->layers, stream, conv_tails, false))
-        return -1;
+    if (conv_tails && tails_copy(e->tails, e->streams, e->layers, stream, conv_tails, false)) return -1;
     return 0;
 }
 

@@ -74,6 +74,8 @@ __device__ __forceinline__ float R(float x) {
 }
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b16) { return u2f(b16 << 16); }
+// The BF16 bits of a BF16-valued float (its top half).
+__device__ __forceinline__ uint16_t bf16_hi(float x) { return (uint16_t)(f2u(x) >> 16); }
 
 // expf and log1pf as the reference's C library evaluates them (glibc 2.35,
 // gdn_libm.h): the engine's transcendentals equal the reference's bit for bit.

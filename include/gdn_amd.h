@@ -490,7 +490,9 @@ int gdn_batch_read_logits(const GDNBatchState *state, uint32_t stream, float *lo
 int gdn_batch_read_final_hidden(const GDNBatchState *state, uint32_t stream, float *hidden, size_t count);
 /* One stream's state in the .gdnstate section layouts (as
  * gdn_load_recurrent_state / gdn_load_conv_tails); either pointer may be
- * NULL.  Sizes must be the full per-stream sizes. */
+ * NULL.  Sizes must be the full per-stream sizes.  The conv tails are kept
+ * as BF16 on the device, so loaded tails must be BF16-exact (-1 otherwise,
+ * before anything is written). */
 int gdn_batch_load_stream_state(GDNBatchState *state, uint32_t stream, const float *recurrent,
                                 size_t recurrent_floats, const float *conv_tails, size_t conv_floats);
 int gdn_batch_save_stream_state(const GDNBatchState *state, uint32_t stream, float *recurrent,

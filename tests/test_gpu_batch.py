@@ -421,6 +421,26 @@ def test_prefill_one_hot_matches_batch1(onehot):
         bs.free()
 
 
+def test_load_rejects_non_bf16_tails(model):
+    """The device keeps each stream's conv tails as BF16: a tail value that
+    is not BF16-exact is refused before anything (tails or state) is
+    written."""
+    bs = g.BatchState(model, 2)
+    try:
+        rec0, conv0 = bs.save_stream_state(1)
+        conv = g.bf16_round(g.synth_normal(conv0.size, 41, 0, std=0.5))
+        conv[5] = np.float32(1.0 + 2.0 ** -10)  # needs 10 mantissa bits
+        with pytest.raises(g.GDNError):
+            bs.load_stream_state(1, rec0 + 1.0, conv)
+        rec, cv = bs.save_stream_state(1)
+        assert equal_values(rec, rec0) and equal_values(cv, conv0)
+        conv[5] = np.float32(1.0)
+        bs.load_stream_state(1, None, conv)
+        assert equal_values(bs.save_stream_state(1)[1], conv)
+    finally:
+        bs.free()
+
+
 def test_prefill_rejects_bad_tokens(model):
     bs = g.BatchState(model, 1)
     try:
