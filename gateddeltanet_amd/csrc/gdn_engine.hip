@@ -697,15 +697,16 @@ constexpr int kCuDown = 8;    // 2048 / 256
 constexpr int kCuLm = 125;    // 32000 / 256
 constexpr int kCuLmSmall = 8; // vocabularies that 125 does not divide
 // Items in flight per thread (16 = every item issued up front).  QKVG and
-// gate/up hold 6 items per thread, down 3; priming only 4, 3 and 2 of them
-// (the rest issued as products free their registers) measured 1 % faster
-// per token than priming all: fewer weight requests are queued chip-wide
-// when the activation reads go out.
+// gate/up hold 6 items per thread, down 3, the LM head 21.  With the
+// stream-order layout, priming 3 of QKVG's, 2 of gate/up's, all 3 of down's
+// and 3 of the LM head's measured 3 % faster per token than 4 / 3 / 2 / 2
+// (the best mix of the earlier layout); gate/up at 1, QKVG at 2 or 6 were
+// slower.
 constexpr int kDepthAll = 16;
-constexpr int kDepthQkvg = 4;
-constexpr int kDepthGu = 3;
-constexpr int kDepthDown = 2;
-constexpr int kDepthLm = 2;  // of 21 items per stream thread (3: 0.7 us per token slower)
+constexpr int kDepthQkvg = 3;
+constexpr int kDepthGu = 2;
+constexpr int kDepthDown = 3;
+constexpr int kDepthLm = 3;
 // Per contract: an FP32 item is 64 bytes (16 VGPRs), so the FP32 control
 // arm keeps fewer in flight within the same 128-VGPR budget.
 template <int C>
