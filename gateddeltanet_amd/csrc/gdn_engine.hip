@@ -762,7 +762,7 @@ __host__ __device__ constexpr size_t stream_piece(int f, int q, int items, int n
 // than DEPTH items in flight (a SIMD holds only about one wave's worth of
 // outstanding loads; a wave that asks for more stalls at issue and cannot
 // multiply the items it already has).
-template <int K, int ROWS, int C, int D, int T0>
+template <int K, int ROWS, int C, int D, int T0, bool NTL = true>
 struct WStream {
     static constexpr int NT = kTB - T0;  // stream threads
     static constexpr int HB = Hb<K>::HB;
@@ -781,8 +781,11 @@ struct WStream {
         if (kFull || u + NT * I < ITEMS) {
             constexpr int span = (kFull || I < NIT - 1) ? NT : ITEMS - NT * (NIT - 1);
 #pragma unroll
-            for (int q = 0; q < WPI; ++q)
-                v[I][q] = __builtin_nontemporal_load(wb + (size_t)NT * WPI * I + q * span + u);
+            for (int q = 0; q < WPI; ++q) {
+                const u32x4 *p = wb + (size_t)NT * WPI * I + q * span + u;
+                if constexpr (NTL) v[I][q] = __builtin_nontemporal_load(p);
+                else v[I][q] = *p;
+            }
         }
     }
 
@@ -945,7 +948,9 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     if constexpr (kActFirst) __builtin_amdgcn_s_barrier();
 
     // 2. the weight stream
-    WStream<K, ROWS, C, D, T0> ws;
+    // non-temporal weight loads, except in the LM head (measured: plain
+    // loads are 1-2 us faster there, and slower in every per-layer GEMV)
+    WStream<K, ROWS, C, D, T0, EPI != EPI_LM> ws;
     if (t >= T0) ws.prime(wblk);
 
     // QKVG extras, read behind the weight loads so they take no load-queue
