@@ -128,6 +128,8 @@ def main():
                     help="3: batch-1 decode (the headline); 5: --streams independent streams per step "
                          "(multi-stream engine, matrix-core projections)")
     ap.add_argument("--streams", type=int, default=64, help="streams per step for --config 5")
+    ap.add_argument("--prefill-mode", default="scan", choices=("scan", "chunked"),
+                    help="--prefill recurrence: token-order scan (bit-exact) or the chunked WY form")
     ap.add_argument("--prefill", type=int, default=0,
                     help="instead: time the on-device prefill of an N-token uniform prompt (the GPU prompt pass "
                          "that produces a .gdnstate) against N batch-1 decode steps")
@@ -365,6 +367,9 @@ def main_prefill(args):
     model = g.Model.synth(num_layers=L, seed=0, std=0.02, bf16=True)
     prompt = g.synth_tokens(n, 0, 1, V)
     bs = g.BatchState(model, 1)
+    chunked = args.prefill_mode == "chunked"
+    if chunked:
+        bs.set_prefill_mode(g.PREFILL_CHUNKED)
     bs.prefill(0, prompt[:min(n, 128)])  # warm
     sync()
     t0 = time.perf_counter()
@@ -398,7 +403,9 @@ def main_prefill(args):
         "dtype": "bf16",
         "data": "synthetic (seeded random-init weights, uniform random prompt)",
         "config": {"workload": f"{n}-token prompt through one stream, 24 layers, FP32 state, chunks of 64",
-                   "arithmetic": "the multi-stream step's, bit for bit"},
+                   "prefill_mode": args.prefill_mode,
+                   "arithmetic": ("the multi-stream step's, with the recurrence in the chunk-parallel (WY) form "
+                                  "(FP32 re-association)" if chunked else "the multi-stream step's, bit for bit")},
         "prefill_ms": round(pre_s * 1000.0, 2),
         "decode_steps_ms": round(dec_s * 1000.0, 2),
         "speedup_vs_decode_steps": round(dec_s / pre_s, 2),

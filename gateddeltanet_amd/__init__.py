@@ -10,6 +10,8 @@ from .engine import (  # noqa: F401
     CONTRACT_FP32,
     CONTRACT_REF,
     GDNError,
+    PREFILL_CHUNKED,
+    PREFILL_SCAN,
     Model,
     RunState,
     batch_gemm,

@@ -15,6 +15,8 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libgdn_amd.
 CONTRACT_REF = 0
 CONTRACT_BF16W_FP32S = 1
 CONTRACT_FP32 = 2
+PREFILL_SCAN = 0     # GDN_PREFILL_SCAN: the recurrence in token order (bit-exact to steps)
+PREFILL_CHUNKED = 1  # GDN_PREFILL_CHUNKED: the chunk-parallel (WY) form
 MAX_STREAMS = 64  # GDN_MAX_STREAMS
 CONTRACT_NAMES = {CONTRACT_REF: "ref", CONTRACT_BF16W_FP32S: "bf16w_fp32s", CONTRACT_FP32: "fp32"}
 
@@ -223,6 +225,7 @@ SIGNATURES = {
     "gdn_batch_save_stream_state": (c_int, [BP, c_uint32, FP, c_size_t, FP, c_size_t]),
     "gdn_batch_run_teacher_forced": (c_int, [BP, IP, c_uint32, IP, FP, FP]),
     "gdn_batch_prefill": (c_int, [BP, c_uint32, IP, c_uint32, IP]),
+    "gdn_batch_set_prefill_mode": (c_int, [BP, c_int]),
     "gdn_batch_profile_kernels": (c_int, [BP, c_uint32, FP, c_uint32]),
     "gdn_batch_set_graph_mode": (c_int, [BP, c_int]),
     "gdn_test_batch_gemm": (c_int, [FP, FP, c_uint32, c_uint32, FP]),

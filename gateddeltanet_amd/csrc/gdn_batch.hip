@@ -940,6 +940,291 @@ __global__ __launch_bounds__(kT) void k_pscan(const float *__restrict__ qkv, con
         *reinterpret_cast<float2 *>(Sw + (size_t)(4 * lane + i) * kHD) = make_float2(sv[0][i], sv[1][i]);
 }
 
+// ---------------------------------------------------- chunked prefill (WY form)
+//
+// The chunk's recurrence in the chunk-parallel form of the gated delta rule
+// (chunk.py:616-686 computes the same quantities with a WY representation).
+// With the state S (key row j, value column i) before the chunk, per-token
+// decay a_m, cumulative log decay G_m = sum_{s<=m} log a_m (so a_{s+1} ...
+// a_m = exp(G_m - G_s)), and normalised k_m, q_m:
+//   L[m][s]  = beta_m exp(G_m - G_s) (k_m . k_s)      s < m
+//   Mq[m][s] = exp(G_m - G_s) (q_m . k_s)             s <= m
+//   delta_m  = beta_m (v_m - exp(G_m) S^T k_m) - sum_{s<m} L[m][s] delta_s
+//   o_m      = (exp(G_m) S^T q_m + sum_{s<=m} Mq[m][s] delta_s) / 16
+//   S'       = exp(G_{n-1}) S + sum_s exp(G_{n-1} - G_s) k_s delta_s^T
+// which is the per-token recurrence of the decode step unrolled over the
+// chunk (delta_m is the step's beta (v - decay S_{m-1}^T k), o_m its
+// S_m^T q / 16).  The sums are associated differently from the step's
+// sequential chains, so this mode matches the scan within a tolerance, not
+// bit for bit; o is rounded to BF16 as the step rounds it.
+
+// L and Mq of one head for rows 4 blockIdx.y .. +3: grid (kNH, kMaxB / 4).
+constexpr int kKp = kHD / 4 + 1;  // padded float4 stride of a staged k/q row
+
+// The chunk's rows of one head ([token][kH] FP32, head h's 256 values),
+// held in registers between the load and the store into LDS rows of stride
+// kKp float4 (zeros from token n on).  The loads of every staged operand
+// are issued at the kernel's start, so their latencies overlap instead of
+// adding up.
+struct RowStage {
+    static constexpr int PER = kMaxB * (kHD / 4) / kT;
+    f32x4 v[PER];
+    __device__ __forceinline__ void load(const float *__restrict__ src, int h, int n) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int idx = threadIdx.x + kT * i, m = idx / (kHD / 4), j4 = idx % (kHD / 4);
+            v[i] = m < n ? *reinterpret_cast<const f32x4 *>(src + (size_t)m * kH + h * kHD + 4 * j4)
+                         : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
+    __device__ __forceinline__ void store(f32x4 (*rows)[kKp]) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int idx = threadIdx.x + kT * i;
+            rows[idx / (kHD / 4)][idx % (kHD / 4)] = v[i];
+        }
+    }
+};
+
+// One head's 64 x 64 matrix, stored into LDS rows of stride kMaxB + 4.
+struct MatStage {
+    static constexpr int PER = kMaxB * kMaxB / 4 / kT;
+    f32x4 v[PER];
+    __device__ __forceinline__ void load(const float *__restrict__ src) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) v[i] = reinterpret_cast<const f32x4 *>(src)[threadIdx.x + kT * i];
+    }
+    __device__ __forceinline__ void store(float (*dst)[kMaxB + 4]) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int q = threadIdx.x + kT * i;
+            *reinterpret_cast<f32x4 *>(&dst[q / (kMaxB / 4)][4 * (q % (kMaxB / 4))]) = v[i];
+        }
+    }
+};
+__device__ __forceinline__ float cum_log_decay(const float *__restrict__ bd, int h, int n, float *glog) {
+    // lanes 0..63 of wave 0: inclusive prefix sum of log(decay) over the chunk
+    const int lane = threadIdx.x;
+    // (a decay that underflowed to 0 is taken as 1e-30: the products it
+    // enters are 0 to FP32 either way, and G stays finite)
+    float v = lane < n ? __logf(fmaxf(bd[lane * 16 + 2 * h + 1], 1e-30f)) : 0.0f;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const float o = __shfl_up(v, d);
+        if (lane >= d) v += o;
+    }
+    glog[lane] = v;
+    return v;
+}
+
+__global__ __launch_bounds__(kT) void k_wy_gram(const float *__restrict__ qn_all, const float *__restrict__ kn_all,
+                                                const float *__restrict__ bd, int n, float *__restrict__ Lout,
+                                                float *__restrict__ Mout) {
+    __shared__ f32x4 ks[kMaxB][kKp];
+    __shared__ f32x4 qr[4][kHD / 4];
+    __shared__ float glog[kMaxB];
+    const int h = blockIdx.x, r0 = 4 * blockIdx.y, t = threadIdx.x;
+    RowStage kst;
+    kst.load(kn_all, h, n);
+    {
+        static_assert(4 * (kHD / 4) == kT, "one q float4 per thread");
+        const int r = t / (kHD / 4), j4 = t % (kHD / 4);
+        qr[r][j4] = (r0 + r < n) ? *reinterpret_cast<const f32x4 *>(qn_all + (size_t)(r0 + r) * kH + h * kHD + 4 * j4)
+                                 : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    kst.store(ks);
+    if (t < 64) cum_log_decay(bd, h, n, glog);
+    __syncthreads();
+    const int r = t >> 6, sidx = t & 63, m = r0 + r;
+    float lv = 0.0f, mv = 0.0f;
+    if (m < n && sidx <= m) {
+        f32x4 dk = {0.0f, 0.0f, 0.0f, 0.0f}, dq = dk;
+#pragma unroll 8
+        for (int j4 = 0; j4 < kHD / 4; ++j4) {
+            const f32x4 km = ks[m][j4], kv = ks[sidx][j4], qv = qr[r][j4];
+            dk += km * kv;
+            dq += qv * kv;
+        }
+        const float ratio = __expf(glog[m] - glog[sidx]);
+        const float gk = (dk.x + dk.y) + (dk.z + dk.w), gq = (dq.x + dq.y) + (dq.z + dq.w);
+        if (sidx < m) lv = bd[m * 16 + 2 * h] * ratio * gk;
+        mv = ratio * gq;
+    }
+    if (m < kMaxB) {
+        Lout[((size_t)h * kMaxB + m) * kMaxB + sidx] = lv;
+        Mout[((size_t)h * kMaxB + m) * kMaxB + sidx] = mv;
+    }
+}
+
+// One head's chunk for 16 state columns: grid (kHD / kWyCols, kNH), 256
+// threads.  The state tile (256 rows x 16 columns) is held one row per
+// thread; Q S and K S are formed from the staged rows (wave w takes key rows
+// 64 w .. 64 w + 63, partial sums added in wave order); the deltas are
+// solved row by row on each column's 16 lanes, which keep them in
+// registers; then o and the new state.
+constexpr int kWyCols = 16;
+
+// X (n x 256, staged rows) times the state tile S0 (256 x 16): thread
+// (wave jq, m block mb, column block cb) forms rows 4 mb .. +3, columns
+// 4 cb .. +3 over key rows 64 jq .. +63 into part[jq].
+__device__ __forceinline__ void wy_xs(const f32x4 (*rows)[kKp], const float (*s0)[kWyCols], float (*part)[kMaxB][kWyCols]) {
+    const int t = threadIdx.x, jq = t >> 6, mb = (t >> 2) & 15, cb = t & 3;
+    f32x4 acc[4] = {};
+#pragma unroll 4
+    for (int j4 = 0; j4 < 16; ++j4) {
+        const int jr = 16 * jq + j4;  // float4 index of key rows 4 jr .. 4 jr + 3
+        f32x4 xr[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xr[r] = rows[4 * mb + r][jr];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const f32x4 sr = *reinterpret_cast<const f32x4 *>(&s0[4 * jr + q][4 * cb]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] += xr[r][q] * sr;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) *reinterpret_cast<f32x4 *>(&part[jq][4 * mb + r][4 * cb]) = acc[r];
+}
+
+__global__ __launch_bounds__(kT) void k_wy_chunk(const float *__restrict__ qkv, const float *__restrict__ qn_all,
+                                                 const float *__restrict__ kn_all, const float *__restrict__ bd,
+                                                 const float *__restrict__ Lg, const float *__restrict__ Mg, int n,
+                                                 float *__restrict__ state, float *__restrict__ attn) {
+    __shared__ f32x4 rows[kMaxB][kKp];                             // Q, then K
+    __shared__ __attribute__((aligned(16))) float s0[kHD][kWyCols];  // the state tile
+    __shared__ __attribute__((aligned(16))) float lm[kMaxB][kMaxB + 4];  // L, then Mq
+    __shared__ __attribute__((aligned(16))) float part[4][kMaxB][kWyCols];
+    __shared__ float qs[kMaxB][kWyCols + 1];                        // S^T q
+    __shared__ __attribute__((aligned(16))) float dl[kMaxB][kWyCols];    // b, then delta
+    __shared__ float glog[kMaxB];
+    const int h = blockIdx.y, c0 = blockIdx.x * kWyCols, t = threadIdx.x, w = t >> 6, lane = t & 63;
+    float *S = state + (size_t)h * kHD * kHD + c0;
+    // every global operand is loaded up front (about 150 registers a
+    // thread; the workgroup is one wave per SIMD)
+    RowStage qst, kst;
+    MatStage lst, mst;
+    qst.load(qn_all, h, n);
+    lst.load(Lg + (size_t)h * kMaxB * kMaxB);
+    kst.load(kn_all, h, n);
+    mst.load(Mg + (size_t)h * kMaxB * kMaxB);
+    constexpr int VPER = kMaxB * kWyCols / kT;
+    float vv[VPER], beta[VPER];
+#pragma unroll
+    for (int k = 0; k < VPER; ++k) {
+        const int i = t + kT * k, m = i >> 4, c = i & 15;
+        vv[k] = m < n ? qkv[((size_t)m * 3 + 2) * kH + h * kHD + c0 + c] : 0.0f;
+        beta[k] = m < n ? bd[m * 16 + 2 * h] : 0.0f;
+    }
+    float sv[kWyCols];
+    {
+        const f32x4 *src = reinterpret_cast<const f32x4 *>(S + (size_t)t * kHD);
+#pragma unroll
+        for (int i = 0; i < kWyCols / 4; ++i) {
+            const f32x4 v = src[i];
+            sv[4 * i] = v.x; sv[4 * i + 1] = v.y; sv[4 * i + 2] = v.z; sv[4 * i + 3] = v.w;
+            *reinterpret_cast<f32x4 *>(&s0[t][4 * i]) = v;
+        }
+    }
+    qst.store(rows);
+    lst.store(lm);
+    if (t < 64) cum_log_decay(bd, h, n, glog);
+    __syncthreads();
+
+    // S^T q for every token
+    wy_xs(rows, s0, part);
+    __syncthreads();
+    for (int i = t; i < kMaxB * kWyCols; i += kT) {
+        const int m = i >> 4, c = i & 15;
+        qs[m][c] = ((part[0][m][c] + part[1][m][c]) + part[2][m][c]) + part[3][m][c];
+    }
+    kst.store(rows);
+    __syncthreads();
+    // S^T k for every token, then b_m = beta_m (v_m - exp(G_m) S^T k_m)
+    wy_xs(rows, s0, part);
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < VPER; ++k) {
+        const int i = t + kT * k, m = i >> 4, c = i & 15;
+        const float sk = ((part[0][m][c] + part[1][m][c]) + part[2][m][c]) + part[3][m][c];
+        dl[m][c] = m < n ? beta[k] * (vv[k] - __expf(glog[m]) * sk) : 0.0f;
+    }
+    __syncthreads();
+
+    // delta_m = b_m - sum_{s<m} L[m][s] delta_s: wave w solves columns
+    // 4 w .. 4 w + 3, lane (cl, p) keeps delta_s for s = p + 16 i
+    {
+        const int cl = lane >> 4, p = lane & 15, c = 4 * w + cl;
+        float dreg[kMaxB / 16] = {};
+        for (int m = 0; m < n; ++m) {
+            float part_sum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kMaxB / 16; ++i) {
+                const int sidx = p + 16 * i;
+                if (sidx < m) part_sum += lm[m][sidx] * dreg[i];
+            }
+            // the 16 lanes' sum on the DPP path (quad swaps, then the
+            // half-row and row mirrors), left in every lane of the row
+            part_sum += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(part_sum), 0xB1, 0xf, 0xf, false));
+            part_sum += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(part_sum), 0x4E, 0xf, 0xf, false));
+            part_sum += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(part_sum), 0x141, 0xf, 0xf, false));
+            part_sum += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(part_sum), 0x140, 0xf, 0xf, false));
+            const float delta = dl[m][c] - part_sum;
+#pragma unroll
+            for (int i = 0; i < kMaxB / 16; ++i)
+                if (m == p + 16 * i) dreg[i] = delta;
+        }
+#pragma unroll
+        for (int i = 0; i < kMaxB / 16; ++i) {
+            const int sidx = p + 16 * i;
+            if (sidx < n) dl[sidx][c] = dreg[i];
+        }
+    }
+    __syncthreads();
+    mst.store(lm);
+    __syncthreads();
+
+    // o_m = (exp(G_m) S^T q_m + sum_{s<=m} Mq[m][s] delta_s) / 16, rounded
+    // (Mq is zero above the diagonal and delta zero from row n on, so every
+    // row runs the full 64 terms, four independent partial sums)
+    for (int i = t; i < n * kWyCols; i += kT) {
+        const int m = i >> 4, c = i & 15;
+        f32x4 a4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s4 = 0; s4 < kMaxB / 4; ++s4) {
+            const f32x4 l4 = *reinterpret_cast<const f32x4 *>(&lm[m][4 * s4]);
+            const f32x4 d4 = {dl[4 * s4][c], dl[4 * s4 + 1][c], dl[4 * s4 + 2][c], dl[4 * s4 + 3][c]};
+            a4 += l4 * d4;
+        }
+        const float acc = __expf(glog[m]) * qs[m][c] + ((a4.x + a4.y) + (a4.z + a4.w));
+        attn[(size_t)m * kH + h * kHD + c0 + c] = rne_bf16(0.0625f * acc);
+    }
+
+    // S' = exp(G_{n-1}) S + sum_s exp(G_{n-1} - G_s) k_s delta_s^T, row t
+    const float gn = glog[n - 1];
+    float acc[kWyCols];
+    const float dn = __expf(gn);
+#pragma unroll
+    for (int c = 0; c < kWyCols; ++c) acc[c] = dn * sv[c];
+    const float *krow = reinterpret_cast<const float *>(&rows[0][0]);
+#pragma unroll 4
+    for (int sidx = 0; sidx < n; ++sidx) {
+        const float f = __expf(gn - glog[sidx]) * krow[sidx * (4 * kKp) + t];
+        const f32x4 *d4 = reinterpret_cast<const f32x4 *>(&dl[sidx][0]);
+#pragma unroll
+        for (int q = 0; q < kWyCols / 4; ++q) {
+            const f32x4 d = d4[q];
+            acc[4 * q] += f * d.x;
+            acc[4 * q + 1] += f * d.y;
+            acc[4 * q + 2] += f * d.z;
+            acc[4 * q + 3] += f * d.w;
+        }
+    }
+    f32x4 *dst = reinterpret_cast<f32x4 *>(S + (size_t)t * kHD);
+#pragma unroll
+    for (int i = 0; i < kWyCols / 4; ++i) dst[i] = (f32x4){acc[4 * i], acc[4 * i + 1], acc[4 * i + 2], acc[4 * i + 3]};
+}
+
 }  // namespace bt
 }  // namespace gdn
 
@@ -972,6 +1257,9 @@ struct GDNBatchEngine {
     // vectors and argmax tokens (per-token buffers of their own, so a
     // prefill leaves the other streams' last step readable)
     float *p_qn = nullptr, *p_kn = nullptr, *p_alpha = nullptr, *p_logits = nullptr, *p_xn = nullptr;
+    // chunked prefill: the chunk's L and Mq per head [kNH][64][64]
+    float *p_wyl = nullptr, *p_wym = nullptr;
+    int prefill_mode = GDN_PREFILL_SCAN;
     int *p_tok = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -1139,6 +1427,8 @@ int b_alloc(GDNBatchEngine *e) {
     GDN_HIP(hipMalloc(&e->p_qn, (size_t)kMaxB * kH * 4));
     GDN_HIP(hipMalloc(&e->p_kn, (size_t)kMaxB * kH * 4));
     GDN_HIP(hipMalloc(&e->p_alpha, (size_t)kMaxB * kNH * 4));
+    GDN_HIP(hipMalloc(&e->p_wyl, (size_t)kNH * kMaxB * kMaxB * 4));
+    GDN_HIP(hipMalloc(&e->p_wym, (size_t)kNH * kMaxB * kMaxB * 4));
     GDN_HIP(hipMalloc(&e->p_logits, (size_t)kMaxB * V * 4));
     GDN_HIP(hipMalloc(&e->p_xn, (size_t)kMaxB * kH * 4));
     GDN_HIP(hipMalloc(&e->p_tok, (size_t)kMaxB * sizeof(int)));
@@ -1329,8 +1619,15 @@ void enqueue_prefill_chunk(GDNBatchEngine *e, int slot, int n, bool last, hipStr
         hipLaunchKernelGGL(k_pconv, dim3(4 * kH / 64), dim3(kConvT), 0, s, e->ypart, n, tl, b_aux(e, l) + kAuxConv,
                            e->qkv, e->gate, e->sgate);
         hipLaunchKernelGGL(k_pqk, dim3(kNH, n), dim3(kT), 0, s, e->qkv, e->p_qn, e->p_kn, e->p_alpha);
-        hipLaunchKernelGGL(k_pscan, dim3(kHD / kScanWgCols, kNH), dim3(kT), 0, s, e->qkv, e->p_qn, e->p_kn,
-                           e->p_alpha, e->bd, n, st, e->attn);
+        if (e->prefill_mode == GDN_PREFILL_CHUNKED) {
+            hipLaunchKernelGGL(k_wy_gram, dim3(kNH, kMaxB / 4), dim3(kT), 0, s, e->p_qn, e->p_kn, e->bd, n,
+                               e->p_wyl, e->p_wym);
+            hipLaunchKernelGGL(k_wy_chunk, dim3(kHD / kWyCols, kNH), dim3(kT), 0, s, e->qkv, e->p_qn, e->p_kn, e->bd,
+                               e->p_wyl, e->p_wym, n, st, e->attn);
+        } else {
+            hipLaunchKernelGGL(k_pscan, dim3(kHD / kScanWgCols, kNH), dim3(kT), 0, s, e->qkv, e->p_qn, e->p_kn,
+                               e->p_alpha, e->bd, n, st, e->attn);
+        }
         hipLaunchKernelGGL(k_bonorm, dim3(kNH, n), dim3(kT), 0, s, e->attn, e->gate, e->sgate,
                            b_aux(e, l) + kAuxONorm, e->eps, e->x_o);
         BEpi eo{};
@@ -1422,6 +1719,8 @@ void b_destroy(GDNBatchEngine *e) {
     (void)hipFree(e->p_qn);
     (void)hipFree(e->p_kn);
     (void)hipFree(e->p_alpha);
+    (void)hipFree(e->p_wyl);
+    (void)hipFree(e->p_wym);
     (void)hipFree(e->p_logits);
     (void)hipFree(e->p_xn);
     (void)hipFree(e->p_tok);
@@ -1569,6 +1868,13 @@ int gdn_batch_save_stream_state(const GDNBatchState *state, uint32_t stream, flo
     if (conv_tails && conv_floats != (size_t)e->layers * kStreamTails) return -1;
     if (recurrent && stream_copy(e->state, kLayerState, e->streams, e->layers, stream, recurrent, false)) return -1;
     if (conv_tails && tails_copy(e->tails, e->streams, e->layers, stream, conv_tails, false)) return -1;
+    return 0;
+}
+
+int gdn_batch_set_prefill_mode(GDNBatchState *state, int mode) {
+    GDNBatchEngine *e = engine_of(state);
+    if (!e || (mode != GDN_PREFILL_SCAN && mode != GDN_PREFILL_CHUNKED)) return -1;
+    e->prefill_mode = mode;
     return 0;
 }
 

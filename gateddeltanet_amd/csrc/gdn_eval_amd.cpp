@@ -18,7 +18,7 @@
 //   gdn_eval_amd <weights.gdnw> <rolling.gdnreq> [output.json] --score
 //       [--score-doc-limit N]
 //   gdn_eval_amd <weights.gdnw> [output.json] --prefill <prompt.txt|ll.gdnreq>
-//       [--example N] --dump-state <out.gdnstate> [--round-bf16]
+//       [--example N] --dump-state <out.gdnstate> [--round-bf16] [--prefill-chunked]
 //
 // --prefill is the GPU prompt pass that produces a .gdnstate
 // (export_gdn_state.py:157-201, :290-366): the prompt (a whitespace token
@@ -27,6 +27,8 @@
 // of the last position (the seed token) are written as a .gdnstate.  The
 // state is the BF16W_FP32S arm's (FP32); --round-bf16 rounds it and the
 // tails to BF16 (RNE) once at the end, so the REF contract can load it.
+// --prefill-chunked runs the recurrence in the chunk-parallel (WY) form
+// (equal to the steps within FP32 re-association) instead of token order.
 //
 // Common options: --contract ref|bf16w|fp32 (default ref, the reference's
 // all-BF16 arithmetic), --synth[=LAYERS] in place of a weights file (the
@@ -72,7 +74,7 @@ struct Options {
     // the timed benchmark protocol, with the reference's defaults (host.cpp:208-211)
     uint32_t bench_idle_s = 60, bench_warmup_s = 30, bench_interval_s = 60, bench_intervals = 3;
     uint32_t example = 0;
-    bool synth = false, host_check = true, score = false, round_bf16 = false;
+    bool synth = false, host_check = true, score = false, round_bf16 = false, prefill_chunked = false;
     int contract = GDN_CONTRACT_REF;
 };
 
@@ -113,6 +115,7 @@ Options parse(int argc, char **argv) {
             o.bench_intervals = parse_u32(next("--benchmark-intervals"), "--benchmark-intervals");
         else if (a == "--score") o.score = true;
         else if (a == "--prefill") o.prefill = next("--prefill");
+        else if (a == "--prefill-chunked") o.prefill_chunked = true;
         else if (a == "--example") o.example = parse_u32(next("--example"), "--example");
         else if (a == "--round-bf16") o.round_bf16 = true;
         else if (a == "--score-doc-limit") o.score_limit = parse_u32(next("--score-doc-limit"), "--score-doc-limit");
@@ -136,7 +139,7 @@ Options parse(int argc, char **argv) {
                 "[--benchmark-intervals N]   (or a fixed count: [--benchmark-steps N] [--benchmark-warmup N])\n"
                 "  gdn_eval_amd <weights|--synth[=L]> <rolling.gdnreq> [out.json] --score [--score-doc-limit N]\n"
                 "  gdn_eval_amd <weights|--synth[=L]> [out.json] --prefill <prompt.txt|ll.gdnreq> [--example N] "
-                "--dump-state S [--round-bf16]\n"
+                "--dump-state S [--round-bf16] [--prefill-chunked]\n"
                 "  common: --contract ref|bf16w|fp32\n");
             std::exit(0);
         } else if (!a.empty() && a[0] == '-') {
@@ -626,6 +629,7 @@ int run_prefill(const Options &o, const Fixture *fx, const GDNModel &model) {
     std::fprintf(stderr, "[progress] prefill of %zu tokens\n", prompt.size());
     int32_t seed = 0;
     const double t0 = now_ms();
+    if (o.prefill_chunked && gdn_batch_set_prefill_mode(&bs, GDN_PREFILL_CHUNKED) != 0) die("prefill mode");
     if (gdn_batch_prefill(&bs, 0, prompt.data(), (uint32_t)prompt.size(), &seed) != 0) die("prefill failed");
     const double ms = now_ms() - t0;
     const size_t rec = (size_t)c.num_layers * c.num_heads * c.head_dim * c.head_dim;

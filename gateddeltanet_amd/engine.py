@@ -19,6 +19,8 @@ from . import _lib as L
 CONTRACT_REF = L.CONTRACT_REF
 CONTRACT_BF16W_FP32S = L.CONTRACT_BF16W_FP32S
 CONTRACT_FP32 = L.CONTRACT_FP32
+PREFILL_SCAN = L.PREFILL_SCAN
+PREFILL_CHUNKED = L.PREFILL_CHUNKED
 
 LAYER_TENSORS = (
     "attn_norm", "a_log", "dt_bias", "q_proj", "k_proj", "v_proj", "a_proj", "b_proj",
@@ -301,6 +303,10 @@ class BatchState:
         seed = np.zeros(1, np.int32)
         _check(L.load().gdn_batch_prefill(self.ptr, stream, iptr(p), p.size, iptr(seed)), "gdn_batch_prefill")
         return int(seed[0])
+
+    def set_prefill_mode(self, mode: int) -> None:
+        """gdn_batch_set_prefill_mode: PREFILL_SCAN (default) or PREFILL_CHUNKED."""
+        _check(L.load().gdn_batch_set_prefill_mode(self.ptr, mode), "gdn_batch_set_prefill_mode")
 
     def logits(self, stream: int) -> np.ndarray:
         out = np.empty(self.model.config.vocab_size, np.float32)

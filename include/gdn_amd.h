@@ -502,11 +502,19 @@ int gdn_batch_save_stream_state(const GDNBatchState *state, uint32_t stream, flo
  * GPU prompt pass that produces a .gdnstate, export_gdn_state.py:157-201,
  * :325-330),
  * in chunks of 64 tokens: token-parallel projections on the matrix cores, the
- * causal conv across the chunk, the recurrence in token order with the state
- * held on chip.  Results equal the steps bit for bit.  *seed_token (may be
- * NULL) receives the argmax of the last position; that position's logits and
- * final hidden vector become the stream's readable ones.  Other streams'
- * states are untouched. */
+ * causal conv across the chunk, and the recurrence -- by default in token
+ * order with the state held on chip, so results equal the steps bit for
+ * bit; in GDN_PREFILL_CHUNKED mode in the chunk-parallel (WY) form of the
+ * gated delta rule (chunk.py:616-686), equal to the steps within FP32
+ * re-association.  *seed_token (may be NULL) receives the argmax of the last
+ * position; that position's logits and final hidden vector become the
+ * stream's readable ones.  Other streams' states are untouched. */
+#define GDN_PREFILL_SCAN 0
+#define GDN_PREFILL_CHUNKED 1
+/* Selects the prefill's recurrence (GDN_PREFILL_SCAN by default).  No
+ * reference counterpart: the reference's GPU prefill is the chunked form
+ * only, its C++ decode the scan's arithmetic. */
+int gdn_batch_set_prefill_mode(GDNBatchState *state, int mode);
 int gdn_batch_prefill(GDNBatchState *state, uint32_t stream, const int32_t *prompt, uint32_t n_tokens,
                       int32_t *seed_token);
 /* n_steps steps with tokens[step][n_streams] fed; per-step argmax

@@ -536,3 +536,97 @@ def test_prefill_random_model_against_exact_product_oracle(orc):
           flush=True)
     assert err <= LOGIT_TOL and check_argmax(logits_ref, seed_ref, seed, err)
     assert rel <= 1e-2 and np.linalg.norm(conv - cv) <= 1e-2 * np.linalg.norm(cv)
+
+
+# ---------------------------------------------------------- chunked prefill
+
+def _rel(a, b):
+    return float(np.linalg.norm(np.asarray(a, np.float64) - b) / np.linalg.norm(np.asarray(b, np.float64)))
+
+
+@pytest.mark.parametrize("n", [1, 8, 64, 150])
+def test_prefill_chunked_recurrence_precision(n):
+    """The chunk-parallel (WY) recurrence against the token-order scan where
+    nothing else differs: after one layer the two modes have the same q, k,
+    v, beta and decay, so the state differs only by the FP32
+    re-association of the recurrence's sums (measured 1.1e-6 relative L2 at
+    n = 64).  Bound: 1e-5."""
+    m = g.Model.synth(num_layers=1, seed=0, std=0.02, bf16=True)
+    prompt = g.synth_tokens(n, 61, 0)
+    bs = g.BatchState(m, 2)
+    try:
+        bs.prefill(0, prompt)
+        rec_scan, conv_scan = bs.save_stream_state(0)
+        bs.set_prefill_mode(g.PREFILL_CHUNKED)
+        bs.prefill(1, prompt)
+        rec, conv = bs.save_stream_state(1)
+    finally:
+        bs.free()
+        m.free()
+    rel = _rel(rec, rec_scan)
+    print(f"[prefill chunked] 1 layer, n={n}: state rel-L2 vs scan {rel:.3e}", flush=True)
+    assert rel <= 1e-5 and same_bits(conv, conv_scan)
+
+
+@pytest.mark.parametrize("n", [64, 150])
+def test_prefill_chunked_full_model_against_scan(model, n):
+    """Over the 24-layer random model the re-association flips occasional
+    BF16 roundings of o, which the later layers amplify, as for the
+    multi-stream projections' summation order.  Measured at n = 64: last
+    logits max-abs 0.125, state relative L2 3.0e-2.  Bounds: logits max-abs
+    <= 0.25, state relative L2 <= 5e-2, seed equal or a near tie."""
+    prompt = g.synth_tokens(n, 61, 0)
+    bs = g.BatchState(model, 2)
+    try:
+        seed_scan = bs.prefill(0, prompt)
+        logits_scan = bs.logits(0)
+        rec_scan, _ = bs.save_stream_state(0)
+        bs.set_prefill_mode(g.PREFILL_CHUNKED)
+        seed = bs.prefill(1, prompt)
+        logits = bs.logits(1)
+        rec, _ = bs.save_stream_state(1)
+    finally:
+        bs.free()
+    err = float(np.abs(logits - logits_scan).max())
+    rel = _rel(rec, rec_scan)
+    print(f"[prefill chunked] 24 layers, n={n} vs scan: logits max-abs {err:.3e}, state rel-L2 {rel:.3e}, "
+          f"seed {seed} vs {seed_scan}", flush=True)
+    assert err <= 0.25 and rel <= 5e-2 and check_argmax(logits_scan, seed_scan, seed, err)
+
+
+def test_prefill_chunked_against_exact_product_oracle(orc):
+    """The chunked prefill on a random 2-layer model against ORC_BF16X
+    stepped token by token (70 tokens, two chunks): the projections' and the
+    recurrence's summation orders are the differences.  Bounds: last logits
+    max-abs <= 5e-2 (seed equal or a near tie), state and conv tails within
+    1e-2 relative L2."""
+    m = g.Model.synth(num_layers=2, seed=4, std=0.02, bf16=True)
+    hdr = orc.header_from(m.config)
+    prompt = g.synth_tokens(70, 50, 0)
+    st = np.zeros(2 * 8 * 256 * 256, np.float32)
+    cv = np.zeros(2 * 3 * 3 * 2048, np.float32)
+    for t in prompt:
+        seed_ref, logits_ref, _ = orc.decode_step(orc.BF16X, hdr, m.blob, st, cv, int(t), orc.LIBM)
+    bs = g.BatchState(m, 1)
+    try:
+        bs.set_prefill_mode(g.PREFILL_CHUNKED)
+        seed = bs.prefill(0, prompt)
+        err = float(np.abs(bs.logits(0) - logits_ref).max())
+        rec, conv = bs.save_stream_state(0)
+    finally:
+        bs.free()
+        m.free()
+    rel = _rel(rec, st)
+    print(f"[prefill chunked] 2 layers x 70 tokens vs ORC_BF16X: logits max-abs {err:.3e}, "
+          f"state rel-L2 {rel:.3e}", flush=True)
+    assert err <= 5e-2 and check_argmax(logits_ref, seed_ref, seed, err)
+    assert rel <= 1e-2 and _rel(conv, cv) <= 1e-2
+
+
+def test_prefill_mode_rejects_unknown(model):
+    bs = g.BatchState(model, 1)
+    try:
+        with pytest.raises(g.GDNError):
+            bs.set_prefill_mode(7)
+    finally:
+        bs.free()

@@ -287,3 +287,24 @@ def test_prefill_mode_writes_the_stepped_state(model, tmp_path):
                 "--contract", "bf16w")
     assert r.returncode == 0, r.stderr
     assert json.load(open(tmp_path / "d.json"))["examples"][0]["gen_traj"][0] == seed
+
+
+def test_prefill_chunked_mode_matches_library(model, tmp_path):
+    """--prefill-chunked writes what the library's chunked prefill leaves
+    (same kernels, so bit for bit), over a prompt that ends mid-chunk."""
+    prompt = [int(t) for t in g.synth_tokens(150, 51, 0)]
+    ptxt = tmp_path / "prompt.txt"
+    ptxt.write_text(" ".join(map(str, prompt)) + "\n")
+    st, out = str(tmp_path / "c.gdnstate"), str(tmp_path / "c.json")
+    r = run_cli("--synth=1", out, "--prefill", str(ptxt), "--dump-state", st, "--prefill-chunked")
+    assert r.returncode == 0, r.stderr
+    v, got_prompt, rec, conv = read_gdnstate(st)
+    bs = g.BatchState(model, 1)
+    try:
+        bs.set_prefill_mode(g.PREFILL_CHUNKED)
+        seed = bs.prefill(0, prompt)
+        rec_ref, conv_ref = bs.save_stream_state(0)
+    finally:
+        bs.free()
+    assert json.load(open(out))["seed_token"] == seed == v[8] and got_prompt == prompt
+    assert same_bits(rec, rec_ref) and same_bits(conv, conv_ref)
