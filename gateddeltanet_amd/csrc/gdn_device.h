@@ -97,6 +97,19 @@ struct Exp2Fill {
         if (threadIdx.x < 32) lds[threadIdx.x] = v;
     }
 };
+// The same table written into LDS by threads 0..31 from immediates: no
+// memory load, so no wait on the vector memory counter (which, in a GEMV's
+// prologue waves, also counts their stores and could not be counted
+// exactly across the prologue's branches).
+__device__ __forceinline__ void fill_exp2_lds_imm(uint64_t *lds) {
+    if (threadIdx.x < 32) {
+        uint64_t v = 0;
+#pragma unroll
+        for (int i = 0; i < 32; ++i)
+            if (threadIdx.x == (unsigned)i) v = gdn_libm::exp2_table(i);
+        lds[threadIdx.x] = v;
+    }
+}
 
 template <class Tab = Exp2Const>
 __device__ __forceinline__ float exp_ref(float x, const Tab &tab = Tab()) { return gdn_libm::gdn_expf_t(x, tab); }

@@ -908,6 +908,9 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     __shared__ uint32_t red[8];
     __shared__ float ybuf[ROWS];
     __shared__ float abpart[Hb<kH>::HB];
+    // expf's table for the epilogue's SiLU / sigmoid (QKVG, gate/up)
+    constexpr bool kExpTab = EPI == EPI_QKVG || EPI == EPI_SWIGLU;
+    __shared__ uint64_t exp2_lds[kExpTab ? 32 : 1];
     // claim the whole register file (128 VGPRs x 16 waves): one workgroup per CU
     asm volatile("" ::: "v127");
     const int t = threadIdx.x, wave = t >> 6;
@@ -945,17 +948,11 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
 #pragma unroll
         for (int q = 0; q < ABW; ++q) abw[q] = src4[q];
     }
-    if constexpr (kActFirst) __builtin_amdgcn_s_barrier();
-
-    // 2. the weight stream
-    // non-temporal weight loads, except in the LM head (measured: plain
-    // loads are 1-2 us faster there, and slower in every per-layer GEMV)
-    WStream<K, ROWS, C, D, T0, EPI != EPI_LM> ws;
-    if (t >= T0) ws.prime(wblk);
-
-    // QKVG extras, read behind the weight loads so they take no load-queue
-    // slot ahead of the stream: the conv tails and taps of each q/k/v row
-    // (its owner lane)
+    // QKVG extras, read with the activations, ahead of the weight stream:
+    // the conv tails and taps of each q/k/v row (its owner lane).  (Read
+    // behind the weight loads, they returned after the CU's first weight
+    // items, and the compiler's wait for the tails, placed where it widens
+    // them, held the prologue waves 0..1 back by about 2 us.)
     const bool owner = wave < CHW && (t & 3) == 0 && (t >> 2) < CR;
     uint16_t tail_b[3] = {0, 0, 0};        // BF16 contracts: the tails' BF16 bits
     float tail_f[3] = {0.0f, 0.0f, 0.0f};  // FP32 contract: FP32 tails
@@ -979,11 +976,32 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
         }
     }
 
+    if constexpr (kActFirst) __builtin_amdgcn_s_barrier();
+
+    // 2. the weight stream
+    // non-temporal weight loads, except in the LM head (measured: plain
+    // loads are 1-2 us faster there, and slower in every per-layer GEMV)
+    WStream<K, ROWS, C, D, T0, EPI != EPI_LM> ws;
+    if (t >= T0) ws.prime(wblk);
+
     // 3. the input vector in LDS and the fast-path verdict: waves 0..3 build
     // it (synchronising only among themselves); the other waves, once their
-    // loads are issued, wait for the prologue's last arrival
+    // loads are issued, wait for the prologue's last arrival.
+    // 4. the products, in each branch (waves 0..3 take part in gate/up and
+    // down).  Where the two branches met before the products, the
+    // compiler's wait for a stream wave's first item became a wait for all
+    // of its primed items (the prologue branch holds stores and loads whose
+    // count it cannot follow); inside the branch it waits item by item.
+    const auto products = [&](bool f) __attribute__((always_inline)) {
+        if (f) ws.template run<true>(xs, part);
+        else ws.template run<false>(xs, part);
+    };
     bool fast;
     if (t < kT) {
+        // the epilogue's expf table into LDS (a lookup in global memory at
+        // the epilogue costs a memory round trip on the kernel's serial
+        // tail); the products' barrier makes it visible
+        if constexpr (kExpTab) fill_exp2_lds_imm(exp2_lds);
         Wave4Sync sync{&arrive, src.err};
         if constexpr (BF) fast = pro.finish_bf16(src, wi, xs, scratch, bcast, red, sync);
         else fast = pro.finish_fp32(src, reinterpret_cast<float *>(xs), scratch, bcast, sync);
@@ -1024,6 +1042,7 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
                 }
             }
         }
+        if constexpr (!kActFirst) products(fast);
     } else {
         if constexpr (BF) {
             wait_count(&arrive, 4 * Prologue<C, K, PRO>::kSyncs, src.err);
@@ -1032,18 +1051,7 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
             wait_count(&arrive, 4 * Prologue<C, K, PRO>::kSyncsFp32, src.err);
             fast = false;
         }
-    }
-    // the product-counter copy of the GEMV input (debug: off in the timed
-    // path, where xdump is null); xs is complete for every wave here
-    if (src.xdump != nullptr && blockIdx.x == 0) {
-        for (int i = t; i < K; i += kTB) src.xdump[i] = xs[i];
-        if (t == 0) src.xdump[K] = fast ? 1u : 0u;
-    }
-
-    // 4. products, barrier, bank chains and the row epilogue
-    if (t >= T0) {
-        if (fast) ws.template run<true>(xs, part);
-        else ws.template run<false>(xs, part);
+        products(fast);
     }
     __syncthreads();
     if (wave < CHW) {
@@ -1080,11 +1088,11 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
                         tl[2 * kH + ch] = yv;
                     }
                     const float s = t0 * taps.x + t1 * taps.y + t2 * taps.z + yv * taps.w;
-                    conv_out = R<C>(silu_ref(s));
+                    conv_out = R<C>(silu_ref(s, Exp2Lds{exp2_lds}));
                     ep.y[r] = conv_out;
                 } else {
                     ep.y2[r - 3 * kH] = yv;
-                    ep.y3[r - 3 * kH] = sigmoid_ref(yv);
+                    ep.y3[r - 3 * kH] = sigmoid_ref(yv, Exp2Lds{exp2_lds});
                 }
             } else if constexpr (EPI == EPI_SWIGLU) {
                 ybuf[rr] = R<C>(y);
@@ -1121,36 +1129,48 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
         __syncthreads();
         if (t < ROWS / 2) {
             const float g = ybuf[t], u = ybuf[t + ROWS / 2];
-            ep.y[blockIdx.x * (ROWS / 2) + t] = R<C>(silu_ref(g) * u);
+            ep.y[blockIdx.x * (ROWS / 2) + t] = R<C>(silu_ref(g, Exp2Lds{exp2_lds}) * u);
         }
     } else if constexpr (EPI == EPI_LM) {
         // the workgroup's argmax in row order: strict '>' within a lane's
         // rows, then a merge that keeps the larger value and, on ties, the
         // lower index (NaN never wins)
         __syncthreads();
-        if (wave != 0) return;
-        float best = -3.402823466e38f;
-        int idx = 0;
-        for (int i = t; i < ROWS; i += 64) {
-            const float v = ybuf[i];
-            if (v > best) {
-                best = v;
-                idx = row0 + i;
+        if (wave == 0) {
+            float best = -3.402823466e38f;
+            int idx = 0;
+            for (int i = t; i < ROWS; i += 64) {
+                const float v = ybuf[i];
+                if (v > best) {
+                    best = v;
+                    idx = row0 + i;
+                }
             }
-        }
 #pragma unroll
-        for (int m = 1; m < 64; m <<= 1) {
-            const float ov = __shfl_xor(best, m);
-            const int oi = __shfl_xor(idx, m);
-            if (ov > best || (ov == best && oi < idx)) {
-                best = ov;
-                idx = oi;
+            for (int m = 1; m < 64; m <<= 1) {
+                const float ov = __shfl_xor(best, m);
+                const int oi = __shfl_xor(idx, m);
+                if (ov > best || (ov == best && oi < idx)) {
+                    best = ov;
+                    idx = oi;
+                }
+            }
+            if (t == 0) {
+                ep.part_val[blockIdx.x] = best;
+                ep.part_idx[blockIdx.x] = idx;
             }
         }
-        if (t == 0) {
-            ep.part_val[blockIdx.x] = best;
-            ep.part_idx[blockIdx.x] = idx;
-        }
+    }
+
+    // the product-counter copy of the GEMV input (debug: off in the timed
+    // path, where xdump is null); xs is unchanged since the prologue.  At
+    // the end, because the compiler cannot count this loop's stores: any
+    // load whose value is used after it would wait for every outstanding
+    // memory operation of the wave (earlier, that held the stream waves'
+    // first products until all their primed items had arrived).
+    if (src.xdump != nullptr && blockIdx.x == 0) {
+        for (int i = t; i < K; i += kTB) src.xdump[i] = xs[i];
+        if (t == 0) src.xdump[K] = fast ? 1u : 0u;
     }
 }
 
