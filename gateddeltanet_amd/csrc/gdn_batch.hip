@@ -1065,8 +1065,11 @@ __global__ __launch_bounds__(kT) void k_wy_gram(const float *__restrict__ qn_all
 constexpr int kWyCols = 16;
 
 // X (n x 256, staged rows) times the state tile S0 (256 x 16): thread
-// (wave jq, m block mb, column block cb) forms rows 4 mb .. +3, columns
-// 4 cb .. +3 over key rows 64 jq .. +63 into part[jq].
+// (wave jq, m block mb, column block cb) forms rows mb + 16 r (r = 0..3),
+// columns 4 cb .. +3 over key rows 64 jq .. +63 into part[jq].  A wave's 16
+// row blocks read 16 consecutive staged rows (odd float4 stride kKp), so
+// their 16-byte reads fall on distinct bank groups.  Fused multiply-adds:
+// this form is held to a tolerance, not to the step's rounding.
 __device__ __forceinline__ void wy_xs(const f32x4 (*rows)[kKp], const float (*s0)[kWyCols], float (*part)[kMaxB][kWyCols]) {
     const int t = threadIdx.x, jq = t >> 6, mb = (t >> 2) & 15, cb = t & 3;
     f32x4 acc[4] = {};
@@ -1075,16 +1078,21 @@ __device__ __forceinline__ void wy_xs(const f32x4 (*rows)[kKp], const float (*s0
         const int jr = 16 * jq + j4;  // float4 index of key rows 4 jr .. 4 jr + 3
         f32x4 xr[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) xr[r] = rows[4 * mb + r][jr];
+        for (int r = 0; r < 4; ++r) xr[r] = rows[mb + 16 * r][jr];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const f32x4 sr = *reinterpret_cast<const f32x4 *>(&s0[4 * jr + q][4 * cb]);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] += xr[r][q] * sr;
+            for (int r = 0; r < 4; ++r) {
+                acc[r].x = __builtin_fmaf(xr[r][q], sr.x, acc[r].x);
+                acc[r].y = __builtin_fmaf(xr[r][q], sr.y, acc[r].y);
+                acc[r].z = __builtin_fmaf(xr[r][q], sr.z, acc[r].z);
+                acc[r].w = __builtin_fmaf(xr[r][q], sr.w, acc[r].w);
+            }
         }
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) *reinterpret_cast<f32x4 *>(&part[jq][4 * mb + r][4 * cb]) = acc[r];
+    for (int r = 0; r < 4; ++r) *reinterpret_cast<f32x4 *>(&part[jq][mb + 16 * r][4 * cb]) = acc[r];
 }
 
 __global__ __launch_bounds__(kT) void k_wy_chunk(const float *__restrict__ qkv, const float *__restrict__ qn_all,
@@ -1097,7 +1105,7 @@ __global__ __launch_bounds__(kT) void k_wy_chunk(const float *__restrict__ qkv, 
     __shared__ __attribute__((aligned(16))) float part[4][kMaxB][kWyCols];
     __shared__ float qs[kMaxB][kWyCols + 1];                        // S^T q
     __shared__ __attribute__((aligned(16))) float dl[kMaxB][kWyCols];    // b, then delta
-    __shared__ float glog[kMaxB];
+    __shared__ float glog[kMaxB], fdec[kMaxB];
     const int h = blockIdx.y, c0 = blockIdx.x * kWyCols, t = threadIdx.x, w = t >> 6, lane = t & 63;
     float *S = state + (size_t)h * kHD * kHD + c0;
     // every global operand is loaded up front (about 150 registers a
@@ -1152,36 +1160,46 @@ __global__ __launch_bounds__(kT) void k_wy_chunk(const float *__restrict__ qkv, 
     __syncthreads();
 
     // delta_m = b_m - sum_{s<m} L[m][s] delta_s: wave w solves columns
-    // 4 w .. 4 w + 3, lane (cl, p) keeps delta_s for s = p + 16 i
+    // 4 w .. 4 w + 3; lane m holds row m of L in registers and, per column,
+    // b_m and the running sum of L[m][s] delta_s.  Step s takes delta_s =
+    // b_s - sum from lane s (a uniform read) and folds L[m][s] delta_s into
+    // every row; L is strictly lower triangular, so rows at or above s add
+    // zero and each lane's b - sum ends as its delta.  The four columns'
+    // chains interleave, and no step waits on LDS.  (16 lanes per column
+    // summing their terms on the DPP path took 8.6 us per chunk; 8 lanes
+    // on two waves 22.7 us.)
     {
-        const int cl = lane >> 4, p = lane & 15, c = 4 * w + cl;
-        float dreg[kMaxB / 16] = {};
-        for (int m = 0; m < n; ++m) {
-            float part_sum = 0.0f;
+        float lrow[kMaxB];
 #pragma unroll
-            for (int i = 0; i < kMaxB / 16; ++i) {
-                const int sidx = p + 16 * i;
-                if (sidx < m) part_sum += lm[m][sidx] * dreg[i];
-            }
-            // the 16 lanes' sum on the DPP path (quad swaps, then the
-            // half-row and row mirrors), left in every lane of the row
-            part_sum += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(part_sum), 0xB1, 0xf, 0xf, false));
-            part_sum += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(part_sum), 0x4E, 0xf, 0xf, false));
-            part_sum += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(part_sum), 0x141, 0xf, 0xf, false));
-            part_sum += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(part_sum), 0x140, 0xf, 0xf, false));
-            const float delta = dl[m][c] - part_sum;
-#pragma unroll
-            for (int i = 0; i < kMaxB / 16; ++i)
-                if (m == p + 16 * i) dreg[i] = delta;
+        for (int s4 = 0; s4 < kMaxB / 4; ++s4) {
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(&lm[lane][4 * s4]);
+            lrow[4 * s4] = v.x;
+            lrow[4 * s4 + 1] = v.y;
+            lrow[4 * s4 + 2] = v.z;
+            lrow[4 * s4 + 3] = v.w;
         }
+        float bq[4], acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int i = 0; i < kMaxB / 16; ++i) {
-            const int sidx = p + 16 * i;
-            if (sidx < n) dl[sidx][c] = dreg[i];
+        for (int j = 0; j < 4; ++j) bq[j] = dl[lane][4 * w + j];
+#pragma unroll
+        for (int sidx = 0; sidx < kMaxB; ++sidx) {
+            if (sidx < n) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float d = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(bq[j] - acc[j]), sidx));
+                    acc[j] = __builtin_fmaf(lrow[sidx], d, acc[j]);
+                }
+            }
+        }
+        if (lane < n) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dl[lane][4 * w + j] = bq[j] - acc[j];
         }
     }
     __syncthreads();
     mst.store(lm);
+    // the state update's decay factors exp(G_{n-1} - G_s)
+    if (t < kMaxB) fdec[t] = __expf(glog[n - 1] - glog[t]);
     __syncthreads();
 
     // o_m = (exp(G_m) S^T q_m + sum_{s<=m} Mq[m][s] delta_s) / 16, rounded
@@ -1193,8 +1211,10 @@ __global__ __launch_bounds__(kT) void k_wy_chunk(const float *__restrict__ qkv, 
 #pragma unroll
         for (int s4 = 0; s4 < kMaxB / 4; ++s4) {
             const f32x4 l4 = *reinterpret_cast<const f32x4 *>(&lm[m][4 * s4]);
-            const f32x4 d4 = {dl[4 * s4][c], dl[4 * s4 + 1][c], dl[4 * s4 + 2][c], dl[4 * s4 + 3][c]};
-            a4 += l4 * d4;
+            a4.x = __builtin_fmaf(l4.x, dl[4 * s4][c], a4.x);
+            a4.y = __builtin_fmaf(l4.y, dl[4 * s4 + 1][c], a4.y);
+            a4.z = __builtin_fmaf(l4.z, dl[4 * s4 + 2][c], a4.z);
+            a4.w = __builtin_fmaf(l4.w, dl[4 * s4 + 3][c], a4.w);
         }
         const float acc = __expf(glog[m]) * qs[m][c] + ((a4.x + a4.y) + (a4.z + a4.w));
         attn[(size_t)m * kH + h * kHD + c0 + c] = rne_bf16(0.0625f * acc);
@@ -1207,17 +1227,17 @@ __global__ __launch_bounds__(kT) void k_wy_chunk(const float *__restrict__ qkv, 
 #pragma unroll
     for (int c = 0; c < kWyCols; ++c) acc[c] = dn * sv[c];
     const float *krow = reinterpret_cast<const float *>(&rows[0][0]);
-#pragma unroll 4
+#pragma unroll 8
     for (int sidx = 0; sidx < n; ++sidx) {
-        const float f = __expf(gn - glog[sidx]) * krow[sidx * (4 * kKp) + t];
+        const float f = fdec[sidx] * krow[sidx * (4 * kKp) + t];
         const f32x4 *d4 = reinterpret_cast<const f32x4 *>(&dl[sidx][0]);
 #pragma unroll
         for (int q = 0; q < kWyCols / 4; ++q) {
             const f32x4 d = d4[q];
-            acc[4 * q] += f * d.x;
-            acc[4 * q + 1] += f * d.y;
-            acc[4 * q + 2] += f * d.z;
-            acc[4 * q + 3] += f * d.w;
+            acc[4 * q] = __builtin_fmaf(f, d.x, acc[4 * q]);
+            acc[4 * q + 1] = __builtin_fmaf(f, d.y, acc[4 * q + 1]);
+            acc[4 * q + 2] = __builtin_fmaf(f, d.z, acc[4 * q + 2]);
+            acc[4 * q + 3] = __builtin_fmaf(f, d.w, acc[4 * q + 3]);
         }
     }
     f32x4 *dst = reinterpret_cast<f32x4 *>(S + (size_t)t * kHD);
