@@ -1057,105 +1057,103 @@ __global__ __launch_bounds__(kT) void k_wy_gram(const float *__restrict__ qn_all
 }
 
 // One head's chunk for 16 state columns: grid (kHD / kWyCols, kNH), 256
-// threads.  The state tile (256 rows x 16 columns) is held one row per
-// thread; Q S and K S are formed from the staged rows (wave w takes key rows
-// 64 w .. 64 w + 63, partial sums added in wave order); the deltas are
-// solved row by row on each column's 16 lanes, which keep them in
-// registers; then o and the new state.
+// threads.  The matrix products run on v_mfma_f32_16x16x4_f32 (FP32
+// operands and sums; this form is held to a tolerance, not to the step's
+// rounding): Q S and K S (wave w: rows 16 w .. +15 of the chunk, all 256
+// keys), o (wave w: rows 16 w .. +15) and the state update (wave w: state
+// rows 64 w .. +63).  An MFMA takes A[i][k] from lane i + 16 k and
+// B[k][j] from lane j + 16 k and leaves D[4 (l / 16) + r][l % 16] in
+// component r of lane l.  A lane reads 4 consecutive k values of its row
+// (or column) in one 16-byte LDS read and feeds them to 4 MFMAs, component
+// q to the q-th, so MFMA q of a group sums the k = 4 (4 g + kk) + q; A and B
+// use the same assignment.  The deltas are solved with row m of L and each
+// column's b_m in lane m of one wave.
 constexpr int kWyCols = 16;
-
-// X (n x 256, staged rows) times the state tile S0 (256 x 16): thread
-// (wave jq, m block mb, column block cb) forms rows mb + 16 r (r = 0..3),
-// columns 4 cb .. +3 over key rows 64 jq .. +63 into part[jq].  A wave's 16
-// row blocks read 16 consecutive staged rows (odd float4 stride kKp), so
-// their 16-byte reads fall on distinct bank groups.  Fused multiply-adds:
-// this form is held to a tolerance, not to the step's rounding.
-__device__ __forceinline__ void wy_xs(const f32x4 (*rows)[kKp], const float (*s0)[kWyCols], float (*part)[kMaxB][kWyCols]) {
-    const int t = threadIdx.x, jq = t >> 6, mb = (t >> 2) & 15, cb = t & 3;
-    f32x4 acc[4] = {};
-#pragma unroll 4
-    for (int j4 = 0; j4 < 16; ++j4) {
-        const int jr = 16 * jq + j4;  // float4 index of key rows 4 jr .. 4 jr + 3
-        f32x4 xr[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) xr[r] = rows[mb + 16 * r][jr];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const f32x4 sr = *reinterpret_cast<const f32x4 *>(&s0[4 * jr + q][4 * cb]);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                acc[r].x = __builtin_fmaf(xr[r][q], sr.x, acc[r].x);
-                acc[r].y = __builtin_fmaf(xr[r][q], sr.y, acc[r].y);
-                acc[r].z = __builtin_fmaf(xr[r][q], sr.z, acc[r].z);
-                acc[r].w = __builtin_fmaf(xr[r][q], sr.w, acc[r].w);
-            }
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) *reinterpret_cast<f32x4 *>(&part[jq][mb + 16 * r][4 * cb]) = acc[r];
-}
+constexpr int kS0p = kHD + 4;    // padded key stride of the transposed state tile
+constexpr int kDtp = kMaxB + 4;  // padded token stride of the transposed deltas
 
 __global__ __launch_bounds__(kT) void k_wy_chunk(const float *__restrict__ qkv, const float *__restrict__ qn_all,
                                                  const float *__restrict__ kn_all, const float *__restrict__ bd,
                                                  const float *__restrict__ Lg, const float *__restrict__ Mg, int n,
                                                  float *__restrict__ state, float *__restrict__ attn) {
-    __shared__ f32x4 rows[kMaxB][kKp];                             // Q, then K
-    __shared__ __attribute__((aligned(16))) float s0[kHD][kWyCols];  // the state tile
+    __shared__ f32x4 rows[kMaxB][kKp];                                   // Q, then K
+    __shared__ __attribute__((aligned(16))) float s0t[kWyCols][kS0p];    // state tile, [column][key]
     __shared__ __attribute__((aligned(16))) float lm[kMaxB][kMaxB + 4];  // L, then Mq
-    __shared__ __attribute__((aligned(16))) float part[4][kMaxB][kWyCols];
-    __shared__ float qs[kMaxB][kWyCols + 1];                        // S^T q
+    __shared__ float qs[kMaxB][kWyCols + 1];                             // S^T q
     __shared__ __attribute__((aligned(16))) float dl[kMaxB][kWyCols];    // b, then delta
+    __shared__ __attribute__((aligned(16))) float dlt[kWyCols][kDtp];    // delta, [column][token]
+    __shared__ __attribute__((aligned(16))) float dft[kWyCols][kDtp];    // exp(G_{n-1} - G_s) delta_s
     __shared__ float glog[kMaxB], fdec[kMaxB];
     const int h = blockIdx.y, c0 = blockIdx.x * kWyCols, t = threadIdx.x, w = t >> 6, lane = t & 63;
+    const int li = lane & 15, kk = lane >> 4;  // MFMA operand row/column, k quarter
     float *S = state + (size_t)h * kHD * kHD + c0;
-    // every global operand is loaded up front (about 150 registers a
-    // thread; the workgroup is one wave per SIMD)
+    // every global operand is loaded up front (the workgroup is one wave
+    // per SIMD)
     RowStage qst, kst;
     MatStage lst, mst;
     qst.load(qn_all, h, n);
     lst.load(Lg + (size_t)h * kMaxB * kMaxB);
     kst.load(kn_all, h, n);
     mst.load(Mg + (size_t)h * kMaxB * kMaxB);
-    constexpr int VPER = kMaxB * kWyCols / kT;
-    float vv[VPER], beta[VPER];
+    // v and beta of this lane's D elements of K S: rows 16 w + 4 kk + r, column li
+    float vv[4], beta[4];
 #pragma unroll
-    for (int k = 0; k < VPER; ++k) {
-        const int i = t + kT * k, m = i >> 4, c = i & 15;
-        vv[k] = m < n ? qkv[((size_t)m * 3 + 2) * kH + h * kHD + c0 + c] : 0.0f;
-        beta[k] = m < n ? bd[m * 16 + 2 * h] : 0.0f;
+    for (int r = 0; r < 4; ++r) {
+        const int m = 16 * w + 4 * kk + r;
+        vv[r] = m < n ? qkv[((size_t)m * 3 + 2) * kH + h * kHD + c0 + li] : 0.0f;
+        beta[r] = m < n ? bd[m * 16 + 2 * h] : 0.0f;
     }
-    float sv[kWyCols];
     {
         const f32x4 *src = reinterpret_cast<const f32x4 *>(S + (size_t)t * kHD);
+        f32x4 v[kWyCols / 4];
+#pragma unroll
+        for (int i = 0; i < kWyCols / 4; ++i) v[i] = src[i];
 #pragma unroll
         for (int i = 0; i < kWyCols / 4; ++i) {
-            const f32x4 v = src[i];
-            sv[4 * i] = v.x; sv[4 * i + 1] = v.y; sv[4 * i + 2] = v.z; sv[4 * i + 3] = v.w;
-            *reinterpret_cast<f32x4 *>(&s0[t][4 * i]) = v;
+            s0t[4 * i][t] = v[i].x;
+            s0t[4 * i + 1][t] = v[i].y;
+            s0t[4 * i + 2][t] = v[i].z;
+            s0t[4 * i + 3][t] = v[i].w;
         }
     }
     qst.store(rows);
     lst.store(lm);
     if (t < 64) cum_log_decay(bd, h, n, glog);
     __syncthreads();
+    if (t < kMaxB) fdec[t] = __expf(glog[n - 1] - glog[t]);
+
+    // X S for the staged rows X (Q, then K): rows 16 w .. +15, 256 keys
+    const auto xs_mfma = [&]() __attribute__((always_inline)) {
+        f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
+#pragma unroll
+        for (int g = 0; g < kHD / 16; ++g) {
+            const f32x4 xa = rows[16 * w + li][4 * g + kk];
+            const f32x4 xb = *reinterpret_cast<const f32x4 *>(&s0t[li][16 * g + 4 * kk]);
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.x, xb.x, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.y, xb.y, acc1, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.z, xb.z, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.w, xb.w, acc1, 0, 0, 0);
+        }
+        return acc0 + acc1;
+    };
 
     // S^T q for every token
-    wy_xs(rows, s0, part);
-    __syncthreads();
-    for (int i = t; i < kMaxB * kWyCols; i += kT) {
-        const int m = i >> 4, c = i & 15;
-        qs[m][c] = ((part[0][m][c] + part[1][m][c]) + part[2][m][c]) + part[3][m][c];
+    {
+        const f32x4 d = xs_mfma();
+#pragma unroll
+        for (int r = 0; r < 4; ++r) qs[16 * w + 4 * kk + r][li] = d[r];
     }
+    __syncthreads();
     kst.store(rows);
     __syncthreads();
     // S^T k for every token, then b_m = beta_m (v_m - exp(G_m) S^T k_m)
-    wy_xs(rows, s0, part);
-    __syncthreads();
+    {
+        const f32x4 d = xs_mfma();
 #pragma unroll
-    for (int k = 0; k < VPER; ++k) {
-        const int i = t + kT * k, m = i >> 4, c = i & 15;
-        const float sk = ((part[0][m][c] + part[1][m][c]) + part[2][m][c]) + part[3][m][c];
-        dl[m][c] = m < n ? beta[k] * (vv[k] - __expf(glog[m]) * sk) : 0.0f;
+        for (int r = 0; r < 4; ++r) {
+            const int m = 16 * w + 4 * kk + r;
+            dl[m][li] = m < n ? beta[r] * (vv[r] - __expf(glog[m]) * d[r]) : 0.0f;
+        }
     }
     __syncthreads();
 
@@ -1163,11 +1161,11 @@ __global__ __launch_bounds__(kT) void k_wy_chunk(const float *__restrict__ qkv, 
     // 4 w .. 4 w + 3; lane m holds row m of L in registers and, per column,
     // b_m and the running sum of L[m][s] delta_s.  Step s takes delta_s =
     // b_s - sum from lane s (a uniform read) and folds L[m][s] delta_s into
-    // every row; L is strictly lower triangular, so rows at or above s add
-    // zero and each lane's b - sum ends as its delta.  The four columns'
-    // chains interleave, and no step waits on LDS.  (16 lanes per column
-    // summing their terms on the DPP path took 8.6 us per chunk; 8 lanes
-    // on two waves 22.7 us.)
+    // every row; L is strictly lower triangular (and zero from row n on), so
+    // rows at or above s add zero and each lane's b - sum ends as its delta.
+    // The four columns' chains interleave, and no step waits on LDS.  (16
+    // lanes per column summing their terms on the DPP path took 8.6 us per
+    // chunk; 8 lanes on two waves 22.7 us.)
     {
         float lrow[kMaxB];
 #pragma unroll
@@ -1191,58 +1189,73 @@ __global__ __launch_bounds__(kT) void k_wy_chunk(const float *__restrict__ qkv, 
                 }
             }
         }
-        if (lane < n) {
+        // every lane: its delta (zero from row n on), transposed for the
+        // MFMA B operands, and scaled by its decay for the state update
+        const float fd = fdec[lane];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) dl[lane][4 * w + j] = bq[j] - acc[j];
+        for (int j = 0; j < 4; ++j) {
+            const float d = bq[j] - acc[j];
+            dlt[4 * w + j][lane] = d;
+            dft[4 * w + j][lane] = fd * d;
         }
     }
     __syncthreads();
     mst.store(lm);
-    // the state update's decay factors exp(G_{n-1} - G_s)
-    if (t < kMaxB) fdec[t] = __expf(glog[n - 1] - glog[t]);
     __syncthreads();
 
-    // o_m = (exp(G_m) S^T q_m + sum_{s<=m} Mq[m][s] delta_s) / 16, rounded
-    // (Mq is zero above the diagonal and delta zero from row n on, so every
-    // row runs the full 64 terms, four independent partial sums)
-    for (int i = t; i < n * kWyCols; i += kT) {
-        const int m = i >> 4, c = i & 15;
-        f32x4 a4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    // o_m = (exp(G_m) S^T q_m + sum_{s<=m} Mq[m][s] delta_s) / 16, rounded:
+    // rows 16 w .. +15
+    {
+        f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
 #pragma unroll
-        for (int s4 = 0; s4 < kMaxB / 4; ++s4) {
-            const f32x4 l4 = *reinterpret_cast<const f32x4 *>(&lm[m][4 * s4]);
-            a4.x = __builtin_fmaf(l4.x, dl[4 * s4][c], a4.x);
-            a4.y = __builtin_fmaf(l4.y, dl[4 * s4 + 1][c], a4.y);
-            a4.z = __builtin_fmaf(l4.z, dl[4 * s4 + 2][c], a4.z);
-            a4.w = __builtin_fmaf(l4.w, dl[4 * s4 + 3][c], a4.w);
+        for (int g = 0; g < kMaxB / 16; ++g) {
+            const f32x4 xa = *reinterpret_cast<const f32x4 *>(&lm[16 * w + li][16 * g + 4 * kk]);
+            const f32x4 xb = *reinterpret_cast<const f32x4 *>(&dlt[li][16 * g + 4 * kk]);
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.x, xb.x, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.y, xb.y, acc1, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.z, xb.z, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.w, xb.w, acc1, 0, 0, 0);
         }
-        const float acc = __expf(glog[m]) * qs[m][c] + ((a4.x + a4.y) + (a4.z + a4.w));
-        attn[(size_t)m * kH + h * kHD + c0 + c] = rne_bf16(0.0625f * acc);
+        const f32x4 d = acc0 + acc1;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = 16 * w + 4 * kk + r;
+            if (m < n) {
+                const float o = __expf(glog[m]) * qs[m][li] + d[r];
+                attn[(size_t)m * kH + h * kHD + c0 + li] = rne_bf16(0.0625f * o);
+            }
+        }
     }
 
-    // S' = exp(G_{n-1}) S + sum_s exp(G_{n-1} - G_s) k_s delta_s^T, row t
-    const float gn = glog[n - 1];
-    float acc[kWyCols];
-    const float dn = __expf(gn);
+    // S' = exp(G_{n-1}) S + sum_s exp(G_{n-1} - G_s) k_s delta_s^T: state
+    // rows 64 w .. +63 as four 16-row tiles; A[j][s] = k_s[j] (token rows
+    // of the staged K), B[s][c] = exp(G_{n-1} - G_s) delta_s[c]
+    {
+        const float dn = __expf(glog[n - 1]);
+        const float *krow = reinterpret_cast<const float *>(&rows[0][0]);
 #pragma unroll
-    for (int c = 0; c < kWyCols; ++c) acc[c] = dn * sv[c];
-    const float *krow = reinterpret_cast<const float *>(&rows[0][0]);
-#pragma unroll 8
-    for (int sidx = 0; sidx < n; ++sidx) {
-        const float f = fdec[sidx] * krow[sidx * (4 * kKp) + t];
-        const f32x4 *d4 = reinterpret_cast<const f32x4 *>(&dl[sidx][0]);
+        for (int tile = 0; tile < 4; ++tile) {
+            const int j0 = 64 * w + 16 * tile;
+            f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
 #pragma unroll
-        for (int q = 0; q < kWyCols / 4; ++q) {
-            const f32x4 d = d4[q];
-            acc[4 * q] = __builtin_fmaf(f, d.x, acc[4 * q]);
-            acc[4 * q + 1] = __builtin_fmaf(f, d.y, acc[4 * q + 1]);
-            acc[4 * q + 2] = __builtin_fmaf(f, d.z, acc[4 * q + 2]);
-            acc[4 * q + 3] = __builtin_fmaf(f, d.w, acc[4 * q + 3]);
+            for (int g = 0; g < kMaxB / 16; ++g) {
+                const int sb = 16 * g + 4 * kk;  // this lane's 4 tokens
+                const f32x4 xb = *reinterpret_cast<const f32x4 *>(&dft[li][sb]);
+                const float a0 = krow[(sb + 0) * (4 * kKp) + j0 + li];
+                const float a1 = krow[(sb + 1) * (4 * kKp) + j0 + li];
+                const float a2 = krow[(sb + 2) * (4 * kKp) + j0 + li];
+                const float a3 = krow[(sb + 3) * (4 * kKp) + j0 + li];
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, xb.x, acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, xb.y, acc1, 0, 0, 0);
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a2, xb.z, acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a3, xb.w, acc1, 0, 0, 0);
+            }
+            const f32x4 d = acc0 + acc1;
+            const f32x4 sv = *reinterpret_cast<const f32x4 *>(&s0t[li][j0 + 4 * kk]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) S[(size_t)(j0 + 4 * kk + r) * kHD + li] = __builtin_fmaf(dn, sv[r], d[r]);
         }
     }
-    f32x4 *dst = reinterpret_cast<f32x4 *>(S + (size_t)t * kHD);
-#pragma unroll
-    for (int i = 0; i < kWyCols / 4; ++i) dst[i] = (f32x4){acc[4 * i], acc[4 * i + 1], acc[4 * i + 2], acc[4 * i + 3]};
 }
 
 }  // namespace bt
