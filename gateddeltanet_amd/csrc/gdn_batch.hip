@@ -958,7 +958,7 @@ __global__ __launch_bounds__(kT) void k_pscan(const float *__restrict__ qkv, con
 // sequential chains, so this mode matches the scan within a tolerance, not
 // bit for bit; o is rounded to BF16 as the step rounds it.
 
-// L and Mq of one head for rows 4 blockIdx.y .. +3: grid (kNH, kMaxB / 4).
+// L and Mq of one head for rows 16 blockIdx.y .. +15: grid (kNH, kMaxB / 16).
 constexpr int kKp = kHD / 4 + 1;  // padded float4 stride of a staged k/q row
 
 // The chunk's rows of one head ([token][kH] FP32, head h's 256 values),
@@ -1021,36 +1021,60 @@ __global__ __launch_bounds__(kT) void k_wy_gram(const float *__restrict__ qn_all
                                                 const float *__restrict__ bd, int n, float *__restrict__ Lout,
                                                 float *__restrict__ Mout) {
     __shared__ f32x4 ks[kMaxB][kKp];
-    __shared__ f32x4 qr[4][kHD / 4];
+    __shared__ f32x4 qr[16][kKp];
     __shared__ float glog[kMaxB];
-    const int h = blockIdx.x, r0 = 4 * blockIdx.y, t = threadIdx.x;
+    const int h = blockIdx.x, r0 = 16 * blockIdx.y, t = threadIdx.x, w = t >> 6, lane = t & 63;
+    const int li = lane & 15, kk = lane >> 4;
     RowStage kst;
     kst.load(kn_all, h, n);
     {
-        static_assert(4 * (kHD / 4) == kT, "one q float4 per thread");
-        const int r = t / (kHD / 4), j4 = t % (kHD / 4);
-        qr[r][j4] = (r0 + r < n) ? *reinterpret_cast<const f32x4 *>(qn_all + (size_t)(r0 + r) * kH + h * kHD + 4 * j4)
-                                 : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        // this block's 16 q rows (zeros from token n on)
+        constexpr int PER = 16 * (kHD / 4) / kT;
+        f32x4 v[PER];
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int idx = t + kT * i, r = idx / (kHD / 4), j4 = idx % (kHD / 4);
+            v[i] = (r0 + r < n) ? *reinterpret_cast<const f32x4 *>(qn_all + (size_t)(r0 + r) * kH + h * kHD + 4 * j4)
+                                : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int idx = t + kT * i;
+            qr[idx / (kHD / 4)][idx % (kHD / 4)] = v[i];
+        }
     }
     kst.store(ks);
     if (t < 64) cum_log_decay(bd, h, n, glog);
     __syncthreads();
-    const int r = t >> 6, sidx = t & 63, m = r0 + r;
-    float lv = 0.0f, mv = 0.0f;
-    if (m < n && sidx <= m) {
-        f32x4 dk = {0.0f, 0.0f, 0.0f, 0.0f}, dq = dk;
-#pragma unroll 8
-        for (int j4 = 0; j4 < kHD / 4; ++j4) {
-            const f32x4 km = ks[m][j4], kv = ks[sidx][j4], qv = qr[r][j4];
-            dk += km * kv;
-            dq += qv * kv;
-        }
-        const float ratio = __expf(glog[m] - glog[sidx]);
-        const float gk = (dk.x + dk.y) + (dk.z + dk.w), gq = (dq.x + dq.y) + (dq.z + dq.w);
-        if (sidx < m) lv = bd[m * 16 + 2 * h] * ratio * gk;
-        mv = ratio * gq;
+    // wave w: columns s = 16 w .. +15 of rows r0 .. r0 + 15: K_m . K_s and
+    // Q_m . K_s on v_mfma_f32_16x16x4_f32 (component q of a lane's 16-byte
+    // read feeds the q-th MFMA of its group, for A and B alike)
+    f32x4 kk0 = {0.0f, 0.0f, 0.0f, 0.0f}, kk1 = kk0, qk0 = kk0, qk1 = kk0;
+#pragma unroll
+    for (int g = 0; g < kHD / 16; ++g) {
+        const f32x4 ka = ks[r0 + li][4 * g + kk];
+        const f32x4 qa = qr[li][4 * g + kk];
+        const f32x4 kb = ks[16 * w + li][4 * g + kk];
+        kk0 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.x, kb.x, kk0, 0, 0, 0);
+        qk0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa.x, kb.x, qk0, 0, 0, 0);
+        kk1 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.y, kb.y, kk1, 0, 0, 0);
+        qk1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa.y, kb.y, qk1, 0, 0, 0);
+        kk0 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.z, kb.z, kk0, 0, 0, 0);
+        qk0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa.z, kb.z, qk0, 0, 0, 0);
+        kk1 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.w, kb.w, kk1, 0, 0, 0);
+        qk1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa.w, kb.w, qk1, 0, 0, 0);
     }
-    if (m < kMaxB) {
+    const f32x4 gk4 = kk0 + kk1, gq4 = qk0 + qk1;
+    const int sidx = 16 * w + li;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int m = r0 + 4 * kk + r;
+        float lv = 0.0f, mv = 0.0f;
+        if (m < n && sidx <= m) {
+            const float ratio = __expf(glog[m] - glog[sidx]);
+            if (sidx < m) lv = bd[m * 16 + 2 * h] * ratio * gk4[r];
+            mv = ratio * gq4[r];
+        }
         Lout[((size_t)h * kMaxB + m) * kMaxB + sidx] = lv;
         Mout[((size_t)h * kMaxB + m) * kMaxB + sidx] = mv;
     }
@@ -1653,7 +1677,7 @@ void enqueue_prefill_chunk(GDNBatchEngine *e, int slot, int n, bool last, hipStr
                            e->qkv, e->gate, e->sgate);
         hipLaunchKernelGGL(k_pqk, dim3(kNH, n), dim3(kT), 0, s, e->qkv, e->p_qn, e->p_kn, e->p_alpha);
         if (e->prefill_mode == GDN_PREFILL_CHUNKED) {
-            hipLaunchKernelGGL(k_wy_gram, dim3(kNH, kMaxB / 4), dim3(kT), 0, s, e->p_qn, e->p_kn, e->bd, n,
+            hipLaunchKernelGGL(k_wy_gram, dim3(kNH, kMaxB / 16), dim3(kT), 0, s, e->p_qn, e->p_kn, e->bd, n,
                                e->p_wyl, e->p_wym);
             hipLaunchKernelGGL(k_wy_chunk, dim3(kHD / kWyCols, kNH), dim3(kT), 0, s, e->qkv, e->p_qn, e->p_kn, e->bd,
                                e->p_wyl, e->p_wym, n, st, e->attn);
