@@ -568,6 +568,38 @@ def test_prefill_chunked_recurrence_precision(n):
     assert rel <= 1e-5 and same_bits(conv, conv_scan)
 
 
+def test_prefill_chunked_from_a_loaded_state_leaves_other_streams():
+    """The chunked recurrence from a nonzero state (N(0, 0.01) per element,
+    BF16 conv tails), on the middle stream of three: against the scan from
+    the same state, one layer, 100 tokens (a full chunk then a partial
+    one), state relative L2 <= 1e-5; the other two streams' states and
+    tails stay bit for bit."""
+    m = g.Model.synth(num_layers=1, seed=2, std=0.02, bf16=True)
+    rng = np.random.default_rng(9)
+    n_rec, n_conv = 8 * 256 * 256, 3 * 3 * 2048
+    states = [rng.normal(0.0, 0.01, n_rec).astype(np.float32) for _ in range(3)]
+    tails = [g.bf16_round(rng.normal(0.0, 1.0, n_conv).astype(np.float32)) for _ in range(3)]
+    prompt = g.synth_tokens(100, 63, 0)
+    out = {}
+    for mode in (g.PREFILL_SCAN, g.PREFILL_CHUNKED):
+        bs = g.BatchState(m, 3)
+        try:
+            bs.set_prefill_mode(mode)
+            for sidx in range(3):
+                bs.load_stream_state(sidx, states[sidx], tails[sidx])
+            bs.prefill(1, prompt)
+            out[mode] = [bs.save_stream_state(sidx) for sidx in range(3)]
+        finally:
+            bs.free()
+    m.free()
+    rel = _rel(out[g.PREFILL_CHUNKED][1][0], out[g.PREFILL_SCAN][1][0])
+    print(f"[prefill chunked] from a loaded state, 1 layer x 100 tokens vs scan: state rel-L2 {rel:.3e}", flush=True)
+    assert rel <= 1e-5 and same_bits(out[g.PREFILL_CHUNKED][1][1], out[g.PREFILL_SCAN][1][1])
+    for sidx in (0, 2):
+        rec, conv = out[g.PREFILL_CHUNKED][sidx]
+        assert same_bits(rec, states[sidx]) and same_bits(conv, tails[sidx])
+
+
 @pytest.mark.parametrize("n", [64, 150])
 def test_prefill_chunked_full_model_against_scan(model, n):
     """Over the 24-layer random model the re-association flips occasional
