@@ -254,8 +254,10 @@ def test_vocab_not_multiple_of_125(orc):
 def test_step_deadline_fails_the_run_state():
     """A deadline far below one step's duration: gdn_decode_step_host returns
     -1 without waiting for the GPU (which finishes the step on its own), and
-    the run state refuses later steps."""
-    m = small_model(1, 512, seed=1)
+    the run state refuses later steps.  24 layers, so the step's GPU time
+    (about 0.8 ms) outlasts whatever the first graph launch takes on the
+    host before the wait starts (a 1-layer step could finish first)."""
+    m = small_model(24, 512, seed=1)
     os.environ["GDN_KERNEL_WAIT_TIMEOUT_MS"] = "0.0001"
     try:
         rs = g.RunState(m, g.CONTRACT_BF16W_FP32S)
