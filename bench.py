@@ -70,8 +70,8 @@ KERNEL_BYTES = {
 # constants from that profile, not measured by this run (the bench line says
 # so in roofline.traffic_source).
 MEASURED_TRAFFIC = {
-    "qkvg": 34_361_000, "recur": 4_519_000, "o_proj": 8_708_000, "gate_up": 46_589_000,
-    "down": 23_379_000, "lm_head": 131_758_000, "argmax": 7_000,
+    "qkvg": 34_382_000, "recur": 4_507_000, "o_proj": 8_718_000, "gate_up": 46_666_000,
+    "down": 23_417_000, "lm_head": 131_754_000, "argmax": 7_000,
 }
 TRAFFIC_SOURCE = ("rocprofv3 FETCH_SIZE + WRITE_SIZE passes, copy-calibrated "
                   "(profiles/k_gemv_cu_gdn13b_bf16w_decode.md); a profile constant, not measured in this run")
