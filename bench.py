@@ -359,9 +359,11 @@ def main_streams(args):
 
 def main_prefill(args):
     """The prompt pass: an N-token uniform prompt through one stream's state
-    (gdn_batch_prefill: 64-token chunks, token-parallel matrix-core
-    projections, in-order recurrence on chip), timed against the same prompt
-    as N batch-1 decode steps (BF16W_FP32S); `value` is prefill tokens/s."""
+    (gdn_batch_prefill: the prompt as one segment of up to 4096 tokens, run
+    layer by layer -- projections as matrix-core GEMMs, the recurrence over
+    64-token chunks in token order or in the WY form), timed against the same
+    prompt as N batch-1 decode steps (BF16W_FP32S); `value` is prefill
+    tokens/s.  The warm-up prefill also allocates the segment buffers."""
     import gateddeltanet_amd as g
     n = args.prefill
     model = g.Model.synth(num_layers=L, seed=0, std=0.02, bf16=True)
@@ -402,7 +404,8 @@ def main_prefill(args):
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded random-init weights, uniform random prompt)",
-        "config": {"workload": f"{n}-token prompt through one stream, 24 layers, FP32 state, chunks of 64",
+        "config": {"workload": f"{n}-token prompt through one stream, 24 layers, FP32 state, "
+                                f"segments of 4096 tokens layer by layer, recurrence chunks of 64",
                    "prefill_mode": args.prefill_mode,
                    "arithmetic": ("the multi-stream step's, with the recurrence in the chunk-parallel (WY) form "
                                   "(FP32 re-association)" if chunked else "the multi-stream step's, bit for bit")},

@@ -18,6 +18,7 @@ from .engine import (  # noqa: F401
     bf16_round,
     default_config,
     gemv,
+    prefill_gemm,
     recurrence,
     synth_normal,
     synth_tokens,

@@ -226,9 +226,11 @@ SIGNATURES = {
     "gdn_batch_run_teacher_forced": (c_int, [BP, IP, c_uint32, IP, FP, FP]),
     "gdn_batch_prefill": (c_int, [BP, c_uint32, IP, c_uint32, IP]),
     "gdn_batch_set_prefill_mode": (c_int, [BP, c_int]),
+    "gdn_batch_set_prefill_segment": (c_int, [BP, c_uint32]),
     "gdn_batch_profile_kernels": (c_int, [BP, c_uint32, FP, c_uint32]),
     "gdn_batch_set_graph_mode": (c_int, [BP, c_int]),
     "gdn_test_batch_gemm": (c_int, [FP, FP, c_uint32, c_uint32, FP]),
+    "gdn_test_prefill_gemm": (c_int, [c_int, FP, FP, c_uint32, c_uint32, FP, FP]),
     "gdn_test_tile_bf16": (None, [POINTER(c_uint16), c_size_t, c_size_t, c_int, POINTER(c_uint16)]),
 }
 

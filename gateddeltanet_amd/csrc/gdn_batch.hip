@@ -75,13 +75,17 @@ __device__ __forceinline__ uint32_t bf16_daz_bits(float v) {
     return ((b & 0x7f800000u) == 0u) ? ((b >> 16) & 0x8000u) : (b >> 16);
 }
 
-// Offset (BF16 elements) of (stream m, column k) in an X tile buffer.
-__device__ __forceinline__ int xt_index(int m, int k) {
-    const int kt = k >> 5, kk = k & 31;
-    return (((kt * 4 + (m >> 4)) * 64 + ((kk >> 3) << 4) + (m & 15)) << 3) + (kk & 7);
+// Offset (BF16 elements) of (stream or token m, column k) in an X tile
+// buffer of K columns: blocks of 64 streams (a step has one; a prefill
+// segment one per 64 tokens), each [k tile][16-stream group][64 lanes][8].
+__device__ __forceinline__ size_t xt_index(int m, int k, int K = kH) {
+    const int kt = k >> 5, kk = k & 31, mm = m & 63;
+    return (size_t)(m >> 6) * 64 * K +
+           (size_t)((((kt * 4 + (mm >> 4)) * 64 + ((kk >> 3) << 4) + (mm & 15)) << 3) + (kk & 7));
 }
 
-// Eight consecutive columns k..k+7 (k % 8 == 0) of stream m, one 16-byte store.
+// Eight consecutive columns k..k+7 (k % 8 == 0) of stream m in a K = kH X
+// tile buffer, one 16-byte store.
 __device__ __forceinline__ void store_x8(uint16_t *x, int m, int k, const float *v) {
     u32x4 w;
     w.x = bf16_daz_bits(v[0]) | (bf16_daz_bits(v[1]) << 16);
@@ -388,7 +392,7 @@ __global__ __launch_bounds__(NW * 64) void k_bgu(const u32x4 *__restrict__ W, co
             const float u = rne_bf16(cc < 16 ? val(1, cc, m) : val(2, cc - 16 + (kGuCh - 16), m));
             packed |= bf16_daz_bits(rne_bf16(silu_ref(g) * u)) << (16 * e);
         }
-        *reinterpret_cast<uint32_t *>(x_next + xt_index(m, rb * kGuCh + 2 * cp)) = packed;
+        *reinterpret_cast<uint32_t *>(x_next + xt_index(m, rb * kGuCh + 2 * cp, kI)) = packed;
     }
 }
 
@@ -752,11 +756,13 @@ __global__ __launch_bounds__(2 * CW) void k_brecur(const float *__restrict__ qkv
 // with the state held in registers.  Every token sees the arithmetic of a
 // multi-stream step, so a prefill of n tokens equals n steps bit for bit.
 
-// The causal conv of one 64-channel block over a chunk of n tokens.  raw is
-// [64 tokens][4 kH] (the unrounded q, k, v, g sums); the tails are the
-// prefilled stream's for this layer, [q,k,v][3 oldest..newest][kH].  Token
-// m's window is (s[m], s[m+1], s[m+2]) and its input s[m+3] in the sequence
-// s = tails ++ R(raw[0..n)); the new tails are s[n], s[n+1], s[n+2].
+// The causal conv of one 64-channel block over 64 tokens of a segment of n:
+// grid (4 kH / 64, ceil(n / 64)).  raw is [n][4 kH] (the unrounded q, k, v,
+// g sums); the tails are the prefilled stream's for this layer,
+// [q,k,v][3 oldest..newest][kH].  Token m's window is (s[m], s[m+1],
+// s[m+2]) and its input s[m+3] in the sequence s = tails ++ R(raw[0..n));
+// the new tails are s[n], s[n+1], s[n+2].  Only the first token block reads
+// the old tails, and it writes the new ones after that read.
 constexpr int kConvT = 1024;  // threads per conv workgroup: 16 token lanes x 64 channels
 __global__ __launch_bounds__(kConvT) void k_pconv(const float *__restrict__ raw, int n, uint16_t *__restrict__ tails,
                                                   const float *__restrict__ conv_w, float *__restrict__ qkv,
@@ -764,32 +770,43 @@ __global__ __launch_bounds__(kConvT) void k_pconv(const float *__restrict__ raw,
     constexpr int MG = kConvT / 64;  // tokens in flight per channel
     __shared__ float xs[kMaxB + 3][64];
     const int row0 = blockIdx.x * 64, t = threadIdx.x, cl = t & 63, mg = t >> 6;
+    const int m0 = (int)blockIdx.y * kMaxB, nb = n - m0 < kMaxB ? n - m0 : kMaxB;
     const int row = row0 + cl, which = row0 / kH, c = row - which * kH;
     if (which < 3) {
         uint16_t *tl = tails + (size_t)which * 3 * kH + c;
         if (t < 64) {
-            xs[0][cl] = bf16_bits_to_f32(tl[0]);
-            xs[1][cl] = bf16_bits_to_f32(tl[kH]);
-            xs[2][cl] = bf16_bits_to_f32(tl[2 * kH]);
+            if (m0 == 0) {
+                xs[0][cl] = bf16_bits_to_f32(tl[0]);
+                xs[1][cl] = bf16_bits_to_f32(tl[kH]);
+                xs[2][cl] = bf16_bits_to_f32(tl[2 * kH]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 3; ++i) xs[i][cl] = rne_bf16(raw[(size_t)(m0 - 3 + i) * 4 * kH + row]);
+            }
         }
-        for (int m = mg; m < n; m += MG) xs[3 + m][cl] = rne_bf16(raw[(size_t)m * 4 * kH + row]);
+        for (int m = mg; m < nb; m += MG) xs[3 + m][cl] = rne_bf16(raw[(size_t)(m0 + m) * 4 * kH + row]);
         __syncthreads();
         const f32x4 cw = *reinterpret_cast<const f32x4 *>(conv_w + ((size_t)which * kH + c) * 4);
-        for (int m = mg; m < n; m += MG) {
+        for (int m = mg; m < nb; m += MG) {
             // gdn_depthwise_conv_silu_head_kind, gdn_model.cpp:1543-1667
             const float sum = xs[m][cl] * cw.x + xs[m + 1][cl] * cw.y + xs[m + 2][cl] * cw.z + xs[m + 3][cl] * cw.w;
-            qkv[((size_t)m * 3 + which) * kH + c] = rne_bf16(silu_ref(sum));
+            qkv[((size_t)(m0 + m) * 3 + which) * kH + c] = rne_bf16(silu_ref(sum));
         }
-        if (t < 64) {
-            tl[0] = bf16_hi(xs[n][cl]);
-            tl[kH] = bf16_hi(xs[n + 1][cl]);
-            tl[2 * kH] = bf16_hi(xs[n + 2][cl]);
+        if (t < 64 && m0 == 0) {
+            if (n <= kMaxB) {
+                tl[0] = bf16_hi(xs[n][cl]);
+                tl[kH] = bf16_hi(xs[n + 1][cl]);
+                tl[2 * kH] = bf16_hi(xs[n + 2][cl]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 3; ++i) tl[i * kH] = bf16_hi(rne_bf16(raw[(size_t)(n - 3 + i) * 4 * kH + row]));
+            }
         }
     } else {
-        for (int m = mg; m < n; m += MG) {
-            const float g = rne_bf16(raw[(size_t)m * 4 * kH + row]);
-            gate[(size_t)m * kH + c] = g;
-            sgate[(size_t)m * kH + c] = sigmoid_ref(g);
+        for (int m = mg; m < nb; m += MG) {
+            const float g = rne_bf16(raw[(size_t)(m0 + m) * 4 * kH + row]);
+            gate[(size_t)(m0 + m) * kH + c] = g;
+            sgate[(size_t)(m0 + m) * kH + c] = sigmoid_ref(g);
         }
     }
 }
@@ -958,7 +975,8 @@ __global__ __launch_bounds__(kT) void k_pscan(const float *__restrict__ qkv, con
 // sequential chains, so this mode matches the scan within a tolerance, not
 // bit for bit; o is rounded to BF16 as the step rounds it.
 
-// L and Mq of one head for rows 16 blockIdx.y .. +15: grid (kNH, kMaxB / 16).
+// L and Mq of one head for rows 16 blockIdx.y .. +15 of chunk blockIdx.z of
+// a segment of n_total tokens: grid (kNH, kMaxB / 16, chunks).
 constexpr int kKp = kHD / 4 + 1;  // padded float4 stride of a staged k/q row
 
 // The chunk's rows of one head ([token][kH] FP32, head h's 256 values),
@@ -1017,9 +1035,13 @@ __device__ __forceinline__ float cum_log_decay(const float *__restrict__ bd, int
     return v;
 }
 
-__global__ __launch_bounds__(kT) void k_wy_gram(const float *__restrict__ qn_all, const float *__restrict__ kn_all,
-                                                const float *__restrict__ bd, int n, float *__restrict__ Lout,
-                                                float *__restrict__ Mout) {
+__global__ __launch_bounds__(kT) void k_wy_gram(const float *__restrict__ qn_seg, const float *__restrict__ kn_seg,
+                                                const float *__restrict__ bd_seg, int n_total,
+                                                float *__restrict__ L_seg, float *__restrict__ M_seg) {
+    const int ch = blockIdx.z, n = n_total - kMaxB * ch < kMaxB ? n_total - kMaxB * ch : kMaxB;
+    const float *qn_all = qn_seg + (size_t)ch * kMaxB * kH, *kn_all = kn_seg + (size_t)ch * kMaxB * kH;
+    const float *bd = bd_seg + (size_t)ch * kMaxB * 16;
+    float *Lout = L_seg + (size_t)ch * kNH * kMaxB * kMaxB, *Mout = M_seg + (size_t)ch * kNH * kMaxB * kMaxB;
     __shared__ f32x4 ks[kMaxB][kKp];
     __shared__ f32x4 qr[16][kKp];
     __shared__ float glog[kMaxB];
@@ -1282,6 +1304,217 @@ __global__ __launch_bounds__(kT) void k_wy_chunk(const float *__restrict__ qkv, 
     }
 }
 
+
+// ------------------------------------------------ prefill projections
+//
+// A prefill segment runs layer by layer, so each layer's projection weights
+// are read once per segment instead of once per 64 tokens.  k_pgemm and
+// k_pgu form the segment's projections as GEMMs: one workgroup per 128 rows
+// (four 32-row blocks of the weight layout) x 128 tokens (two 64-token X
+// tile blocks), four waves of 64 rows x 64 tokens, the k tile's fragments
+// staged once through LDS (double buffer, two k tiles of loads in flight
+// per thread).  Every output element is formed with the step's operations
+// in the step's order: the same v_mfma_f32_16x16x32_bf16 fragments; the k
+// tiles of class c (c, c + NW, ... within a split) chained from zero in
+// increasing order, as wave c of k_bgemm / k_bgu chains them; the classes
+// added in order, as k_bgemm adds its waves' sums; and the splits' sums
+// added in split order, as the step's norm adds k_bgemm's split partials.
+// A prefill therefore still equals the steps bit for bit.
+constexpr int kPgT = 256;  // threads per prefill GEMM workgroup (4 waves)
+constexpr int kPgTok = 128;  // tokens per workgroup (2 X tile blocks)
+constexpr int kSegDefault = 4096;  // prefill tokens per segment by default
+constexpr int kSegMax = 32768;     // largest segment (k_pqk's grid.y holds it)
+
+// The j-th k tile in class order: split s, class c, i-th tile of the class.
+template <int KT, int NW, int S>
+__device__ __forceinline__ int pg_tile(int j) {
+    constexpr int KTS = KT / S, KTW = KTS / NW;
+    const int s = j / KTS, r = j - s * KTS, c = r / KTW, i = r - c * KTW;
+    return s * KTS + c + NW * i;
+}
+
+// Class bookkeeping after k tile j: the class chain joins the split's sum
+// (the first class is taken as it is), the split's sum joins the total.
+template <int KT, int NW, int S, int NB>
+__device__ __forceinline__ void pg_close(int j, f32x4 (&chain)[NB], f32x4 (&part)[NB], f32x4 (&tot)[NB]) {
+    constexpr int KTS = KT / S, KTW = KTS / NW;
+    if ((j + 1) % KTW != 0) return;
+    const int cls = ((j + 1) / KTW - 1) % NW, sp = j / KTS;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        part[b] = cls == 0 ? chain[b] : part[b] + chain[b];
+        chain[b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    if (S > 1 && cls == NW - 1) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) tot[b] = sp == 0 ? part[b] : tot[b] + part[b];
+    }
+}
+
+// y[m][row] for rows 128 blockIdx.x .. +127 and tokens 128 blockIdx.y ..
+// +127: the sum k_bgemm<2, KT, NW, S, EPI_RAW> forms for the row (S = 1) or
+// the in-order sum of its S split partials.  W in the 32-row block layout
+// ([row block][k tile][2 tiles][64 lanes]); X in 64-token X tile blocks;
+// y has the padded token count's rows.
+template <int KT, int NW, int S>
+__global__ __launch_bounds__(kPgT) void k_pgemm(const u32x4 *__restrict__ W, const u32x4 *__restrict__ X,
+                                                float *__restrict__ y, int n_rows) {
+    constexpr int AU = 4 * 2 * 64, BU = 2 * 4 * 64, PT = (AU + BU) / kPgT;
+    static_assert(PT == 4 && AU == 2 * kPgT, "two A and two B entries per thread and k tile");
+    static_assert(KT % 2 == 0, "k tiles in pairs");
+    __shared__ u32x4 stg[2][AU + BU];
+    const int t = threadIdx.x, w = t >> 6, l = t & 63, wr = w & 1, wt = w >> 1;
+    // entry q = t + 256 i: A (row block q / 128, entry q % 128) for i < 2,
+    // else B (token block, entry)
+    const u32x4 *a0 = W + (size_t)(4 * blockIdx.x + t / 128) * KT * 128 + (t % 128);
+    const u32x4 *a1 = W + (size_t)(4 * blockIdx.x + 2 + t / 128) * KT * 128 + (t % 128);
+    const u32x4 *b0 = X + (size_t)(2 * blockIdx.y) * KT * 256 + t;
+    const u32x4 *b1 = X + (size_t)(2 * blockIdx.y + 1) * KT * 256 + t;
+    auto fetch = [&](u32x4 (&r)[PT], int kt) __attribute__((always_inline)) {
+        r[0] = a0[(size_t)kt * 128];
+        r[1] = a1[(size_t)kt * 128];
+        r[2] = b0[(size_t)kt * 256];
+        r[3] = b1[(size_t)kt * 256];
+    };
+    f32x4 chain[16], part[16], tot[S > 1 ? 16 : 1];
+#pragma unroll
+    for (int b = 0; b < 16; ++b) chain[b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    u32x4 rg[2][PT];
+    fetch(rg[0], pg_tile<KT, NW, S>(0));
+    fetch(rg[1], pg_tile<KT, NW, S>(1));
+    for (int j0 = 0; j0 < KT; j0 += 2) {
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+            const int j = j0 + d;
+#pragma unroll
+            for (int i = 0; i < PT; ++i) stg[d][t + kPgT * i] = rg[d][i];
+            if (j + 2 < KT) fetch(rg[d], pg_tile<KT, NW, S>(j + 2));
+            __syncthreads();
+            u32x4 fa[4], fb[4];
+#pragma unroll
+            for (int f = 0; f < 4; ++f) {
+                fa[f] = stg[d][256 * wr + 64 * f + l];
+                fb[f] = stg[d][AU + 256 * wt + 64 * f + l];
+            }
+#pragma unroll
+            for (int f = 0; f < 4; ++f)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    chain[4 * f + g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(bf16x8, fa[f]), __builtin_bit_cast(bf16x8, fb[g]), chain[4 * f + g], 0,
+                        0, 0);
+            if constexpr (S > 1) pg_close<KT, NW, S, 16>(j, chain, part, tot);
+            else pg_close<KT, NW, S, 16>(j, chain, part, part);
+        }
+    }
+    // row tile f: rows 128 bx + 64 wr + 16 f + 4 (l / 16) .. +3; token
+    // group g: token 128 by + 64 wt + 16 g + l % 16
+    const int row = 128 * blockIdx.x + 64 * wr + 4 * (l >> 4);
+    const int m = kPgTok * blockIdx.y + 64 * wt + (l & 15);
+#pragma unroll
+    for (int f = 0; f < 4; ++f)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            *reinterpret_cast<f32x4 *>(y + (size_t)(m + 16 * g) * n_rows + row + 16 * f) =
+                S > 1 ? tot[S > 1 ? 4 * f + g : 0] : part[4 * f + g];
+}
+
+// Gate/up + SwiGLU for channel groups 2 blockIdx.x, +1 (k_bgu's layout and
+// sums: four classes of 16 k tiles) and tokens 128 blockIdx.y .. +127 (the
+// first n_tok are written).  Wave w: group w & 1, token block w >> 1.
+__global__ __launch_bounds__(kPgT) void k_pgu(const u32x4 *__restrict__ W, const u32x4 *__restrict__ X,
+                                              uint16_t *__restrict__ x_next, int n_tok) {
+    constexpr int KT = kKtH, NW = kGuWaves;
+    constexpr int AU = 2 * kGuTileU4, BU = 2 * 4 * 64, PT = 4;
+    static_assert(AU + BU <= PT * kPgT && AU > kPgT && AU + BU > 3 * kPgT, "entries 0, 1 (part), 2, 3 (part)");
+    __shared__ u32x4 stg[2][AU + BU];
+    __shared__ f32x4 red[4][12 * 64];
+    const int t = threadIdx.x, w = t >> 6, l = t & 63, wg = w & 1, wt = w >> 1;
+    const int gb = 2 * blockIdx.x;
+    // entry q = t + 256 i: A (group q / kGuTileU4) below AU, else B
+    const u32x4 *src[PT];
+    int stride[PT];
+    bool live[PT];
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+        const int q = t + kPgT * i;
+        live[i] = q < AU + BU;
+        if (q < AU) {
+            src[i] = W + (size_t)(gb + q / kGuTileU4) * KT * kGuTileU4 + (q % kGuTileU4);
+            stride[i] = kGuTileU4;
+        } else {
+            const int qb = live[i] ? q - AU : 0;
+            src[i] = X + (size_t)(2 * blockIdx.y + qb / 256) * KT * 256 + (qb % 256);
+            stride[i] = 256;
+        }
+    }
+    auto fetch = [&](u32x4 (&r)[PT], int kt) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < PT; ++i)
+            if (live[i]) r[i] = src[i][(size_t)kt * stride[i]];
+    };
+    const bool p2 = (l & 15) < kGuTail2;
+    const int o2 = 128 + (p2 ? (l >> 4) * kGuTail2 + (l & 15) : 0);
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+    f32x4 chain[12], part[12];
+#pragma unroll
+    for (int b = 0; b < 12; ++b) chain[b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    u32x4 rg[2][PT];
+    fetch(rg[0], pg_tile<KT, NW, 1>(0));
+    fetch(rg[1], pg_tile<KT, NW, 1>(1));
+    for (int j0 = 0; j0 < KT; j0 += 2) {
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+            const int j = j0 + d;
+#pragma unroll
+            for (int i = 0; i < PT; ++i)
+                if (live[i]) stg[d][t + kPgT * i] = rg[d][i];
+            if (j + 2 < KT) fetch(rg[d], pg_tile<KT, NW, 1>(j + 2));
+            __syncthreads();
+            u32x4 fa[3], fb[4];
+            fa[0] = stg[d][wg * kGuTileU4 + l];
+            fa[1] = stg[d][wg * kGuTileU4 + 64 + l];
+            fa[2] = p2 ? stg[d][wg * kGuTileU4 + o2] : zero;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) fb[g] = stg[d][AU + 256 * wt + 64 * g + l];
+#pragma unroll
+            for (int f = 0; f < 3; ++f)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    chain[4 * f + g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(bf16x8, fa[f]), __builtin_bit_cast(bf16x8, fb[g]), chain[4 * f + g], 0,
+                        0, 0);
+            pg_close<KT, NW, 1, 12>(j, chain, part, part);
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < 12; ++b) red[w][b * 64 + l] = part[b];
+    // the wave reads only its own sums
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // row rr of tile r, token m of the block: lane (rr / 4) * 16 + m % 16 of
+    // token group m / 16, component rr % 4 (k_bgu's val)
+    auto val = [&](int r, int rr, int m) {
+        return reinterpret_cast<const float *>(red[w])[4 * ((r * 4 + (m >> 4)) * 64 + (rr >> 2) * 16 + (m & 15)) +
+                                                       (rr & 3)];
+    };
+    const int mb = kPgTok * blockIdx.y + 64 * wt;
+    for (int q = l; q < 64 * (kGuCh / 2); q += 64) {
+        const int m = q / (kGuCh / 2), cp = q - m * (kGuCh / 2);
+        if (mb + m >= n_tok) continue;
+        uint32_t packed = 0;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int cc = 2 * cp + e;
+            const float g = rne_bf16(cc < 16 ? val(0, cc, m) : val(2, cc - 16, m));
+            const float u = rne_bf16(cc < 16 ? val(1, cc, m) : val(2, cc - 16 + (kGuCh - 16), m));
+            packed |= bf16_daz_bits(rne_bf16(silu_ref(g) * u)) << (16 * e);
+        }
+        *reinterpret_cast<uint32_t *>(x_next + xt_index(mb + m, (gb + wg) * kGuCh + 2 * cp, kI)) = packed;
+    }
+}
+
 }  // namespace bt
 }  // namespace gdn
 
@@ -1307,17 +1540,24 @@ struct GDNBatchEngine {
           *attn = nullptr, *ypart = nullptr, *xn = nullptr, *logits = nullptr, *part_val = nullptr;
     int *part_idx = nullptr;
     uint16_t *x_h = nullptr, *x_o = nullptr, *x_d = nullptr;  // X tiles, K = 2048 / 2048 / 5632
-    int *tok_dev = nullptr;   // a prefill chunk's tokens [0..63]
-    int *tok_host = nullptr;  // pinned, mapped, coherent, same layout
+    int *tok_host = nullptr;  // pinned, mapped, coherent: [0..64) tokens in, [64..128) argmaxes out
     int *tok_map = nullptr;   // the device's address of tok_host (the step's tokens)
-    // prefill: the chunk's normalized q / k, alpha, its logits, final hidden
-    // vectors and argmax tokens (per-token buffers of their own, so a
-    // prefill leaves the other streams' last step readable)
-    float *p_qn = nullptr, *p_kn = nullptr, *p_alpha = nullptr, *p_logits = nullptr, *p_xn = nullptr;
-    // chunked prefill: the chunk's L and Mq per head [kNH][64][64]
-    float *p_wyl = nullptr, *p_wym = nullptr;
-    int prefill_mode = GDN_PREFILL_SCAN;
+    // prefill: the last token block's logits and argmax tokens (buffers of
+    // their own, so a prefill leaves the other streams' last step readable)
+    float *p_logits = nullptr;
     int *p_tok = nullptr;
+    int prefill_mode = GDN_PREFILL_SCAN;
+    // prefill segment buffers, allocated at the first prefill for seg_cap
+    // tokens (per token: residual ping-pong, projection sums, q/k/v, gate,
+    // sigmoid(gate), beta/decay, attention output, normalised q/k, alpha,
+    // the chunk matrices L and Mq, final hidden; X tiles of three widths)
+    int seg_tokens = kSegDefault, seg_cap = 0;
+    void *seg_mem = nullptr;
+    float *s_h = nullptr, *s_y = nullptr, *s_qkv = nullptr, *s_gate = nullptr, *s_sgate = nullptr, *s_bd = nullptr,
+          *s_attn = nullptr, *s_qn = nullptr, *s_kn = nullptr, *s_alpha = nullptr, *s_wyl = nullptr,
+          *s_wym = nullptr, *s_xn = nullptr;
+    uint16_t *s_xh = nullptr, *s_xo = nullptr, *s_xd = nullptr;
+    int *s_tok = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     bool use_graph = true;
@@ -1481,18 +1721,10 @@ int b_alloc(GDNBatchEngine *e) {
     GDN_HIP(hipMemset(e->x_h, 0, (size_t)kMaxB * kH * 2));
     GDN_HIP(hipMemset(e->x_o, 0, (size_t)kMaxB * kH * 2));
     GDN_HIP(hipMemset(e->x_d, 0, (size_t)kMaxB * kI * 2));
-    GDN_HIP(hipMalloc(&e->p_qn, (size_t)kMaxB * kH * 4));
-    GDN_HIP(hipMalloc(&e->p_kn, (size_t)kMaxB * kH * 4));
-    GDN_HIP(hipMalloc(&e->p_alpha, (size_t)kMaxB * kNH * 4));
-    GDN_HIP(hipMalloc(&e->p_wyl, (size_t)kNH * kMaxB * kMaxB * 4));
-    GDN_HIP(hipMalloc(&e->p_wym, (size_t)kNH * kMaxB * kMaxB * 4));
     GDN_HIP(hipMalloc(&e->p_logits, (size_t)kMaxB * V * 4));
-    GDN_HIP(hipMalloc(&e->p_xn, (size_t)kMaxB * kH * 4));
     GDN_HIP(hipMalloc(&e->p_tok, (size_t)kMaxB * sizeof(int)));
-    GDN_HIP(hipMalloc(&e->tok_dev, 2 * kMaxB * sizeof(int)));
-    GDN_HIP(hipMemset(e->tok_dev, 0, 2 * kMaxB * sizeof(int)));
     // a step reads its tokens from and writes its argmaxes to host memory
-    // directly (prefill chunks still stage through tok_dev)
+    // directly
     GDN_HIP(hipHostMalloc(&e->tok_host, 2 * kMaxB * sizeof(int), hipHostMallocMapped | hipHostMallocCoherent));
     std::memset(e->tok_host, 0, 2 * kMaxB * sizeof(int));
     GDN_HIP(hipHostGetDevicePointer(reinterpret_cast<void **>(&e->tok_map), e->tok_host, 0));
@@ -1656,72 +1888,137 @@ int b_run_step(GDNBatchEngine *e, const int32_t *tokens, int32_t *next, float *i
     return 0;
 }
 
-// One prefill chunk of n tokens (already in tok_dev[0..n)) through stream
-// `slot`'s state: the step's kernels with the tokens as the streams, the
-// conv over the chunk (k_pconv) and the in-order recurrence (k_pqk, k_pscan).
-void enqueue_prefill_chunk(GDNBatchEngine *e, int slot, int n, bool last, hipStream_t s) {
-    BNorm p0 = bnorm(e, nullptr, b_aux(e, 0) + kAuxAttnNorm, e->x_h, 0, 0, 0);
+// Prefill segment buffers for e->seg_tokens tokens (kept while the segment
+// length stays).
+int seg_alloc(GDNBatchEngine *e) {
+    if (e->seg_cap == e->seg_tokens && e->seg_mem) return 0;
+    GDN_HIP(hipStreamSynchronize(e->stream));
+    (void)hipFree(e->seg_mem);
+    e->seg_mem = nullptr;
+    e->seg_cap = 0;
+    const size_t T = (size_t)e->seg_tokens, chunks = T / kMaxB;
+    const size_t floats = T * (2 * kH + 4 * kH + 3 * kH + kH + kH + 16 + kH + kH + kH + kNH + kH) +
+                          2 * chunks * kNH * kMaxB * kMaxB;
+    const size_t halves = T * (kH + kH + kI);
+    const size_t bytes = floats * 4 + halves * 2 + T * sizeof(int);
+    GDN_HIP(hipMalloc(&e->seg_mem, bytes));
+    // X tiles of padded tokens are read by the GEMMs (their sums unused):
+    // start them at zero, on the engine's stream (a plain hipMemset may
+    // return before it completes, and the non-blocking stream would not
+    // wait for it)
+    GDN_HIP(hipMemsetAsync(e->seg_mem, 0, bytes, e->stream));
+    float *p = static_cast<float *>(e->seg_mem);
+    e->s_h = p; p += 2 * T * kH;
+    e->s_y = p; p += 4 * T * kH;
+    e->s_qkv = p; p += 3 * T * kH;
+    e->s_gate = p; p += T * kH;
+    e->s_sgate = p; p += T * kH;
+    e->s_bd = p; p += T * 16;
+    e->s_attn = p; p += T * kH;
+    e->s_qn = p; p += T * kH;
+    e->s_kn = p; p += T * kH;
+    e->s_alpha = p; p += T * kNH;
+    e->s_xn = p; p += T * kH;
+    e->s_wyl = p; p += chunks * kNH * kMaxB * kMaxB;
+    e->s_wym = p; p += chunks * kNH * kMaxB * kMaxB;
+    uint16_t *q = reinterpret_cast<uint16_t *>(p);
+    e->s_xh = q; q += T * kH;
+    e->s_xo = q; q += T * kH;
+    e->s_xd = q; q += T * kI;
+    e->s_tok = reinterpret_cast<int *>(q);
+    e->seg_cap = e->seg_tokens;
+    return 0;
+}
+
+// A segment's norm: the residual of layer l's attention block in buffer
+// l & 1 (as in the step), segment-sized.
+BNorm seg_norm(GDNBatchEngine *e, const float *y, const float *w, uint16_t *x_out, int ab_layer, int l_in,
+               int l_out) {
+    BNorm p{};
+    p.h_in = e->s_h + (size_t)(l_in & 1) * e->seg_cap * kH;
+    p.h_out = e->s_h + (size_t)(l_out & 1) * e->seg_cap * kH;
+    p.y = y;
+    p.w = w;
+    p.x_out = x_out;
+    p.eps = e->eps;
+    if (ab_layer >= 0) {
+        float *a = b_aux(e, ab_layer);
+        p.ab_w = a + kAuxAB;
+        p.a_log = a + kAuxALog;
+        p.dt_bias = a + kAuxDtBias;
+        p.bd = e->s_bd;
+    }
+    return p;
+}
+
+// One prefill segment of n tokens (already in s_tok[0..n)) through stream
+// `slot`'s state, layer by layer: the step's kernels with the tokens as the
+// streams (k_pgemm / k_pgu in place of the step's GEMMs, same sums), the
+// conv across the segment (k_pconv), and the recurrence chunk by chunk of
+// 64 tokens, in token order (k_pqk, k_pscan) or in the WY form (k_wy_gram
+// over every chunk at once, then k_wy_chunk per chunk).
+void enqueue_prefill_segment(GDNBatchEngine *e, int slot, int n, bool last, hipStream_t s) {
+    const int blocks = (n + kMaxB - 1) / kMaxB, tiles = (n + kPgTok - 1) / kPgTok;
+    const size_t kq = (size_t)kNH * kMaxB * kMaxB;  // one chunk's L (or Mq)
+    BNorm p0 = seg_norm(e, nullptr, b_aux(e, 0) + kAuxAttnNorm, e->s_xh, 0, 0, 0);
     p0.emb = e->emb;
-    p0.tok = e->tok_dev;
+    p0.tok = e->s_tok;
     hipLaunchKernelGGL((k_bnorm<0, true, true>), dim3(n, kAbSplit), dim3(kT), 0, s, p0);
+    const u32x4 *xh = reinterpret_cast<const u32x4 *>(e->s_xh), *xo = reinterpret_cast<const u32x4 *>(e->s_xo),
+                *xd = reinterpret_cast<const u32x4 *>(e->s_xd);
     for (int l = 0; l < e->layers; ++l) {
         float *st = b_state(e, l) + (size_t)slot * kLayerState;
         uint16_t *tl = b_tails(e, l) + (size_t)slot * kStreamTails;
-        BEpi raw{};
-        raw.n_streams = n;
-        raw.n_rows = 4 * kH;
-        raw.y = e->ypart;
-        hipLaunchKernelGGL((k_bgemm<2, kKtH, 8, 1, EPI_RAW>), dim3(4 * kH / 32), dim3(8 * 64), 0, s, e->w_qkvg[l],
-                           reinterpret_cast<const u32x4 *>(e->x_h), raw);
-        hipLaunchKernelGGL(k_pconv, dim3(4 * kH / 64), dim3(kConvT), 0, s, e->ypart, n, tl, b_aux(e, l) + kAuxConv,
-                           e->qkv, e->gate, e->sgate);
-        hipLaunchKernelGGL(k_pqk, dim3(kNH, n), dim3(kT), 0, s, e->qkv, e->p_qn, e->p_kn, e->p_alpha);
-        if (e->prefill_mode == GDN_PREFILL_CHUNKED) {
-            hipLaunchKernelGGL(k_wy_gram, dim3(kNH, kMaxB / 16), dim3(kT), 0, s, e->p_qn, e->p_kn, e->bd, n,
-                               e->p_wyl, e->p_wym);
-            hipLaunchKernelGGL(k_wy_chunk, dim3(kHD / kWyCols, kNH), dim3(kT), 0, s, e->qkv, e->p_qn, e->p_kn, e->bd,
-                               e->p_wyl, e->p_wym, n, st, e->attn);
-        } else {
-            hipLaunchKernelGGL(k_pscan, dim3(kHD / kScanWgCols, kNH), dim3(kT), 0, s, e->qkv, e->p_qn, e->p_kn,
-                               e->p_alpha, e->bd, n, st, e->attn);
+        hipLaunchKernelGGL((k_pgemm<kKtH, 8, 1>), dim3(4 * kH / 128, tiles), dim3(kPgT), 0, s, e->w_qkvg[l], xh,
+                           e->s_y, 4 * kH);
+        hipLaunchKernelGGL(k_pconv, dim3(4 * kH / 64, blocks), dim3(kConvT), 0, s, e->s_y, n, tl,
+                           b_aux(e, l) + kAuxConv, e->s_qkv, e->s_gate, e->s_sgate);
+        hipLaunchKernelGGL(k_pqk, dim3(kNH, n), dim3(kT), 0, s, e->s_qkv, e->s_qn, e->s_kn, e->s_alpha);
+        if (e->prefill_mode == GDN_PREFILL_CHUNKED)
+            hipLaunchKernelGGL(k_wy_gram, dim3(kNH, kMaxB / 16, blocks), dim3(kT), 0, s, e->s_qn, e->s_kn, e->s_bd,
+                               n, e->s_wyl, e->s_wym);
+        for (int c = 0; c < blocks; ++c) {
+            const int nc = std::min(kMaxB, n - c * kMaxB);
+            const size_t m0 = (size_t)c * kMaxB;
+            if (e->prefill_mode == GDN_PREFILL_CHUNKED)
+                hipLaunchKernelGGL(k_wy_chunk, dim3(kHD / kWyCols, kNH), dim3(kT), 0, s, e->s_qkv + m0 * 3 * kH,
+                                   e->s_qn + m0 * kH, e->s_kn + m0 * kH, e->s_bd + m0 * 16, e->s_wyl + c * kq,
+                                   e->s_wym + c * kq, nc, st, e->s_attn + m0 * kH);
+            else
+                hipLaunchKernelGGL(k_pscan, dim3(kHD / kScanWgCols, kNH), dim3(kT), 0, s, e->s_qkv + m0 * 3 * kH,
+                                   e->s_qn + m0 * kH, e->s_kn + m0 * kH, e->s_alpha + m0 * kNH, e->s_bd + m0 * 16,
+                                   nc, st, e->s_attn + m0 * kH);
         }
-        hipLaunchKernelGGL(k_bonorm, dim3(kNH, n), dim3(kT), 0, s, e->attn, e->gate, e->sgate,
-                           b_aux(e, l) + kAuxONorm, e->eps, e->x_o);
-        BEpi eo{};
-        eo.n_streams = n;
-        eo.n_rows = kH;
-        eo.y = e->ypart;
-        hipLaunchKernelGGL((k_bgemm<kRtO, kKtH, 4, kSplitO, EPI_RAW>), dim3(kH / (16 * kRtO), kSplitO), dim3(kT), 0,
-                           s, e->w_o[l], reinterpret_cast<const u32x4 *>(e->x_o), eo);
-        const BNorm pm = bnorm(e, e->ypart, b_aux(e, l) + kAuxMlpNorm, e->x_h, -1, l, l);
-        hipLaunchKernelGGL((k_bnorm<kSplitO, false, false>), dim3(n), dim3(kT), 0, s, pm);
-        hipLaunchKernelGGL(k_bgu<kGuWaves>, dim3(kGuWgs), dim3(kGuWaves * 64), 0, s, e->w_gu[l],
-                           reinterpret_cast<const u32x4 *>(e->x_h), e->x_d, n);
-        BEpi ed{};
-        ed.n_streams = n;
-        ed.n_rows = kH;
-        ed.y = e->ypart;
-        hipLaunchKernelGGL((k_bgemm<kRtDown, kKtI, 4, kSplitDown, EPI_RAW>), dim3(kH / (16 * kRtDown), kSplitDown),
-                           dim3(kT), 0, s, e->w_down[l], reinterpret_cast<const u32x4 *>(e->x_d), ed);
+        hipLaunchKernelGGL(k_bonorm, dim3(kNH, n), dim3(kT), 0, s, e->s_attn, e->s_gate, e->s_sgate,
+                           b_aux(e, l) + kAuxONorm, e->eps, e->s_xo);
+        hipLaunchKernelGGL((k_pgemm<kKtH, 4, kSplitO>), dim3(kH / 128, tiles), dim3(kPgT), 0, s, e->w_o[l], xo,
+                           e->s_y, kH);
+        const BNorm pm = seg_norm(e, e->s_y, b_aux(e, l) + kAuxMlpNorm, e->s_xh, -1, l, l);
+        hipLaunchKernelGGL((k_bnorm<1, false, false>), dim3(n), dim3(kT), 0, s, pm);
+        hipLaunchKernelGGL(k_pgu, dim3(kGuWgs / 2, tiles), dim3(kPgT), 0, s, e->w_gu[l], xh, e->s_xd, n);
+        hipLaunchKernelGGL((k_pgemm<kKtI, 4, kSplitDown>), dim3(kH / 128, tiles), dim3(kPgT), 0, s, e->w_down[l],
+                           xd, e->s_y, kH);
         if (l + 1 < e->layers) {
-            const BNorm pa = bnorm(e, e->ypart, b_aux(e, l + 1) + kAuxAttnNorm, e->x_h, l + 1, l, l + 1);
-            hipLaunchKernelGGL((k_bnorm<kSplitDown, false, true>), dim3(n, kAbSplit), dim3(kT), 0, s, pa);
+            const BNorm pa = seg_norm(e, e->s_y, b_aux(e, l + 1) + kAuxAttnNorm, e->s_xh, l + 1, l, l + 1);
+            hipLaunchKernelGGL((k_bnorm<1, false, true>), dim3(n, kAbSplit), dim3(kT), 0, s, pa);
         } else {
-            BNorm pf = bnorm(e, e->ypart, e->aux + (size_t)e->layers * kAuxLayer, e->x_h, -1, l, l);
-            pf.xn_out = e->p_xn;
-            hipLaunchKernelGGL((k_bnorm<kSplitDown, false, false>), dim3(n), dim3(kT), 0, s, pf);
+            BNorm pf = seg_norm(e, e->s_y, e->aux + (size_t)e->layers * kAuxLayer, e->s_xh, -1, l, l);
+            pf.xn_out = e->s_xn;
+            hipLaunchKernelGGL((k_bnorm<1, false, false>), dim3(n), dim3(kT), 0, s, pf);
         }
     }
     if (!last) return;
+    // the LM head over the last token block
+    const int lb = blocks - 1, nl = n - lb * kMaxB;
     BEpi lm{};
-    lm.n_streams = n;
+    lm.n_streams = nl;
     lm.n_rows = e->vocab;
     lm.logits = e->p_logits;
     lm.part_val = e->part_val;
     lm.part_idx = e->part_idx;
     hipLaunchKernelGGL((k_bgemm<2, kKtH, 4, 1, EPI_LM>), dim3(lm_wgs(e)), dim3(kT), 0, s, e->w_lm,
-                       reinterpret_cast<const u32x4 *>(e->x_h), lm);
-    hipLaunchKernelGGL(k_bargmax, dim3(n), dim3(kT), 0, s, e->part_val, e->part_idx, lm_wgs(e), e->p_tok);
+                       reinterpret_cast<const u32x4 *>(e->s_xh + (size_t)lb * kMaxB * kH), lm);
+    hipLaunchKernelGGL(k_bargmax, dim3(nl), dim3(kT), 0, s, e->part_val, e->part_idx, lm_wgs(e), e->p_tok);
 }
 
 int b_prefill(GDNBatchEngine *e, int slot, const int32_t *prompt, uint32_t n_tokens, int32_t *seed) {
@@ -1731,24 +2028,23 @@ int b_prefill(GDNBatchEngine *e, int slot, const int32_t *prompt, uint32_t n_tok
             return -1;
         }
     }
+    if (seg_alloc(e)) return -1;
+    const uint32_t seg = (uint32_t)e->seg_cap;
     int n = 0;
-    for (uint32_t off = 0; off < n_tokens; off += (uint32_t)kMaxB) {
-        n = (int)std::min<uint32_t>((uint32_t)kMaxB, n_tokens - off);
-        // the pinned staging word is reused only after the previous chunk's
-        // copy has left it
-        GDN_HIP(hipStreamSynchronize(e->stream));
-        std::memcpy(e->tok_host, prompt + off, (size_t)n * sizeof(int));
-        GDN_HIP(hipMemcpyAsync(e->tok_dev, e->tok_host, (size_t)n * sizeof(int), hipMemcpyHostToDevice, e->stream));
-        enqueue_prefill_chunk(e, slot, n, off + (uint32_t)n == n_tokens, e->stream);
+    for (uint32_t off = 0; off < n_tokens; off += seg) {
+        n = (int)std::min<uint32_t>(seg, n_tokens - off);
+        GDN_HIP(hipMemcpyAsync(e->s_tok, prompt + off, (size_t)n * sizeof(int), hipMemcpyHostToDevice, e->stream));
+        enqueue_prefill_segment(e, slot, n, off + (uint32_t)n == n_tokens, e->stream);
         GDN_HIP(hipGetLastError());
     }
     // the last position's logits, final hidden vector and token into the
     // stream's rows of the step buffers
-    GDN_HIP(hipMemcpyAsync(e->logits + (size_t)slot * e->vocab, e->p_logits + (size_t)(n - 1) * e->vocab,
+    const int nl = n - ((n - 1) / kMaxB) * kMaxB;
+    GDN_HIP(hipMemcpyAsync(e->logits + (size_t)slot * e->vocab, e->p_logits + (size_t)(nl - 1) * e->vocab,
                            (size_t)e->vocab * 4, hipMemcpyDeviceToDevice, e->stream));
-    GDN_HIP(hipMemcpyAsync(e->xn + (size_t)slot * kH, e->p_xn + (size_t)(n - 1) * kH, (size_t)kH * 4,
+    GDN_HIP(hipMemcpyAsync(e->xn + (size_t)slot * kH, e->s_xn + (size_t)(n - 1) * kH, (size_t)kH * 4,
                            hipMemcpyDeviceToDevice, e->stream));
-    GDN_HIP(hipMemcpyAsync(e->tok_host + kMaxB + slot, e->p_tok + (n - 1), sizeof(int), hipMemcpyDeviceToHost,
+    GDN_HIP(hipMemcpyAsync(e->tok_host + kMaxB + slot, e->p_tok + (nl - 1), sizeof(int), hipMemcpyDeviceToHost,
                            e->stream));
     GDN_HIP(hipStreamSynchronize(e->stream));
     if (seed) *seed = e->tok_host[kMaxB + slot];
@@ -1772,15 +2068,9 @@ void b_destroy(GDNBatchEngine *e) {
     (void)hipFree(e->x_h);
     (void)hipFree(e->x_o);
     (void)hipFree(e->x_d);
-    (void)hipFree(e->tok_dev);
-    (void)hipFree(e->p_qn);
-    (void)hipFree(e->p_kn);
-    (void)hipFree(e->p_alpha);
-    (void)hipFree(e->p_wyl);
-    (void)hipFree(e->p_wym);
     (void)hipFree(e->p_logits);
-    (void)hipFree(e->p_xn);
     (void)hipFree(e->p_tok);
+    (void)hipFree(e->seg_mem);
     if (e->tok_host) (void)hipHostFree(e->tok_host);
     delete e;
 }
@@ -1935,6 +2225,17 @@ int gdn_batch_set_prefill_mode(GDNBatchState *state, int mode) {
     return 0;
 }
 
+int gdn_batch_set_prefill_segment(GDNBatchState *state, uint32_t tokens) {
+    GDNBatchEngine *e = engine_of(state);
+    if (!e) return -1;
+    if (tokens < (uint32_t)kPgTok || tokens > (uint32_t)kSegMax || tokens % kPgTok != 0) {
+        gdn_error("gdn: a prefill segment is a multiple of 128 tokens, 128..32768");
+        return -1;
+    }
+    e->seg_tokens = (int)tokens;
+    return 0;
+}
+
 int gdn_batch_prefill(GDNBatchState *state, uint32_t stream, const int32_t *prompt, uint32_t n_tokens,
                       int32_t *seed_token) {
     GDNBatchEngine *e = engine_of(state);
@@ -2037,6 +2338,104 @@ int gdn_test_batch_gemm(const float *W, const float *X, uint32_t N, uint32_t K, 
     (void)hipFree(dw);
     (void)hipFree(dx);
     (void)hipFree(dy);
+    return 0;
+}
+
+int gdn_test_prefill_gemm(int kind, const float *W, const float *X, uint32_t N, uint32_t T, float *Y,
+                          float *Y_step) {
+    // kind 0: q/k/v/g configuration (K 2048, 8 classes); 1: o_proj (K 2048,
+    // 4 classes, 4 splits); 2: down (K 5632, 4 classes, 4 splits); 3:
+    // gate/up + SwiGLU (W = gate then up rows, N = 5632)
+    if (kind < 0 || kind > 3 || T == 0 || T > (uint32_t)kSegMax || N == 0 ||
+        (kind < 3 && (N % 128) != 0) || (kind == 3 && N != (uint32_t)kI)) {
+        gdn_error("gdn_test_prefill_gemm: kind 0..3, N a multiple of 128 (5632 for gate/up), T 1..32768");
+        return -1;
+    }
+    const uint32_t K = kind == 2 ? (uint32_t)kI : (uint32_t)kH;
+    const uint32_t blocks = (T + kMaxB - 1) / kMaxB, tp = (T + kPgTok - 1) / kPgTok * kPgTok;
+    const size_t wn = (kind == 3 ? 2 : 1) * (size_t)N * K;
+    std::vector<uint16_t> wb, wt(wn), xb, xt((size_t)tp * K, 0);
+    to_bf16(W, wn, wb);
+    if (kind == 3) tile_gu(wb.data(), wb.data() + (size_t)N * K, wt.data());
+    else gdn_tile_bf16(wb.data(), N, K, 2, wt.data());
+    std::vector<float> xpad((size_t)blocks * kMaxB * K, 0.0f);
+    std::memcpy(xpad.data(), X, (size_t)T * K * 4);
+    to_bf16(xpad.data(), xpad.size(), xb);
+    for (uint32_t b = 0; b < blocks; ++b)
+        gdn_tile_bf16(xb.data() + (size_t)b * kMaxB * K, kMaxB, K, 4, xt.data() + (size_t)b * kMaxB * K);
+    const size_t out_elems = kind == 3 ? (size_t)tp * kI : (size_t)kSplitDown * tp * N;
+    void *dw = nullptr, *dx = nullptr, *dy = nullptr, *dr = nullptr;
+    GDN_HIP(hipMalloc(&dw, wt.size() * 2));
+    GDN_HIP(hipMalloc(&dx, xt.size() * 2));
+    GDN_HIP(hipMalloc(&dy, out_elems * 4));
+    GDN_HIP(hipMalloc(&dr, out_elems * 4));
+    GDN_HIP(hipMemset(dy, 0, out_elems * 4));
+    GDN_HIP(hipMemset(dr, 0, out_elems * 4));
+    GDN_HIP(hipMemcpy(dw, wt.data(), wt.size() * 2, hipMemcpyHostToDevice));
+    GDN_HIP(hipMemcpy(dx, xt.data(), xt.size() * 2, hipMemcpyHostToDevice));
+    const u32x4 *w4 = static_cast<const u32x4 *>(dw), *x4 = static_cast<const u32x4 *>(dx);
+    const dim3 pg(N / 128, tp / kPgTok);
+    if (kind == 0) hipLaunchKernelGGL((k_pgemm<kKtH, 8, 1>), pg, dim3(kPgT), 0, 0, w4, x4, (float *)dy, (int)N);
+    if (kind == 1)
+        hipLaunchKernelGGL((k_pgemm<kKtH, 4, kSplitO>), pg, dim3(kPgT), 0, 0, w4, x4, (float *)dy, (int)N);
+    if (kind == 2)
+        hipLaunchKernelGGL((k_pgemm<kKtI, 4, kSplitDown>), pg, dim3(kPgT), 0, 0, w4, x4, (float *)dy, (int)N);
+    if (kind == 3)
+        hipLaunchKernelGGL(k_pgu, dim3(kGuWgs / 2, tp / kPgTok), dim3(kPgT), 0, 0, w4, x4,
+                           static_cast<uint16_t *>(dy), (int)T);
+    // the step's kernels, one 64-token block at a time
+    for (uint32_t b = 0; b < blocks; ++b) {
+        const u32x4 *xb4 = x4 + (size_t)b * kMaxB * K / 8;
+        BEpi ep{};
+        ep.n_streams = kMaxB;
+        ep.n_rows = (int)N;
+        ep.y = static_cast<float *>(dr) + (size_t)b * kSplitDown * kMaxB * N;
+        if (kind == 0)
+            hipLaunchKernelGGL((k_bgemm<2, kKtH, 8, 1, EPI_RAW>), dim3(N / 32), dim3(8 * 64), 0, 0, w4, xb4, ep);
+        if (kind == 1)
+            hipLaunchKernelGGL((k_bgemm<kRtO, kKtH, 4, kSplitO, EPI_RAW>), dim3(N / 32, kSplitO), dim3(kT), 0, 0,
+                               w4, xb4, ep);
+        if (kind == 2)
+            hipLaunchKernelGGL((k_bgemm<kRtDown, kKtI, 4, kSplitDown, EPI_RAW>), dim3(N / 32, kSplitDown),
+                               dim3(kT), 0, 0, w4, xb4, ep);
+        if (kind == 3)
+            hipLaunchKernelGGL(k_bgu<kGuWaves>, dim3(kGuWgs), dim3(kGuWaves * 64), 0, 0, w4, xb4,
+                               static_cast<uint16_t *>(dr) + (size_t)b * kMaxB * kI, kMaxB);
+    }
+    GDN_HIP(hipGetLastError());
+    GDN_HIP(hipDeviceSynchronize());
+    if (kind == 3) {
+        // both outputs are X tiles of width kI: untile the first T tokens
+        std::vector<uint16_t> a((size_t)tp * kI), r((size_t)tp * kI);
+        GDN_HIP(hipMemcpy(a.data(), dy, a.size() * 2, hipMemcpyDeviceToHost));
+        GDN_HIP(hipMemcpy(r.data(), dr, r.size() * 2, hipMemcpyDeviceToHost));
+        for (uint32_t m = 0; m < T; ++m)
+            for (uint32_t k = 0; k < (uint32_t)kI; ++k) {
+                const uint32_t kt = k >> 5, kk = k & 31, mm = m & 63;
+                const size_t idx = (size_t)(m >> 6) * 64 * kI +
+                                   (size_t)((((kt * 4 + (mm >> 4)) * 64 + ((kk >> 3) << 4) + (mm & 15)) << 3) + (kk & 7));
+                const uint32_t ya = (uint32_t)a[idx] << 16, yr = (uint32_t)r[idx] << 16;
+                std::memcpy(Y + (size_t)m * kI + k, &ya, 4);
+                std::memcpy(Y_step + (size_t)m * kI + k, &yr, 4);
+            }
+    } else {
+        std::vector<float> a((size_t)tp * N), r(out_elems);
+        GDN_HIP(hipMemcpy(a.data(), dy, a.size() * 4, hipMemcpyDeviceToHost));
+        GDN_HIP(hipMemcpy(r.data(), dr, r.size() * 4, hipMemcpyDeviceToHost));
+        const int splits = kind == 0 ? 1 : kSplitDown;
+        for (uint32_t m = 0; m < T; ++m)
+            for (uint32_t n = 0; n < N; ++n) {
+                const size_t base = (size_t)(m / kMaxB) * kSplitDown * kMaxB * N + (size_t)(m % kMaxB) * N + n;
+                float v = r[base];
+                for (int sp = 1; sp < splits; ++sp) v = v + r[base + (size_t)sp * kMaxB * N];
+                Y[(size_t)m * N + n] = a[(size_t)m * N + n];
+                Y_step[(size_t)m * N + n] = v;
+            }
+    }
+    (void)hipFree(dw);
+    (void)hipFree(dx);
+    (void)hipFree(dy);
+    (void)hipFree(dr);
     return 0;
 }
 

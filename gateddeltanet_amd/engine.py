@@ -308,6 +308,10 @@ class BatchState:
         """gdn_batch_set_prefill_mode: PREFILL_SCAN (default) or PREFILL_CHUNKED."""
         _check(L.load().gdn_batch_set_prefill_mode(self.ptr, mode), "gdn_batch_set_prefill_mode")
 
+    def set_prefill_segment(self, tokens: int) -> None:
+        """gdn_batch_set_prefill_segment: prefill tokens per segment (a multiple of 128)."""
+        _check(L.load().gdn_batch_set_prefill_segment(self.ptr, tokens), "gdn_batch_set_prefill_segment")
+
     def logits(self, stream: int) -> np.ndarray:
         out = np.empty(self.model.config.vocab_size, np.float32)
         _check(L.load().gdn_batch_read_logits(self.ptr, stream, fptr(out), out.size), "gdn_batch_read_logits")
@@ -416,6 +420,19 @@ def batch_gemm(W: np.ndarray, X: np.ndarray) -> np.ndarray:
     Y = np.empty((L.MAX_STREAMS, N), np.float32)
     _check(L.load().gdn_test_batch_gemm(fptr(W), fptr(X), N, K, fptr(Y)), "gdn_test_batch_gemm")
     return Y
+
+
+def prefill_gemm(kind: int, W: np.ndarray, X: np.ndarray):
+    """gdn_test_prefill_gemm: (prefill GEMM [T][N], the step's GEMM per 64-token block [T][N])."""
+    W = _f32(W)
+    X = _f32(X)
+    T, K = X.shape
+    N = W.shape[-2]
+    Y = np.empty((T, N), np.float32)
+    Y_step = np.empty((T, N), np.float32)
+    _check(L.load().gdn_test_prefill_gemm(kind, fptr(W), fptr(X), N, T, fptr(Y), fptr(Y_step)),
+           "gdn_test_prefill_gemm")
+    return Y, Y_step
 
 
 def recurrence(contract: int, q, k, v, a, b, a_log, dt_bias, S):

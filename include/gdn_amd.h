@@ -501,20 +501,28 @@ int gdn_batch_save_stream_state(const GDNBatchState *state, uint32_t stream, flo
  * n_tokens gdn_batch_decode_step calls would feed them to that stream (the
  * GPU prompt pass that produces a .gdnstate, export_gdn_state.py:157-201,
  * :325-330),
- * in chunks of 64 tokens: token-parallel projections on the matrix cores, the
- * causal conv across the chunk, and the recurrence -- by default in token
- * order with the state held on chip, so results equal the steps bit for
- * bit; in GDN_PREFILL_CHUNKED mode in the chunk-parallel (WY) form of the
- * gated delta rule (chunk.py:616-686), equal to the steps within FP32
- * re-association.  *seed_token (may be NULL) receives the argmax of the last
- * position; that position's logits and final hidden vector become the
- * stream's readable ones.  Other streams' states are untouched. */
+ * in segments of up to 4096 tokens (gdn_batch_set_prefill_segment), each
+ * layer by layer: token-parallel projections as GEMMs on the matrix cores,
+ * the causal conv across the segment, and the recurrence over chunks of 64
+ * tokens -- by default in token order with the state held on chip, so
+ * results equal the steps bit for bit; in GDN_PREFILL_CHUNKED mode in the
+ * chunk-parallel (WY) form of the gated delta rule (chunk.py:616-686), equal
+ * to the steps within FP32 re-association.  *seed_token (may be NULL)
+ * receives the argmax of the last position; that position's logits and final
+ * hidden vector become the stream's readable ones.  Other streams' states
+ * are untouched.  The first prefill allocates the segment's buffers (about
+ * 150 KB per segment token, 0.6 GB at 4096), kept until the engine is freed
+ * or the segment length changes. */
 #define GDN_PREFILL_SCAN 0
 #define GDN_PREFILL_CHUNKED 1
 /* Selects the prefill's recurrence (GDN_PREFILL_SCAN by default).  No
  * reference counterpart: the reference's GPU prefill is the chunked form
  * only, its C++ decode the scan's arithmetic. */
 int gdn_batch_set_prefill_mode(GDNBatchState *state, int mode);
+/* Tokens per prefill segment: a multiple of 128 in 128..32768 (default
+ * 4096).  Longer prompts run as consecutive segments; the results do not
+ * depend on the segment length.  No reference counterpart. */
+int gdn_batch_set_prefill_segment(GDNBatchState *state, uint32_t tokens);
 int gdn_batch_prefill(GDNBatchState *state, uint32_t stream, const int32_t *prompt, uint32_t n_tokens,
                       int32_t *seed_token);
 /* n_steps steps with tokens[step][n_streams] fed; per-step argmax
@@ -537,6 +545,14 @@ void gdn_test_tile_bf16(const uint16_t *src, size_t n_rows, size_t k, int rt, ui
  * rounding of the sums); W and X BF16-exact, K = 2048 (N % 32 == 0) or
  * K = 5632 (N % 16 == 0). */
 int gdn_test_batch_gemm(const float *W, const float *X, uint32_t N, uint32_t K, float *Y);
+/* Test hook: the prefill's projection GEMM over T tokens (Y [T][N]) beside
+ * the step's GEMM run on each 64-token block (Y_step, split sums added in
+ * split order).  kind 0: the q/k/v/g configuration (K 2048); 1: o_proj's
+ * (K 2048, 4 splits); 2: down's (K 5632, 4 splits); 3: gate/up + SwiGLU
+ * (W = gate [5632][2048] then up rows, N = 5632; Y the BF16 SwiGLU values).
+ * N a multiple of 128 for kinds 0-2; W and X BF16-exact. */
+int gdn_test_prefill_gemm(int kind, const float *W, const float *X, uint32_t N, uint32_t T, float *Y,
+                          float *Y_step);
 
 #ifdef __cplusplus
 }

@@ -81,6 +81,23 @@ def test_batch_gemm_rounding_bound(K, N):
     assert np.abs(Y - exact).max() > 0 or K == 0  # genuinely FP32 sums
 
 
+@pytest.mark.parametrize("kind,N,T", [(0, 256, 192), (1, 256, 130), (2, 128, 64), (3, 5632, 70)])
+def test_prefill_gemm_equals_step_gemm(kind, N, T):
+    """The prefill's projection GEMMs (128 rows x 128 tokens per workgroup,
+    LDS-staged) form every sum of the step's GEMMs bit for bit: the q/k/v/g
+    configuration (8 classes of k tiles), o_proj's and down's (4 classes x 4
+    splits, split sums in order) and gate/up + SwiGLU (k_bgu's layout); token
+    counts that leave partial 64- and 128-token tiles."""
+    rng = np.random.default_rng(100 + kind)
+    K = 5632 if kind == 2 else 2048
+    shape = (2, N, K) if kind == 3 else (N, K)
+    W = g.bf16_round(rng.normal(0, 0.02, shape).astype(np.float32)).reshape(shape)
+    X = g.bf16_round(rng.normal(0, 1, (T, K)).astype(np.float32)).reshape(T, K)
+    y, y_step = g.prefill_gemm(kind, W, X)
+    assert np.isfinite(y_step).all() and np.abs(y_step).max() > 0
+    assert same_bits(y, y_step)
+
+
 def batch1_reference(m, tokens, init=None):
     """Per-stream batch-1 runs (BF16W_FP32S): logits [steps][B][V], tokens,
     final states."""
@@ -660,5 +677,36 @@ def test_prefill_mode_rejects_unknown(model):
     try:
         with pytest.raises(g.GDNError):
             bs.set_prefill_mode(7)
+        for bad in (0, 64, 200, 32768 + 128):
+            with pytest.raises(g.GDNError):
+                bs.set_prefill_segment(bad)
     finally:
         bs.free()
+
+
+@pytest.mark.parametrize("mode", ["scan", "chunked"])
+def test_prefill_segments(model, mode):
+    """A 300-token prompt run as segments of 128 tokens (128 + 128 + 44: the
+    conv window and the state cross segment edges, the last segment is a
+    partial token tile) gives the results of one segment bit for bit, in
+    both recurrence modes; in scan mode both equal 300 steps."""
+    prompt = g.synth_tokens(300, 49, 0)
+    out = []
+    for seg in (None, 128):
+        bs = g.BatchState(model, 2)
+        try:
+            bs.set_prefill_mode(g.PREFILL_SCAN if mode == "scan" else g.PREFILL_CHUNKED)
+            if seg:
+                bs.set_prefill_segment(seg)
+            seed = bs.prefill(1, prompt)
+            out.append((seed, bs.logits(1), bs.final_hidden(1), *bs.save_stream_state(1)))
+        finally:
+            bs.free()
+    one, segs = out
+    assert one[0] == segs[0]
+    assert all(same_bits(a, b) for a, b in zip(one[1:], segs[1:]))
+    if mode == "scan":
+        seed_ref, logits_ref, hidden_ref, (rec_ref, conv_ref) = stepped_reference(model, prompt)
+        assert one[0] == seed_ref
+        assert same_bits(one[1], logits_ref) and same_bits(one[2], hidden_ref)
+        assert same_bits(one[3], rec_ref) and same_bits(one[4], conv_ref)
