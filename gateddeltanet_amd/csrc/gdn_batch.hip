@@ -1102,8 +1102,10 @@ __global__ __launch_bounds__(kT) void k_wy_gram(const float *__restrict__ qn_seg
     }
 }
 
-// One head's chunk for 16 state columns: grid (kHD / kWyCols, kNH), 256
-// threads.  The matrix products run on v_mfma_f32_16x16x4_f32 (FP32
+// One head's recurrence over a segment's chunks for 16 state columns: grid
+// (kHD / kWyCols, kNH), 256 threads, the state tile held in LDS from the
+// first chunk to the last and each chunk's operands loaded into registers
+// while the previous chunk computes.  The matrix products run on v_mfma_f32_16x16x4_f32 (FP32
 // operands and sums; this form is held to a tolerance, not to the step's
 // rounding): Q S and K S (wave w: rows 16 w .. +15 of the chunk, all 256
 // keys), o (wave w: rows 16 w .. +15) and the state update (wave w: state
@@ -1118,10 +1120,10 @@ constexpr int kWyCols = 16;
 constexpr int kS0p = kHD + 4;    // padded key stride of the transposed state tile
 constexpr int kDtp = kMaxB + 4;  // padded token stride of the transposed deltas
 
-__global__ __launch_bounds__(kT) void k_wy_chunk(const float *__restrict__ qkv, const float *__restrict__ qn_all,
-                                                 const float *__restrict__ kn_all, const float *__restrict__ bd,
-                                                 const float *__restrict__ Lg, const float *__restrict__ Mg, int n,
-                                                 float *__restrict__ state, float *__restrict__ attn) {
+__global__ __launch_bounds__(kT) void k_wy_seq(const float *__restrict__ qkv, const float *__restrict__ qn_seg,
+                                               const float *__restrict__ kn_seg, const float *__restrict__ bd_seg,
+                                               const float *__restrict__ L_seg, const float *__restrict__ M_seg,
+                                               int n_total, float *__restrict__ state, float *__restrict__ attn) {
     __shared__ f32x4 rows[kMaxB][kKp];                                   // Q, then K
     __shared__ __attribute__((aligned(16))) float s0t[kWyCols][kS0p];    // state tile, [column][key]
     __shared__ __attribute__((aligned(16))) float lm[kMaxB][kMaxB + 4];  // L, then Mq
@@ -1132,23 +1134,31 @@ __global__ __launch_bounds__(kT) void k_wy_chunk(const float *__restrict__ qkv, 
     __shared__ float glog[kMaxB], fdec[kMaxB];
     const int h = blockIdx.y, c0 = blockIdx.x * kWyCols, t = threadIdx.x, w = t >> 6, lane = t & 63;
     const int li = lane & 15, kk = lane >> 4;  // MFMA operand row/column, k quarter
+    const int chunks = (n_total + kMaxB - 1) / kMaxB;
+    const size_t mat = (size_t)kNH * kMaxB * kMaxB;  // one chunk's L (or Mq), every head
     float *S = state + (size_t)h * kHD * kHD + c0;
-    // every global operand is loaded up front (the workgroup is one wave
-    // per SIMD)
+    auto chunk_len = [&](int c) { return n_total - kMaxB * c < kMaxB ? n_total - kMaxB * c : kMaxB; };
+    // the operands of chunk c into registers (issued a chunk ahead)
     RowStage qst, kst;
     MatStage lst, mst;
-    qst.load(qn_all, h, n);
-    lst.load(Lg + (size_t)h * kMaxB * kMaxB);
-    kst.load(kn_all, h, n);
-    mst.load(Mg + (size_t)h * kMaxB * kMaxB);
-    // v and beta of this lane's D elements of K S: rows 16 w + 4 kk + r, column li
-    float vv[4], beta[4];
+    float vv[4], beta[4], dec = 1.0f;
+    auto load_vb = [&](int c) __attribute__((always_inline)) {
+        const int n = chunk_len(c);
+        const size_t m0 = (size_t)c * kMaxB;
+        // v and beta of this lane's D elements of K S: rows 16 w + 4 kk + r, column li
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int m = 16 * w + 4 * kk + r;
-        vv[r] = m < n ? qkv[((size_t)m * 3 + 2) * kH + h * kHD + c0 + li] : 0.0f;
-        beta[r] = m < n ? bd[m * 16 + 2 * h] : 0.0f;
-    }
+        for (int r = 0; r < 4; ++r) {
+            const int m = 16 * w + 4 * kk + r;
+            vv[r] = m < n ? qkv[((m0 + m) * 3 + 2) * kH + h * kHD + c0 + li] : 0.0f;
+            beta[r] = m < n ? bd_seg[(m0 + m) * 16 + 2 * h] : 0.0f;
+        }
+        dec = lane < n ? bd_seg[(m0 + lane) * 16 + 2 * h + 1] : 1.0f;
+    };
+    qst.load(qn_seg, h, chunk_len(0));
+    lst.load(L_seg + (size_t)h * kMaxB * kMaxB);
+    kst.load(kn_seg, h, chunk_len(0));
+    mst.load(M_seg + (size_t)h * kMaxB * kMaxB);
+    load_vb(0);
     {
         const f32x4 *src = reinterpret_cast<const f32x4 *>(S + (size_t)t * kHD);
         f32x4 v[kWyCols / 4];
@@ -1162,11 +1172,6 @@ __global__ __launch_bounds__(kT) void k_wy_chunk(const float *__restrict__ qkv, 
             s0t[4 * i + 3][t] = v[i].w;
         }
     }
-    qst.store(rows);
-    lst.store(lm);
-    if (t < 64) cum_log_decay(bd, h, n, glog);
-    __syncthreads();
-    if (t < kMaxB) fdec[t] = __expf(glog[n - 1] - glog[t]);
 
     // X S for the staged rows X (Q, then K): rows 16 w .. +15, 256 keys
     const auto xs_mfma = [&]() __attribute__((always_inline)) {
@@ -1183,127 +1188,167 @@ __global__ __launch_bounds__(kT) void k_wy_chunk(const float *__restrict__ qkv, 
         return acc0 + acc1;
     };
 
-    // S^T q for every token
-    {
-        const f32x4 d = xs_mfma();
-#pragma unroll
-        for (int r = 0; r < 4; ++r) qs[16 * w + 4 * kk + r][li] = d[r];
-    }
-    __syncthreads();
-    kst.store(rows);
-    __syncthreads();
-    // S^T k for every token, then b_m = beta_m (v_m - exp(G_m) S^T k_m)
-    {
-        const f32x4 d = xs_mfma();
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = 16 * w + 4 * kk + r;
-            dl[m][li] = m < n ? beta[r] * (vv[r] - __expf(glog[m]) * d[r]) : 0.0f;
+    for (int c = 0; c < chunks; ++c) {
+        const int n = chunk_len(c);
+        const bool more = c + 1 < chunks;
+        const size_t m0 = (size_t)c * kMaxB, m1 = m0 + kMaxB;
+        qst.store(rows);
+        lst.store(lm);
+        if (more) {
+            qst.load(qn_seg + m1 * kH, h, chunk_len(c + 1));
+            lst.load(L_seg + (c + 1) * mat + (size_t)h * kMaxB * kMaxB);
         }
-    }
-    __syncthreads();
+        if (t < 64) {
+            // inclusive prefix sum of log(decay) over the chunk (a decay that
+            // underflowed to 0 is taken as 1e-30: the products it enters are 0
+            // to FP32 either way, and G stays finite)
+            float v = lane < n ? __logf(fmaxf(dec, 1e-30f)) : 0.0f;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const float o = __shfl_up(v, d);
+                if (lane >= d) v += o;
+            }
+            glog[lane] = v;
+        }
+        __syncthreads();
+        if (t < kMaxB) fdec[t] = __expf(glog[n - 1] - glog[t]);
 
-    // delta_m = b_m - sum_{s<m} L[m][s] delta_s: wave w solves columns
-    // 4 w .. 4 w + 3; lane m holds row m of L in registers and, per column,
-    // b_m and the running sum of L[m][s] delta_s.  Step s takes delta_s =
-    // b_s - sum from lane s (a uniform read) and folds L[m][s] delta_s into
-    // every row; L is strictly lower triangular (and zero from row n on), so
-    // rows at or above s add zero and each lane's b - sum ends as its delta.
-    // The four columns' chains interleave, and no step waits on LDS.  (16
-    // lanes per column summing their terms on the DPP path took 8.6 us per
-    // chunk; 8 lanes on two waves 22.7 us.)
-    {
-        float lrow[kMaxB];
+        // S^T q for every token
+        {
+            const f32x4 d = xs_mfma();
 #pragma unroll
-        for (int s4 = 0; s4 < kMaxB / 4; ++s4) {
-            const f32x4 v = *reinterpret_cast<const f32x4 *>(&lm[lane][4 * s4]);
-            lrow[4 * s4] = v.x;
-            lrow[4 * s4 + 1] = v.y;
-            lrow[4 * s4 + 2] = v.z;
-            lrow[4 * s4 + 3] = v.w;
+            for (int r = 0; r < 4; ++r) qs[16 * w + 4 * kk + r][li] = d[r];
         }
-        float bq[4], acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        __syncthreads();
+        kst.store(rows);
+        if (more) kst.load(kn_seg + m1 * kH, h, chunk_len(c + 1));
+        __syncthreads();
+        // S^T k for every token, then b_m = beta_m (v_m - exp(G_m) S^T k_m)
+        {
+            const f32x4 d = xs_mfma();
 #pragma unroll
-        for (int j = 0; j < 4; ++j) bq[j] = dl[lane][4 * w + j];
+            for (int r = 0; r < 4; ++r) {
+                const int m = 16 * w + 4 * kk + r;
+                dl[m][li] = m < n ? beta[r] * (vv[r] - __expf(glog[m]) * d[r]) : 0.0f;
+            }
+        }
+        __syncthreads();
+        if (more) load_vb(c + 1);
+
+        // delta_m = b_m - sum_{s<m} L[m][s] delta_s: wave w solves columns
+        // 4 w .. 4 w + 3; lane m holds row m of L in registers and, per
+        // column, b_m and the running sum of L[m][s] delta_s.  Step s takes
+        // delta_s = b_s - sum from lane s (a uniform read) and folds
+        // L[m][s] delta_s into every row; L is strictly lower triangular
+        // (and zero from row n on), so rows at or above s add zero and each
+        // lane's b - sum ends as its delta.  The four columns' chains
+        // interleave, and no step waits on LDS.  (16 lanes per column
+        // summing their terms on the DPP path took 8.6 us per chunk; 8
+        // lanes on two waves 22.7 us.)
+        {
+            float lrow[kMaxB];
 #pragma unroll
-        for (int sidx = 0; sidx < kMaxB; ++sidx) {
-            if (sidx < n) {
+            for (int s4 = 0; s4 < kMaxB / 4; ++s4) {
+                const f32x4 v = *reinterpret_cast<const f32x4 *>(&lm[lane][4 * s4]);
+                lrow[4 * s4] = v.x;
+                lrow[4 * s4 + 1] = v.y;
+                lrow[4 * s4 + 2] = v.z;
+                lrow[4 * s4 + 3] = v.w;
+            }
+            float bq[4], acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float d = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(bq[j] - acc[j]), sidx));
-                    acc[j] = __builtin_fmaf(lrow[sidx], d, acc[j]);
+            for (int j = 0; j < 4; ++j) bq[j] = dl[lane][4 * w + j];
+#pragma unroll
+            for (int sidx = 0; sidx < kMaxB; ++sidx) {
+                if (sidx < n) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const float d = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(bq[j] - acc[j]), sidx));
+                        acc[j] = __builtin_fmaf(lrow[sidx], d, acc[j]);
+                    }
                 }
             }
-        }
-        // every lane: its delta (zero from row n on), transposed for the
-        // MFMA B operands, and scaled by its decay for the state update
-        const float fd = fdec[lane];
+            // every lane: its delta (zero from row n on), transposed for the
+            // MFMA B operands, and scaled by its decay for the state update
+            const float fd = fdec[lane];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float d = bq[j] - acc[j];
-            dlt[4 * w + j][lane] = d;
-            dft[4 * w + j][lane] = fd * d;
-        }
-    }
-    __syncthreads();
-    mst.store(lm);
-    __syncthreads();
-
-    // o_m = (exp(G_m) S^T q_m + sum_{s<=m} Mq[m][s] delta_s) / 16, rounded:
-    // rows 16 w .. +15
-    {
-        f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
-#pragma unroll
-        for (int g = 0; g < kMaxB / 16; ++g) {
-            const f32x4 xa = *reinterpret_cast<const f32x4 *>(&lm[16 * w + li][16 * g + 4 * kk]);
-            const f32x4 xb = *reinterpret_cast<const f32x4 *>(&dlt[li][16 * g + 4 * kk]);
-            acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.x, xb.x, acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.y, xb.y, acc1, 0, 0, 0);
-            acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.z, xb.z, acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.w, xb.w, acc1, 0, 0, 0);
-        }
-        const f32x4 d = acc0 + acc1;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = 16 * w + 4 * kk + r;
-            if (m < n) {
-                const float o = __expf(glog[m]) * qs[m][li] + d[r];
-                attn[(size_t)m * kH + h * kHD + c0 + li] = rne_bf16(0.0625f * o);
+            for (int j = 0; j < 4; ++j) {
+                const float d = bq[j] - acc[j];
+                dlt[4 * w + j][lane] = d;
+                dft[4 * w + j][lane] = fd * d;
             }
         }
-    }
+        __syncthreads();
+        mst.store(lm);
+        if (more) mst.load(M_seg + (c + 1) * mat + (size_t)h * kMaxB * kMaxB);
+        __syncthreads();
 
-    // S' = exp(G_{n-1}) S + sum_s exp(G_{n-1} - G_s) k_s delta_s^T: state
-    // rows 64 w .. +63 as four 16-row tiles; A[j][s] = k_s[j] (token rows
-    // of the staged K), B[s][c] = exp(G_{n-1} - G_s) delta_s[c]
-    {
-        const float dn = __expf(glog[n - 1]);
-        const float *krow = reinterpret_cast<const float *>(&rows[0][0]);
-#pragma unroll
-        for (int tile = 0; tile < 4; ++tile) {
-            const int j0 = 64 * w + 16 * tile;
+        // o_m = (exp(G_m) S^T q_m + sum_{s<=m} Mq[m][s] delta_s) / 16,
+        // rounded: rows 16 w .. +15
+        {
             f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
 #pragma unroll
             for (int g = 0; g < kMaxB / 16; ++g) {
-                const int sb = 16 * g + 4 * kk;  // this lane's 4 tokens
-                const f32x4 xb = *reinterpret_cast<const f32x4 *>(&dft[li][sb]);
-                const float a0 = krow[(sb + 0) * (4 * kKp) + j0 + li];
-                const float a1 = krow[(sb + 1) * (4 * kKp) + j0 + li];
-                const float a2 = krow[(sb + 2) * (4 * kKp) + j0 + li];
-                const float a3 = krow[(sb + 3) * (4 * kKp) + j0 + li];
-                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, xb.x, acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, xb.y, acc1, 0, 0, 0);
-                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a2, xb.z, acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a3, xb.w, acc1, 0, 0, 0);
+                const f32x4 xa = *reinterpret_cast<const f32x4 *>(&lm[16 * w + li][16 * g + 4 * kk]);
+                const f32x4 xb = *reinterpret_cast<const f32x4 *>(&dlt[li][16 * g + 4 * kk]);
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.x, xb.x, acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.y, xb.y, acc1, 0, 0, 0);
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.z, xb.z, acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.w, xb.w, acc1, 0, 0, 0);
             }
             const f32x4 d = acc0 + acc1;
-            const f32x4 sv = *reinterpret_cast<const f32x4 *>(&s0t[li][j0 + 4 * kk]);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) S[(size_t)(j0 + 4 * kk + r) * kHD + li] = __builtin_fmaf(dn, sv[r], d[r]);
+            for (int r = 0; r < 4; ++r) {
+                const int m = 16 * w + 4 * kk + r;
+                if (m < n) {
+                    const float o = __expf(glog[m]) * qs[m][li] + d[r];
+                    attn[(m0 + m) * kH + h * kHD + c0 + li] = rne_bf16(0.0625f * o);
+                }
+            }
         }
+
+        // S' = exp(G_{n-1}) S + sum_s exp(G_{n-1} - G_s) k_s delta_s^T:
+        // state rows 64 w .. +63 as four 16-row tiles; A[j][s] = k_s[j]
+        // (token rows of the staged K), B[s][c] = exp(G_{n-1} - G_s)
+        // delta_s[c].  Each element is read and rewritten in place by the
+        // lane that owns it.
+        {
+            const float dn = __expf(glog[n - 1]);
+            const float *krow = reinterpret_cast<const float *>(&rows[0][0]);
+#pragma unroll
+            for (int tile = 0; tile < 4; ++tile) {
+                const int j0 = 64 * w + 16 * tile;
+                f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
+#pragma unroll
+                for (int g = 0; g < kMaxB / 16; ++g) {
+                    const int sb = 16 * g + 4 * kk;  // this lane's 4 tokens
+                    const f32x4 xb = *reinterpret_cast<const f32x4 *>(&dft[li][sb]);
+                    const float a0 = krow[(sb + 0) * (4 * kKp) + j0 + li];
+                    const float a1 = krow[(sb + 1) * (4 * kKp) + j0 + li];
+                    const float a2 = krow[(sb + 2) * (4 * kKp) + j0 + li];
+                    const float a3 = krow[(sb + 3) * (4 * kKp) + j0 + li];
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, xb.x, acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, xb.y, acc1, 0, 0, 0);
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a2, xb.z, acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a3, xb.w, acc1, 0, 0, 0);
+                }
+                const f32x4 d = acc0 + acc1;
+                f32x4 *sp = reinterpret_cast<f32x4 *>(&s0t[li][j0 + 4 * kk]);
+                const f32x4 sv = *sp;
+                *sp = (f32x4){__builtin_fmaf(dn, sv[0], d[0]), __builtin_fmaf(dn, sv[1], d[1]),
+                              __builtin_fmaf(dn, sv[2], d[2]), __builtin_fmaf(dn, sv[3], d[3])};
+            }
+        }
+        // the next chunk overwrites rows, lm and the deltas
+        __syncthreads();
+    }
+    {
+        f32x4 *dst = reinterpret_cast<f32x4 *>(S + (size_t)t * kHD);
+#pragma unroll
+        for (int i = 0; i < kWyCols / 4; ++i)
+            dst[i] = (f32x4){s0t[4 * i][t], s0t[4 * i + 1][t], s0t[4 * i + 2][t], s0t[4 * i + 3][t]};
     }
 }
-
 
 // ------------------------------------------------ prefill projections
 //
@@ -1956,10 +2001,9 @@ BNorm seg_norm(GDNBatchEngine *e, const float *y, const float *w, uint16_t *x_ou
 // streams (k_pgemm / k_pgu in place of the step's GEMMs, same sums), the
 // conv across the segment (k_pconv), and the recurrence chunk by chunk of
 // 64 tokens, in token order (k_pqk, k_pscan) or in the WY form (k_wy_gram
-// over every chunk at once, then k_wy_chunk per chunk).
+// over every chunk at once, then k_wy_seq over the chunks in order).
 void enqueue_prefill_segment(GDNBatchEngine *e, int slot, int n, bool last, hipStream_t s) {
     const int blocks = (n + kMaxB - 1) / kMaxB, tiles = (n + kPgTok - 1) / kPgTok;
-    const size_t kq = (size_t)kNH * kMaxB * kMaxB;  // one chunk's L (or Mq)
     BNorm p0 = seg_norm(e, nullptr, b_aux(e, 0) + kAuxAttnNorm, e->s_xh, 0, 0, 0);
     p0.emb = e->emb;
     p0.tok = e->s_tok;
@@ -1977,17 +2021,17 @@ void enqueue_prefill_segment(GDNBatchEngine *e, int slot, int n, bool last, hipS
         if (e->prefill_mode == GDN_PREFILL_CHUNKED)
             hipLaunchKernelGGL(k_wy_gram, dim3(kNH, kMaxB / 16, blocks), dim3(kT), 0, s, e->s_qn, e->s_kn, e->s_bd,
                                n, e->s_wyl, e->s_wym);
-        for (int c = 0; c < blocks; ++c) {
-            const int nc = std::min(kMaxB, n - c * kMaxB);
-            const size_t m0 = (size_t)c * kMaxB;
-            if (e->prefill_mode == GDN_PREFILL_CHUNKED)
-                hipLaunchKernelGGL(k_wy_chunk, dim3(kHD / kWyCols, kNH), dim3(kT), 0, s, e->s_qkv + m0 * 3 * kH,
-                                   e->s_qn + m0 * kH, e->s_kn + m0 * kH, e->s_bd + m0 * 16, e->s_wyl + c * kq,
-                                   e->s_wym + c * kq, nc, st, e->s_attn + m0 * kH);
-            else
+        if (e->prefill_mode == GDN_PREFILL_CHUNKED) {
+            hipLaunchKernelGGL(k_wy_seq, dim3(kHD / kWyCols, kNH), dim3(kT), 0, s, e->s_qkv, e->s_qn, e->s_kn,
+                               e->s_bd, e->s_wyl, e->s_wym, n, st, e->s_attn);
+        } else {
+            for (int c = 0; c < blocks; ++c) {
+                const int nc = std::min(kMaxB, n - c * kMaxB);
+                const size_t m0 = (size_t)c * kMaxB;
                 hipLaunchKernelGGL(k_pscan, dim3(kHD / kScanWgCols, kNH), dim3(kT), 0, s, e->s_qkv + m0 * 3 * kH,
                                    e->s_qn + m0 * kH, e->s_kn + m0 * kH, e->s_alpha + m0 * kNH, e->s_bd + m0 * 16,
                                    nc, st, e->s_attn + m0 * kH);
+            }
         }
         hipLaunchKernelGGL(k_bonorm, dim3(kNH, n), dim3(kT), 0, s, e->s_attn, e->s_gate, e->s_sgate,
                            b_aux(e, l) + kAuxONorm, e->eps, e->s_xo);
