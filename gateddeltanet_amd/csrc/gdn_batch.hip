@@ -1366,6 +1366,10 @@ __global__ __launch_bounds__(kT) void k_wy_seq(const float *__restrict__ qkv, co
 // added in split order, as the step's norm adds k_bgemm's split partials.
 // A prefill therefore still equals the steps bit for bit.
 constexpr int kPgT = 256;  // threads per prefill GEMM workgroup (4 waves)
+#ifndef GDN_PG_DEPTH
+#define GDN_PG_DEPTH 2
+#endif
+constexpr int kPgD = GDN_PG_DEPTH;  // k tiles of operand loads in flight per thread
 constexpr int kPgTok = 128;  // tokens per workgroup (2 X tile blocks)
 constexpr int kSegDefault = 4096;  // prefill tokens per segment by default
 constexpr int kSegMax = 32768;     // largest segment (k_pqk's grid.y holds it)
@@ -1406,7 +1410,7 @@ __global__ __launch_bounds__(kPgT) void k_pgemm(const u32x4 *__restrict__ W, con
                                                 float *__restrict__ y, int n_rows) {
     constexpr int AU = 4 * 2 * 64, BU = 2 * 4 * 64, PT = (AU + BU) / kPgT;
     static_assert(PT == 4 && AU == 2 * kPgT, "two A and two B entries per thread and k tile");
-    static_assert(KT % 2 == 0, "k tiles in pairs");
+    static_assert(KT % kPgD == 0 && kPgD % 2 == 0, "whole groups of kPgD k tiles");
     __shared__ u32x4 stg[2][AU + BU];
     const int t = threadIdx.x, w = t >> 6, l = t & 63, wr = w & 1, wt = w >> 1;
     // entry q = t + 256 i: A (row block q / 128, entry q % 128) for i < 2,
@@ -1424,22 +1428,25 @@ __global__ __launch_bounds__(kPgT) void k_pgemm(const u32x4 *__restrict__ W, con
     f32x4 chain[16], part[16], tot[S > 1 ? 16 : 1];
 #pragma unroll
     for (int b = 0; b < 16; ++b) chain[b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-    u32x4 rg[2][PT];
-    fetch(rg[0], pg_tile<KT, NW, S>(0));
-    fetch(rg[1], pg_tile<KT, NW, S>(1));
-    for (int j0 = 0; j0 < KT; j0 += 2) {
+    u32x4 rg[kPgD][PT];
 #pragma unroll
-        for (int d = 0; d < 2; ++d) {
-            const int j = j0 + d;
+    for (int d = 0; d < kPgD; ++d) fetch(rg[d], pg_tile<KT, NW, S>(d));
+    for (int j0 = 0; j0 < KT; j0 += kPgD) {
 #pragma unroll
-            for (int i = 0; i < PT; ++i) stg[d][t + kPgT * i] = rg[d][i];
-            if (j + 2 < KT) fetch(rg[d], pg_tile<KT, NW, S>(j + 2));
+        for (int d = 0; d < kPgD; ++d) {
+            const int j = j0 + d, sb = d & 1;
+#pragma unroll
+            for (int i = 0; i < PT; ++i) stg[sb][t + kPgT * i] = rg[d][i];
+            // issued on every pass (the last passes re-read the final tile,
+            // unused): a conditional load would make the compiler's wait
+            // for the next stage a wait for every load in flight
+            fetch(rg[d], pg_tile<KT, NW, S>(j + kPgD < KT ? j + kPgD : KT - 1));
             __syncthreads();
             u32x4 fa[4], fb[4];
 #pragma unroll
             for (int f = 0; f < 4; ++f) {
-                fa[f] = stg[d][256 * wr + 64 * f + l];
-                fb[f] = stg[d][AU + 256 * wt + 64 * f + l];
+                fa[f] = stg[sb][256 * wr + 64 * f + l];
+                fb[f] = stg[sb][AU + 256 * wt + 64 * f + l];
             }
 #pragma unroll
             for (int f = 0; f < 4; ++f)
@@ -1472,6 +1479,7 @@ __global__ __launch_bounds__(kPgT) void k_pgu(const u32x4 *__restrict__ W, const
     constexpr int KT = kKtH, NW = kGuWaves;
     constexpr int AU = 2 * kGuTileU4, BU = 2 * 4 * 64, PT = 4;
     static_assert(AU + BU <= PT * kPgT && AU > kPgT && AU + BU > 3 * kPgT, "entries 0, 1 (part), 2, 3 (part)");
+    static_assert(KT % kPgD == 0 && kPgD % 2 == 0, "whole groups of kPgD k tiles");
     __shared__ u32x4 stg[2][AU + BU];
     __shared__ f32x4 red[4][12 * 64];
     const int t = threadIdx.x, w = t >> 6, l = t & 63, wg = w & 1, wt = w >> 1;
@@ -1484,6 +1492,8 @@ __global__ __launch_bounds__(kPgT) void k_pgu(const u32x4 *__restrict__ W, const
     for (int i = 0; i < PT; ++i) {
         const int q = t + kPgT * i;
         live[i] = q < AU + BU;
+        // entries past the end re-read B entry 0 (loaded, not stored), so
+        // every load is unconditional
         if (q < AU) {
             src[i] = W + (size_t)(gb + q / kGuTileU4) * KT * kGuTileU4 + (q % kGuTileU4);
             stride[i] = kGuTileU4;
@@ -1495,8 +1505,7 @@ __global__ __launch_bounds__(kPgT) void k_pgu(const u32x4 *__restrict__ W, const
     }
     auto fetch = [&](u32x4 (&r)[PT], int kt) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < PT; ++i)
-            if (live[i]) r[i] = src[i][(size_t)kt * stride[i]];
+        for (int i = 0; i < PT; ++i) r[i] = src[i][(size_t)kt * stride[i]];
     };
     const bool p2 = (l & 15) < kGuTail2;
     const int o2 = 128 + (p2 ? (l >> 4) * kGuTail2 + (l & 15) : 0);
@@ -1504,24 +1513,24 @@ __global__ __launch_bounds__(kPgT) void k_pgu(const u32x4 *__restrict__ W, const
     f32x4 chain[12], part[12];
 #pragma unroll
     for (int b = 0; b < 12; ++b) chain[b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-    u32x4 rg[2][PT];
-    fetch(rg[0], pg_tile<KT, NW, 1>(0));
-    fetch(rg[1], pg_tile<KT, NW, 1>(1));
-    for (int j0 = 0; j0 < KT; j0 += 2) {
+    u32x4 rg[kPgD][PT];
 #pragma unroll
-        for (int d = 0; d < 2; ++d) {
-            const int j = j0 + d;
+    for (int d = 0; d < kPgD; ++d) fetch(rg[d], pg_tile<KT, NW, 1>(d));
+    for (int j0 = 0; j0 < KT; j0 += kPgD) {
+#pragma unroll
+        for (int d = 0; d < kPgD; ++d) {
+            const int j = j0 + d, sb = d & 1;
 #pragma unroll
             for (int i = 0; i < PT; ++i)
-                if (live[i]) stg[d][t + kPgT * i] = rg[d][i];
-            if (j + 2 < KT) fetch(rg[d], pg_tile<KT, NW, 1>(j + 2));
+                if (live[i]) stg[sb][t + kPgT * i] = rg[d][i];
+            fetch(rg[d], pg_tile<KT, NW, 1>(j + kPgD < KT ? j + kPgD : KT - 1));
             __syncthreads();
             u32x4 fa[3], fb[4];
-            fa[0] = stg[d][wg * kGuTileU4 + l];
-            fa[1] = stg[d][wg * kGuTileU4 + 64 + l];
-            fa[2] = p2 ? stg[d][wg * kGuTileU4 + o2] : zero;
+            fa[0] = stg[sb][wg * kGuTileU4 + l];
+            fa[1] = stg[sb][wg * kGuTileU4 + 64 + l];
+            fa[2] = p2 ? stg[sb][wg * kGuTileU4 + o2] : zero;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) fb[g] = stg[d][AU + 256 * wt + 64 * g + l];
+            for (int g = 0; g < 4; ++g) fb[g] = stg[sb][AU + 256 * wt + 64 * g + l];
 #pragma unroll
             for (int f = 0; f < 3; ++f)
 #pragma unroll
