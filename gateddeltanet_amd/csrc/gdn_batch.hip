@@ -1382,26 +1382,44 @@ __device__ __forceinline__ int pg_tile(int j) {
     return s * KTS + c + NW * i;
 }
 
+// The workgroup's (row tile, token tile).  Workgroups are dealt to the 8
+// XCDs round robin in launch order; when the grid allows, the 32 that one
+// XCD runs together cover 4 row tiles x 8 token tiles (a "super tile"), so
+// that XCD's L2 serves each weight tile to 8 of them and each activation
+// tile to 4.  Otherwise the plain (blockIdx.x, blockIdx.y).
+__device__ __forceinline__ void pg_place(int &rt, int &tt) {
+    const int R = gridDim.x, C = gridDim.y, L = blockIdx.x + R * blockIdx.y;
+    if (R % 4 == 0 && C % 8 == 0 && (R * C) % 256 == 0) {
+        const int x = L & 7, s = L >> 3;
+        const int u = 8 * (s >> 5) + x, q = s & 31, gr = R / 4;
+        rt = 4 * (u % gr) + (q & 3);
+        tt = 8 * (u / gr) + (q >> 2);
+    } else {
+        rt = blockIdx.x;
+        tt = blockIdx.y;
+    }
+}
+
 // Class bookkeeping after k tile j: the class chain joins the split's sum
-// (the first class is taken as it is), the split's sum joins the total.
+// (the first class is taken as it is).  Returns true when the tile closes a
+// split (its sum is complete in part).
 template <int KT, int NW, int S, int NB>
-__device__ __forceinline__ void pg_close(int j, f32x4 (&chain)[NB], f32x4 (&part)[NB], f32x4 (&tot)[NB]) {
+__device__ __forceinline__ bool pg_close(int j, f32x4 (&chain)[NB], f32x4 (&part)[NB]) {
     constexpr int KTS = KT / S, KTW = KTS / NW;
-    if ((j + 1) % KTW != 0) return;
-    const int cls = ((j + 1) / KTW - 1) % NW, sp = j / KTS;
+    if ((j + 1) % KTW != 0) return false;
+    const int cls = ((j + 1) / KTW - 1) % NW;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         part[b] = cls == 0 ? chain[b] : part[b] + chain[b];
         chain[b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
     }
-    if (S > 1 && cls == NW - 1) {
-#pragma unroll
-        for (int b = 0; b < NB; ++b) tot[b] = sp == 0 ? part[b] : tot[b] + part[b];
-    }
+    return cls == NW - 1;
 }
 
-// y[m][row] for rows 128 blockIdx.x .. +127 and tokens 128 blockIdx.y ..
-// +127: the sum k_bgemm<2, KT, NW, S, EPI_RAW> forms for the row (S = 1) or
+// y[m][row] for rows 128 rt .. +127 and tokens 128 tt .. +127 (pg_place):
+// with splits, the running total lives in the output tile itself (each
+// lane rewrites only its own elements, after its own earlier store), so two
+// accumulator sets fit the registers of two workgroups per CU: the sum k_bgemm<2, KT, NW, S, EPI_RAW> forms for the row (S = 1) or
 // the in-order sum of its S split partials.  W in the 32-row block layout
 // ([row block][k tile][2 tiles][64 lanes]); X in 64-token X tile blocks;
 // y has the padded token count's rows.
@@ -1413,21 +1431,28 @@ __global__ __launch_bounds__(kPgT) void k_pgemm(const u32x4 *__restrict__ W, con
     static_assert(KT % kPgD == 0 && kPgD % 2 == 0, "whole groups of kPgD k tiles");
     __shared__ u32x4 stg[2][AU + BU];
     const int t = threadIdx.x, w = t >> 6, l = t & 63, wr = w & 1, wt = w >> 1;
+    int rt, tt;
+    pg_place(rt, tt);
     // entry q = t + 256 i: A (row block q / 128, entry q % 128) for i < 2,
     // else B (token block, entry)
-    const u32x4 *a0 = W + (size_t)(4 * blockIdx.x + t / 128) * KT * 128 + (t % 128);
-    const u32x4 *a1 = W + (size_t)(4 * blockIdx.x + 2 + t / 128) * KT * 128 + (t % 128);
-    const u32x4 *b0 = X + (size_t)(2 * blockIdx.y) * KT * 256 + t;
-    const u32x4 *b1 = X + (size_t)(2 * blockIdx.y + 1) * KT * 256 + t;
+    const u32x4 *a0 = W + (size_t)(4 * rt + t / 128) * KT * 128 + (t % 128);
+    const u32x4 *a1 = W + (size_t)(4 * rt + 2 + t / 128) * KT * 128 + (t % 128);
+    const u32x4 *b0 = X + (size_t)(2 * tt) * KT * 256 + t;
+    const u32x4 *b1 = X + (size_t)(2 * tt + 1) * KT * 256 + t;
     auto fetch = [&](u32x4 (&r)[PT], int kt) __attribute__((always_inline)) {
         r[0] = a0[(size_t)kt * 128];
         r[1] = a1[(size_t)kt * 128];
         r[2] = b0[(size_t)kt * 256];
         r[3] = b1[(size_t)kt * 256];
     };
-    f32x4 chain[16], part[16], tot[S > 1 ? 16 : 1];
+    f32x4 chain[16], part[16];
 #pragma unroll
     for (int b = 0; b < 16; ++b) chain[b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    // row tile f: rows 128 rt + 64 wr + 16 f + 4 (l / 16) .. +3; token
+    // group g: token 128 tt + 64 wt + 16 g + l % 16
+    const int row = 128 * rt + 64 * wr + 4 * (l >> 4);
+    const int m = kPgTok * tt + 64 * wt + (l & 15);
+    auto out = [&](int b) { return reinterpret_cast<f32x4 *>(y + (size_t)(m + 16 * (b & 3)) * n_rows + row + 16 * (b >> 2)); };
     u32x4 rg[kPgD][PT];
 #pragma unroll
     for (int d = 0; d < kPgD; ++d) fetch(rg[d], pg_tile<KT, NW, S>(d));
@@ -1455,24 +1480,18 @@ __global__ __launch_bounds__(kPgT) void k_pgemm(const u32x4 *__restrict__ W, con
                     chain[4 * f + g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                         __builtin_bit_cast(bf16x8, fa[f]), __builtin_bit_cast(bf16x8, fb[g]), chain[4 * f + g], 0,
                         0, 0);
-            if constexpr (S > 1) pg_close<KT, NW, S, 16>(j, chain, part, tot);
-            else pg_close<KT, NW, S, 16>(j, chain, part, part);
+            if (pg_close<KT, NW, S, 16>(j, chain, part)) {
+                // the split's sum joins the total in split order
+                const bool first = j < KT / S;
+#pragma unroll
+                for (int b = 0; b < 16; ++b) *out(b) = first ? part[b] : *out(b) + part[b];
+            }
         }
     }
-    // row tile f: rows 128 bx + 64 wr + 16 f + 4 (l / 16) .. +3; token
-    // group g: token 128 by + 64 wt + 16 g + l % 16
-    const int row = 128 * blockIdx.x + 64 * wr + 4 * (l >> 4);
-    const int m = kPgTok * blockIdx.y + 64 * wt + (l & 15);
-#pragma unroll
-    for (int f = 0; f < 4; ++f)
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-            *reinterpret_cast<f32x4 *>(y + (size_t)(m + 16 * g) * n_rows + row + 16 * f) =
-                S > 1 ? tot[S > 1 ? 4 * f + g : 0] : part[4 * f + g];
 }
 
-// Gate/up + SwiGLU for channel groups 2 blockIdx.x, +1 (k_bgu's layout and
-// sums: four classes of 16 k tiles) and tokens 128 blockIdx.y .. +127 (the
+// Gate/up + SwiGLU for channel groups 2 rt, +1 (k_bgu's layout and sums:
+// four classes of 16 k tiles) and tokens 128 tt .. +127 (pg_place; the
 // first n_tok are written).  Wave w: group w & 1, token block w >> 1.
 __global__ __launch_bounds__(kPgT) void k_pgu(const u32x4 *__restrict__ W, const u32x4 *__restrict__ X,
                                               uint16_t *__restrict__ x_next, int n_tok) {
@@ -1483,7 +1502,9 @@ __global__ __launch_bounds__(kPgT) void k_pgu(const u32x4 *__restrict__ W, const
     __shared__ u32x4 stg[2][AU + BU];
     __shared__ f32x4 red[4][12 * 64];
     const int t = threadIdx.x, w = t >> 6, l = t & 63, wg = w & 1, wt = w >> 1;
-    const int gb = 2 * blockIdx.x;
+    int rt, tt;
+    pg_place(rt, tt);
+    const int gb = 2 * rt;
     // entry q = t + 256 i: A (group q / kGuTileU4) below AU, else B
     const u32x4 *src[PT];
     int stride[PT];
@@ -1499,7 +1520,7 @@ __global__ __launch_bounds__(kPgT) void k_pgu(const u32x4 *__restrict__ W, const
             stride[i] = kGuTileU4;
         } else {
             const int qb = live[i] ? q - AU : 0;
-            src[i] = X + (size_t)(2 * blockIdx.y + qb / 256) * KT * 256 + (qb % 256);
+            src[i] = X + (size_t)(2 * tt + qb / 256) * KT * 256 + (qb % 256);
             stride[i] = 256;
         }
     }
@@ -1538,7 +1559,7 @@ __global__ __launch_bounds__(kPgT) void k_pgu(const u32x4 *__restrict__ W, const
                     chain[4 * f + g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                         __builtin_bit_cast(bf16x8, fa[f]), __builtin_bit_cast(bf16x8, fb[g]), chain[4 * f + g], 0,
                         0, 0);
-            pg_close<KT, NW, 1, 12>(j, chain, part, part);
+            (void)pg_close<KT, NW, 1, 12>(j, chain, part);
         }
     }
 #pragma unroll
@@ -1553,7 +1574,7 @@ __global__ __launch_bounds__(kPgT) void k_pgu(const u32x4 *__restrict__ W, const
         return reinterpret_cast<const float *>(red[w])[4 * ((r * 4 + (m >> 4)) * 64 + (rr >> 2) * 16 + (m & 15)) +
                                                        (rr & 3)];
     };
-    const int mb = kPgTok * blockIdx.y + 64 * wt;
+    const int mb = kPgTok * tt + 64 * wt;
     for (int q = l; q < 64 * (kGuCh / 2); q += 64) {
         const int m = q / (kGuCh / 2), cp = q - m * (kGuCh / 2);
         if (mb + m >= n_tok) continue;
