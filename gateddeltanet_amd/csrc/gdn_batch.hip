@@ -966,7 +966,9 @@ __global__ __launch_bounds__(kT) void k_pscan(const float *__restrict__ qkv, con
 // a_m = exp(G_m - G_s)), and normalised k_m, q_m:
 //   L[m][s]  = beta_m exp(G_m - G_s) (k_m . k_s)      s < m
 //   Mq[m][s] = exp(G_m - G_s) (q_m . k_s)             s <= m
-//   delta_m  = beta_m (v_m - exp(G_m) S^T k_m) - sum_{s<m} L[m][s] delta_s
+//   delta_m  = beta_m (v_m - exp(G_m) S^T k_m) - sum_{s<m} L[m][s] delta_s,
+//              i.e. delta = T b with T = (I + L)^-1 (formed per chunk by
+//              k_wy_inv, chunk.py's solve of the same triangular system)
 //   o_m      = (exp(G_m) S^T q_m + sum_{s<=m} Mq[m][s] delta_s) / 16
 //   S'       = exp(G_{n-1}) S + sum_s exp(G_{n-1} - G_s) k_s delta_s^T
 // which is the per-token recurrence of the decode step unrolled over the
@@ -1102,33 +1104,68 @@ __global__ __launch_bounds__(kT) void k_wy_gram(const float *__restrict__ qn_seg
     }
 }
 
+// T = (I + L)^-1 of one (head, chunk), in place of L: grid (kNH, chunks),
+// one wave.  Lane j forms column j by forward substitution in row order,
+// T[m][j] = [m == j] - sum_{s<m} L[m][s] T[s][j] (s ascending), so the
+// chunk's deltas (I + L) delta = b become one matrix product, delta = T b,
+// off the sequential path.  Rows of L from the chunk's length on are zero,
+// so T is the identity there.
+__global__ __launch_bounds__(64) void k_wy_inv(float *__restrict__ L_seg) {
+    __shared__ __attribute__((aligned(16))) float ls[kMaxB][kMaxB];
+    const int h = blockIdx.x, ch = blockIdx.y, j = threadIdx.x;
+    float *lp = L_seg + ((size_t)ch * kNH + h) * kMaxB * kMaxB;
+#pragma unroll 8
+    for (int m = 0; m < kMaxB; ++m) ls[m][j] = lp[m * kMaxB + j];
+    __syncthreads();
+    // every row runs over all 64 columns (constant bounds, so the column
+    // stays in registers): L[m][s] is exactly zero for s >= m and tc[s] is
+    // still zero there, so those terms add exact zeros after the real ones
+    float tc[kMaxB];
+#pragma unroll
+    for (int m = 0; m < kMaxB; ++m) tc[m] = 0.0f;
+#pragma unroll
+    for (int m = 0; m < kMaxB; ++m) {
+        float acc = m == j ? 1.0f : 0.0f;
+#pragma unroll
+        for (int s4 = 0; s4 < kMaxB; s4 += 4) {
+            const f32x4 lv = *reinterpret_cast<const f32x4 *>(&ls[m][s4]);
+            acc = __builtin_fmaf(-lv.x, tc[s4], acc);
+            acc = __builtin_fmaf(-lv.y, tc[s4 + 1], acc);
+            acc = __builtin_fmaf(-lv.z, tc[s4 + 2], acc);
+            acc = __builtin_fmaf(-lv.w, tc[s4 + 3], acc);
+        }
+        tc[m] = acc;
+    }
+#pragma unroll
+    for (int m = 0; m < kMaxB; ++m) lp[m * kMaxB + j] = tc[m];
+}
+
 // One head's recurrence over a segment's chunks for 16 state columns: grid
 // (kHD / kWyCols, kNH), 256 threads, the state tile held in LDS from the
 // first chunk to the last and each chunk's operands loaded into registers
-// while the previous chunk computes.  The matrix products run on v_mfma_f32_16x16x4_f32 (FP32
-// operands and sums; this form is held to a tolerance, not to the step's
-// rounding): Q S and K S (wave w: rows 16 w .. +15 of the chunk, all 256
-// keys), o (wave w: rows 16 w .. +15) and the state update (wave w: state
-// rows 64 w .. +63).  An MFMA takes A[i][k] from lane i + 16 k and
+// while the previous chunk computes.  The matrix products run on
+// v_mfma_f32_16x16x4_f32 (FP32 operands and sums; this form is held to a
+// tolerance, not to the step's rounding): Q S and K S (wave w: rows 16 w ..
+// +15 of the chunk, all 256 keys), the deltas T b and o (wave w: rows 16 w
+// .. +15) and the state update (wave w: state rows 64 w .. +63).  An MFMA takes A[i][k] from lane i + 16 k and
 // B[k][j] from lane j + 16 k and leaves D[4 (l / 16) + r][l % 16] in
 // component r of lane l.  A lane reads 4 consecutive k values of its row
 // (or column) in one 16-byte LDS read and feeds them to 4 MFMAs, component
 // q to the q-th, so MFMA q of a group sums the k = 4 (4 g + kk) + q; A and B
-// use the same assignment.  The deltas are solved with row m of L and each
-// column's b_m in lane m of one wave.
+// use the same assignment.
 constexpr int kWyCols = 16;
 constexpr int kS0p = kHD + 4;    // padded key stride of the transposed state tile
 constexpr int kDtp = kMaxB + 4;  // padded token stride of the transposed deltas
 
 __global__ __launch_bounds__(kT) void k_wy_seq(const float *__restrict__ qkv, const float *__restrict__ qn_seg,
                                                const float *__restrict__ kn_seg, const float *__restrict__ bd_seg,
-                                               const float *__restrict__ L_seg, const float *__restrict__ M_seg,
+                                               const float *__restrict__ T_seg, const float *__restrict__ M_seg,
                                                int n_total, float *__restrict__ state, float *__restrict__ attn) {
     __shared__ f32x4 rows[kMaxB][kKp];                                   // Q, then K
     __shared__ __attribute__((aligned(16))) float s0t[kWyCols][kS0p];    // state tile, [column][key]
-    __shared__ __attribute__((aligned(16))) float lm[kMaxB][kMaxB + 4];  // L, then Mq
+    __shared__ __attribute__((aligned(16))) float lm[kMaxB][kMaxB + 4];  // T, then Mq
     __shared__ float qs[kMaxB][kWyCols + 1];                             // S^T q
-    __shared__ __attribute__((aligned(16))) float dl[kMaxB][kWyCols];    // b, then delta
+    __shared__ __attribute__((aligned(16))) float bt[kWyCols][kDtp];     // b, [column][token]
     __shared__ __attribute__((aligned(16))) float dlt[kWyCols][kDtp];    // delta, [column][token]
     __shared__ __attribute__((aligned(16))) float dft[kWyCols][kDtp];    // exp(G_{n-1} - G_s) delta_s
     __shared__ float glog[kMaxB], fdec[kMaxB];
@@ -1155,7 +1192,7 @@ __global__ __launch_bounds__(kT) void k_wy_seq(const float *__restrict__ qkv, co
         dec = lane < n ? bd_seg[(m0 + lane) * 16 + 2 * h + 1] : 1.0f;
     };
     qst.load(qn_seg, h, chunk_len(0));
-    lst.load(L_seg + (size_t)h * kMaxB * kMaxB);
+    lst.load(T_seg + (size_t)h * kMaxB * kMaxB);
     kst.load(kn_seg, h, chunk_len(0));
     mst.load(M_seg + (size_t)h * kMaxB * kMaxB);
     load_vb(0);
@@ -1196,7 +1233,7 @@ __global__ __launch_bounds__(kT) void k_wy_seq(const float *__restrict__ qkv, co
         lst.store(lm);
         if (more) {
             qst.load(qn_seg + m1 * kH, h, chunk_len(c + 1));
-            lst.load(L_seg + (c + 1) * mat + (size_t)h * kMaxB * kMaxB);
+            lst.load(T_seg + (c + 1) * mat + (size_t)h * kMaxB * kMaxB);
         }
         if (t < 64) {
             // inclusive prefix sum of log(decay) over the chunk (a decay that
@@ -1226,57 +1263,36 @@ __global__ __launch_bounds__(kT) void k_wy_seq(const float *__restrict__ qkv, co
         // S^T k for every token, then b_m = beta_m (v_m - exp(G_m) S^T k_m)
         {
             const f32x4 d = xs_mfma();
+            f32x4 b;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = 16 * w + 4 * kk + r;
-                dl[m][li] = m < n ? beta[r] * (vv[r] - __expf(glog[m]) * d[r]) : 0.0f;
+                b[r] = m < n ? beta[r] * (vv[r] - __expf(glog[m]) * d[r]) : 0.0f;
             }
+            *reinterpret_cast<f32x4 *>(&bt[li][16 * w + 4 * kk]) = b;
         }
         __syncthreads();
         if (more) load_vb(c + 1);
 
-        // delta_m = b_m - sum_{s<m} L[m][s] delta_s: wave w solves columns
-        // 4 w .. 4 w + 3; lane m holds row m of L in registers and, per
-        // column, b_m and the running sum of L[m][s] delta_s.  Step s takes
-        // delta_s = b_s - sum from lane s (a uniform read) and folds
-        // L[m][s] delta_s into every row; L is strictly lower triangular
-        // (and zero from row n on), so rows at or above s add zero and each
-        // lane's b - sum ends as its delta.  The four columns' chains
-        // interleave, and no step waits on LDS.  (16 lanes per column
-        // summing their terms on the DPP path took 8.6 us per chunk; 8
-        // lanes on two waves 22.7 us.)
+        // delta = T b: rows 16 w .. +15 (zero from row n on, where b is
+        // zero and T the identity), transposed for the MFMA B operands and
+        // scaled by their decay for the state update
         {
-            float lrow[kMaxB];
+            f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
 #pragma unroll
-            for (int s4 = 0; s4 < kMaxB / 4; ++s4) {
-                const f32x4 v = *reinterpret_cast<const f32x4 *>(&lm[lane][4 * s4]);
-                lrow[4 * s4] = v.x;
-                lrow[4 * s4 + 1] = v.y;
-                lrow[4 * s4 + 2] = v.z;
-                lrow[4 * s4 + 3] = v.w;
+            for (int g = 0; g < kMaxB / 16; ++g) {
+                const f32x4 xa = *reinterpret_cast<const f32x4 *>(&lm[16 * w + li][16 * g + 4 * kk]);
+                const f32x4 xb = *reinterpret_cast<const f32x4 *>(&bt[li][16 * g + 4 * kk]);
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.x, xb.x, acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.y, xb.y, acc1, 0, 0, 0);
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.z, xb.z, acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.w, xb.w, acc1, 0, 0, 0);
             }
-            float bq[4], acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) bq[j] = dl[lane][4 * w + j];
-#pragma unroll
-            for (int sidx = 0; sidx < kMaxB; ++sidx) {
-                if (sidx < n) {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const float d = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(bq[j] - acc[j]), sidx));
-                        acc[j] = __builtin_fmaf(lrow[sidx], d, acc[j]);
-                    }
-                }
-            }
-            // every lane: its delta (zero from row n on), transposed for the
-            // MFMA B operands, and scaled by its decay for the state update
-            const float fd = fdec[lane];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float d = bq[j] - acc[j];
-                dlt[4 * w + j][lane] = d;
-                dft[4 * w + j][lane] = fd * d;
-            }
+            const f32x4 d = acc0 + acc1;
+            const int m = 16 * w + 4 * kk;
+            *reinterpret_cast<f32x4 *>(&dlt[li][m]) = d;
+            *reinterpret_cast<f32x4 *>(&dft[li][m]) =
+                (f32x4){fdec[m] * d[0], fdec[m + 1] * d[1], fdec[m + 2] * d[2], fdec[m + 3] * d[3]};
         }
         __syncthreads();
         mst.store(lm);
@@ -2051,6 +2067,8 @@ void enqueue_prefill_segment(GDNBatchEngine *e, int slot, int n, bool last, hipS
         if (e->prefill_mode == GDN_PREFILL_CHUNKED)
             hipLaunchKernelGGL(k_wy_gram, dim3(kNH, kMaxB / 16, blocks), dim3(kT), 0, s, e->s_qn, e->s_kn, e->s_bd,
                                n, e->s_wyl, e->s_wym);
+        if (e->prefill_mode == GDN_PREFILL_CHUNKED)
+            hipLaunchKernelGGL(k_wy_inv, dim3(kNH, blocks), dim3(64), 0, s, e->s_wyl);
         if (e->prefill_mode == GDN_PREFILL_CHUNKED) {
             hipLaunchKernelGGL(k_wy_seq, dim3(kHD / kWyCols, kNH), dim3(kT), 0, s, e->s_qkv, e->s_qn, e->s_kn,
                                e->s_bd, e->s_wyl, e->s_wym, n, st, e->s_attn);
