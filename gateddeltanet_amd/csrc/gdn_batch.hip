@@ -1371,17 +1371,16 @@ __global__ __launch_bounds__(kT) void k_wy_seq(const float *__restrict__ qkv, co
 // A prefill segment runs layer by layer, so each layer's projection weights
 // are read once per segment instead of once per 64 tokens.  k_pgemm and
 // k_pgu form the segment's projections as GEMMs: one workgroup per 128 rows
-// (four 32-row blocks of the weight layout) x 128 tokens (two 64-token X
-// tile blocks), four waves of 64 rows x 64 tokens, the k tile's fragments
-// staged once through LDS (double buffer, two k tiles of loads in flight
-// per thread).  Every output element is formed with the step's operations
+// (four 32-row blocks of the weight layout; gate/up: two channel groups) x
+// 128 tokens (two 64-token X tile blocks), eight waves of 64 rows x 32
+// tokens, the k tile's fragments staged once through LDS (double buffer,
+// two k tiles of loads in flight per thread).  Every output element is formed with the step's operations
 // in the step's order: the same v_mfma_f32_16x16x32_bf16 fragments; the k
 // tiles of class c (c, c + NW, ... within a split) chained from zero in
 // increasing order, as wave c of k_bgemm / k_bgu chains them; the classes
 // added in order, as k_bgemm adds its waves' sums; and the splits' sums
 // added in split order, as the step's norm adds k_bgemm's split partials.
 // A prefill therefore still equals the steps bit for bit.
-constexpr int kPgT = 256;  // threads per prefill GEMM workgroup (4 waves)
 #ifndef GDN_PG_DEPTH
 #define GDN_PG_DEPTH 2
 #endif
@@ -1439,36 +1438,55 @@ __device__ __forceinline__ bool pg_close(int j, f32x4 (&chain)[NB], f32x4 (&part
 // the in-order sum of its S split partials.  W in the 32-row block layout
 // ([row block][k tile][2 tiles][64 lanes]); X in 64-token X tile blocks;
 // y has the padded token count's rows.
+// Waves per k_pgemm workgroup: 8 of 64 rows x 32 tokens (108 VGPRs, four
+// waves per SIMD) measured 98.4k against 95.9k prefill tokens/s for 4 of
+// 64 x 64 (two per SIMD), with twice the LDS fragment reads.
+#ifndef GDN_PG_WAVES
+#define GDN_PG_WAVES 8
+#endif
+constexpr int kPgW = GDN_PG_WAVES;
+
 template <int KT, int NW, int S>
-__global__ __launch_bounds__(kPgT) void k_pgemm(const u32x4 *__restrict__ W, const u32x4 *__restrict__ X,
-                                                float *__restrict__ y, int n_rows) {
-    constexpr int AU = 4 * 2 * 64, BU = 2 * 4 * 64, PT = (AU + BU) / kPgT;
-    static_assert(PT == 4 && AU == 2 * kPgT, "two A and two B entries per thread and k tile");
+__global__ __launch_bounds__(kPgW * 64) void k_pgemm(const u32x4 *__restrict__ W, const u32x4 *__restrict__ X,
+                                                     float *__restrict__ y, int n_rows) {
+    constexpr int GT = kPgW * 64, AU = 4 * 2 * 64, BU = 2 * 4 * 64, PT = (AU + BU) / GT;
+    constexpr int TG = kPgW == 4 ? 4 : 2;  // 16-token groups per wave
+    constexpr int NB = 4 * TG;            // 16 x 16 blocks per wave
+    static_assert(kPgW == 4 || kPgW == 8, "four or eight waves");
     static_assert(KT % kPgD == 0 && kPgD % 2 == 0, "whole groups of kPgD k tiles");
     __shared__ u32x4 stg[2][AU + BU];
     const int t = threadIdx.x, w = t >> 6, l = t & 63, wr = w & 1, wt = w >> 1;
     int rt, tt;
     pg_place(rt, tt);
-    // entry q = t + 256 i: A (row block q / 128, entry q % 128) for i < 2,
+    // entry q = t + GT i: A (row block q / 128, entry q % 128) below AU,
     // else B (token block, entry)
-    const u32x4 *a0 = W + (size_t)(4 * rt + t / 128) * KT * 128 + (t % 128);
-    const u32x4 *a1 = W + (size_t)(4 * rt + 2 + t / 128) * KT * 128 + (t % 128);
-    const u32x4 *b0 = X + (size_t)(2 * tt) * KT * 256 + t;
-    const u32x4 *b1 = X + (size_t)(2 * tt + 1) * KT * 256 + t;
-    auto fetch = [&](u32x4 (&r)[PT], int kt) __attribute__((always_inline)) {
-        r[0] = a0[(size_t)kt * 128];
-        r[1] = a1[(size_t)kt * 128];
-        r[2] = b0[(size_t)kt * 256];
-        r[3] = b1[(size_t)kt * 256];
-    };
-    f32x4 chain[16], part[16];
+    const u32x4 *src[PT];
+    int stride[PT];
 #pragma unroll
-    for (int b = 0; b < 16; ++b) chain[b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < PT; ++i) {
+        const int q = t + GT * i;
+        if (q < AU) {
+            src[i] = W + (size_t)(4 * rt + q / 128) * KT * 128 + (q % 128);
+            stride[i] = 128;
+        } else {
+            src[i] = X + (size_t)(2 * tt + (q - AU) / 256) * KT * 256 + ((q - AU) % 256);
+            stride[i] = 256;
+        }
+    }
+    auto fetch = [&](u32x4 (&r)[PT], int kt) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < PT; ++i) r[i] = src[i][(size_t)kt * stride[i]];
+    };
+    f32x4 chain[NB], part[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) chain[b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
     // row tile f: rows 128 rt + 64 wr + 16 f + 4 (l / 16) .. +3; token
-    // group g: token 128 tt + 64 wt + 16 g + l % 16
+    // group g of the wave: token 128 tt + 16 (TG wt + g) + l % 16
     const int row = 128 * rt + 64 * wr + 4 * (l >> 4);
-    const int m = kPgTok * tt + 64 * wt + (l & 15);
-    auto out = [&](int b) { return reinterpret_cast<f32x4 *>(y + (size_t)(m + 16 * (b & 3)) * n_rows + row + 16 * (b >> 2)); };
+    const int m = kPgTok * tt + 16 * TG * wt + (l & 15);
+    auto out = [&](int b) {
+        return reinterpret_cast<f32x4 *>(y + (size_t)(m + 16 * (b % TG)) * n_rows + row + 16 * (b / TG));
+    };
     u32x4 rg[kPgD][PT];
 #pragma unroll
     for (int d = 0; d < kPgD; ++d) fetch(rg[d], pg_tile<KT, NW, S>(d));
@@ -1477,30 +1495,29 @@ __global__ __launch_bounds__(kPgT) void k_pgemm(const u32x4 *__restrict__ W, con
         for (int d = 0; d < kPgD; ++d) {
             const int j = j0 + d, sb = d & 1;
 #pragma unroll
-            for (int i = 0; i < PT; ++i) stg[sb][t + kPgT * i] = rg[d][i];
+            for (int i = 0; i < PT; ++i) stg[sb][t + GT * i] = rg[d][i];
             // issued on every pass (the last passes re-read the final tile,
             // unused): a conditional load would make the compiler's wait
             // for the next stage a wait for every load in flight
             fetch(rg[d], pg_tile<KT, NW, S>(j + kPgD < KT ? j + kPgD : KT - 1));
             __syncthreads();
-            u32x4 fa[4], fb[4];
+            u32x4 fa[4], fb[TG];
 #pragma unroll
-            for (int f = 0; f < 4; ++f) {
-                fa[f] = stg[sb][256 * wr + 64 * f + l];
-                fb[f] = stg[sb][AU + 256 * wt + 64 * f + l];
-            }
+            for (int f = 0; f < 4; ++f) fa[f] = stg[sb][256 * wr + 64 * f + l];
+#pragma unroll
+            for (int g = 0; g < TG; ++g) fb[g] = stg[sb][AU + 64 * (TG * wt + g) + l];
 #pragma unroll
             for (int f = 0; f < 4; ++f)
 #pragma unroll
-                for (int g = 0; g < 4; ++g)
-                    chain[4 * f + g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        __builtin_bit_cast(bf16x8, fa[f]), __builtin_bit_cast(bf16x8, fb[g]), chain[4 * f + g], 0,
+                for (int g = 0; g < TG; ++g)
+                    chain[TG * f + g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(bf16x8, fa[f]), __builtin_bit_cast(bf16x8, fb[g]), chain[TG * f + g], 0,
                         0, 0);
-            if (pg_close<KT, NW, S, 16>(j, chain, part)) {
+            if (pg_close<KT, NW, S, NB>(j, chain, part)) {
                 // the split's sum joins the total in split order
                 const bool first = j < KT / S;
 #pragma unroll
-                for (int b = 0; b < 16; ++b) *out(b) = first ? part[b] : *out(b) + part[b];
+                for (int b = 0; b < NB; ++b) *out(b) = first ? part[b] : *out(b) + part[b];
             }
         }
     }
@@ -1509,25 +1526,27 @@ __global__ __launch_bounds__(kPgT) void k_pgemm(const u32x4 *__restrict__ W, con
 // Gate/up + SwiGLU for channel groups 2 rt, +1 (k_bgu's layout and sums:
 // four classes of 16 k tiles) and tokens 128 tt .. +127 (pg_place; the
 // first n_tok are written).  Wave w: group w & 1, token block w >> 1.
-__global__ __launch_bounds__(kPgT) void k_pgu(const u32x4 *__restrict__ W, const u32x4 *__restrict__ X,
-                                              uint16_t *__restrict__ x_next, int n_tok) {
-    constexpr int KT = kKtH, NW = kGuWaves;
-    constexpr int AU = 2 * kGuTileU4, BU = 2 * 4 * 64, PT = 4;
-    static_assert(AU + BU <= PT * kPgT && AU > kPgT && AU + BU > 3 * kPgT, "entries 0, 1 (part), 2, 3 (part)");
+__global__ __launch_bounds__(kPgW * 64) void k_pgu(const u32x4 *__restrict__ W, const u32x4 *__restrict__ X,
+                                                   uint16_t *__restrict__ x_next, int n_tok) {
+    constexpr int KT = kKtH, NW = kGuWaves, GT = kPgW * 64;
+    constexpr int AU = 2 * kGuTileU4, BU = 2 * 4 * 64, PT = (AU + BU + GT - 1) / GT;
+    constexpr int TG = kPgW == 4 ? 4 : 2;  // 16-token groups per wave
+    constexpr int NB = 3 * TG;            // 16 x 16 blocks per wave
+    static_assert(kPgW == 4 || kPgW == 8, "four or eight waves");
     static_assert(KT % kPgD == 0 && kPgD % 2 == 0, "whole groups of kPgD k tiles");
     __shared__ u32x4 stg[2][AU + BU];
-    __shared__ f32x4 red[4][12 * 64];
+    __shared__ f32x4 red[kPgW][NB * 64];
     const int t = threadIdx.x, w = t >> 6, l = t & 63, wg = w & 1, wt = w >> 1;
     int rt, tt;
     pg_place(rt, tt);
     const int gb = 2 * rt;
-    // entry q = t + 256 i: A (group q / kGuTileU4) below AU, else B
+    // entry q = t + GT i: A (group q / kGuTileU4) below AU, else B
     const u32x4 *src[PT];
     int stride[PT];
     bool live[PT];
 #pragma unroll
     for (int i = 0; i < PT; ++i) {
-        const int q = t + kPgT * i;
+        const int q = t + GT * i;
         live[i] = q < AU + BU;
         // entries past the end re-read B entry 0 (loaded, not stored), so
         // every load is unconditional
@@ -1547,9 +1566,9 @@ __global__ __launch_bounds__(kPgT) void k_pgu(const u32x4 *__restrict__ W, const
     const bool p2 = (l & 15) < kGuTail2;
     const int o2 = 128 + (p2 ? (l >> 4) * kGuTail2 + (l & 15) : 0);
     const u32x4 zero = {0u, 0u, 0u, 0u};
-    f32x4 chain[12], part[12];
+    f32x4 chain[NB], part[NB];
 #pragma unroll
-    for (int b = 0; b < 12; ++b) chain[b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int b = 0; b < NB; ++b) chain[b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
     u32x4 rg[kPgD][PT];
 #pragma unroll
     for (int d = 0; d < kPgD; ++d) fetch(rg[d], pg_tile<KT, NW, 1>(d));
@@ -1559,39 +1578,39 @@ __global__ __launch_bounds__(kPgT) void k_pgu(const u32x4 *__restrict__ W, const
             const int j = j0 + d, sb = d & 1;
 #pragma unroll
             for (int i = 0; i < PT; ++i)
-                if (live[i]) stg[sb][t + kPgT * i] = rg[d][i];
+                if (live[i]) stg[sb][t + GT * i] = rg[d][i];
             fetch(rg[d], pg_tile<KT, NW, 1>(j + kPgD < KT ? j + kPgD : KT - 1));
             __syncthreads();
-            u32x4 fa[3], fb[4];
+            u32x4 fa[3], fb[TG];
             fa[0] = stg[sb][wg * kGuTileU4 + l];
             fa[1] = stg[sb][wg * kGuTileU4 + 64 + l];
             fa[2] = p2 ? stg[sb][wg * kGuTileU4 + o2] : zero;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) fb[g] = stg[sb][AU + 256 * wt + 64 * g + l];
+            for (int g = 0; g < TG; ++g) fb[g] = stg[sb][AU + 64 * (TG * wt + g) + l];
 #pragma unroll
             for (int f = 0; f < 3; ++f)
 #pragma unroll
-                for (int g = 0; g < 4; ++g)
-                    chain[4 * f + g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        __builtin_bit_cast(bf16x8, fa[f]), __builtin_bit_cast(bf16x8, fb[g]), chain[4 * f + g], 0,
+                for (int g = 0; g < TG; ++g)
+                    chain[TG * f + g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(bf16x8, fa[f]), __builtin_bit_cast(bf16x8, fb[g]), chain[TG * f + g], 0,
                         0, 0);
-            (void)pg_close<KT, NW, 1, 12>(j, chain, part);
+            (void)pg_close<KT, NW, 1, NB>(j, chain, part);
         }
     }
 #pragma unroll
-    for (int b = 0; b < 12; ++b) red[w][b * 64 + l] = part[b];
+    for (int b = 0; b < NB; ++b) red[w][b * 64 + l] = part[b];
     // the wave reads only its own sums
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // row rr of tile r, token m of the block: lane (rr / 4) * 16 + m % 16 of
+    // row rr of tile r, token m of the wave: lane (rr / 4) * 16 + m % 16 of
     // token group m / 16, component rr % 4 (k_bgu's val)
     auto val = [&](int r, int rr, int m) {
-        return reinterpret_cast<const float *>(red[w])[4 * ((r * 4 + (m >> 4)) * 64 + (rr >> 2) * 16 + (m & 15)) +
+        return reinterpret_cast<const float *>(red[w])[4 * ((r * TG + (m >> 4)) * 64 + (rr >> 2) * 16 + (m & 15)) +
                                                        (rr & 3)];
     };
-    const int mb = kPgTok * tt + 64 * wt;
-    for (int q = l; q < 64 * (kGuCh / 2); q += 64) {
+    const int mb = kPgTok * tt + 16 * TG * wt;
+    for (int q = l; q < 16 * TG * (kGuCh / 2); q += 64) {
         const int m = q / (kGuCh / 2), cp = q - m * (kGuCh / 2);
         if (mb + m >= n_tok) continue;
         uint32_t packed = 0;
@@ -2059,7 +2078,7 @@ void enqueue_prefill_segment(GDNBatchEngine *e, int slot, int n, bool last, hipS
     for (int l = 0; l < e->layers; ++l) {
         float *st = b_state(e, l) + (size_t)slot * kLayerState;
         uint16_t *tl = b_tails(e, l) + (size_t)slot * kStreamTails;
-        hipLaunchKernelGGL((k_pgemm<kKtH, 8, 1>), dim3(4 * kH / 128, tiles), dim3(kPgT), 0, s, e->w_qkvg[l], xh,
+        hipLaunchKernelGGL((k_pgemm<kKtH, 8, 1>), dim3(4 * kH / 128, tiles), dim3(kPgW * 64), 0, s, e->w_qkvg[l], xh,
                            e->s_y, 4 * kH);
         hipLaunchKernelGGL(k_pconv, dim3(4 * kH / 64, blocks), dim3(kConvT), 0, s, e->s_y, n, tl,
                            b_aux(e, l) + kAuxConv, e->s_qkv, e->s_gate, e->s_sgate);
@@ -2083,12 +2102,12 @@ void enqueue_prefill_segment(GDNBatchEngine *e, int slot, int n, bool last, hipS
         }
         hipLaunchKernelGGL(k_bonorm, dim3(kNH, n), dim3(kT), 0, s, e->s_attn, e->s_gate, e->s_sgate,
                            b_aux(e, l) + kAuxONorm, e->eps, e->s_xo);
-        hipLaunchKernelGGL((k_pgemm<kKtH, 4, kSplitO>), dim3(kH / 128, tiles), dim3(kPgT), 0, s, e->w_o[l], xo,
+        hipLaunchKernelGGL((k_pgemm<kKtH, 4, kSplitO>), dim3(kH / 128, tiles), dim3(kPgW * 64), 0, s, e->w_o[l], xo,
                            e->s_y, kH);
         const BNorm pm = seg_norm(e, e->s_y, b_aux(e, l) + kAuxMlpNorm, e->s_xh, -1, l, l);
         hipLaunchKernelGGL((k_bnorm<1, false, false>), dim3(n), dim3(kT), 0, s, pm);
-        hipLaunchKernelGGL(k_pgu, dim3(kGuWgs / 2, tiles), dim3(kPgT), 0, s, e->w_gu[l], xh, e->s_xd, n);
-        hipLaunchKernelGGL((k_pgemm<kKtI, 4, kSplitDown>), dim3(kH / 128, tiles), dim3(kPgT), 0, s, e->w_down[l],
+        hipLaunchKernelGGL(k_pgu, dim3(kGuWgs / 2, tiles), dim3(kPgW * 64), 0, s, e->w_gu[l], xh, e->s_xd, n);
+        hipLaunchKernelGGL((k_pgemm<kKtI, 4, kSplitDown>), dim3(kH / 128, tiles), dim3(kPgW * 64), 0, s, e->w_down[l],
                            xd, e->s_y, kH);
         if (l + 1 < e->layers) {
             const BNorm pa = seg_norm(e, e->s_y, b_aux(e, l + 1) + kAuxAttnNorm, e->s_xh, l + 1, l, l + 1);
@@ -2467,13 +2486,13 @@ int gdn_test_prefill_gemm(int kind, const float *W, const float *X, uint32_t N, 
     GDN_HIP(hipMemcpy(dx, xt.data(), xt.size() * 2, hipMemcpyHostToDevice));
     const u32x4 *w4 = static_cast<const u32x4 *>(dw), *x4 = static_cast<const u32x4 *>(dx);
     const dim3 pg(N / 128, tp / kPgTok);
-    if (kind == 0) hipLaunchKernelGGL((k_pgemm<kKtH, 8, 1>), pg, dim3(kPgT), 0, 0, w4, x4, (float *)dy, (int)N);
+    if (kind == 0) hipLaunchKernelGGL((k_pgemm<kKtH, 8, 1>), pg, dim3(kPgW * 64), 0, 0, w4, x4, (float *)dy, (int)N);
     if (kind == 1)
-        hipLaunchKernelGGL((k_pgemm<kKtH, 4, kSplitO>), pg, dim3(kPgT), 0, 0, w4, x4, (float *)dy, (int)N);
+        hipLaunchKernelGGL((k_pgemm<kKtH, 4, kSplitO>), pg, dim3(kPgW * 64), 0, 0, w4, x4, (float *)dy, (int)N);
     if (kind == 2)
-        hipLaunchKernelGGL((k_pgemm<kKtI, 4, kSplitDown>), pg, dim3(kPgT), 0, 0, w4, x4, (float *)dy, (int)N);
+        hipLaunchKernelGGL((k_pgemm<kKtI, 4, kSplitDown>), pg, dim3(kPgW * 64), 0, 0, w4, x4, (float *)dy, (int)N);
     if (kind == 3)
-        hipLaunchKernelGGL(k_pgu, dim3(kGuWgs / 2, tp / kPgTok), dim3(kPgT), 0, 0, w4, x4,
+        hipLaunchKernelGGL(k_pgu, dim3(kGuWgs / 2, tp / kPgTok), dim3(kPgW * 64), 0, 0, w4, x4,
                            static_cast<uint16_t *>(dy), (int)T);
     // the step's kernels, one 64-token block at a time
     for (uint32_t b = 0; b < blocks; ++b) {
