@@ -769,8 +769,11 @@ __global__ __launch_bounds__(kConvT) void k_pconv(const float *__restrict__ raw,
                                                   float *__restrict__ gate, float *__restrict__ sgate) {
     constexpr int MG = kConvT / 64;  // tokens in flight per channel
     __shared__ float xs[kMaxB + 3][64];
+    __shared__ uint64_t exp2_lds[32];  // expf's table, read per SiLU / sigmoid
     const int row0 = blockIdx.x * 64, t = threadIdx.x, cl = t & 63, mg = t >> 6;
     const int m0 = (int)blockIdx.y * kMaxB, nb = n - m0 < kMaxB ? n - m0 : kMaxB;
+    fill_exp2_lds_imm(exp2_lds);
+    const Exp2Lds tab{exp2_lds};
     const int row = row0 + cl, which = row0 / kH, c = row - which * kH;
     if (which < 3) {
         uint16_t *tl = tails + (size_t)which * 3 * kH + c;
@@ -790,7 +793,7 @@ __global__ __launch_bounds__(kConvT) void k_pconv(const float *__restrict__ raw,
         for (int m = mg; m < nb; m += MG) {
             // gdn_depthwise_conv_silu_head_kind, gdn_model.cpp:1543-1667
             const float sum = xs[m][cl] * cw.x + xs[m + 1][cl] * cw.y + xs[m + 2][cl] * cw.z + xs[m + 3][cl] * cw.w;
-            qkv[((size_t)(m0 + m) * 3 + which) * kH + c] = rne_bf16(silu_ref(sum));
+            qkv[((size_t)(m0 + m) * 3 + which) * kH + c] = rne_bf16(silu_ref(sum, tab));
         }
         if (t < 64 && m0 == 0) {
             if (n <= kMaxB) {
@@ -803,10 +806,11 @@ __global__ __launch_bounds__(kConvT) void k_pconv(const float *__restrict__ raw,
             }
         }
     } else {
+        __syncthreads();
         for (int m = mg; m < nb; m += MG) {
             const float g = rne_bf16(raw[(size_t)(m0 + m) * 4 * kH + row]);
             gate[(size_t)(m0 + m) * kH + c] = g;
-            sgate[(size_t)(m0 + m) * kH + c] = sigmoid_ref(g);
+            sgate[(size_t)(m0 + m) * kH + c] = sigmoid_ref(g, tab);
         }
     }
 }
@@ -1536,10 +1540,12 @@ __global__ __launch_bounds__(kPgW * 64) void k_pgu(const u32x4 *__restrict__ W, 
     static_assert(KT % kPgD == 0 && kPgD % 2 == 0, "whole groups of kPgD k tiles");
     __shared__ u32x4 stg[2][AU + BU];
     __shared__ f32x4 red[kPgW][NB * 64];
+    __shared__ uint64_t exp2_lds[32];  // expf's table for the SwiGLU epilogue
     const int t = threadIdx.x, w = t >> 6, l = t & 63, wg = w & 1, wt = w >> 1;
     int rt, tt;
     pg_place(rt, tt);
     const int gb = 2 * rt;
+    fill_exp2_lds_imm(exp2_lds);
     // entry q = t + GT i: A (group q / kGuTileU4) below AU, else B
     const u32x4 *src[PT];
     int stride[PT];
@@ -1619,7 +1625,7 @@ __global__ __launch_bounds__(kPgW * 64) void k_pgu(const u32x4 *__restrict__ W, 
             const int cc = 2 * cp + e;
             const float g = rne_bf16(cc < 16 ? val(0, cc, m) : val(2, cc - 16, m));
             const float u = rne_bf16(cc < 16 ? val(1, cc, m) : val(2, cc - 16 + (kGuCh - 16), m));
-            packed |= bf16_daz_bits(rne_bf16(silu_ref(g) * u)) << (16 * e);
+            packed |= bf16_daz_bits(rne_bf16(silu_ref(g, Exp2Lds{exp2_lds}) * u)) << (16 * e);
         }
         *reinterpret_cast<uint32_t *>(x_next + xt_index(mb + m, (gb + wg) * kGuCh + 2 * cp, kI)) = packed;
     }
