@@ -129,6 +129,8 @@ __global__ __launch_bounds__(NW * 64) void k_bgemm(const u32x4 *__restrict__ W, 
     __shared__ f32x4 red[NW * RT * 4 * 64];
     __shared__ float lm_v[RT * 4][64];
     __shared__ int lm_i[RT * 4][64];
+    __shared__ uint64_t exp2_lds[EPI == EPI_QKVG ? 32 : 1];  // expf's table for the epilogue
+    if constexpr (EPI == EPI_QKVG) fill_exp2_lds_imm(exp2_lds);
     // QKVG: consecutive row blocks on one XCD (workgroups are dealt to the 8
     // XCDs round-robin), so the two 64-byte halves of a conv-tail line are
     // fetched into one XCD's L2 once instead of into two
@@ -265,10 +267,10 @@ __global__ __launch_bounds__(NW * 64) void k_bgemm(const u32x4 *__restrict__ W, 
                 tl[0] = bf16_hi(tv.y);
                 tl[kH] = bf16_hi(tv.z);
                 tl[2 * kH] = bf16_hi(raw);
-                ep.qkv[((size_t)m * 3 + which) * kH + c] = rne_bf16(silu_ref(sum));
+                ep.qkv[((size_t)m * 3 + which) * kH + c] = rne_bf16(silu_ref(sum, Exp2Lds{exp2_lds}));
             } else {
                 ep.gate[(size_t)m * kH + c] = raw;
-                ep.sgate[(size_t)m * kH + c] = sigmoid_ref(raw);
+                ep.sgate[(size_t)m * kH + c] = sigmoid_ref(raw, Exp2Lds{exp2_lds});
             }
         }
     }
@@ -319,7 +321,9 @@ __global__ __launch_bounds__(NW * 64) void k_bgu(const u32x4 *__restrict__ W, co
     constexpr int D = KTW < 4 ? KTW : 4;
     constexpr size_t WSTEP = (size_t)NW * kGuTileU4, XSTEP = (size_t)NW * 4 * 64;
     __shared__ f32x4 red[NW * RT * 4 * 64];
+    __shared__ uint64_t exp2_lds[32];  // expf's table for the SwiGLU epilogue
     const int t = threadIdx.x, w = t >> 6, l = t & 63, rb = blockIdx.x;
+    fill_exp2_lds_imm(exp2_lds);
     // the 12-row tile: lanes of rows 12..15 read entry 0 (in bounds) and
     // zero it
     const bool p2 = (l & 15) < kGuTail2;
@@ -390,7 +394,7 @@ __global__ __launch_bounds__(NW * 64) void k_bgu(const u32x4 *__restrict__ W, co
             const int cc = 2 * cp + e;
             const float g = rne_bf16(cc < 16 ? val(0, cc, m) : val(2, cc - 16, m));
             const float u = rne_bf16(cc < 16 ? val(1, cc, m) : val(2, cc - 16 + (kGuCh - 16), m));
-            packed |= bf16_daz_bits(rne_bf16(silu_ref(g) * u)) << (16 * e);
+            packed |= bf16_daz_bits(rne_bf16(silu_ref(g, Exp2Lds{exp2_lds}) * u)) << (16 * e);
         }
         *reinterpret_cast<uint32_t *>(x_next + xt_index(m, rb * kGuCh + 2 * cp, kI)) = packed;
     }
