@@ -631,6 +631,77 @@ __global__ __launch_bounds__(kT) void k_bnorm(BNorm p) {
     }
 }
 
+// The a/b rows and beta/decay of kPabTok tokens per workgroup, from their
+// normalised inputs (the prefill's split of k_bnorm's AB part, whose
+// workgroups each re-read their 32 KB of rows): grid (kAbSplit, ceil(n /
+// kPabTok)).  Workgroup j loads its four rows once.  Per token the thread
+// tasks, products, quad sums, the 64-beat chains and the head scalars are
+// k_bnorm's, so every value is the step's.
+constexpr int kPabTok = 16;
+__global__ __launch_bounds__(kT) void k_pab(const float *__restrict__ xn, int n, const float *__restrict__ ab_w,
+                                            const float *__restrict__ a_log, const float *__restrict__ dt_bias,
+                                            float *__restrict__ bd) {
+    constexpr int ABR = 2 * kAbHeads, ABN = ABR * kH / (4 * kT);
+    static_assert(kPabTok * ABR <= kT, "one chain thread per (token, row)");
+    __shared__ __attribute__((aligned(16))) float tab[kPabTok][ABR][64][2];
+    __shared__ float abv[kPabTok][ABR];
+    __shared__ uint64_t exp2_lds[32];
+    const int j = blockIdx.x, m0 = (int)blockIdx.y * kPabTok, t = threadIdx.x;
+    fill_exp2_lds_imm(exp2_lds);
+    // local row r: the a row of head kAbHeads j + r (r < kAbHeads), else the
+    // b row of head kAbHeads j + r - kAbHeads
+    auto ab_row = [&](int r) { return r < kAbHeads ? kAbHeads * j + r : kNH + kAbHeads * j + r - kAbHeads; };
+    f32x4 wq[ABN];
+#pragma unroll
+    for (int i = 0; i < ABN; ++i) {
+        const int q = t + kT * i, grp = q >> 3, sub = q & 7;
+        wq[i] = *reinterpret_cast<const f32x4 *>(ab_w + (size_t)ab_row(grp >> 6) * kH + 32 * (grp & 63) + 4 * sub);
+    }
+    for (int mt = 0; mt < kPabTok && m0 + mt < n; ++mt) {
+        const float *x = xn + (size_t)(m0 + mt) * kH;
+#pragma unroll
+        for (int i = 0; i < ABN; ++i) {
+            const int q = t + kT * i, grp = q >> 3, sub = q & 7;
+            const f32x4 xq = *reinterpret_cast<const f32x4 *>(x + 32 * (grp & 63) + 4 * sub);
+            const f32x4 w = wq[i];
+            float s = (xq.x * w.x + xq.y * w.y) + (xq.z * w.z + xq.w * w.w);
+            s = quad_sum(s);
+            if ((sub & 3) == 0) tab[mt][grp >> 6][grp & 63][sub >> 2] = s;
+        }
+    }
+    __syncthreads();
+    if (t < kPabTok * ABR) {
+        const int mt = t / ABR, r = t % ABR;
+        if (m0 + mt < n) {
+            float v[128];
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                const f32x4 q = reinterpret_cast<const f32x4 *>(&tab[mt][r][0][0])[i];
+                v[4 * i] = q.x;
+                v[4 * i + 1] = q.y;
+                v[4 * i + 2] = q.z;
+                v[4 * i + 3] = q.w;
+            }
+            float acc = 0.0f;
+#pragma unroll
+            for (int bt = 0; bt < 64; ++bt) acc = (acc + v[2 * bt]) + v[2 * bt + 1];
+            abv[mt][r] = rne_bf16(acc);
+        }
+    }
+    __syncthreads();
+    if (t < kPabTok * kAbHeads) {
+        const int mt = t / kAbHeads, hh = t % kAbHeads, m = m0 + mt;
+        if (m < n) {
+            const int hd = kAbHeads * j + hh;
+            float beta, decay;
+            head_scalars(abv[mt][hh], abv[mt][kAbHeads + hh], a_log[hd], dt_bias[hd], beta, decay,
+                         Exp2Lds{exp2_lds});
+            bd[m * 16 + 2 * hd] = beta;
+            bd[m * 16 + 2 * hd + 1] = decay;
+        }
+    }
+}
+
 // Per (head, stream): the output RMSNorm times the gate and sigmoid(gate)
 // (gdn_output_norm_and_gate, gdn_model.cpp:3226-3349) into X tiles.
 __global__ __launch_bounds__(kT) void k_bonorm(const float *__restrict__ attn, const float *__restrict__ gate,
@@ -2073,16 +2144,26 @@ BNorm seg_norm(GDNBatchEngine *e, const float *y, const float *w, uint16_t *x_ou
 
 // One prefill segment of n tokens (already in s_tok[0..n)) through stream
 // `slot`'s state, layer by layer: the step's kernels with the tokens as the
-// streams (k_pgemm / k_pgu in place of the step's GEMMs, same sums), the
-// conv across the segment (k_pconv), and the recurrence chunk by chunk of
-// 64 tokens, in token order (k_pqk, k_pscan) or in the WY form (k_wy_gram
-// over every chunk at once, then k_wy_seq over the chunks in order).
+// streams (k_pgemm / k_pgu in place of the step's GEMMs, k_bnorm + k_pab in
+// place of the split a/b norm; same sums), the conv across the segment
+// (k_pconv), and the recurrence chunk by chunk of 64 tokens, in token order
+// (k_pqk, k_pscan) or in the WY form (k_wy_gram and k_wy_inv over every
+// chunk at once, then k_wy_seq over the chunks in order).
 void enqueue_prefill_segment(GDNBatchEngine *e, int slot, int n, bool last, hipStream_t s) {
     const int blocks = (n + kMaxB - 1) / kMaxB, tiles = (n + kPgTok - 1) / kPgTok;
-    BNorm p0 = seg_norm(e, nullptr, b_aux(e, 0) + kAuxAttnNorm, e->s_xh, 0, 0, 0);
+    const int pab_blocks = (n + kPabTok - 1) / kPabTok;
+    // a norm's a/b rows and beta/decay, from its normalised copy in s_xn
+    auto launch_ab = [&](int l_ab) {
+        const float *a = b_aux(e, l_ab);
+        hipLaunchKernelGGL(k_pab, dim3(kAbSplit, pab_blocks), dim3(kT), 0, s, e->s_xn, n, a + kAuxAB, a + kAuxALog,
+                           a + kAuxDtBias, e->s_bd);
+    };
+    BNorm p0 = seg_norm(e, nullptr, b_aux(e, 0) + kAuxAttnNorm, e->s_xh, -1, 0, 0);
     p0.emb = e->emb;
     p0.tok = e->s_tok;
-    hipLaunchKernelGGL((k_bnorm<0, true, true>), dim3(n, kAbSplit), dim3(kT), 0, s, p0);
+    p0.xn_out = e->s_xn;
+    hipLaunchKernelGGL((k_bnorm<0, true, false>), dim3(n), dim3(kT), 0, s, p0);
+    launch_ab(0);
     const u32x4 *xh = reinterpret_cast<const u32x4 *>(e->s_xh), *xo = reinterpret_cast<const u32x4 *>(e->s_xo),
                 *xd = reinterpret_cast<const u32x4 *>(e->s_xd);
     for (int l = 0; l < e->layers; ++l) {
@@ -2120,8 +2201,10 @@ void enqueue_prefill_segment(GDNBatchEngine *e, int slot, int n, bool last, hipS
         hipLaunchKernelGGL((k_pgemm<kKtI, 4, kSplitDown>), dim3(kH / 128, tiles), dim3(kPgW * 64), 0, s, e->w_down[l],
                            xd, e->s_y, kH);
         if (l + 1 < e->layers) {
-            const BNorm pa = seg_norm(e, e->s_y, b_aux(e, l + 1) + kAuxAttnNorm, e->s_xh, l + 1, l, l + 1);
-            hipLaunchKernelGGL((k_bnorm<1, false, true>), dim3(n, kAbSplit), dim3(kT), 0, s, pa);
+            BNorm pa = seg_norm(e, e->s_y, b_aux(e, l + 1) + kAuxAttnNorm, e->s_xh, -1, l, l + 1);
+            pa.xn_out = e->s_xn;
+            hipLaunchKernelGGL((k_bnorm<1, false, false>), dim3(n), dim3(kT), 0, s, pa);
+            launch_ab(l + 1);
         } else {
             BNorm pf = seg_norm(e, e->s_y, e->aux + (size_t)e->layers * kAuxLayer, e->s_xh, -1, l, l);
             pf.xn_out = e->s_xn;
