@@ -916,11 +916,14 @@ __global__ __launch_bounds__(kT) void k_pqk(const float *__restrict__ qkv, float
     if (t == 0) alpha_out[m * kNH + h] = (red2[0] + red2[1]) + (red2[2] + red2[3]);
 }
 
-// The recurrence over a chunk's n tokens in order, one wave per pair of
-// state columns and no workgroup barrier inside the token loop: grid
-// (kHD / kScanWgCols, kNH), four independent waves per workgroup (one per
-// SIMD, one workgroup per CU; a wave64 add holds its SIMD whatever its
-// active lanes, so two chain waves on one SIMD would take turns).  Lane l
+// The recurrence over a segment's n_total tokens in order, chunk by chunk of
+// 64, one launch per layer, one wave per pair of state columns and no
+// workgroup barrier inside a chunk's token loop: grid (kHD / kScanWgCols,
+// kNH), four independent waves per workgroup (one per SIMD, one workgroup
+// per CU; a wave64 add holds its SIMD whatever its active lanes, so two
+// chain waves on one SIMD would take turns).  The state stays in registers
+// from the first chunk to the last, and the next chunk's k, q, v, beta,
+// decay and alpha are loaded into registers during the current token loop.  Lane l
 // holds rows 4 l .. 4 l + 3 of the wave's columns c0, c0 + 1 for the whole
 // chunk (one 16-byte LDS access per chain row piece).  Per token: every lane writes its products S[j][c] * kn[j]
 // and S[j][c] * qn[j] to the wave's LDS rows; lanes 0..3 sum the chains (r
@@ -931,31 +934,42 @@ __global__ __launch_bounds__(kT) void k_pqk(const float *__restrict__ qkv, float
 // and q (2 x n x 256 FP32) are staged in LDS once.  Each value is formed
 // as the decode step's k_brecur forms it.
 constexpr int kScanWgCols = 8;  // 4 waves x 2 columns
-__global__ __launch_bounds__(kT) void k_pscan(const float *__restrict__ qkv, const float *__restrict__ qn_all,
-                                               const float *__restrict__ kn_all, const float *__restrict__ alpha_all,
-                                               const float *__restrict__ bd, int n, float *__restrict__ state,
-                                               float *__restrict__ attn) {
+__global__ __launch_bounds__(kT) void k_pscan(const float *__restrict__ qkv, const float *__restrict__ qn_seg,
+                                               const float *__restrict__ kn_seg, const float *__restrict__ alpha_seg,
+                                               const float *__restrict__ bd_seg, int n_total, float *__restrict__ state,
+                                               float *__restrict__ attn_seg) {
     constexpr int kPad = kHD + 4;  // chain rows 16 bytes apart in bank
+    constexpr int KQ = kMaxB * 2 * (kHD / 4) / kT;  // staged 16-byte pieces per thread and chunk
     __shared__ __attribute__((aligned(16))) float kqs[kMaxB][2][kHD];  // [token][k|q][row]
     __shared__ __attribute__((aligned(16))) float prod[4][4 * kPad];   // [wave][chain][row]
     const int h = blockIdx.y, t = threadIdx.x, w = t >> 6, lane = t & 63;
     const int c0 = blockIdx.x * kScanWgCols + 2 * w;
-    for (int i = t; i < n * 2 * (kHD / 4); i += kT) {
-        const int m = i / (2 * (kHD / 4)), rest = i - m * 2 * (kHD / 4), kind = rest / (kHD / 4),
-                  r4 = rest - kind * (kHD / 4);
-        const float *src = (kind == 0 ? kn_all : qn_all) + (size_t)m * kH + h * kHD + 4 * r4;
-        *reinterpret_cast<f32x4 *>(&kqs[m][kind][4 * r4]) = *reinterpret_cast<const f32x4 *>(src);
-    }
-    // lane m < n: token m's v of both columns, beta, decay, alpha
+    const int chunks = (n_total + kMaxB - 1) / kMaxB;
+    auto chunk_len = [&](int c) { return n_total - kMaxB * c < kMaxB ? n_total - kMaxB * c : kMaxB; };
+    // chunk c's normalised k and q (piece i = t + kT j: token, k|q, 4-row
+    // group) and, in lane m, token m's v of both columns, beta, decay and
+    // alpha: loaded into registers a chunk ahead
+    f32x4 kq[KQ];
     float v0 = 0.0f, v1 = 0.0f, beta_l = 0.0f, decay_l = 0.0f, alpha_l = 0.0f;
-    if (lane < n) {
-        const float *vp = qkv + ((size_t)lane * 3 + 2) * kH + h * kHD + c0;
-        v0 = vp[0];
-        v1 = vp[1];
-        beta_l = bd[lane * 16 + 2 * h];
-        decay_l = bd[lane * 16 + 2 * h + 1];
-        alpha_l = alpha_all[lane * kNH + h];
-    }
+    auto load_chunk = [&](int c) __attribute__((always_inline)) {
+        const int n = chunk_len(c);
+        const size_t mb = (size_t)c * kMaxB;
+#pragma unroll
+        for (int j = 0; j < KQ; ++j) {
+            const int i = t + kT * j, m = i / (2 * (kHD / 4)), rest = i - m * 2 * (kHD / 4),
+                      kind = rest / (kHD / 4), r4 = rest - kind * (kHD / 4);
+            const float *src = (kind == 0 ? kn_seg : qn_seg) + (mb + m) * kH + h * kHD + 4 * r4;
+            kq[j] = m < n ? *reinterpret_cast<const f32x4 *>(src) : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        if (lane < n) {
+            const float *vp = qkv + ((mb + lane) * 3 + 2) * kH + h * kHD + c0;
+            v0 = vp[0];
+            v1 = vp[1];
+            beta_l = bd_seg[(mb + lane) * 16 + 2 * h];
+            decay_l = bd_seg[(mb + lane) * 16 + 2 * h + 1];
+            alpha_l = alpha_seg[(mb + lane) * kNH + h];
+        }
+    };
     float *S = state + (size_t)h * kHD * kHD + c0;
     float sv[2][4];
 #pragma unroll
@@ -964,70 +978,86 @@ __global__ __launch_bounds__(kT) void k_pscan(const float *__restrict__ qkv, con
         sv[0][i] = s2.x;
         sv[1][i] = s2.y;
     }
-    __syncthreads();
+    load_chunk(0);
     float *pw = prod[w];
-    f32x4 k4n = *reinterpret_cast<const f32x4 *>(&kqs[0][0][4 * lane]);
-    f32x4 q4n = *reinterpret_cast<const f32x4 *>(&kqs[0][1][4 * lane]);
-    for (int m = 0; m < n; ++m) {
-        const f32x4 k4 = k4n, q4 = q4n;
-        const float kn[4] = {k4.x, k4.y, k4.z, k4.w};
+    for (int c = 0; c < chunks; ++c) {
+        const int n = chunk_len(c);
+        float *attn = attn_seg + (size_t)c * kMaxB * kH;
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            *reinterpret_cast<f32x4 *>(pw + e * kPad + 4 * lane) =
-                (f32x4){sv[e][0] * k4.x, sv[e][1] * k4.y, sv[e][2] * k4.z, sv[e][3] * k4.w};
-            *reinterpret_cast<f32x4 *>(pw + (2 + e) * kPad + 4 * lane) =
-                (f32x4){sv[e][0] * q4.x, sv[e][1] * q4.y, sv[e][2] * q4.z, sv[e][3] * q4.w};
+        for (int j = 0; j < KQ; ++j) {
+            const int i = t + kT * j, m = i / (2 * (kHD / 4)), rest = i - m * 2 * (kHD / 4), kind = rest / (kHD / 4),
+                      r4 = rest - kind * (kHD / 4);
+            *reinterpret_cast<f32x4 *>(&kqs[m][kind][4 * r4]) = kq[j];
         }
-        // the wave's own LDS writes, then its reads of other lanes' rows
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        {
-            // the next token's k and q, read while the chains run
-            const int mn = m + 1 < n ? m + 1 : m;
-            k4n = *reinterpret_cast<const f32x4 *>(&kqs[mn][0][4 * lane]);
-            q4n = *reinterpret_cast<const f32x4 *>(&kqs[mn][1][4 * lane]);
-        }
-        float acc = 0.0f;
-        if (lane < 4) {
-            const f32x4 *col = reinterpret_cast<const f32x4 *>(pw + lane * kPad);
-            f32x4 cur[8];
+        // this chunk's per-token scalars, held through its token loop
+        const float cv0 = v0, cv1 = v1, cbeta = beta_l, cdecay = decay_l, calpha = alpha_l;
+        __syncthreads();
+        if (c + 1 < chunks) load_chunk(c + 1);
+        f32x4 k4n = *reinterpret_cast<const f32x4 *>(&kqs[0][0][4 * lane]);
+        f32x4 q4n = *reinterpret_cast<const f32x4 *>(&kqs[0][1][4 * lane]);
+        for (int m = 0; m < n; ++m) {
+            const f32x4 k4 = k4n, q4 = q4n;
+            const float kn[4] = {k4.x, k4.y, k4.z, k4.w};
 #pragma unroll
-            for (int j = 0; j < 8; ++j) cur[j] = col[j];
-#pragma unroll
-            for (int b = 0; b < kHD / 32; ++b) {
-                f32x4 nxt[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) nxt[j] = (b + 1 < kHD / 32) ? col[8 * (b + 1) + j] : cur[j];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc = (((acc + cur[j].x) + cur[j].y) + cur[j].z) + cur[j].w;
-                asm volatile("" : "+v"(acc) : : "memory");
-#pragma unroll
-                for (int j = 0; j < 8; ++j) cur[j] = nxt[j];
+            for (int e = 0; e < 2; ++e) {
+                *reinterpret_cast<f32x4 *>(pw + e * kPad + 4 * lane) =
+                    (f32x4){sv[e][0] * k4.x, sv[e][1] * k4.y, sv[e][2] * k4.z, sv[e][3] * k4.w};
+                *reinterpret_cast<f32x4 *>(pw + (2 + e) * kPad + 4 * lane) =
+                    (f32x4){sv[e][0] * q4.x, sv[e][1] * q4.y, sv[e][2] * q4.z, sv[e][3] * q4.w};
             }
-        }
-        const float ra = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 0));
-        const float rb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 1));
-        const float pa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 2));
-        const float pb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 3));
-        const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_l), m));
-        const float decay = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(decay_l), m));
-        const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_l), m));
-        const float va = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v0), m));
-        const float vb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v1), m));
-        const float da = beta * (va - decay * ra);
-        const float db = beta * (vb - decay * rb);
-        if (lane < 2) {
-            const float o = lane == 0 ? 0.0625f * (decay * pa + alpha * da) : 0.0625f * (decay * pb + alpha * db);
-            attn[(size_t)m * kH + h * kHD + c0 + lane] = rne_bf16(o);
-        }
+            // the wave's own LDS writes, then its reads of other lanes' rows
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            {
+                // the next token's k and q, read while the chains run
+                const int mn = m + 1 < n ? m + 1 : m;
+                k4n = *reinterpret_cast<const f32x4 *>(&kqs[mn][0][4 * lane]);
+                q4n = *reinterpret_cast<const f32x4 *>(&kqs[mn][1][4 * lane]);
+            }
+            float acc = 0.0f;
+            if (lane < 4) {
+                const f32x4 *col = reinterpret_cast<const f32x4 *>(pw + lane * kPad);
+                f32x4 cur[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            sv[0][i] = decay * sv[0][i] + kn[i] * da;
-            sv[1][i] = decay * sv[1][i] + kn[i] * db;
+                for (int j = 0; j < 8; ++j) cur[j] = col[j];
+#pragma unroll
+                for (int b = 0; b < kHD / 32; ++b) {
+                    f32x4 nxt[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) nxt[j] = (b + 1 < kHD / 32) ? col[8 * (b + 1) + j] : cur[j];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) acc = (((acc + cur[j].x) + cur[j].y) + cur[j].z) + cur[j].w;
+                    asm volatile("" : "+v"(acc) : : "memory");
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) cur[j] = nxt[j];
+                }
+            }
+            const float ra = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 0));
+            const float rb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 1));
+            const float pa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 2));
+            const float pb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 3));
+            const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cbeta), m));
+            const float decay = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cdecay), m));
+            const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(calpha), m));
+            const float va = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cv0), m));
+            const float vb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cv1), m));
+            const float da = beta * (va - decay * ra);
+            const float db = beta * (vb - decay * rb);
+            if (lane < 2) {
+                const float o = lane == 0 ? 0.0625f * (decay * pa + alpha * da) : 0.0625f * (decay * pb + alpha * db);
+                attn[(size_t)m * kH + h * kHD + c0 + lane] = rne_bf16(o);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sv[0][i] = decay * sv[0][i] + kn[i] * da;
+                sv[1][i] = decay * sv[1][i] + kn[i] * db;
+            }
+            // the next token's products overwrite the rows the chains just read
+            __builtin_amdgcn_wave_barrier();
         }
-        // the next token's products overwrite the rows the chains just read
-        __builtin_amdgcn_wave_barrier();
+        // every wave is done with this chunk's rows before the next are stored
+        __syncthreads();
     }
     float *Sw = S;
     asm volatile("" : "+v"(Sw));
@@ -2179,18 +2209,12 @@ void enqueue_prefill_segment(GDNBatchEngine *e, int slot, int n, bool last, hipS
                                n, e->s_wyl, e->s_wym);
         if (e->prefill_mode == GDN_PREFILL_CHUNKED)
             hipLaunchKernelGGL(k_wy_inv, dim3(kNH, blocks), dim3(64), 0, s, e->s_wyl);
-        if (e->prefill_mode == GDN_PREFILL_CHUNKED) {
+        if (e->prefill_mode == GDN_PREFILL_CHUNKED)
             hipLaunchKernelGGL(k_wy_seq, dim3(kHD / kWyCols, kNH), dim3(kT), 0, s, e->s_qkv, e->s_qn, e->s_kn,
                                e->s_bd, e->s_wyl, e->s_wym, n, st, e->s_attn);
-        } else {
-            for (int c = 0; c < blocks; ++c) {
-                const int nc = std::min(kMaxB, n - c * kMaxB);
-                const size_t m0 = (size_t)c * kMaxB;
-                hipLaunchKernelGGL(k_pscan, dim3(kHD / kScanWgCols, kNH), dim3(kT), 0, s, e->s_qkv + m0 * 3 * kH,
-                                   e->s_qn + m0 * kH, e->s_kn + m0 * kH, e->s_alpha + m0 * kNH, e->s_bd + m0 * 16,
-                                   nc, st, e->s_attn + m0 * kH);
-            }
-        }
+        else
+            hipLaunchKernelGGL(k_pscan, dim3(kHD / kScanWgCols, kNH), dim3(kT), 0, s, e->s_qkv, e->s_qn, e->s_kn,
+                               e->s_alpha, e->s_bd, n, st, e->s_attn);
         hipLaunchKernelGGL(k_bonorm, dim3(kNH, n), dim3(kT), 0, s, e->s_attn, e->s_gate, e->s_sgate,
                            b_aux(e, l) + kAuxONorm, e->eps, e->s_xo);
         hipLaunchKernelGGL((k_pgemm<kKtH, 4, kSplitO>), dim3(kH / 128, tiles), dim3(kPgW * 64), 0, s, e->w_o[l], xo,
