@@ -923,16 +923,16 @@ __global__ __launch_bounds__(kT) void k_pqk(const float *__restrict__ qkv, float
 // per CU; a wave64 add holds its SIMD whatever its active lanes, so two
 // chain waves on one SIMD would take turns).  The state stays in registers
 // from the first chunk to the last, and the next chunk's k, q, v, beta,
-// decay and alpha are loaded into registers during the current token loop.  Lane l
-// holds rows 4 l .. 4 l + 3 of the wave's columns c0, c0 + 1 for the whole
-// chunk (one 16-byte LDS access per chain row piece).  Per token: every lane writes its products S[j][c] * kn[j]
-// and S[j][c] * qn[j] to the wave's LDS rows; lanes 0..3 sum the chains (r
-// of c0, r of c0 + 1, p of c0, p of c0 + 1) in row order j = 0..255 (the
-// reference's chain order, adds only); the four sums and the token's v,
-// beta, decay, alpha (held in lane m) are read across the wave, and every
-// lane forms delta, o and its updated elements.  The chunk's normalised k
-// and q (2 x n x 256 FP32) are staged in LDS once.  Each value is formed
-// as the decode step's k_brecur forms it.
+// decay and alpha are loaded into registers during the current token loop.
+// Lane l holds rows 4 l .. 4 l + 3 of the wave's columns c0, c0 + 1 (one
+// 16-byte LDS access per chain row piece).  Per token: every lane writes its
+// products S[j][c] * kn[j] and S[j][c] * qn[j] to the wave's LDS rows; lanes
+// 0..3 sum the chains (r of c0, r of c0 + 1, p of c0, p of c0 + 1) in row
+// order j = 0..255 (the reference's chain order, adds only); the four sums
+// and the token's v, beta, decay, alpha (held in lane m) are read across
+// the wave, and every lane forms delta, o and its updated elements.  Each
+// chunk's normalised k and q (2 x 64 x 256 FP32) are staged in LDS once.
+// Each value is formed as the decode step's k_brecur forms it.
 constexpr int kScanWgCols = 8;  // 4 waves x 2 columns
 __global__ __launch_bounds__(kT) void k_pscan(const float *__restrict__ qkv, const float *__restrict__ qn_seg,
                                                const float *__restrict__ kn_seg, const float *__restrict__ alpha_seg,
