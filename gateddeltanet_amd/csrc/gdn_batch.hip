@@ -1483,13 +1483,14 @@ __global__ __launch_bounds__(kT) void k_wy_seq(const float *__restrict__ qkv, co
 // (four 32-row blocks of the weight layout; gate/up: two channel groups) x
 // 128 tokens (two 64-token X tile blocks), eight waves of 64 rows x 32
 // tokens, the k tile's fragments staged once through LDS (double buffer,
-// two k tiles of loads in flight per thread).  Every output element is formed with the step's operations
-// in the step's order: the same v_mfma_f32_16x16x32_bf16 fragments; the k
-// tiles of class c (c, c + NW, ... within a split) chained from zero in
-// increasing order, as wave c of k_bgemm / k_bgu chains them; the classes
-// added in order, as k_bgemm adds its waves' sums; and the splits' sums
-// added in split order, as the step's norm adds k_bgemm's split partials.
-// A prefill therefore still equals the steps bit for bit.
+// two k tiles of loads in flight per thread).  Every output element is
+// formed with the step's operations in the step's order: the same
+// v_mfma_f32_16x16x32_bf16 fragments; the k tiles of class c (c, c + NW,
+// ... within a split) chained from zero in increasing order, as wave c of
+// k_bgemm / k_bgu chains them; the classes added in order, as k_bgemm adds
+// its waves' sums; and the splits' sums added in split order, as the
+// step's norm adds k_bgemm's split partials.  A prefill therefore still
+// equals the steps bit for bit.
 #ifndef GDN_PG_DEPTH
 #define GDN_PG_DEPTH 2
 #endif
@@ -1541,13 +1542,14 @@ __device__ __forceinline__ bool pg_close(int j, f32x4 (&chain)[NB], f32x4 (&part
 }
 
 // y[m][row] for rows 128 rt .. +127 and tokens 128 tt .. +127 (pg_place):
-// with splits, the running total lives in the output tile itself (each
-// lane rewrites only its own elements, after its own earlier store), so two
-// accumulator sets fit the registers of two workgroups per CU: the sum k_bgemm<2, KT, NW, S, EPI_RAW> forms for the row (S = 1) or
-// the in-order sum of its S split partials.  W in the 32-row block layout
-// ([row block][k tile][2 tiles][64 lanes]); X in 64-token X tile blocks;
-// y has the padded token count's rows.
-// Waves per k_pgemm workgroup: 8 of 64 rows x 32 tokens (108 VGPRs, four
+// the sum k_bgemm<2, KT, NW, S, EPI_RAW> forms for the row (S = 1), or the
+// in-order sum of its S split partials.  With splits the running total
+// lives in the output tile itself (each lane rewrites only its own
+// elements, after its own earlier store), so a wave holds only two
+// accumulator sets (the class chain and the split's sum).  W in the 32-row
+// block layout ([row block][k tile][2 tiles][64 lanes]); X in 64-token X
+// tile blocks; y has the padded token count's rows.
+// Waves per workgroup: 8 of 64 rows x 32 tokens (about 100 VGPRs, four
 // waves per SIMD) measured 98.4k against 95.9k prefill tokens/s for 4 of
 // 64 x 64 (two per SIMD), with twice the LDS fragment reads.
 #ifndef GDN_PG_WAVES
