@@ -24,6 +24,12 @@ measured here with HIP events on the engine stream over every layer's
 weights.  `cpu_baseline` times the CPU oracle (a port of the reference's
 native decode arithmetic, glibc transcendentals) on this host's cores for a
 few tokens of the same workload, starting from the GPU's post-prompt state.
+
+`secondary` (default run only; --eager or --no-secondary skip it): the other
+BASELINE figures measured in the same process after the headline leg --
+config 4 (FP32 arm, 1024 steps after a 64-token prompt), config 5 (64
+streams, 256 timed steps) and the 4096-token prompt pass in both recurrence
+modes.  --config 5 and --prefill N run those legs alone, at full length.
 """
 import argparse
 import json
@@ -133,6 +139,9 @@ def main():
     ap.add_argument("--prefill", type=int, default=0,
                     help="instead: time the on-device prefill of an N-token uniform prompt (the GPU prompt pass "
                          "that produces a .gdnstate) against N batch-1 decode steps")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the secondary legs of the default run (config 4, config 5, prefill); "
+                         "--eager skips them too")
     ap.add_argument("--eager", action="store_true",
                     help="launch the step's kernels one by one instead of the captured hipGraph "
                          "(for rocprofv3 kernel tracing, which aborts the queue on graph launches)")
@@ -155,17 +164,27 @@ def main():
         return main_prefill(args)
     if args.config == 5:
         return main_streams(args)
+    out = run_batch1(args.contract, args.steps, args.warmup, args.profile_rounds, args.eager,
+                     args.cpu_tokens, args.cpu_single_tokens)
+    if args.contract == "bf16w_fp32s" and not args.eager and not args.no_secondary:
+        out["secondary"] = secondary_legs()
+    print(json.dumps(out), flush=True)
+
+
+def run_batch1(contract_name, steps, warmup, profile_rounds, eager, cpu_tokens, cpu_single_tokens):
+    """One batch-1 decode run (or config 4 with the fp32
+    contract): the bench line's fields as a dict."""
     import gateddeltanet_amd as g
-    contract = {"ref": g.CONTRACT_REF, "bf16w_fp32s": g.CONTRACT_BF16W_FP32S, "fp32": g.CONTRACT_FP32}[args.contract]
+    contract = {"ref": g.CONTRACT_REF, "bf16w_fp32s": g.CONTRACT_BF16W_FP32S, "fp32": g.CONTRACT_FP32}[contract_name]
     t_setup = time.perf_counter()
     model = g.Model.synth(num_layers=L, seed=0, std=0.02, bf16=(contract != g.CONTRACT_FP32))
     rs = g.RunState(model, contract)
-    if args.eager:
+    if eager:
         rs.set_graph(False)
-    prompt = g.synth_tokens(max(args.warmup, 1), 0, 1, V)
+    prompt = g.synth_tokens(max(warmup, 1), 0, 1, V)
     stream = g.synth_tokens(4096, 0, 2, V)
-    if args.warmup > 0:
-        rs.teacher_forced(prompt, args.warmup, timing=False)
+    if warmup > 0:
+        rs.teacher_forced(prompt, warmup, timing=False)
     post_prompt = rs.save_state()
     setup_s = time.perf_counter() - t_setup
 
@@ -173,27 +192,27 @@ def main():
     # on the stream); inner / outer medians: a separate instrumented run
     sync()
     t0 = time.perf_counter()
-    rs.teacher_forced(stream, args.steps, timing=False)
+    rs.teacher_forced(stream, steps, timing=False)
     sync()
     wall = time.perf_counter() - t0
-    ms_per_step = wall * 1000.0 / args.steps
-    _, inner, outer = rs.teacher_forced(stream, min(args.steps, 1024))
+    ms_per_step = wall * 1000.0 / steps
+    _, inner, outer = rs.teacher_forced(stream, min(steps, 1024))
 
-    prof = rs.profile_kernels(args.profile_rounds)
+    prof = rs.profile_kernels(profile_rounds)
     per_token = {k: prof[k] * LAUNCHES_PER_TOKEN[k] for k in prof}
     dom = max(per_token, key=per_token.get)
     kb = KERNEL_BYTES[dom] * (2 if contract == g.CONTRACT_FP32 and dom not in ("recur", "argmax") else 1)
     achieved_k = kb / (prof[dom] * 1e-6) / 1e9
     inner_med = float(np.median(inner))
-    bytes_tok = BYTES_PER_TOKEN[args.contract]
+    bytes_tok = BYTES_PER_TOKEN[contract_name]
     achieved = bytes_tok / (inner_med * 1e-3) / 1e9
     achieved_outer = bytes_tok / (ms_per_step * 1e-3) / 1e9
 
     cpu = None
-    if args.cpu_tokens > 0:
+    if cpu_tokens > 0:
         threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
         ms_cpu, n_cpu, single = cpu_baseline(model, contract, post_prompt[0], post_prompt[1],
-                                             stream[:args.cpu_tokens + 1], threads, args.cpu_single_tokens)
+                                             stream[:cpu_tokens + 1], threads, cpu_single_tokens)
         cpu = {"value": round(ms_cpu, 3), "unit": "ms/token", "cores": threads, "kind": "port",
                "sample": f"{n_cpu} teacher-forced tokens of the same 24-layer model from the GPU's post-prompt "
                          f"state, CPU oracle (gdn_model.cpp arithmetic, glibc expf/log1pf, OpenMP rows), "
@@ -205,8 +224,8 @@ def main():
         "value": round(ms_per_step, 5),
         "unit": "ms/token",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": False,
         "scaling": "weak",
@@ -218,11 +237,11 @@ def main():
                          "state (precision control arm; GB/s at double the weight bytes), 24 layers, batch 1, "
                          if contract == g.CONTRACT_FP32 else
                          "BASELINE config 3: GatedDeltaNet-1.3B decode, 24 layers, batch 1, ")
-                        + f"{args.warmup}-token uniform prompt then {args.steps} teacher-forced steps over a "
+                        + f"{warmup}-token uniform prompt then {steps} teacher-forced steps over a "
                         "fixed 4096-token uniform stream (cyclic), greedy argmax",
-            "contract": args.contract,
+            "contract": contract_name,
             "state_dtype": "bf16" if contract == g.CONTRACT_REF else "fp32",
-            "launch": "eager (122 kernel launches per token)" if args.eager
+            "launch": "eager (122 kernel launches per token)" if eager
                       else "one hipGraph per token (122 kernels)",
         },
         "outer_ms_median": round(float(np.median(outer)), 5),
@@ -252,7 +271,55 @@ def main():
     }
     rs.free()
     model.free()
-    print(json.dumps(out), flush=True)
+    return out
+
+
+# The default run's secondary legs (the "secondary" block of the headline
+# line): BASELINE configs 4 and 5 and the prompt pass, measured in the same
+# process after the headline leg, at bounded lengths so that the default run
+# still finishes within a few minutes.  Decode cost per token does not depend
+# on the context length, so the shorter config-4/5 runs time the same step.
+SEC_C4_STEPS, SEC_C4_WARMUP = 1024, 64
+SEC_C5_STREAMS, SEC_C5_STEPS, SEC_C5_WARMUP = 64, 256, 16
+SEC_PREFILL_TOKENS = 4096
+
+
+def secondary_legs():
+    sec = {"note": "measured in this run after the headline leg, on the same GPU; not part of value"}
+
+    def leg(name, fn):
+        try:
+            sec[name] = fn()
+        except Exception as exc:  # a failed leg is reported; the headline line still prints
+            sec[name] = {"error": f"{type(exc).__name__}: {exc}"}
+
+    def c4():
+        r = run_batch1("fp32", SEC_C4_STEPS, SEC_C4_WARMUP, 1, False, 0, 0)
+        keep = ("value", "unit", "steps", "warmup", "inner_ms_median", "outer_ms_median", "bytes_per_token",
+                "achieved_GBps_inner", "achieved_GBps_outer", "hbm_frac_inner", "kernel_us_per_launch")
+        d = {k: r[k] for k in keep}
+        d["workload"] = ("BASELINE config 4: FP32 weights, activations and state, 24 layers, batch 1; "
+                         "GB/s at the FP32 byte count")
+        return d
+
+    def c5():
+        r = run_streams(SEC_C5_STREAMS, SEC_C5_STEPS, SEC_C5_WARMUP, False, 1, 0)
+        keep = ("value", "unit", "steps", "warmup", "ms_per_step", "inner_ms_median", "bytes_per_step",
+                "achieved_GBps_inner", "hbm_frac_inner", "kernel_us_per_launch")
+        d = {k: r[k] for k in keep}
+        d["roofline"] = {k: r["roofline"][k] for k in ("kernel", "achieved", "frac", "avg_launch_us")}
+        d["workload"] = r["config"]["workload"]
+        return d
+
+    def pre(mode):
+        r = run_prefill(SEC_PREFILL_TOKENS, mode, False, decode_steps=False)
+        return {k: r[k] for k in ("value", "unit", "steps", "prefill_ms", "seed_token")}
+
+    leg("config4_fp32", c4)
+    leg("config5_64_streams", c5)
+    leg("prefill_4096_chunked", lambda: pre("chunked"))
+    leg("prefill_4096_scan", lambda: pre("scan"))
+    return sec
 
 
 # Multi-stream decode: per step every stream reads the
@@ -274,14 +341,19 @@ def main_streams(args):
     per step; --warmup untimed steps then --steps timed steps, teacher-forced
     with uniform-random tokens.  `value` is aggregate tokens/s (streams x
     steps / wall time of the timed loop, host tokens in -> host tokens out)."""
-    import gateddeltanet_amd as g
-    B = args.streams
     steps = args.steps if args.steps != 4096 else 1024
     warm = args.warmup if args.warmup != 4096 else 64
+    out = run_streams(args.streams, steps, warm, args.eager, args.profile_rounds, args.cpu_tokens)
+    print(json.dumps(out), flush=True)
+
+
+def run_streams(B, steps, warm, eager, profile_rounds, cpu_tokens):
+    """One config-5 run; the bench line's fields as a dict."""
+    import gateddeltanet_amd as g
     t_setup = time.perf_counter()
     model = g.Model.synth(num_layers=L, seed=0, std=0.02, bf16=True)
     bs = g.BatchState(model, B)
-    if args.eager:
+    if eager:
         bs.set_graph(False)
     toks = g.synth_tokens((warm + steps) * B, 0, 3, V).reshape(warm + steps, B)
     if warm:
@@ -296,15 +368,15 @@ def main_streams(args):
     _, inner, outer = bs.teacher_forced(toks[warm:warm + min(steps, 256)])
     inner_med = float(np.median(inner))
     bytes_step = DENSE + AUX + B * PER_STREAM
-    prof = bs.profile_kernels(args.profile_rounds)
+    prof = bs.profile_kernels(profile_rounds)
     per_step = {k: v * (1 if k in ("embed", "lm_head", "argmax") else L) for k, v in prof.items()}
     rb = STREAM_KERNEL_BYTES["recur"] * B
     cpu = None
-    if args.cpu_tokens > 0:
+    if cpu_tokens > 0:
         threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
         st = np.zeros(L * 8 * 256 * 256, np.float32)
         cv = np.zeros(L * 3 * 3 * H, np.float32)
-        ms_cpu, n_cpu, _ = cpu_baseline(model, g.CONTRACT_BF16W_FP32S, st, cv, toks[:args.cpu_tokens + 1, 0],
+        ms_cpu, n_cpu, _ = cpu_baseline(model, g.CONTRACT_BF16W_FP32S, st, cv, toks[:cpu_tokens + 1, 0],
                                         threads, 0)
         cpu = {"value": round(1000.0 / ms_cpu, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
                "sample": f"{n_cpu} tokens of one stream of the same 24-layer model, CPU oracle (gdn_model.cpp "
@@ -329,7 +401,7 @@ def main_streams(args):
             "streams": B,
             "arithmetic": "BF16 operands, exact products summed in FP32 on the matrix cores for the "
                           "projections; batch-1 BF16W_FP32S arithmetic elsewhere",
-            "launch": "eager" if args.eager else "one hipGraph per step (195 kernels)",
+            "launch": "eager" if eager else "one hipGraph per step (195 kernels)",
         },
         "inner_ms_median": round(inner_med, 5),
         "outer_ms_median": round(float(np.median(outer)), 5),
@@ -354,7 +426,7 @@ def main_streams(args):
     }
     bs.free()
     model.free()
-    print(json.dumps(out), flush=True)
+    return out
 
 
 def main_prefill(args):
@@ -364,12 +436,17 @@ def main_prefill(args):
     64-token chunks in token order or in the WY form), timed against the same
     prompt as N batch-1 decode steps (BF16W_FP32S); `value` is prefill
     tokens/s.  The warm-up prefill also allocates the segment buffers."""
+    print(json.dumps(run_prefill(args.prefill, args.prefill_mode, args.eager)), flush=True)
+
+
+def run_prefill(n, mode, eager, decode_steps=True):
+    """One prefill run; the bench line's fields as a dict (without the
+    decode-steps comparison when decode_steps is false)."""
     import gateddeltanet_amd as g
-    n = args.prefill
     model = g.Model.synth(num_layers=L, seed=0, std=0.02, bf16=True)
     prompt = g.synth_tokens(n, 0, 1, V)
     bs = g.BatchState(model, 1)
-    chunked = args.prefill_mode == "chunked"
+    chunked = mode == "chunked"
     if chunked:
         bs.set_prefill_mode(g.PREFILL_CHUNKED)
     bs.prefill(0, prompt[:min(n, 128)])  # warm
@@ -379,17 +456,19 @@ def main_prefill(args):
     sync()
     pre_s = time.perf_counter() - t0
     bs.free()
-    rs = g.RunState(model, g.CONTRACT_BF16W_FP32S)
-    if args.eager:
-        rs.set_graph(False)
-    rs.teacher_forced(prompt[:16], 16, timing=False)
-    rs.load_state(np.zeros(rs.n_state, np.float32), np.zeros(rs.n_conv, np.float32))
-    sync()
-    t0 = time.perf_counter()
-    rs.teacher_forced(prompt, n, timing=False)
-    sync()
-    dec_s = time.perf_counter() - t0
-    rs.free()
+    dec_s = None
+    if decode_steps:
+        rs = g.RunState(model, g.CONTRACT_BF16W_FP32S)
+        if eager:
+            rs.set_graph(False)
+        rs.teacher_forced(prompt[:16], 16, timing=False)
+        rs.load_state(np.zeros(rs.n_state, np.float32), np.zeros(rs.n_conv, np.float32))
+        sync()
+        t0 = time.perf_counter()
+        rs.teacher_forced(prompt, n, timing=False)
+        sync()
+        dec_s = time.perf_counter() - t0
+        rs.free()
     model.free()
     out = {
         "metric": "prefill tokens/s, GDN-1.3B prompt pass (the .gdnstate producer)",
@@ -406,15 +485,15 @@ def main_prefill(args):
         "data": "synthetic (seeded random-init weights, uniform random prompt)",
         "config": {"workload": f"{n}-token prompt through one stream, 24 layers, FP32 state, "
                                 f"segments of 4096 tokens layer by layer, recurrence chunks of 64",
-                   "prefill_mode": args.prefill_mode,
+                   "prefill_mode": mode,
                    "arithmetic": ("the multi-stream step's, with the recurrence in the chunk-parallel (WY) form "
                                   "(FP32 re-association)" if chunked else "the multi-stream step's, bit for bit")},
         "prefill_ms": round(pre_s * 1000.0, 2),
-        "decode_steps_ms": round(dec_s * 1000.0, 2),
-        "speedup_vs_decode_steps": round(dec_s / pre_s, 2),
+        "decode_steps_ms": None if dec_s is None else round(dec_s * 1000.0, 2),
+        "speedup_vs_decode_steps": None if dec_s is None else round(dec_s / pre_s, 2),
         "seed_token": seed,
     }
-    print(json.dumps(out), flush=True)
+    return out
 
 
 if __name__ == "__main__":
