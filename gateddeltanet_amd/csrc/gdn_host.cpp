@@ -28,6 +28,16 @@ float u2f(uint32_t u) { float f; std::memcpy(&f, &u, 4); return f; }
 
 // What is wrong with a .gdnw header, or nullptr when the engine's host side
 // accepts it.  The message names the offending fields and their values.
+// gdn_total_weight_floats in 128-bit arithmetic, which cannot wrap for any
+// 32-bit header fields (the largest term, 3 H^2 L, stays below 2^98).
+unsigned __int128 payload_floats_wide(const GDNWeightHeader *c) {
+    using u128 = unsigned __int128;
+    const u128 H = c->hidden_size, nh = c->num_heads, hd = c->head_dim;
+    const u128 I = c->intermediate_size, cs = c->conv_size, V = c->vocab_size, L = c->num_layers;
+    const u128 layer = H + 2 * nh + 3 * H * H + 2 * nh * H + 3 * H * cs + H * H + hd + H * H + H + 2 * I * H + H * I;
+    return V * H + L * layer + H + V * H;
+}
+
 const char *header_problem(const GDNWeightHeader *c, char *buf, size_t n) {
     static_assert(sizeof(GDNWeightHeader) == 60, "GDNWeightHeader is 60 bytes");
     if (std::memcmp(c->magic, "GDNWv1", 6) != 0) {
@@ -37,9 +47,18 @@ const char *header_problem(const GDNWeightHeader *c, char *buf, size_t n) {
     } else if (c->num_heads != c->num_v_heads) {
         std::snprintf(buf, n, "gdn: weight header has %u key heads and %u value heads; they must match",
                       c->num_heads, c->num_v_heads);
-    } else if (c->hidden_size != c->num_heads * c->head_dim) {
+    } else if ((uint64_t)c->hidden_size != (uint64_t)c->num_heads * c->head_dim) {
+        // (in 64 bits: a 32-bit product that wraps would match a small hidden_size)
         std::snprintf(buf, n, "gdn: hidden_size %u differs from num_heads %u x head_dim %u", c->hidden_size,
                       c->num_heads, c->head_dim);
+    } else if (c->vocab_size == 0 || c->hidden_size == 0 || c->intermediate_size == 0 || c->conv_size == 0) {
+        // conv_size - 1 sizes the conv tails, the vocabulary the argmax
+        std::snprintf(buf, n, "gdn: weight header has a zero dimension (vocab %u, hidden %u, intermediate %u, conv %u)",
+                      c->vocab_size, c->hidden_size, c->intermediate_size, c->conv_size);
+    } else if (payload_floats_wide(c) > (unsigned __int128)(PTRDIFF_MAX / sizeof(float))) {
+        // the size_t payload arithmetic would wrap, and a wrapped total would
+        // pass the file-size check with a small file
+        std::snprintf(buf, n, "gdn: weight header dimensions describe more payload than this process can address");
     } else {
         return nullptr;
     }
