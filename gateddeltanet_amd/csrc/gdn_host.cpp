@@ -696,13 +696,20 @@ int gdn_load_gdnstate(GDNRunState *state, const GDNModel *model, const char *pat
         return -1;
     }
     const GDNWeightHeader *c = &model->config;
-    if (h.layers != c->num_layers || h.heads != c->num_heads || h.dk != c->head_dim ||
+    if (h.version != 1) {
+        std::fprintf(stderr, "gdn: %s is .gdnstate version %u, this library reads version 1\n", path, h.version);
+        return -1;
+    }
+    // Every dimension that sizes a section is checked against the model, the
+    // value dimension included (the sections are sized from the file's own
+    // header below, so an unchecked one could ask for any allocation).
+    if (h.layers != c->num_layers || h.heads != c->num_heads || h.dk != c->head_dim || h.dv != c->head_dim ||
         h.hidden != c->hidden_size || h.width != c->conv_size) {
         std::fprintf(stderr,
-                     "gdn: %s describes %u layers x %u heads x %u, hidden %u, conv %u; the model has "
-                     "%u x %u x %u, hidden %u, conv %u\n",
-                     path, h.layers, h.heads, h.dk, h.hidden, h.width, c->num_layers, c->num_heads, c->head_dim,
-                     c->hidden_size, c->conv_size);
+                     "gdn: %s describes %u layers x %u heads x %u x %u, hidden %u, conv %u; the model has "
+                     "%u x %u x %u x %u, hidden %u, conv %u\n",
+                     path, h.layers, h.heads, h.dk, h.dv, h.hidden, h.width, c->num_layers, c->num_heads,
+                     c->head_dim, c->head_dim, c->hidden_size, c->conv_size);
         return -1;
     }
     const size_t rec = (size_t)h.layers * h.heads * h.dk * h.dv;

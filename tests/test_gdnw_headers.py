@@ -5,7 +5,10 @@ never a crash.  Header checks that 32-bit arithmetic would get wrong are
 pinned with hand-made headers: a num_heads x head_dim product that wraps, a
 payload size that wraps size_t, and zero dimensions (the conv tails are sized
 by conv_size - 1).  The reference's loader (gdn_model.cpp:1161-1229) reads
-the header and then the payload it describes."""
+the header and then the payload it describes.  The .gdnstate reader
+(gdn_eval.cpp:196-267) is held to the same rule: every dimension that sizes a
+section, the value dimension included, must match the model before a buffer
+is sized from it."""
 import ctypes
 import random
 import struct
@@ -130,3 +133,56 @@ def test_synth_refuses_the_same_headers():
     cfg.conv_size = 0
     with pytest.raises(g.GDNError):
         g.Model.synth(config=cfg)
+
+
+def write_gdnstate(path, cfg, version=1, dv=None, prompt=(), payload=True):
+    """A .gdnstate in the reference's layout (export_gdn_state.py:340-362)."""
+    hd = cfg.head_dim
+    v = [version, cfg.num_layers, cfg.num_heads, hd, hd if dv is None else dv, cfg.hidden_size,
+         cfg.conv_size, len(prompt), 0]
+    rec = cfg.num_layers * cfg.num_heads * hd * hd
+    conv = cfg.num_layers * 3 * (cfg.conv_size - 1) * cfg.hidden_size
+    with open(path, "wb") as f:
+        f.write(b"GDNSTAT1" + struct.pack("<9I", *v) + struct.pack(f"<{len(prompt)}i", *prompt))
+        if payload:
+            f.write(b"\0" * 4 * (rec + conv))
+
+
+@pytest.mark.parametrize("case", ["dv_huge", "dv_small", "version", "layers", "short"])
+def test_gdnstate_header_checked_before_any_allocation(tmp_path, capfd, case):
+    """gdn_load_gdnstate refuses a header that disagrees with the model
+    before it sizes a buffer from it.  Without a GPU the run state has no
+    engine, so a file that passes the header checks stops at the first
+    device upload instead ("not initialised")."""
+    cfg = g.default_config(1)
+    cfg.vocab_size, cfg.hidden_size, cfg.num_heads, cfg.num_v_heads = 64, 64, 1, 1
+    cfg.head_dim, cfg.intermediate_size = 64, 128
+    m = g.Model.synth(config=cfg, seed=1)
+    lib = _lib.load()
+    p = tmp_path / "s.gdnstate"
+    expect = {"dv_huge": "x 64 x 4294967295", "dv_small": "x 64 x 32", "version": "version 2",
+              "layers": "2 layers", "short": "ends inside its recurrent-state section"}[case]
+    if case == "dv_huge":
+        write_gdnstate(p, cfg, dv=0xffffffff)   # about 2^38 floats if sized from the file
+    elif case == "dv_small":
+        write_gdnstate(p, cfg, dv=32)
+    elif case == "version":
+        write_gdnstate(p, cfg, version=2)
+    elif case == "layers":
+        c2 = g.default_config(2)
+        for k in ("vocab_size", "hidden_size", "num_heads", "num_v_heads", "head_dim", "intermediate_size"):
+            setattr(c2, k, getattr(cfg, k))
+        write_gdnstate(p, c2)
+    else:
+        write_gdnstate(p, cfg, prompt=[1, 2, 3], payload=False)
+    capfd.readouterr()
+    rs = _lib.GDNRunState()
+    plen, seed = ctypes.c_uint32(), ctypes.c_int32()
+    rc = lib.gdn_load_gdnstate(ctypes.byref(rs), m.ptr, str(p).encode(), ctypes.byref(plen), ctypes.byref(seed))
+    assert rc == -1
+    assert expect in capfd.readouterr().err
+    # the well-formed file passes the header and stops only at the missing engine
+    write_gdnstate(p, cfg, prompt=[5, 6])
+    rc = lib.gdn_load_gdnstate(ctypes.byref(rs), m.ptr, str(p).encode(), ctypes.byref(plen), ctypes.byref(seed))
+    assert rc == -1 and "not initialised" in capfd.readouterr().err
+    m.free()
