@@ -2397,6 +2397,10 @@ int gdn_batch_set_graph_mode(GDNBatchState *state, int use_graph) {
 int gdn_batch_decode_step(GDNBatchState *state, const int32_t *tokens, int32_t *next_tokens) {
     GDNBatchEngine *e = engine_of(state);
     if (!e) return -1;
+    if (tokens == nullptr || next_tokens == nullptr) {
+        gdn_error("gdn_batch_decode_step: tokens and next_tokens are required");
+        return -1;
+    }
     return b_run_step(e, tokens, next_tokens, nullptr);
 }
 
@@ -2477,6 +2481,10 @@ int gdn_batch_run_teacher_forced(GDNBatchState *state, const int32_t *tokens, ui
                                  int32_t *argmax_out, float *inner_ms, float *outer_ms) {
     GDNBatchEngine *e = engine_of(state);
     if (!e) return -1;
+    if (tokens == nullptr && n_steps > 0) {
+        gdn_error("gdn_batch_run_teacher_forced: no tokens");
+        return -1;
+    }
     const size_t B = (size_t)e->streams;
     std::vector<int32_t> next(B);
     for (uint32_t i = 0; i < n_steps; ++i) {

@@ -2186,6 +2186,10 @@ int gdn_set_graph_mode(GDNRunState *state, int use_graph) {
 }
 
 int gdn_decode_step_host(const GDNModel *model, GDNRunState *state, const int32_t *token) {
+    if (model == nullptr || token == nullptr) {
+        gdn_error("gdn_decode_step_host: model and token are required");
+        return -1;
+    }
     if (*token < 0 || (uint32_t)*token >= model->config.vocab_size) {
         std::fprintf(stderr, "gdn: token %d is outside the vocabulary [0, %u)\n", *token,
                      model->config.vocab_size);
@@ -2368,7 +2372,7 @@ int gdn_run_teacher_forced(GDNRunState *state, const int32_t *tokens, uint32_t n
                            float *outer_ms) {
     GDNEngine *e = engine_of(state);
     if (!e) return -1;
-    if (n_tokens == 0) {
+    if (n_tokens == 0 || tokens == nullptr) {
         gdn_error("gdn_run_teacher_forced: no tokens");
         return -1;
     }

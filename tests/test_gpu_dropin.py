@@ -19,6 +19,7 @@
 * the step deadline (GDN_KERNEL_WAIT_TIMEOUT_MS) fails the step and the run
   state without waiting for the GPU.
 """
+import ctypes
 import json
 import os
 import struct
@@ -274,4 +275,28 @@ def test_step_deadline_fails_the_run_state():
     try:
         rs.decode_step(3)
     finally:
+        rs.free()
+
+
+def test_null_token_pointers_are_refused():
+    """The stepping entry points refuse missing token arrays with -1 before
+    any device work, and the run states stay usable."""
+    lib = _lib.load()
+    m = small_model(1, 512, seed=3)
+    rs = g.RunState(m, g.CONTRACT_BF16W_FP32S)
+    bs = g.BatchState(m, 2)
+    try:
+        assert lib.gdn_decode_step_host(m.ptr, rs.ptr, None) == -1
+        assert lib.gdn_run_teacher_forced(rs.ptr, None, 4, 4, None, None, None) == -1
+        nxt = (ctypes.c_int32 * 2)()
+        toks = (ctypes.c_int32 * 2)(1, 2)
+        assert lib.gdn_batch_decode_step(bs.ptr, None, nxt) == -1
+        assert lib.gdn_batch_decode_step(bs.ptr, toks, None) == -1
+        assert lib.gdn_batch_run_teacher_forced(bs.ptr, None, 3, None, None, None) == -1
+        # both engines still step
+        assert 0 <= rs.decode_step(7) < 512
+        assert lib.gdn_batch_decode_step(bs.ptr, toks, nxt) == 0
+        assert all(0 <= int(v) < 512 for v in nxt)
+    finally:
+        bs.free()
         rs.free()
