@@ -231,6 +231,13 @@ __device__ __forceinline__ float vector_load(const float *p) {
     return *(const __attribute__((address_space(1))) float *)p;
 }
 
+// Four consecutive floats (16-byte aligned) through one vector memory
+// instruction, for the same reason as vector_load.
+__device__ __forceinline__ f32x4 vector_load4(const float *p) {
+    asm volatile("" : "+v"(p));
+    return *(const __attribute__((address_space(1))) f32x4 *)p;
+}
+
 // Per-head (beta, decay) for recur_block: read from precomputed pairs, or
 // computed from the raw a_h and b_h (head_scalars).  read() issues the loads
 // (after the state loads), get() returns the pair; recur_block evaluates it
@@ -300,6 +307,20 @@ __device__ __forceinline__ void recur_block(const float *__restrict__ qp, const 
     const size_t sidx = state_index<TILED, CB>(h, t, c0);
     Exp2Fill e2;
 
+    // With PRE the head's 16 + 16 norm partials are requested first: loads
+    // complete in issue order, so behind the state tile their wait would
+    // also wait for the tile, and the norms could not run while it arrives.
+    // They go through vector loads: as scalar loads (their address is
+    // uniform) the wait for the kernel arguments, which the state's address
+    // needs, would also wait for them.
+    f32x4 qpart[PRE ? 4 : 1], kpart[PRE ? 4 : 1];
+    if constexpr (PRE) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            qpart[i] = vector_load4(qk_part + h * 16 + 4 * i);
+            kpart[i] = vector_load4(qk_part + 128 + h * 16 + 4 * i);
+        }
+    }
     const float q = qp[h * kHD + t], k = kp[h * kHD + t];
     const float vi = (t < CB) ? vp[h * kHD + c0 + t] : 0.0f;
     float sv[EPT];  // S[t][c0 + e]
@@ -332,12 +353,10 @@ __device__ __forceinline__ void recur_block(const float *__restrict__ qp, const 
 
     float q_sq, k_sq;
     if constexpr (PRE) {
-        const f32x4 *qp4 = reinterpret_cast<const f32x4 *>(qk_part + h * 16);
-        const f32x4 *kp4 = reinterpret_cast<const f32x4 *>(qk_part + 128 + h * 16);
         float qv[16], kv[16];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const f32x4 a = qp4[i], b = kp4[i];
+            const f32x4 a = qpart[i], b = kpart[i];
             qv[4 * i] = a.x; qv[4 * i + 1] = a.y; qv[4 * i + 2] = a.z; qv[4 * i + 3] = a.w;
             kv[4 * i] = b.x; kv[4 * i + 1] = b.y; kv[4 * i + 2] = b.z; kv[4 * i + 3] = b.w;
         }
