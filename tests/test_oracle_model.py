@@ -105,3 +105,32 @@ def test_compute_logits_matches_gemv(orc):
     a = orc.compute_logits(hdr, m.blob, h)
     b = orc.gemv(0, m.lm_head.reshape(m.config.vocab_size, 2048), h)
     assert (np.abs(a - b) <= 1e-3 + 1e-4 * np.abs(b)).all()
+
+
+def test_compute_logits_sums_in_hidden_order(orc):
+    """gdn_compute_logits, gdn_model.cpp:3953-3961: sum += product for
+    hidden index 0..H-1 in order, from +0.0f.
+
+    Row 0: products 2^24 (index 0), 1 (index 1), 1, 1 (indices 1000, 1001).
+    In order each +1 onto 2^24 is a tie that rounds back: 2^24.  A reversed
+    sum gives 2^24 + 4, and the banked GEMV order (the 1s at 1000, 1001 meet
+    first in one half-beat) gives 2^24 + 2.
+    Row 1: products 1, 1, 1 (indices 10..12) then 2^24 (index 13): in order
+    3 + 2^24 = 2^24 + 3, which rounds to 2^24 + 4; reversed gives 2^24.
+    Every product is exact (BF16 operands 4096 and 1)."""
+    m = small_model(layers=1, bf16=True)
+    hdr = orc.header_from(m.config)
+    H = 2048
+    lm = m.lm_head.reshape(m.config.vocab_size, H)
+    lm[0:2] = 0.0
+    lm[0, [0, 1, 1000, 1001]] = [4096.0, 1.0, 1.0, 1.0]
+    lm[1, [10, 11, 12, 13]] = [1.0, 1.0, 1.0, 4096.0]
+    h = np.zeros(H, np.float32)
+    h[[0, 1, 1000, 1001, 10, 11, 12]] = 1.0
+    h[0] = h[13] = 4096.0
+    logits = orc.compute_logits(hdr, m.blob, h)
+    assert logits[0] == np.float32(2.0 ** 24)
+    assert logits[1] == np.float32(2.0 ** 24 + 4)
+    # the banked LM head of the decode path groups the same products otherwise
+    banked = orc.gemv(0, lm[0:2], h)
+    assert banked[0] == np.float32(2.0 ** 24 + 2)

@@ -406,3 +406,155 @@ def test_argmax_rules(orc):
     assert orc.argmax(np.full(5, -np.inf, F)) == 0                  # nothing beats -FLT_MAX
     assert orc.argmax(np.array([-3.402823466e38, -3.402823466e38], F)) == 0
     assert orc.argmax(np.array([0, np.inf, np.inf], F)) == 1
+
+
+# ------------------------------------------- order-sensitive association pins
+#
+# Each test below feeds inputs whose float32 result changes under any other
+# grouping, FMA contraction or summation direction of the same terms, and
+# asserts the exact bits the reference's expression gives.  The expected bits
+# are derived in the comments; where a result is computed in numpy, the test
+# also asserts that the plausible alternative groupings disagree with it on
+# these inputs, so a regrouped oracle fails.
+
+HALF_KEYS = (0, 1, 100, 101)
+
+
+def _keys_at(rows):
+    # 2^19 at four rows: the sum of squares is 2^40 in any order and
+    # 2^40 + 1e-6f == 2^40, so 1/sqrtf(.) = 2^-20 and kn = 1/2 exactly there.
+    assert len(rows) == 4
+    k = np.zeros(256, F)
+    k[list(rows)] = 2.0 ** 19
+    return k
+
+
+@pytest.mark.parametrize("contract", [0, 2])
+def test_recurrence_chains_are_sequential_over_rows(orc, contract):
+    # gdn_model.cpp:2612-2615: r_i = r_i + S[j][i]*kn_j and p_i likewise,
+    # row j = 0..255 in order.  kn = qn = 1/2 at rows 0, 1, 100, 101
+    # (alpha = 4 * 1/4 = 1) and S = 2^25, 2, 2, 2 there, so the terms are
+    # 2^24, 1, 1, 1.  In order every +1 onto 2^24 is a tie that rounds back:
+    # r = p = 2^24.  A tree (the 1s at rows 100, 101 paired first), 64-row
+    # blocks summed in order, or a reversed sum give 2^24 + 2, 2^24 + 2 and
+    # 2^24 + 4.  With beta = decay = 1 and v = 2^24 + 8:
+    #   delta = v - r = 8 (6 or 4 for the alternatives)
+    #   o = (1/16)(p + alpha*delta) = (2^24 + 8)/16 = 2^20 + 1/2
+    #   S'[j] = S[j] + kn_j*delta: 2^25 + 4 at row 0, 6 at rows 1, 100, 101.
+    k = _keys_at(HALF_KEYS)
+    S = np.zeros((256, 256), F)
+    S[0], S[1], S[100], S[101] = 2.0 ** 25, 2.0, 2.0, 2.0
+    v = np.full(256, 2.0 ** 24 + 8, F)
+    o, S2 = orc.recurrence_head_scalars(contract, k, k, v, 1.0, 1.0, S)
+    if contract == 2:
+        assert (o == F(2.0 ** 20 + 0.5)).all()
+        assert (S2[0] == F(2.0 ** 25 + 4)).all()
+    else:  # outputs and state rounded to BF16 (8 significant bits)
+        assert (o == F(2.0 ** 20)).all()
+        assert (S2[0] == F(2.0 ** 25)).all()
+    for j in (1, 100, 101):
+        assert (S2[j] == 6.0).all()          # delta = 8: the sum in row order
+    rest = np.ones(256, bool)
+    rest[list(HALF_KEYS)] = False
+    assert (S2[rest] == 0).all()
+
+
+# decay = 1 - 2^-24 (the float below 1) and a state entry 1 + 2^-23 at row 0:
+# the exact product decay * (0.5 + 2^-24) = 0.5 + 2^-25 - 2^-48 lies just
+# below the midpoint of 0.5 and its successor, so the rounded product is
+# 0.5, while a fused multiply-add keeps the 2^-25 - 2^-48.
+DECAY_BELOW_1 = float(np.nextafter(F(1), F(0)))
+S_ROW0 = 1.0 + 2.0 ** -23
+
+
+def _delta_case(orc, v, beta):
+    k = _keys_at((0, 1, 2, 3))              # kn = qn = 1/2 at rows 0..3
+    S = np.zeros((256, 256), F)
+    S[0] = S_ROW0                           # r = p = (1 + 2^-23)/2 = 0.5 + 2^-24
+    return orc.recurrence_head_scalars(2, k, k, np.full(256, v, F), beta, DECAY_BELOW_1, S)
+
+
+def test_delta_and_output_round_each_product(orc):
+    # gdn_model.cpp:2671-2673, delta = beta*(v - decay*r) and
+    # o = q_scale*(decay*p + alpha*delta), every product rounded before the
+    # add (no FMA); round(decay*r) = round(decay*p) = 0.5.
+    # v = 0, beta = 1: delta = -0.5; o = (0.5 + 1*(-0.5))/16 = 0 (an FMA gives
+    # (2^-25 - 2^-48)/16); S'[0] = round(decay*(1 + 2^-23)) + (1/2)(-1/2)
+    # = 1 - 0.25 = 0.75 (an FMA in the update gives 0.75 + 2^-24).
+    o, S2 = _delta_case(orc, 0.0, 1.0)
+    assert (o == 0).all()
+    assert (S2[0] == F(0.75)).all() and (S2[1] == F(-0.25)).all()
+    # v = 0.5, beta = 1: delta = 0.5 - 0.5 = 0 (an FMA gives -(2^-25 - 2^-48),
+    # visible in S'[1] = 0 + (1/2) delta); o = (0.5 + 0)/16 = 1/32.
+    o, S2 = _delta_case(orc, 0.5, 1.0)
+    assert (S2[1] == 0).all() and (S2[0] == 1.0).all()
+    assert (o == F(1.0 / 32)).all()
+
+
+def test_delta_scales_the_difference(orc):
+    # beta*(v - decay*r) with v = 0.5 + 2^-24: v - round(decay*r) = 2^-24
+    # exactly, so delta = f32(1/3) * 2^-24 exactly and S'[1] = delta/2 =
+    # f32(1/3) * 2^-25.  Distributing beta (beta*v - beta*(decay*r)) rounds
+    # beta*v up by one ulp of 1/6 and gives delta = 2^-26, S'[1] = 2^-27.
+    third = float(F(1.0 / 3.0))
+    _, S2 = _delta_case(orc, 0.5 + 2.0 ** -24, third)
+    assert (S2[1] == F(third * 2.0 ** -25)).all()
+    assert F(third * 2.0 ** -25) != F(2.0 ** -27)
+
+
+def _sig(orc, x, tmode):
+    f = orc.lib().orc_sigmoid
+    return np.array([f(float(v), tmode) for v in x], F)
+
+
+@pytest.mark.parametrize("contract", [0, 2])
+def test_swiglu_association(orc, contract):
+    # gdn_model.cpp:4763: h = R(silu(g) * u) with silu(g) = g * sigmoid(g)
+    # (gdn_model.cpp:1318), i.e. R((g*s)*u), on gate/up values already at the
+    # BF16 point.  sigmoid itself is pinned against glibc (test_libm.py).
+    rng = np.random.default_rng(21)
+    g = bf(rng.normal(0, 2, 4096).astype(F))
+    u = bf(rng.normal(0, 2, 4096).astype(F))
+    s = _sig(orc, g, orc.LIBM)
+    rnd = bf if contract == 0 else (lambda x: x)
+    want = rnd(F(g * s) * u)
+    h = orc.swiglu(contract, g, u)
+    assert (h.view(np.uint32) == want.view(np.uint32)).all()
+    # the same terms grouped otherwise differ on a share of these inputs in
+    # the FP32 arm (the oracle runs one grouping for every contract; in the
+    # BF16 arm a one-ulp FP32 difference shows only next to a BF16 tie)
+    if contract == 2:
+        for alt in (g * F(s * u), F(g * u) * s):
+            assert (alt != want).mean() > 0.2
+
+
+@pytest.mark.parametrize("contract", [0, 2])
+def test_output_gate_association(orc, contract):
+    # gdn_model.cpp:5808-5810: normalized = (a * scale) * w, then
+    # out = R((normalized * g) * sigmoid(g)).  Integer head values make the
+    # sum of squares exact in any order (the chunked order is pinned by
+    # test_output_norm_sum_is_chunked_per_head), so
+    # scale = 1/sqrtf(sum/256 + 1e-6f) is computed here in float32.
+    rng = np.random.default_rng(22)
+    a = rng.integers(1, 4, 2048).astype(F) * rng.choice([-1, 1], 2048).astype(F)
+    w = bf(rng.normal(1, 0.3, 256).astype(F))
+    g = bf(rng.normal(0, 2, 2048).astype(F))
+    out = orc.output_norm_gate(contract, a, g, w, 8, 256)
+    rnd = bf if contract == 0 else (lambda x: x)
+    s = _sig(orc, g, orc.LIBM)
+    want = np.empty(2048, F)
+    alts = [np.empty(2048, F) for _ in range(4)]
+    for h in range(8):
+        sl = slice(256 * h, 256 * (h + 1))
+        total = F((a[sl].astype(np.float64) ** 2).sum())
+        scale = F(1) / np.sqrt(total / F(256) + F(1e-6))
+        nrm = F(a[sl] * scale) * w
+        want[sl] = rnd(F(nrm * g[sl]) * s[sl])
+        alts[0][sl] = rnd(F(nrm * F(g[sl] * s[sl])))               # normalized * silu(g)
+        alts[1][sl] = rnd(F(F(a[sl] * F(scale * w)) * g[sl]) * s[sl])  # a * (scale * w)
+        alts[2][sl] = rnd(F(nrm * s[sl]) * g[sl])                  # sigmoid before g
+        alts[3][sl] = rnd(F(F(a[sl] * scale) * F(w * g[sl])) * s[sl])  # w * g first
+    assert (out.view(np.uint32) == want.view(np.uint32)).all()
+    if contract == 2:  # one grouping for every contract (see test_swiglu_association)
+        for alt in alts:
+            assert (alt != want).mean() > 0.05
