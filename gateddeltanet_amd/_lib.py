@@ -179,6 +179,9 @@ SIGNATURES = {
     "gdn_write_gdnstate": (c_int, [POINTER(GDNWeightHeader), ctypes.c_char_p, FP, FP, IP, c_uint32, c_int32]),
     "gdn_run_teacher_forced": (c_int, [POINTER(GDNRunState), IP, c_uint32, c_uint32, IP, FP, FP]),
     "gdn_set_graph_mode": (c_int, [POINTER(GDNRunState), c_int]),
+    "gdn_set_persistent": (c_int, [POINTER(GDNRunState), c_int]),
+    "gdn_get_persistent": (c_int, [POINTER(GDNRunState)]),
+    "gdn_test_step_buffers": (c_int, [POINTER(GDNRunState), c_int, c_void_p, c_size_t]),
     "gdn_profile_kernels": (c_int, [POINTER(GDNRunState), c_uint32, FP, c_uint32]),
     "gdn_get_contract": (c_int, [POINTER(GDNRunState)]),
     "gdn_compute_logits": (None, [POINTER(GDNModel), FP, FP]),

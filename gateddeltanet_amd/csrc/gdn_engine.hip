@@ -27,6 +27,7 @@
 // (gdn_libm.h), so they match the reference's C library bit for bit too.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -38,154 +39,12 @@
 
 #include "gdn_amd.h"
 #include "gdn_device.h"
+#include "gdn_gemv.h"
 #include "gdn_internal.h"
+#include "gdn_persist.h"
 
 namespace gdn {
 
-constexpr int kCB = 16;    // state columns per recurrence workgroup
-
-// Smallest nonzero and largest |w| of a matrix (after DAZ) and whether any
-// is not finite.
-struct WInfo {
-    float min_abs;
-    float max_abs;
-    int nonfinite;
-};
-
-// The native BF16 product with every special case of gdn_model.cpp:401-462:
-// DAZ inputs, canonical NaN, signed infinities/zeros, FTZ below 0x007fc000.
-__device__ __forceinline__ float native_exact(uint32_t w, float xf) {
-    const uint32_t x = f2u(xf) >> 16;
-    const uint32_t ew = (w >> 7) & 0xffu, fw = w & 0x7fu;
-    const uint32_t ex = (x >> 7) & 0xffu, fx = x & 0x7fu;
-    const bool w_nan = ew == 0xffu && fw, x_nan = ex == 0xffu && fx;
-    const bool w_inf = ew == 0xffu && !fw, x_inf = ex == 0xffu && !fx;
-    const bool w_zero = ew == 0, x_zero = ex == 0;
-    const uint32_t sign = (w ^ x) & 0x8000u;
-    if (w_nan || x_nan || (w_inf && x_zero) || (x_inf && w_zero)) return u2f(0x7fc00000u);
-    if (w_inf || x_inf) return u2f((sign | 0x7f80u) << 16);
-    if (w_zero || x_zero) return u2f(sign << 16);
-    const float prod = bf16_bits_to_f32(w) * bf16_bits_to_f32(x);
-    const uint32_t pb = f2u(prod), mag = pb & 0x7fffffffu;
-    if (mag == 0x7f800000u) return prod;
-    if (mag < 0x007fc000u) return u2f(pb & 0x80000000u);
-    const uint32_t r = (pb + 0x7fffu + ((pb >> 16) & 1u)) & 0xffff0000u;
-    if ((r & 0x7f800000u) == 0) return u2f(r & 0x80000000u);
-    return u2f(r);
-}
-
-__device__ __forceinline__ void lds_load16(const float *src, float *v) {
-    const f32x4 *s4 = reinterpret_cast<const f32x4 *>(src);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const f32x4 t = s4[q];
-        v[4 * q + 0] = t.x;
-        v[4 * q + 1] = t.y;
-        v[4 * q + 2] = t.z;
-        v[4 * q + 3] = t.w;
-    }
-}
-
-__device__ __forceinline__ void lds_load16u(const uint32_t *src, uint32_t *v) {
-    const u32x4 *s4 = reinterpret_cast<const u32x4 *>(src);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const u32x4 t = s4[q];
-        v[4 * q + 0] = t.x;
-        v[4 * q + 1] = t.y;
-        v[4 * q + 2] = t.z;
-        v[4 * q + 3] = t.w;
-    }
-}
-
-// Eight BF16 x BF16 products rounded to BF16, packed in pairs: r[j] holds
-// R(w[j].lo * x[2j]) in bits 0..15 and R(w[j].hi * x[2j+1]) in bits 16..31.
-// Each product is one v_dot2_f32_bf16 with a zero accumulator: the
-// activation word carries its BF16 in the lane of the weight it meets and
-// zero in the other lane, so the dot product is the single FP32 product --
-// exact for BF16 operands whose product is a normal FP32 number -- and
-// v_cvt_pk_bf16_f32 rounds two of them to nearest even.  A VALU read of a
-// v_dot2 result needs 3 wait states on gfx950, which the compiler cannot see
-// inside inline assembly: the block issues all eight products, one s_nop,
-// then the conversions, so every read is at least 4 slots after its write.
-__device__ __forceinline__ void dot8_bf16(const uint32_t *w, const uint32_t *x, uint32_t *r) {
-    float t0, t1, t2, t3, t4, t5, t6, t7;
-    asm("v_dot2_f32_bf16 %4, %12, %16, 0\n\t"
-        "v_dot2_f32_bf16 %5, %12, %17, 0\n\t"
-        "v_dot2_f32_bf16 %6, %13, %18, 0\n\t"
-        "v_dot2_f32_bf16 %7, %13, %19, 0\n\t"
-        "v_dot2_f32_bf16 %8, %14, %20, 0\n\t"
-        "v_dot2_f32_bf16 %9, %14, %21, 0\n\t"
-        "v_dot2_f32_bf16 %10, %15, %22, 0\n\t"
-        "v_dot2_f32_bf16 %11, %15, %23, 0\n\t"
-        "s_nop 0\n\t"
-        "v_cvt_pk_bf16_f32 %0, %4, %5\n\t"
-        "v_cvt_pk_bf16_f32 %1, %6, %7\n\t"
-        "v_cvt_pk_bf16_f32 %2, %8, %9\n\t"
-        "v_cvt_pk_bf16_f32 %3, %10, %11"
-        : "=v"(r[0]), "=v"(r[1]), "=v"(r[2]), "=v"(r[3]), "=&v"(t0), "=&v"(t1), "=&v"(t2),
-          "=&v"(t3), "=&v"(t4), "=&v"(t5), "=&v"(t6), "=&v"(t7)
-        : "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]), "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]),
-          "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]));
-}
-
-// Swap values between lane pairs (2i, 2i + 1) with a DPP quad permutation.
-__device__ __forceinline__ float swap_lane_pair(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false));
-}
-
-// Running magnitude statistics of BF16 activation pairs, per 16-bit half:
-// the largest |x| bits and the smallest (|x| bits - 1), where zero wraps to
-// 0xffff and so never wins.
-struct PairStats {
-    uint32_t mx = 0u, mnm1 = 0xffffffffu;
-    __device__ __forceinline__ void add(uint32_t pair) {
-        const u16x2 m = __builtin_bit_cast(u16x2, pair & 0x7fff7fffu);
-        const u16x2 one = {1, 1};
-        mx = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, mx), m));
-        mnm1 = __builtin_bit_cast(uint32_t,
-                                  __builtin_elementwise_min(__builtin_bit_cast(u16x2, mnm1), (u16x2)(m - one)));
-    }
-};
-
-
-// ------------------------------------------------------------------ GEMV core
-//
-// A workgroup owns RB consecutive rows of the device matrix (row-major, so
-// the block is one contiguous stream).  Work item f is one 16-column
-// half-beat of one row: row f / (K/16), half-beat f % (K/16), at element
-// offset 16 f of the block -- consecutive threads read consecutive 32-byte
-// (BF16) or 64-byte (FP32) pieces.  Each item's 16 products are reduced
-// in-lane with tree16 into LDS; then lanes 0..4RB-1 of wave 0 each run one
-// of the reference's four bank chains (lower/upper half x even/odd beat, in
-// beat order from +0.0f) and two XOR shuffles form
-// (even_lo + even_hi) + (odd_lo + odd_hi).
-//
-// Every kernel issues its weight loads before any activation-dependent
-// work: the activation prologue (residual add, RMSNorm, output norm * gate)
-// runs while the weight stream is in flight, and s_barrier does not wait
-// on outstanding global loads.
-//
-// The GEMV input lives in LDS as one 32-bit word per element.  BF16
-// contracts: element k's BF16 bits sit in the half of the word that meets
-// weight k in the packed weight pair (low half for even k, high half for odd
-// k) and the other half is zero -- the operand form of dot2_bf16, and for odd
-// k also the FP32 value itself.  FP32 contract: the FP32 value.
-
-template <int K>
-struct Hb {
-    static constexpr int HB = K / 16;     // half-beats per row
-    static constexpr int HBP = HB + 4;    // padded LDS row stride
-    static constexpr int NB = K / 32;     // 32-column beats per row
-};
-
-__device__ __forceinline__ float lane_word_value(uint32_t w, int k) {
-    return (k & 1) ? u2f(w) : u2f(w << 16);
-}
-
-// ---------------------------------------------------------------- prologues
-
-enum { PRO_PLAIN = 0, PRO_RESNORM = 1, PRO_EMBED = 2, PRO_ONORM = 3 };
 
 // Where a GEMV's input vector comes from.
 //   PRO_PLAIN    x = a[0..K)
@@ -220,127 +79,6 @@ struct XSrc {
 // reaches 4 x phase.  The spin is bounded so no wave can hang; the bound
 // (about a second) is never reached while the four waves run; if it were,
 // the wave sets the error word, which the host turns into a failed step.
-struct BlockSync {
-    __device__ __forceinline__ void operator()() { __syncthreads(); }
-};
-
-constexpr int kSpinMax = 1 << 24;
-
-__device__ __forceinline__ void wait_count(int *ctr, int target, int *err) {
-    int spins = 0;
-    while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target &&
-           ++spins < kSpinMax)
-        __builtin_amdgcn_s_sleep(1);
-    if (spins >= kSpinMax && err != nullptr && (threadIdx.x & 63) == 0)
-        __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-}
-
-struct Wave4Sync {
-    int *ctr;
-    int *err;
-    int phase = 0;
-    __device__ __forceinline__ void operator()() {
-        ++phase;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        if ((threadIdx.x & 63) == 0)
-            __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        wait_count(ctr, 4 * phase, err);
-    }
-};
-
-// Fast-path verdict (BF16 contracts): every input finite and normal or
-// zero, every weight finite, and every product |x| |w| inside
-// [2^-123, 2^126) -- so no product reaches the flush threshold or overflows
-// and dot2_bf16 + v_cvt_pk_bf16_f32 equal the native product.
-// The input-owning waves 0..3 publish their statistics, then any thread
-// decides from the published values.
-__device__ __forceinline__ void publish_stats(PairStats st, uint32_t *red) {
-    uint32_t mx = max(st.mx & 0xffffu, st.mx >> 16);
-    uint32_t mn = min(st.mnm1 & 0xffffu, st.mnm1 >> 16);
-    mx = wave_reduce64(mx, [](uint32_t a, uint32_t b) { return max(a, b); });
-    mn = wave_reduce64(mn, [](uint32_t a, uint32_t b) { return min(a, b); });
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    if (lane == 0 && w < 4) {
-        red[w] = mx;
-        red[4 + w] = mn;
-    }
-}
-
-__device__ __forceinline__ bool decide_fast(const uint32_t *red, WInfo wi) {
-    const uint32_t mx = max(max(red[0], red[1]), max(red[2], red[3]));
-    const uint32_t mn = min(min(red[4], red[5]), min(red[6], red[7]));
-    if (mx >= 0x7f80u || wi.nonfinite) return false;  // an input NaN/infinity or a weight
-    if (mn == 0xffffu) return true;                     // every input is zero
-    const uint32_t mn_mag = mn + 1u;
-    if (mn_mag < 0x0080u) return false;                 // a subnormal input
-    const double lo = (double)u2f(mn_mag << 16) * (double)wi.min_abs;
-    const double hi = (double)u2f(mx << 16) * (double)wi.max_abs;
-    return lo >= 0x1p-123 && hi < 0x1p126;
-}
-
-// Serial sum of the 128 chunk sums in scratch by wave 0 (the other waves
-// wait at the barrier instead of spending issue slots on the same chain);
-// every thread returns the total.  Two barriers.
-template <class Sync>
-__device__ __forceinline__ float chunk_total(const float *scratch, float *bcast, Sync &sync) {
-    sync();
-    const int t = threadIdx.x;
-    if (t < 64) {
-        const f32x4 *s4 = reinterpret_cast<const f32x4 *>(scratch);
-        float sum = 0.0f;
-#pragma unroll 8
-        for (int i = 0; i < kH / 64; ++i) {
-            const f32x4 c = s4[i];
-            sum += c.x;
-            sum += c.y;
-            sum += c.z;
-            sum += c.w;
-        }
-        if (t == 0) bcast[0] = sum;
-    }
-    sync();
-    return bcast[0];
-}
-
-// Sum of squares of 16-value chunks in order, when thread 2c holds the first
-// 8 values of chunk c and thread 2c + 1 the last 8: the even lane's running
-// sum moves to the odd lane, which finishes the chunk.  Odd lanes return the
-// chunk sum.
-__device__ __forceinline__ float chunk_sumsq8(const float *r) {
-    float sq[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) sq[e] = r[e] * r[e];
-    float s = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) s += sq[e];
-    float c = swap_lane_pair(s);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) c += sq[e];
-    return c;
-}
-
-// Store 8 (BF16 pairs ->) lane words for elements [8t, 8t + 8).
-__device__ __forceinline__ void store_pairs8(uint32_t *xs, const uint32_t *pairs, PairStats &st) {
-    u32x4 lo, hi;
-    uint32_t lw[8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        st.add(pairs[j]);
-        lw[2 * j] = pairs[j] & 0xffffu;
-        lw[2 * j + 1] = pairs[j] & 0xffff0000u;
-    }
-    lo.x = lw[0]; lo.y = lw[1]; lo.z = lw[2]; lo.w = lw[3];
-    hi.x = lw[4]; hi.y = lw[5]; hi.z = lw[6]; hi.w = lw[7];
-    u32x4 *d = reinterpret_cast<u32x4 *>(xs + 8 * threadIdx.x);
-    d[0] = lo;
-    d[1] = hi;
-}
-
-__device__ __forceinline__ void unpack8(const f32x4 *v, float *o) {
-    o[0] = v[0].x; o[1] = v[0].y; o[2] = v[0].z; o[3] = v[0].w;
-    o[4] = v[1].x; o[5] = v[1].y; o[6] = v[1].z; o[7] = v[1].w;
-}
 
 // The GEMV input for one workgroup.  load() issues the activation reads (the
 // kernel issues the weight stream right after), finish() builds the input in
@@ -660,9 +398,6 @@ struct Prologue {
     }
 };
 
-// ---------------------------------------------------------------- epilogues
-
-enum { EPI_RAW = 0, EPI_STORE = 1, EPI_QKVG = 2, EPI_SWIGLU = 3, EPI_LM = 4 };
 
 struct Epi {
     float *y;          // RAW/STORE/SWIGLU/LM: results; QKVG: conv outputs q,k,v
@@ -677,82 +412,6 @@ struct Epi {
     int *part_idx;
 };
 
-// ------------------------------------------------ CU-resident GEMV
-//
-// One 1024-thread workgroup per CU (it claims all 512 VGPRs of every SIMD,
-// so no two share one) owns ROWS consecutive rows of the matrix, a
-// contiguous slice of the weight stream, as 16-element items held in
-// registers (WStream).  Waves 0..3 read the activations and build the GEMV
-// input (residual add, norms) once per CU while the weights stream in.  The
-// vector memory path of a CU serves requests in order, so the activation
-// reads are issued before the weight loads: in the input-first kernels a
-// barrier orders them ahead of every weight load and only waves 4..15 carry
-// items; in gate/up and down all 16 waves stream.
-constexpr int kTB = 1024;  // threads per CU-resident workgroup
-// Rows per CU-resident workgroup (grids of 256 workgroups).
-constexpr int kCuQkvg = 32;   // 8192 / 256
-constexpr int kCuO = 8;       // 2048 / 256
-constexpr int kCuGu = 44;     // 22 gate + 22 up rows: 11264 / 256
-constexpr int kCuDown = 8;    // 2048 / 256
-constexpr int kCuLm = 125;    // 32000 / 256
-constexpr int kCuLmSmall = 8; // vocabularies that 125 does not divide
-// Items in flight per thread (16 = every item issued up front).  QKVG and
-// gate/up hold 6 items per thread, down 3, the LM head 21.  With the
-// stream-order layout, priming 3 of QKVG's, 2 of gate/up's, all 3 of down's
-// and 3 of the LM head's measured 3 % faster per token than 4 / 3 / 2 / 2
-// (the best mix of the earlier layout); gate/up at 1, QKVG at 2 or 6 were
-// slower.
-constexpr int kDepthAll = 16;
-constexpr int kDepthQkvg = 3;
-constexpr int kDepthGu = 2;
-constexpr int kDepthDown = 3;
-constexpr int kDepthLm = 3;
-// Per contract: an FP32 item is 64 bytes (16 VGPRs), so the FP32 control
-// arm keeps fewer in flight within the same 128-VGPR budget.
-template <int C>
-struct Depth {
-    static constexpr bool F = C == kFp32;
-    static constexpr int qkvg = F ? 3 : kDepthQkvg;
-    static constexpr int o = F ? 2 : kDepthAll;
-    static constexpr int gu = F ? 3 : kDepthGu;
-    static constexpr int down = F ? 2 : kDepthDown;
-    static constexpr int lm = F ? 2 : kDepthLm;
-    static constexpr int lm_small = F ? 2 : kDepthAll;
-};
-
-// Partial sums of the CU-resident GEMV, bank-contiguous: row r, bank
-// (beat parity, half) = 2 * (beat & 1) + half, position beat / 2.  A bank
-// segment is padded to 4 (mod 32) words so the four chain lanes of a row
-// read distinct LDS banks.
-template <int K>
-struct BankLayout {
-    static constexpr int NB2 = Hb<K>::NB / 2;                       // beats per bank chain
-    static constexpr int BSTR = ((NB2 + 3) / 4) * 4 + ((((NB2 + 3) / 4) * 4) % 32 == 4 ? 0 : 4);
-    static constexpr int RSTR = 4 * BSTR;
-    __device__ static constexpr int index(int row, int hb) {
-        return row * RSTR + (2 * ((hb >> 1) & 1) + (hb & 1)) * BSTR + (hb >> 2);
-    }
-};
-
-// Input-first GEMVs (QKVG, o_proj, LM head): waves 0..3 build the input and
-// own no weight items, so kTB - kT threads stream; the others stream on all
-// kTB threads.
-constexpr bool act_first(int pro, int epi) { return epi == EPI_QKVG || pro == PRO_ONORM || epi == EPI_LM; }
-constexpr int stream_threads(int pro, int epi) { return act_first(pro, epi) ? kTB - kT : kTB; }
-
-// Device order of a workgroup's weight slice.  Item f (16 elements: row
-// f / (K/16), half-beat f % (K/16)) is held by stream thread u = f % NT as its
-// item I = f / NT and arrives in WPI 16-byte pieces (2 for BF16, 4 for FP32).
-// Piece q of every item of group I of the NT threads is stored contiguously,
-// so each load instruction of a wave reads 1 KB of consecutive bytes: piece
-// (f, q) sits at 16-byte position NT WPI I + q span + u, span = NT (or the
-// item count of the last group when NT does not divide the items).
-__host__ __device__ constexpr size_t stream_piece(int f, int q, int items, int nt, int wpi) {
-    const int I = f / nt, u = f - I * nt;
-    const int full = items / nt;  // complete groups
-    const int span = I < full ? nt : items - full * nt;
-    return (size_t)nt * wpi * I + (size_t)q * span + u;
-}
 
 // A workgroup's weight rows as a stream of 16-element items (stream_piece
 // order); stream thread u = threadIdx.x - T0 takes items u + (kTB - T0) i
@@ -861,31 +520,6 @@ struct WStream {
 // Bank chains of CR rows: thread L < 4 CR runs chain L & 3 of row L >> 2
 // (the waves that hold those threads call this); lane 4r ends with row r.
 // The chain's whole bank segment is read before its serial adds.
-template <int K, int CR>
-__device__ __forceinline__ float chain_rows(const float *part) {
-    using BL = BankLayout<K>;
-    constexpr int NV = (BL::NB2 + 3) / 4;
-    const int L = threadIdx.x;
-    float acc = 0.0f;
-    if (L < CR * 4) {
-        const f32x4 *seg = reinterpret_cast<const f32x4 *>(part + (L >> 2) * BL::RSTR + (L & 3) * BL::BSTR);
-        f32x4 v[NV];
-#pragma unroll
-        for (int i = 0; i < NV; ++i) v[i] = seg[i];
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            if (4 * i + 0 < BL::NB2) acc = acc + v[i].x;
-            if (4 * i + 1 < BL::NB2) acc = acc + v[i].y;
-            if (4 * i + 2 < BL::NB2) acc = acc + v[i].z;
-            if (4 * i + 3 < BL::NB2) acc = acc + v[i].w;
-        }
-    }
-    return quad_sum(acc);  // (lo + hi) per parity, then the two parities
-}
-
-template <int N>
-using IC = std::integral_constant<int, N>;
-
 // ROWS rows per workgroup (grid = M / ROWS), at most D items in flight per
 // thread.
 //   EPI_QKVG    rows are q|k|v|g; workgroups 0..15 also run one row of the
@@ -893,7 +527,9 @@ using IC = std::integral_constant<int, N>;
 //   EPI_SWIGLU  a workgroup's rows are ROWS/2 gate rows then the matching
 //               ROWS/2 up rows
 //   EPI_LM      FP32 logits and the workgroup's argmax
-template <int C, int K, int ROWS, int D, int PRO, int EPI>
+// NTS: stream threads (0: stream_threads(PRO, EPI)); the persistent step's
+// weight layout is streamed by 512 (waves 8..15).
+template <int C, int K, int ROWS, int D, int PRO, int EPI, int NTS = 0>
 __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, WInfo wi, XSrc src,
                                                    Epi ep) {
     constexpr int CR = ROWS;
@@ -931,7 +567,8 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     // (measured faster so) let all 16 waves issue weights at once, the input
     // waves after their activation reads.
     constexpr bool kActFirst = act_first(PRO, EPI);
-    constexpr int T0 = kTB - stream_threads(PRO, EPI);
+    constexpr int T0 = kTB - (NTS ? NTS : stream_threads(PRO, EPI));
+    static_assert(T0 == 0 || T0 == kT || T0 == 2 * kT, "stream threads: 1024, 768 or 512");
     Prologue<C, K, PRO> pro;
     if (t < kT) pro.load(src);
     // QKVG workgroup j < 16: row j of the tiny a|b projection (a_h for
@@ -1042,7 +679,7 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
                 }
             }
         }
-        if constexpr (!kActFirst) products(fast);
+        if constexpr (!kActFirst && T0 == 0) products(fast);
     } else {
         if constexpr (BF) {
             wait_count(&arrive, 4 * Prologue<C, K, PRO>::kSyncs, src.err);
@@ -1051,7 +688,7 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
             wait_count(&arrive, 4 * Prologue<C, K, PRO>::kSyncsFp32, src.err);
             fast = false;
         }
-        products(fast);
+        if (t >= T0) products(fast);
     }
     __syncthreads();
     if (wave < CHW) {
@@ -1275,6 +912,7 @@ struct GDNEngine {
     float *tails = nullptr;
     // activations and step outputs
     float *act = nullptr;
+    size_t act_floats = 0;
     float *resid = nullptr, *resid_alt = nullptr, *fhid = nullptr, *qkv = nullptr,
           *gate = nullptr, *sgate = nullptr, *ab = nullptr, *attn = nullptr,
           *ybuf_o = nullptr, *dbuf = nullptr, *hbuf = nullptr, *lm_val = nullptr,
@@ -1289,6 +927,13 @@ struct GDNEngine {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     bool use_graph = true;
+    // the persistent step (gdn_persist.hip): available (weights packed in
+    // its stream order, exchange area held), and chosen for captured steps
+    bool persist = false;
+    bool use_persist = false;
+    uint32_t *xbuf = nullptr;
+    uint32_t tag0 = 0;
+    pst::Params pp{};
     // product counters: GEMV inputs of one step (device, lane words + the
     // fast-path verdict per launch) and the weights' column counts
     uint32_t *xdump = nullptr;
@@ -1385,11 +1030,12 @@ struct Packer {
         filled += n;
     }
     // Reorders the staged matrix into the CU-resident GEMV's stream order
-    // (stream_piece), one workgroup slice of `rows` rows at a time.
-    void stream_order(size_t rows, size_t K, int pro, int epi) {
+    // (stream_piece) for nt stream threads, one workgroup slice of `rows`
+    // rows at a time.
+    void stream_order(size_t rows, size_t K, int nt) {
         const size_t es = welem(contract), wpi = es;  // 16-byte pieces per 16-element item
         const size_t slice = rows * K * es, nslices = filled * es / slice;
-        const int items = (int)(rows * K / 16), nt = stream_threads(pro, epi);
+        const int items = (int)(rows * K / 16);
         std::vector<unsigned char> tmp(slice);
         for (size_t b = 0; b < nslices; ++b) {
             unsigned char *sl = staging.data() + b * slice;
@@ -1445,6 +1091,9 @@ int upload_weights(GDNEngine *e, const GDNModel *m, bool verify = false, size_t 
     const size_t per_layer = 4 * H * H + H * H + 2 * I * H + H * I;
     const size_t total = L * per_layer + 2 * V * H;
     const size_t es = welem(e->contract);
+    // stream threads of each matrix's layout: the per-kernel step's, or the
+    // persistent step's (which the per-kernel kernels then also stream)
+    const auto nts = [e](int pro, int epi) { return e->persist ? pst::kNT : stream_threads(pro, epi); };
     if (!verify) GDN_HIP(hipMalloc(&e->wmem, total * es));
     char *p = static_cast<char *>(e->wmem);
     Packer pk{e->contract, {}};
@@ -1456,7 +1105,7 @@ int upload_weights(GDNEngine *e, const GDNModel *m, bool verify = false, size_t 
         pk.rows(w.k_proj, H * H);
         pk.rows(w.v_proj, H * H);
         pk.rows(w.g_proj, H * H);
-        pk.stream_order(kCuQkvg, H, PRO_RESNORM, EPI_QKVG);
+        pk.stream_order(kCuQkvg, H, nts(PRO_RESNORM, EPI_QKVG));
         e->w_qkvg[l] = p;
         e->i_qkvg[l] = pk.info();
         if (pk.upload(p)) return -1;
@@ -1464,7 +1113,7 @@ int upload_weights(GDNEngine *e, const GDNModel *m, bool verify = false, size_t 
 
         pk.begin(H * H);
         pk.rows(w.o_proj, H * H);
-        pk.stream_order(kCuO, H, PRO_ONORM, EPI_STORE);
+        pk.stream_order(kCuO, H, nts(PRO_ONORM, EPI_STORE));
         e->w_o[l] = p;
         e->i_o[l] = pk.info();
         if (pk.upload(p)) return -1;
@@ -1478,7 +1127,7 @@ int upload_weights(GDNEngine *e, const GDNModel *m, bool verify = false, size_t 
             pk.rows(w.mlp_gate_proj + blk * G * H, G * H);
             pk.rows(w.mlp_up_proj + blk * G * H, G * H);
         }
-        pk.stream_order(kCuGu, H, PRO_RESNORM, EPI_SWIGLU);
+        pk.stream_order(kCuGu, H, nts(PRO_RESNORM, EPI_SWIGLU));
         e->w_gu[l] = p;
         e->i_gu[l] = pk.info();
         if (pk.upload(p)) return -1;
@@ -1486,7 +1135,7 @@ int upload_weights(GDNEngine *e, const GDNModel *m, bool verify = false, size_t 
 
         pk.begin(H * I);
         pk.rows(w.mlp_down_proj, H * I);
-        pk.stream_order(kCuDown, I, PRO_PLAIN, EPI_STORE);
+        pk.stream_order(kCuDown, I, nts(PRO_PLAIN, EPI_STORE));
         e->w_down[l] = p;
         e->i_down[l] = pk.info();
         if (pk.upload(p)) return -1;
@@ -1494,7 +1143,7 @@ int upload_weights(GDNEngine *e, const GDNModel *m, bool verify = false, size_t 
     }
     pk.begin(V * H);
     pk.rows(m->lm_head, V * H);
-    pk.stream_order((V % kCuLm) == 0 ? kCuLm : kCuLmSmall, H, PRO_RESNORM, EPI_LM);
+    pk.stream_order((V % kCuLm) == 0 ? kCuLm : kCuLmSmall, H, nts(PRO_RESNORM, EPI_LM));
     e->w_lm = p;
     e->i_lm = pk.info();
     if (pk.upload(p)) return -1;
@@ -1552,6 +1201,7 @@ int alloc_buffers(GDNEngine *e) {
     const size_t act_floats = 3 * kH + 3 * kH + 2 * kH + 64 + 3 * kH + kI + up64(nblk_lm) + kH +
                               up64((size_t)e->vocab) + 2 * kNH * 16 + kNH * (kHD / 16);
     GDN_HIP(hipMalloc(&e->act, act_floats * 4));
+    e->act_floats = act_floats;
     GDN_HIP(hipMemset(e->act, 0, act_floats * 4));
     float *p = e->act;
     e->resid = p; p += kH;
@@ -1587,6 +1237,38 @@ int alloc_buffers(GDNEngine *e) {
     return 0;
 }
 
+// The persistent step's kernel arguments (everything but the tag base).
+void fill_persist_params(GDNEngine *e) {
+    pst::Params &p = e->pp;
+    for (int l = 0; l < e->layers; ++l) {
+        p.w_qkvg[l] = e->w_qkvg[l];
+        p.w_o[l] = e->w_o[l];
+        p.w_gu[l] = e->w_gu[l];
+        p.w_down[l] = e->w_down[l];
+        p.i_qkvg[l] = e->i_qkvg[l];
+        p.i_o[l] = e->i_o[l];
+        p.i_gu[l] = e->i_gu[l];
+        p.i_down[l] = e->i_down[l];
+    }
+    p.w_lm = e->w_lm;
+    p.i_lm = e->i_lm;
+    p.w_emb = e->w_emb;
+    p.aux = e->aux;
+    p.ab16 = e->ab16;
+    p.state = e->state;
+    p.tails = e->tails;
+    p.xbuf = e->xbuf;
+    p.logits = e->logits;
+    p.fhid = e->fhid;
+    p.resid = e->resid;
+    p.xrow = e->xrow;
+    p.tok = e->tok_map;
+    p.layers = e->layers;
+    p.eps = e->eps;
+    p.tag0 = 0;
+    p.stamps = nullptr;
+}
+
 XSrc xsrc(GDNEngine *e, const float *a, const float *b, const float *c, const float *w, float *res_out,
           float *aux_out, uint32_t *xdump) {
     XSrc x{};
@@ -1600,6 +1282,19 @@ XSrc xsrc(GDNEngine *e, const float *a, const float *b, const float *c, const fl
     x.xdump = xdump;
     x.eps = e->eps;
     return x;
+}
+
+// k_gemv_cu in the stream order of the engine's weights (the persistent
+// step's 512-thread order when the engine has it).
+template <int C, int K, int ROWS, int D, int PRO, int EPI>
+void launch_gemv(GDNEngine *e, dim3 grid, hipStream_t s, const void *W, WInfo wi, const XSrc &x, const Epi &ep) {
+    if constexpr (C != kFp32) {
+        if (e->persist) {
+            hipLaunchKernelGGL((k_gemv_cu<C, K, ROWS, D, PRO, EPI, pst::kNT>), grid, dim3(kTB), 0, s, W, wi, x, ep);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((k_gemv_cu<C, K, ROWS, D, PRO, EPI>), grid, dim3(kTB), 0, s, W, wi, x, ep);
 }
 
 // Per-kernel launches.  The QKVG prologue (PRO0) takes the embedding row
@@ -1625,8 +1320,8 @@ void launch_qkvg(GDNEngine *e, int l, const float *res_a, const float *res_b, hi
         xq.vocab = e->vocab;
         xq.aux_out = e->xrow;
     }
-    hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuQkvg, Depth<C>::qkvg, PRO0, EPI_QKVG>), dim3(4 * kH / kCuQkvg),
-                       dim3(kTB), 0, s, e->w_qkvg[l], e->i_qkvg[l], xq, q);
+    launch_gemv<C, kH, kCuQkvg, Depth<C>::qkvg, PRO0, EPI_QKVG>(e, dim3(4 * kH / kCuQkvg), s, e->w_qkvg[l],
+                                                                e->i_qkvg[l], xq, q);
 }
 
 template <int C>
@@ -1644,8 +1339,8 @@ void launch_o(GDNEngine *e, int l, hipStream_t s) {
     XSrc xo = xsrc(e, e->attn, e->gate, e->sgate, layer_aux(e, l) + kAuxONorm, nullptr, nullptr,
                    dump_slot(e, 4 * l + 1));
     xo.osum = e->osum;
-    hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuO, Depth<C>::o, PRO_ONORM, EPI_STORE>), dim3(kH / kCuO), dim3(kTB), 0,
-                       s, e->w_o[l], e->i_o[l], xo, st);
+    launch_gemv<C, kH, kCuO, Depth<C>::o, PRO_ONORM, EPI_STORE>(e, dim3(kH / kCuO), s, e->w_o[l], e->i_o[l], xo,
+                                                                st);
 }
 
 template <int C>
@@ -1654,8 +1349,8 @@ void launch_gu(GDNEngine *e, int l, hipStream_t s) {
     sw.y = e->hbuf;
     const XSrc xg = xsrc(e, e->resid, e->ybuf_o, nullptr, layer_aux(e, l) + kAuxMlpNorm, e->resid_alt,
                          nullptr, dump_slot(e, 4 * l + 2));
-    hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuGu, Depth<C>::gu, PRO_RESNORM, EPI_SWIGLU>), dim3(2 * kI / kCuGu),
-                       dim3(kTB), 0, s, e->w_gu[l], e->i_gu[l], xg, sw);
+    launch_gemv<C, kH, kCuGu, Depth<C>::gu, PRO_RESNORM, EPI_SWIGLU>(e, dim3(2 * kI / kCuGu), s, e->w_gu[l],
+                                                                     e->i_gu[l], xg, sw);
 }
 
 template <int C>
@@ -1663,8 +1358,8 @@ void launch_down(GDNEngine *e, int l, hipStream_t s) {
     Epi dn{};
     dn.y = e->dbuf;
     const XSrc xd = xsrc(e, e->hbuf, nullptr, nullptr, nullptr, nullptr, nullptr, dump_slot(e, 4 * l + 3));
-    hipLaunchKernelGGL((k_gemv_cu<C, kI, kCuDown, Depth<C>::down, PRO_PLAIN, EPI_STORE>), dim3(kH / kCuDown),
-                       dim3(kTB), 0, s, e->w_down[l], e->i_down[l], xd, dn);
+    launch_gemv<C, kI, kCuDown, Depth<C>::down, PRO_PLAIN, EPI_STORE>(e, dim3(kH / kCuDown), s, e->w_down[l],
+                                                                      e->i_down[l], xd, dn);
 }
 
 // LM-head workgroups (= first-stage argmax results) of a contract/vocabulary.
@@ -1682,8 +1377,7 @@ void launch_lm(GDNEngine *e, hipStream_t s) {
                          dump_slot(e, 4 * e->layers));
     const dim3 grid(lm_blocks(e));
     if ((e->vocab % kCuLm) == 0) {
-        hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuLm, Depth<C>::lm, PRO_RESNORM, EPI_LM>), grid, dim3(kTB), 0, s,
-                           e->w_lm, e->i_lm, xl, lm);
+        launch_gemv<C, kH, kCuLm, Depth<C>::lm, PRO_RESNORM, EPI_LM>(e, grid, s, e->w_lm, e->i_lm, xl, lm);
     } else {
         hipLaunchKernelGGL((k_gemv_cu<C, kH, kCuLmSmall, Depth<C>::lm_small, PRO_RESNORM, EPI_LM>), grid,
                            dim3(kTB), 0, s, e->w_lm, e->i_lm, xl, lm);
@@ -1803,11 +1497,15 @@ int run_step(GDNEngine *e, int32_t token, int32_t *tok_out, float *inner_ms) {
         gdn_error("gdn: this run state failed an earlier step");
         return -1;
     }
-    if (e->use_graph && ensure_graph(e) != 0) return -1;
+    if (e->use_graph && !(e->use_persist && !e->counting) && ensure_graph(e) != 0) return -1;
     e->tok_host[0] = token;  // read by layer 0's kernel through tok_map
     __atomic_store_n(&e->tok_host[1], -1, __ATOMIC_RELEASE);
     if (inner_ms) GDN_HIP(hipEventRecord(e->ev0, e->stream));
-    if (e->use_graph) {
+    if (e->use_graph && e->use_persist && !e->counting) {
+        e->pp.tag0 = e->tag0;
+        e->tag0 = (e->tag0 + 256u) & 0xffffu;
+        if (persist_launch(e->contract, e->pp, e->stream) != 0) return -1;
+    } else if (e->use_graph) {
         GDN_HIP(hipGraphLaunch(e->exec, e->stream));
     } else {
         enqueue_step(e, e->stream);
@@ -1877,6 +1575,8 @@ void destroy_engine(GDNEngine *e) {
     (void)hipFree(e->lm_idx);
     (void)hipFree(e->xdump);
     if (e->tok_host) (void)hipHostFree(e->tok_host);
+    persist_xbuf_release(e->xbuf);
+    (void)hipFree(e->pp.stamps);
     delete e;
 }
 
@@ -2151,9 +1851,26 @@ int gdn_run_state_init_contract(GDNRunState *state, const GDNModel *model, uint3
         std::lock_guard<std::mutex> lock(g_mirrors_mu);
         g_mirrors.push_back(hm);
     }
+    // the persistent step (opt-in: GDN_PERSIST=1 at init, since it measured
+    // slower than the captured graph): BF16 contracts, the 32000-row LM head
+    // it is laid out for, a device that holds its grid
+    {
+        const char *env = std::getenv("GDN_PERSIST");
+        const bool on = env != nullptr && env[0] == '1';
+        if (on && contract != kFp32 && e->vocab == pst::kWG * pst::kLmRows && persist_supported(contract)) {
+            e->xbuf = persist_xbuf_acquire();
+            e->persist = e->use_persist = e->xbuf != nullptr;
+        }
+    }
     if (alloc_buffers(e) != 0 || upload_weights(e, model) != 0) {
         destroy_engine(e);
         return -1;
+    }
+    if (e->persist) fill_persist_params(e);
+    if (e->persist && std::getenv("GDN_PERSIST_STAMPS")) {
+        // phase stamps of every step (gdn_test_step_buffers, which = 2)
+        GDN_HIP(hipMalloc(&e->pp.stamps, (size_t)pst::kWG * (kMaxLayers + 1) * pst::kStamps * 8));
+        GDN_HIP(hipMemset(e->pp.stamps, 0, (size_t)pst::kWG * (kMaxLayers + 1) * pst::kStamps * 8));
     }
     state->engine = e;
     state->workspace = reinterpret_cast<Beat512 *>(hm.workspace);
@@ -2183,6 +1900,23 @@ int gdn_set_graph_mode(GDNRunState *state, int use_graph) {
     if (!e) return -1;
     e->use_graph = use_graph != 0;
     return 0;
+}
+
+int gdn_set_persistent(GDNRunState *state, int on) {
+    GDNEngine *e = engine_of(state);
+    if (!e) return -1;
+    if (on && !e->persist) {
+        gdn_error("gdn_set_persistent: this run state has no persistent step (contract, vocabulary or device)");
+        return -1;
+    }
+    e->use_persist = on != 0;
+    return 0;
+}
+
+int gdn_get_persistent(const GDNRunState *state) {
+    const GDNEngine *e = state ? state->engine : nullptr;
+    if (!e) return -1;
+    return (e->use_persist && e->use_graph) ? 1 : 0;
 }
 
 int gdn_decode_step_host(const GDNModel *model, GDNRunState *state, const int32_t *token) {
@@ -2419,7 +2153,7 @@ int gdn_test_gemv(int contract, const float *W, const float *x, uint32_t M, uint
     Packer pk{contract, {}};
     pk.begin((size_t)M * K);
     pk.rows(W, (size_t)M * K);
-    pk.stream_order(kRows, K, PRO_PLAIN, EPI_RAW);
+    pk.stream_order(kRows, K, stream_threads(PRO_PLAIN, EPI_RAW));
     void *dW = nullptr;
     float *dx = nullptr, *dy = nullptr;
     GDN_HIP(hipMalloc(&dW, (size_t)M * K * welem(contract)));
@@ -2526,6 +2260,24 @@ int gdn_test_recurrence(int contract, uint32_t n_heads, uint32_t n_steps, const 
 
 // Layer `layer` of the run state for n_steps residual inputs x_in[s] (H
 // floats each); x_out[s] receives the layer's residual output.
+int gdn_test_step_buffers(const GDNRunState *state, int which, void *out, size_t bytes) {
+    GDNEngine *e = engine_of(state);
+    if (!e || out == nullptr) return -1;
+    if (which == 0) {
+        if (e->xbuf == nullptr) {
+            gdn_error("gdn_test_step_buffers: this run state has no persistent step");
+            return -1;
+        }
+        return d2h(e, out, e->xbuf, std::min(bytes, (size_t)pst::XWORDS * 4));
+    }
+    if (which == 1) return d2h(e, out, e->act, std::min(bytes, e->act_floats * 4));
+    if (which == 2 && e->pp.stamps)
+        return d2h(e, out, e->pp.stamps, std::min(bytes, (size_t)pst::kWG * (kMaxLayers + 1) * pst::kStamps * 8));
+    gdn_error("gdn_test_step_buffers: which is 0 (exchange area), 1 (activations) or 2 (persistent-step stamps, "
+              "GDN_PERSIST_STAMPS=1 at init)");
+    return -1;
+}
+
 int gdn_test_layer(GDNRunState *state, uint32_t layer, uint32_t n_steps, const float *x_in,
                    float *x_out) {
     GDNEngine *e = state->engine;

@@ -58,6 +58,22 @@ def default_config(num_layers: int = 24) -> L.GDNWeightHeader:
     return cfg
 
 
+# The per-kernel step's activation buffers in device order (float32 counts;
+# vocabularies of 32000, for which the LM head's 8-row partial buffer is
+# 4032 long): residual ping-pong, final hidden, q|k|v after conv, gate,
+# sigmoid(gate), a|b, attention output o, o_proj output, down output, SwiGLU
+# output, LM-head partial maxima, embedding row, logits, q/k partial sums of
+# squares, output-norm chunk sums.
+ACTIVATION_LAYOUT = (("resid", 2048), ("resid_alt", 2048), ("fhid", 2048), ("qkv", 3 * 2048), ("gate", 2048),
+                     ("sgate", 2048), ("ab", 64), ("attn", 2048), ("ybuf_o", 2048), ("dbuf", 2048), ("hbuf", 5632),
+                     ("lm_val", 4032), ("xrow", 2048), ("logits", 32000), ("qkpart", 256), ("osum", 128))
+
+# Exchange regions of the persistent step (word offsets, gdn_persist.h).
+EXCHANGE_REGIONS = dict(qkv=0, g=6144, qk_part=8192, ab=8704, o=8768, osum=10816, y_o=11072, h=13120, y_down=18752,
+                        argmax=20800)
+EXCHANGE_WORDS = 21888
+
+
 class Model:
     """A host model in .gdnw order (FP32 words)."""
 
@@ -176,6 +192,34 @@ class RunState:
 
     def set_graph(self, use_graph: bool) -> None:
         _check(L.load().gdn_set_graph_mode(self.ptr, 1 if use_graph else 0), "gdn_set_graph_mode")
+
+    def step_buffers(self, which: int, nbytes: int) -> np.ndarray:
+        """gdn_test_step_buffers: the last step's exchange area (which = 0,
+        uint32 words), activations (1, float32, ACTIVATION_LAYOUT) or the
+        persistent step's phase stamps (2, uint64)."""
+        dt = {0: np.uint32, 1: np.float32, 2: np.uint64}[which]
+        out = np.empty(nbytes // np.dtype(dt).itemsize, dt)
+        _check(L.load().gdn_test_step_buffers(self.ptr, which, out.ctypes.data, out.nbytes), "gdn_test_step_buffers")
+        return out
+
+    def activations(self) -> Dict[str, np.ndarray]:
+        """The per-kernel step's activation buffers after the last step."""
+        n = sum(size for _, size in ACTIVATION_LAYOUT)
+        buf = self.step_buffers(1, 4 * n)
+        out, o = {}, 0
+        for name, size in ACTIVATION_LAYOUT:
+            out[name] = buf[o:o + size]
+            o += size
+        return out
+
+    def set_persistent(self, on: bool) -> None:
+        """Switch between the persistent one-launch step (a run state made
+        with GDN_PERSIST=1 in the environment has it) and the captured graph."""
+        _check(L.load().gdn_set_persistent(self.ptr, 1 if on else 0), "gdn_set_persistent")
+
+    @property
+    def persistent(self) -> bool:
+        return int(L.load().gdn_get_persistent(ctypes.byref(self._s))) == 1
 
     def decode_step(self, token: int) -> int:
         """gdn_decode_step_host; returns the device argmax token."""

@@ -342,6 +342,20 @@ int gdn_profile_kernels(GDNRunState *state, uint32_t rounds, float *avg_us,
                         uint32_t n_kinds);
 /* 0: launch kernels one by one; 1 (default): one captured hipGraph/step. */
 int gdn_set_graph_mode(GDNRunState *state, int use_graph);
+/* The persistent step: one cooperative launch of 256 one-per-CU workgroups
+ * runs the whole token (every layer, the LM head and the argmax), stages
+ * handing their outputs over as tagged words in uncached memory read through
+ * the scalar path.  Opt-in: a run state has it when the environment sets
+ * GDN_PERSIST=1 at gdn_run_state_init, its contract is GDN_CONTRACT_REF or
+ * GDN_CONTRACT_BF16W_FP32S, the vocabulary is 32000 (256 x 125 LM-head rows)
+ * and the device holds the grid; its steps then replace the captured graph
+ * (results are bit-identical; it measured slower than the graph, which is
+ * why it is not the default).  gdn_set_persistent(state, 0) switches back to
+ * the graph (1 switches again); it returns -1 when the run state has no
+ * persistent step.  gdn_get_persistent: 1 if steps run persistent, 0 if not,
+ * -1 on a bad run state.  No reference counterpart. */
+int gdn_set_persistent(GDNRunState *state, int on);
+int gdn_get_persistent(const GDNRunState *state);
 int gdn_get_contract(const GDNRunState *state);
 
 /* ===== reference host helpers ===== */
@@ -403,6 +417,14 @@ int gdn_recurrence_noalloc(int contract, uint32_t n_heads, uint32_t n_steps, con
  * over n inputs: the same code the kernels run, a restatement of the methods
  * of the reference's C library (glibc 2.35) that equals it on every input. */
 void gdn_test_libm_array(int which, const float *in, float *out, size_t n);
+/* Test hook: copies the last step's device buffers to `out` (at most
+ * `bytes`): which = 0, the persistent step's exchange area (32-bit words
+ * (tag << 16) | payload); which = 1, the per-kernel step's activation
+ * buffers (FP32; layout in gateddeltanet_amd/engine.py); which = 2, the
+ * persistent step's phase stamps when GDN_PERSIST_STAMPS=1 was set at init
+ * (uint64 [256 workgroups][25][16] of the 100 MHz real-time counter).  No
+ * reference counterpart. */
+int gdn_test_step_buffers(const GDNRunState *state, int which, void *out, size_t bytes);
 /* Layer `layer` of the run state's model for n_steps teacher-forced residual
  * inputs x_in[step][H] (BF16-exact for the BF16 contracts): the same kernels
  * a decode step runs for that layer, against the run state's persistent
