@@ -19,17 +19,27 @@ run of up to 1024 steps (the two events cost about 5 us per token).  Achieved GB
 (weights + aux + state read/write + conv tails + embedding row + logits).
 
 `roofline` is the dominant kernel kind (largest share of per-token kernel
-time): its algorithmic bytes per launch over its average launch duration,
-measured here with HIP events on the engine stream over every layer's
-weights.  `cpu_baseline` times the CPU oracle (a port of the reference's
-native decode arithmetic, glibc transcendentals) on this host's cores for a
-few tokens of the same workload, starting from the GPU's post-prompt state.
+time in the captured graph): its algorithmic bytes per launch over its mean
+duration in the graph, first workgroup's start to last workgroup's end,
+from in-kernel phase stamps (the 100 MHz real-time counter) of an
+instrumented copy of the step's kernels over --stamp-steps steps, measured
+here after the timed leg (gateddeltanet_amd/phase_stamps.py; the stamped
+copy runs a few per cent slower, so its durations are upper bounds).  The
+HIP-event figure per launch (each kind launched back to back eagerly over
+every layer's weights, so it includes a kernel boundary) is printed beside
+it.  `cpu_baseline` times the CPU oracle (a port of the reference's native
+decode arithmetic, glibc transcendentals) on this host's cores for a few
+tokens of the same workload, starting from the GPU's post-prompt state.
+Nothing but the engine's own calls runs in a timed window: every step
+returns after its argmax has reached host memory.
 
 `secondary` (default run only; --eager or --no-secondary skip it): the other
 BASELINE figures measured in the same process after the headline leg --
-config 4 (FP32 arm, 1024 steps after a 64-token prompt), config 5 (64
-streams, 256 timed steps) and the 4096-token prompt pass in both recurrence
-modes.  --config 5 and --prefill N run those legs alone, at full length.
+config 1 (one layer, 64 teacher-forced steps: GPU and CPU oracle), config 4
+(FP32 arm, 1024 steps after a 64-token prompt, with its CPU oracle timing),
+config 5 (64 streams, 256 timed steps) and the 4096-token prompt pass in
+both recurrence modes.  --config 5 and --prefill N run those legs alone, at
+full length.
 """
 import argparse
 import json
@@ -61,15 +71,7 @@ BYTES_PER_TOKEN = {
 }
 # Algorithmic bytes per launch of each kernel kind (bf16 arm): weights at
 # BF16 plus the state / conv-tail traffic the kernel must move.
-KERNEL_BYTES = {
-    "qkvg": 4 * H * H * 2 + 2 * 8 * H * 2 + 3 * H * 4 * 4 + 3 * 3 * H * 2 * 2 + 2 * H * 2,
-    "recur": 8 * 256 * 256 * 4 * 2,
-    "o_proj": H * H * 2 + 256 * 2,
-    "gate_up": 2 * I * H * 2 + H * 2,
-    "down": H * I * 2,
-    "lm_head": V * H * 2 + H * 2 + V * 4,
-    "argmax": (V // 125) * 8,
-}
+from gateddeltanet_amd.phase_stamps import KERNEL_BYTES  # noqa: E402
 # DRAM bytes per launch (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy of
 # known size) from the counter passes summarised in
 # profiles/k_gemv_cu_gdn13b_bf16w_decode.md (bf16w_fp32s arm).  These are
@@ -82,15 +84,6 @@ MEASURED_TRAFFIC = {
 TRAFFIC_SOURCE = ("rocprofv3 FETCH_SIZE + WRITE_SIZE passes, copy-calibrated "
                   "(profiles/k_gemv_cu_gdn13b_bf16w_decode.md); a profile constant, not measured in this run")
 LAUNCHES_PER_TOKEN = {"qkvg": L, "recur": L, "o_proj": L, "gate_up": L, "down": L, "lm_head": 1, "argmax": 1}
-
-
-def sync():
-    try:
-        import torch
-        if torch.cuda.is_available():
-            torch.cuda.synchronize()
-    except Exception:
-        pass
 
 
 def cpu_baseline(model, contract_id, state, conv, tokens, threads, single_tokens):
@@ -125,6 +118,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=4096, help="untimed prompt tokens")
     ap.add_argument("--contract", default="bf16w_fp32s", choices=sorted(BYTES_PER_TOKEN))
     ap.add_argument("--profile-rounds", type=int, default=4)
+    ap.add_argument("--stamp-steps", type=int, default=256,
+                    help="steps of the phase-stamped graph the roofline is taken from (0: HIP events only)")
     ap.add_argument("--cpu-tokens", type=int, default=6, help="oracle tokens timed on all cores (0: skip)")
     ap.add_argument("--cpu-single-tokens", type=int, default=1, help="oracle tokens timed on one core")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -165,13 +160,13 @@ def main():
     if args.config == 5:
         return main_streams(args)
     out = run_batch1(args.contract, args.steps, args.warmup, args.profile_rounds, args.eager,
-                     args.cpu_tokens, args.cpu_single_tokens)
+                     args.cpu_tokens, args.cpu_single_tokens, args.stamp_steps)
     if args.contract == "bf16w_fp32s" and not args.eager and not args.no_secondary:
         out["secondary"] = secondary_legs()
     print(json.dumps(out), flush=True)
 
 
-def run_batch1(contract_name, steps, warmup, profile_rounds, eager, cpu_tokens, cpu_single_tokens):
+def run_batch1(contract_name, steps, warmup, profile_rounds, eager, cpu_tokens, cpu_single_tokens, stamp_steps=0):
     """One batch-1 decode run (or config 4 with the fp32
     contract): the bench line's fields as a dict."""
     import gateddeltanet_amd as g
@@ -189,20 +184,34 @@ def run_batch1(contract_name, steps, warmup, profile_rounds, eager, cpu_tokens, 
     setup_s = time.perf_counter() - t_setup
 
     # `value`: the wall clock of an uninstrumented loop (no timing events
-    # on the stream); inner / outer medians: a separate instrumented run
-    sync()
+    # on the stream; each step returns once its argmax is in host memory);
+    # inner / outer medians: a separate instrumented run
     t0 = time.perf_counter()
     rs.teacher_forced(stream, steps, timing=False)
-    sync()
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1000.0 / steps
     _, inner, outer = rs.teacher_forced(stream, min(steps, 1024))
 
     prof = rs.profile_kernels(profile_rounds)
     per_token = {k: prof[k] * LAUNCHES_PER_TOKEN[k] for k in prof}
-    dom = max(per_token, key=per_token.get)
+    stamps = None
+    if stamp_steps > 0 and contract == g.CONTRACT_BF16W_FP32S and not eager:
+        from gateddeltanet_amd import phase_stamps as ps
+        S, inner_st, inner_pl = ps.stamped_steps(model, stamp_steps, 64, plain_state=rs)
+        stamps = ps.summarize(S, L)
+        stamps["inner_ms_stamped"] = inner_st
+        stamps["inner_ms_plain"] = inner_pl
+    if stamps is not None:
+        dom, avg_us, _, _ = ps.roofline_from(stamps, KERNEL_BYTES, PEAK_HBM_GBPS)
+        avg_source = (f"in-kernel phase stamps of the captured graph (instrumented copy), mean first-workgroup "
+                      f"start to last-workgroup end over {stamp_steps} steps x {LAUNCHES_PER_TOKEN[dom]} launches")
+    else:
+        dom = max(per_token, key=per_token.get)
+        avg_us = prof[dom]
+        avg_source = "HIP events around back-to-back eager launches over every layer (includes the boundary)"
     kb = KERNEL_BYTES[dom] * (2 if contract == g.CONTRACT_FP32 and dom not in ("recur", "argmax") else 1)
-    achieved_k = kb / (prof[dom] * 1e-6) / 1e9
+    achieved_k = kb / (avg_us * 1e-6) / 1e9
+    achieved_ev = kb / (prof[dom] * 1e-6) / 1e9
     inner_med = float(np.median(inner))
     bytes_tok = BYTES_PER_TOKEN[contract_name]
     achieved = bytes_tok / (inner_med * 1e-3) / 1e9
@@ -263,7 +272,22 @@ def run_batch1(contract_name, steps, warmup, profile_rounds, eager, cpu_tokens, 
             "traffic": MEASURED_TRAFFIC[dom] if contract == g.CONTRACT_BF16W_FP32S else None,
             "traffic_source": TRAFFIC_SOURCE if contract == g.CONTRACT_BF16W_FP32S else None,
             "algorithmic_bytes_per_launch": kb,
-            "avg_launch_us": round(prof[dom], 3),
+            "avg_launch_us": round(avg_us, 3),
+            "avg_launch_source": avg_source,
+            "hip_event_us_per_launch": round(prof[dom], 3),
+            "frac_hip_events": round(achieved_ev / PEAK_HBM_GBPS, 4),
+        },
+        "graph_stamps": None if stamps is None else {
+            "steps": stamps["steps"],
+            "span_us_mean": round(stamps["span_us_mean"], 1),
+            "kernel_us_per_token": round(stamps["kernel_us_per_token"], 1),
+            "gap_us_per_token": round(stamps["gap_us_per_token"], 1),
+            "gap_us_per_boundary": round(stamps["gap_us_per_boundary"], 3),
+            "inner_ms_stamped": round(stamps["inner_ms_stamped"], 5),
+            "inner_ms_plain": round(stamps["inner_ms_plain"], 5),
+            "kernels": {k: {"dur_us": round(v["dur_us_mean"], 3), "gap_before_us": round(v["gap_before_us_mean"], 3),
+                            "input_ready_median_wg_us": round(v.get("input_ready_median_wg_us", float("nan")), 2)}
+                        for k, v in stamps["kinds"].items()},
         },
         "cpu_baseline": cpu,
         "setup_s": round(setup_s, 1),
@@ -279,7 +303,8 @@ def run_batch1(contract_name, steps, warmup, profile_rounds, eager, cpu_tokens, 
 # process after the headline leg, at bounded lengths so that the default run
 # still finishes within a few minutes.  Decode cost per token does not depend
 # on the context length, so the shorter config-4/5 runs time the same step.
-SEC_C4_STEPS, SEC_C4_WARMUP = 1024, 64
+SEC_C4_STEPS, SEC_C4_WARMUP, SEC_C4_CPU_TOKENS = 1024, 64, 4
+C1_STEPS = 64
 SEC_C5_STREAMS, SEC_C5_STEPS, SEC_C5_WARMUP = 64, 256, 16
 SEC_PREFILL_TOKENS = 4096
 
@@ -293,10 +318,14 @@ def secondary_legs():
         except Exception as exc:  # a failed leg is reported; the headline line still prints
             sec[name] = {"error": f"{type(exc).__name__}: {exc}"}
 
+    def c1():
+        return run_config1()
+
     def c4():
-        r = run_batch1("fp32", SEC_C4_STEPS, SEC_C4_WARMUP, 1, False, 0, 0)
+        r = run_batch1("fp32", SEC_C4_STEPS, SEC_C4_WARMUP, 1, False, SEC_C4_CPU_TOKENS, 0)
         keep = ("value", "unit", "steps", "warmup", "inner_ms_median", "outer_ms_median", "bytes_per_token",
-                "achieved_GBps_inner", "achieved_GBps_outer", "hbm_frac_inner", "kernel_us_per_launch")
+                "achieved_GBps_inner", "achieved_GBps_outer", "hbm_frac_inner", "kernel_us_per_launch",
+                "cpu_baseline")
         d = {k: r[k] for k in keep}
         d["workload"] = ("BASELINE config 4: FP32 weights, activations and state, 24 layers, batch 1; "
                          "GB/s at the FP32 byte count")
@@ -315,11 +344,59 @@ def secondary_legs():
         r = run_prefill(SEC_PREFILL_TOKENS, mode, False, decode_steps=False)
         return {k: r[k] for k in ("value", "unit", "steps", "prefill_ms", "seed_token")}
 
+    leg("config1_single_layer", c1)
     leg("config4_fp32", c4)
     leg("config5_64_streams", c5)
     leg("prefill_4096_chunked", lambda: pre("chunked"))
     leg("prefill_4096_scan", lambda: pre("scan"))
     return sec
+
+
+def run_config1():
+    """one layer (BF16 weights N(0, 0.02), seed 0), FP32
+    state N(0, 0.01), zero conv tails, 64 teacher-forced N(0, 1) BF16 inputs:
+    the GPU's layer kernels (gdn_test_layer: one call for the 64 steps, host
+    copies of the inputs and outputs included) and the CPU oracle on all
+    cores and on one, from the same state."""
+    import gateddeltanet_amd as g
+    from oracle import oracle as O
+    m = g.Model.synth(num_layers=1, seed=0, std=0.02, bf16=True)
+    try:
+        S0 = g.synth_normal(8 * 256 * 256, 0, 1000, std=0.01)
+        xs = g.synth_normal(C1_STEPS * H, 0, 1001, bf16=True).reshape(C1_STEPS, H)
+        conv0 = np.zeros(3 * 3 * H, np.float32)
+        rs = g.RunState(m, g.CONTRACT_BF16W_FP32S)
+        try:
+            rs.load_state(S0, conv0)
+            rs.layer_steps(0, xs[:4])  # warm
+            rs.load_state(S0, conv0)
+            t0 = time.perf_counter()
+            xo = rs.layer_steps(0, xs)
+            gpu_ms = (time.perf_counter() - t0) * 1000.0 / C1_STEPS
+        finally:
+            rs.free()
+        hdr = O.header_from(m.config)
+        threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+        res = {}
+        for n in (threads, 1):
+            O.set_threads(n)
+            st, cv = S0.copy(), conv0.copy()
+            t0 = time.perf_counter()
+            for s in range(C1_STEPS):
+                xr, st, cv, _ = O.layer_forward(g.CONTRACT_BF16W_FP32S, hdr, m.blob, 0, xs[s], st, cv, O.LIBM)
+            res[n] = (time.perf_counter() - t0) * 1000.0 / C1_STEPS
+        O.set_threads(threads)
+        same = bool((xo[-1].view(np.uint32) == np.asarray(xr, np.float32).view(np.uint32)).all())
+        return {"workload": "BASELINE config 1: one GatedDeltaNet layer, 64 teacher-forced steps, FP32 state "
+                            "N(0, 0.01), BF16 N(0, 1) inputs (bf16 weights, FP32-state contract)",
+                "gpu_ms_per_step": round(gpu_ms, 4),
+                "gpu_note": "gdn_test_layer over the 64 steps in one call, host copies included",
+                "cpu_ms_per_step": round(res[threads], 3), "cpu_cores": threads,
+                "cpu_single_thread_ms_per_step": round(res[1], 3),
+                "cpu_kind": "port (CPU oracle: gdn_model.cpp arithmetic, glibc expf/log1pf)",
+                "last_output_bit_exact": same}
+    finally:
+        m.free()
 
 
 # Multi-stream decode (BASELINE config 5): per step every stream reads the
@@ -359,10 +436,8 @@ def run_streams(B, steps, warm, eager, profile_rounds, cpu_tokens):
     if warm:
         bs.teacher_forced(toks[:warm], timing=False)
     setup_s = time.perf_counter() - t_setup
-    sync()
     t0 = time.perf_counter()
-    bs.teacher_forced(toks[warm:], timing=False)
-    sync()
+    bs.teacher_forced(toks[warm:], timing=False)  # returns with every stream's token in host memory
     wall = time.perf_counter() - t0
     ms_step = wall * 1000.0 / steps
     _, inner, outer = bs.teacher_forced(toks[warm:warm + min(steps, 256)])
@@ -450,10 +525,8 @@ def run_prefill(n, mode, eager, decode_steps=True):
     if chunked:
         bs.set_prefill_mode(g.PREFILL_CHUNKED)
     bs.prefill(0, prompt[:min(n, 128)])  # warm
-    sync()
     t0 = time.perf_counter()
-    seed = bs.prefill(0, prompt)
-    sync()
+    seed = bs.prefill(0, prompt)  # returns with the seed token (the prompt's last argmax) in host memory
     pre_s = time.perf_counter() - t0
     bs.free()
     dec_s = None
@@ -463,10 +536,8 @@ def run_prefill(n, mode, eager, decode_steps=True):
             rs.set_graph(False)
         rs.teacher_forced(prompt[:16], 16, timing=False)
         rs.load_state(np.zeros(rs.n_state, np.float32), np.zeros(rs.n_conv, np.float32))
-        sync()
         t0 = time.perf_counter()
         rs.teacher_forced(prompt, n, timing=False)
-        sync()
         dec_s = time.perf_counter() - t0
         rs.free()
     model.free()

@@ -54,6 +54,19 @@ typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------- scalar math
 
+// Phase stamps of the instrumented kernels (ST: compiled only into their
+// own instantiations, so the uninstrumented kernels carry no trace of
+// them): thread 0 of workgroup wg stores the 100 MHz real-time counter in
+// slot k of its kStampSlots.  Slots: 0 start, 1 input ready, 2 products
+// done, 3 end.
+constexpr int kStampSlots = 4;
+template <bool ST>
+__device__ __forceinline__ void phase_stamp(uint64_t *stamps, int wg, int k) {
+    if constexpr (ST) {
+        if (threadIdx.x == 0) stamps[wg * kStampSlots + k] = __builtin_amdgcn_s_memrealtime();
+    }
+}
+
 __device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
 __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
 
@@ -287,12 +300,12 @@ struct ScalarsFromAB {
 //   With OSUM (CB = 16: one tile is one 16-value chunk of the output norm)
 //   the workgroup also writes sum_i R(o_i)^2 in order, the chunk's sum of
 //   squares, to o_sum[h*16 + c0/16].
-template <int C, int CB, bool TILED, bool PRE, bool OSUM, class Scal>
+template <int C, int CB, bool TILED, bool PRE, bool OSUM, bool ST = false, class Scal>
 __device__ __forceinline__ void recur_block(const float *__restrict__ qp, const float *__restrict__ kp,
                                             const float *__restrict__ vp, Scal scal,
                                             const float *__restrict__ qk_part, void *__restrict__ state,
                                             float *__restrict__ attn, float *__restrict__ o_sum, const int h,
-                                            const int c0) {
+                                            const int c0, uint64_t *stamps = nullptr, const int wg = 0) {
     static_assert(CB == 16 || CB == 32, "one wave runs both chains of every column; a thread holds one row");
     static_assert(!OSUM || CB == 16, "an output-norm chunk is 16 columns");
     constexpr int EPT = CB;                             // state elements per thread (its row)
@@ -306,6 +319,7 @@ __device__ __forceinline__ void recur_block(const float *__restrict__ qp, const 
     const int lane = t & 63, w = t >> 6;
     const size_t sidx = state_index<TILED, CB>(h, t, c0);
     Exp2Fill e2;
+    phase_stamp<ST>(stamps, wg, 0);
 
     // With PRE the head's 16 + 16 norm partials are requested first: loads
     // complete in issue order, so behind the state tile their wait would
@@ -384,6 +398,7 @@ __device__ __forceinline__ void recur_block(const float *__restrict__ qp, const 
     }
     e2.store(exp2_lds);
     __syncthreads();
+    phase_stamp<ST>(stamps, wg, 1);
 
     // wave 0: the column chains; meanwhile wave 3 evaluates beta and decay
     float acc = 0.0f, pv = 0.0f;
@@ -443,6 +458,7 @@ __device__ __forceinline__ void recur_block(const float *__restrict__ qp, const 
         }
     }
     __syncthreads();
+    phase_stamp<ST>(stamps, wg, 2);
 
     float nv[EPT];
 #pragma unroll
@@ -476,6 +492,10 @@ __device__ __forceinline__ void recur_block(const float *__restrict__ qp, const 
             v.x = nv[4 * i + 0]; v.y = nv[4 * i + 1]; v.z = nv[4 * i + 2]; v.w = nv[4 * i + 3];
             reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(state) + sidx)[i] = v;
         }
+    }
+    if constexpr (ST) {
+        __syncthreads();
+        phase_stamp<ST>(stamps, wg, 3);
     }
 }
 

@@ -66,6 +66,7 @@ struct XSrc {
     const float *osum; // PRO_ONORM (BF16): the output norm's 16-value chunk sums [8 heads][16]
     int *err;          // host-mapped error word: set when a bounded wait runs out
     uint32_t *xdump;   // when set, workgroup 0 stores its GEMV input (K lane words) and fast-path verdict
+    uint64_t *stamps;  // the stamped kernels (ST): each workgroup's phase stamps
     int vocab;
     float eps;
 };
@@ -528,8 +529,9 @@ struct WStream {
 //               ROWS/2 up rows
 //   EPI_LM      FP32 logits and the workgroup's argmax
 // NTS: stream threads (0: stream_threads(PRO, EPI)); the persistent step's
-// weight layout is streamed by 512 (waves 8..15).
-template <int C, int K, int ROWS, int D, int PRO, int EPI, int NTS = 0>
+// weight layout is streamed by 512 (waves 8..15).  ST: the instrumented copy
+// (phase stamps at start, input ready, products done and end).
+template <int C, int K, int ROWS, int D, int PRO, int EPI, int NTS = 0, bool ST = false>
 __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, WInfo wi, XSrc src,
                                                    Epi ep) {
     constexpr int CR = ROWS;
@@ -550,6 +552,7 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
     // claim the whole register file (128 VGPRs x 16 waves): one workgroup per CU
     asm volatile("" ::: "v127");
     const int t = threadIdx.x, wave = t >> 6;
+    phase_stamp<ST>(src.stamps, blockIdx.x, 0);
     constexpr bool BF = C != kFp32;
     const int row0 = blockIdx.x * ROWS;
     const char *wblk = static_cast<const char *>(W) + (size_t)row0 * K * (BF ? 2 : 4);
@@ -642,6 +645,7 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
         Wave4Sync sync{&arrive, src.err};
         if constexpr (BF) fast = pro.finish_bf16(src, wi, xs, scratch, bcast, red, sync);
         else fast = pro.finish_fp32(src, reinterpret_cast<float *>(xs), scratch, bcast, sync);
+        phase_stamp<ST>(src.stamps, blockIdx.x, 1);
         if constexpr (EPI == EPI_QKVG) {
             if (ab_blk) {
                 // a_h or b_h while the weights stream (gdn_gemv_tiny_ab):
@@ -691,6 +695,7 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
         if (t >= T0) products(fast);
     }
     __syncthreads();
+    phase_stamp<ST>(src.stamps, blockIdx.x, 2);
     if (wave < CHW) {
         const float y = chain_rows<K, CR>(part);
         float conv_out = 0.0f;  // QKVG: the row's conv + SiLU output (owner lanes)
@@ -809,14 +814,20 @@ __global__ __launch_bounds__(kTB, 1) void k_gemv_cu(const void *__restrict__ W, 
         for (int i = t; i < K; i += kTB) src.xdump[i] = xs[i];
         if (t == 0) src.xdump[K] = fast ? 1u : 0u;
     }
+    if constexpr (ST) {
+        __syncthreads();
+        phase_stamp<ST>(src.stamps, blockIdx.x, 3);
+    }
 }
 
 // Second argmax stage over the LM head's per-block results, which are in
 // index order: strict '>' within a thread's increasing indices, then a
 // merge that keeps the larger value and, on ties, the lower index.
+template <bool ST>
 __global__ __launch_bounds__(kT) void k_argmax(const float *__restrict__ part_val,
                                                const int *__restrict__ part_idx, int n,
-                                               int *__restrict__ tok_out) {
+                                               int *__restrict__ tok_out, uint64_t *stamps) {
+    phase_stamp<ST>(stamps, 0, 0);
     __shared__ float bv[4];
     __shared__ int bi[4];
     float best = -3.402823466e38f;
@@ -850,6 +861,7 @@ __global__ __launch_bounds__(kT) void k_argmax(const float *__restrict__ part_va
                 idx = bi[i];
             }
         }
+        phase_stamp<ST>(stamps, 0, 3);
         tok_out[0] = idx;  // host-mapped: the step's completion signal
     }
 }
@@ -858,14 +870,15 @@ __global__ __launch_bounds__(kT) void k_argmax(const float *__restrict__ part_va
 // in the tiled layout.  beta_h and decay_h are evaluated from the QKVG
 // kernel's a_h and b_h in every workgroup of head h.  PRE: the q/k sums of squares come from the QKVG
 // kernel and the output norm's chunk sums go to o_sum (BF16 contracts).
-template <int C, int CB, bool PRE>
+template <int C, int CB, bool PRE, bool ST = false>
 __global__ __launch_bounds__(kT) void k_recur(const float *__restrict__ qp,
                                               const float *__restrict__ kp,
                                               const float *__restrict__ vp, ScalarsFromAB scal,
                                               const float *__restrict__ qk_part,
                                               void *__restrict__ state, float *__restrict__ attn,
-                                              float *__restrict__ o_sum) {
-    recur_block<C, CB, true, PRE, PRE>(qp, kp, vp, scal, qk_part, state, attn, o_sum, blockIdx.y, blockIdx.x * CB);
+                                              float *__restrict__ o_sum, uint64_t *stamps) {
+    recur_block<C, CB, true, PRE, PRE, ST>(qp, kp, vp, scal, qk_part, state, attn, o_sum, blockIdx.y,
+                                           blockIdx.x * CB, stamps, blockIdx.y * gridDim.x + blockIdx.x);
 }
 
 // out = R(a + b) over the hidden vector (layer output for the layer hook).
@@ -931,6 +944,11 @@ struct GDNEngine {
     // its stream order, exchange area held), and chosen for captured steps
     bool persist = false;
     bool use_persist = false;
+    // phase stamps of every kernel of the step (GDN_GRAPH_STAMPS=1 at init):
+    // [node][kStampWGs][kStampSlots], node 5 l + {0 QKVG, 1 recurrence,
+    // 2 o_proj, 3 gate/up, 4 down} for layer l, then 5 L the LM head and
+    // 5 L + 1 the argmax; null when off
+    uint64_t *gstamps = nullptr;
     uint32_t *xbuf = nullptr;
     uint32_t tag0 = 0;
     pst::Params pp{};
@@ -944,9 +962,17 @@ struct GDNEngine {
     GDNRunState *owner = nullptr;
 };
 
+constexpr int kStampWGs = 256;                   // slots per node: the widest grid
+constexpr int kStampNodes = 5 * kMaxLayers + 2;  // nodes of the largest step
+constexpr size_t kStampBytes = (size_t)kStampNodes * kStampWGs * kStampSlots * 8;
+
 namespace {
 
 size_t welem(int contract) { return contract == kFp32 ? 4 : 2; }
+
+uint64_t *node_stamps(GDNEngine *e, int node) {
+    return e->gstamps ? e->gstamps + (size_t)node * kStampWGs * kStampSlots : nullptr;
+}
 
 float *layer_aux(GDNEngine *e, int l) { return e->aux + (size_t)l * kAuxLayer; }
 float *final_norm(GDNEngine *e) { return e->aux + (size_t)e->layers * kAuxLayer; }
@@ -1288,6 +1314,12 @@ XSrc xsrc(GDNEngine *e, const float *a, const float *b, const float *c, const fl
 // step's 512-thread order when the engine has it).
 template <int C, int K, int ROWS, int D, int PRO, int EPI>
 void launch_gemv(GDNEngine *e, dim3 grid, hipStream_t s, const void *W, WInfo wi, const XSrc &x, const Epi &ep) {
+    if constexpr (C == kBf16w) {
+        if (e->gstamps) {  // the stamped copy (never with the persistent layout: init refuses both)
+            hipLaunchKernelGGL((k_gemv_cu<C, K, ROWS, D, PRO, EPI, 0, true>), grid, dim3(kTB), 0, s, W, wi, x, ep);
+            return;
+        }
+    }
     if constexpr (C != kFp32) {
         if (e->persist) {
             hipLaunchKernelGGL((k_gemv_cu<C, K, ROWS, D, PRO, EPI, pst::kNT>), grid, dim3(kTB), 0, s, W, wi, x, ep);
@@ -1314,6 +1346,7 @@ void launch_qkvg(GDNEngine *e, int l, const float *res_a, const float *res_b, hi
     q.ab = e->ab;
     q.qk_part = e->qkpart;
     XSrc xq = xsrc(e, res_a, res_b, nullptr, aux + kAuxAttnNorm, e->resid, nullptr, dump_slot(e, 4 * l));
+    xq.stamps = node_stamps(e, 5 * l);
     if constexpr (PRO0 == PRO_EMBED) {
         xq.emb = e->w_emb;
         xq.tok = e->tok_map;
@@ -1328,8 +1361,16 @@ template <int C>
 void launch_recur(GDNEngine *e, int l, hipStream_t s) {
     const float *aux = layer_aux(e, l);
     const ScalarsFromAB scal{e->ab, e->ab + kNH, aux + kAuxALog, aux + kAuxDtBias};
+    if constexpr (C == kBf16w) {
+        if (e->gstamps) {
+            hipLaunchKernelGGL((k_recur<C, kCB, true, true>), dim3(kHD / kCB, kNH), dim3(kT), 0, s, e->qkv,
+                               e->qkv + kH, e->qkv + 2 * kH, scal, e->qkpart, layer_state(e, l), e->attn, e->osum,
+                               node_stamps(e, 5 * l + 1));
+            return;
+        }
+    }
     hipLaunchKernelGGL((k_recur<C, kCB, C != kFp32>), dim3(kHD / kCB, kNH), dim3(kT), 0, s, e->qkv,
-                       e->qkv + kH, e->qkv + 2 * kH, scal, e->qkpart, layer_state(e, l), e->attn, e->osum);
+                       e->qkv + kH, e->qkv + 2 * kH, scal, e->qkpart, layer_state(e, l), e->attn, e->osum, nullptr);
 }
 
 template <int C>
@@ -1339,6 +1380,7 @@ void launch_o(GDNEngine *e, int l, hipStream_t s) {
     XSrc xo = xsrc(e, e->attn, e->gate, e->sgate, layer_aux(e, l) + kAuxONorm, nullptr, nullptr,
                    dump_slot(e, 4 * l + 1));
     xo.osum = e->osum;
+    xo.stamps = node_stamps(e, 5 * l + 2);
     launch_gemv<C, kH, kCuO, Depth<C>::o, PRO_ONORM, EPI_STORE>(e, dim3(kH / kCuO), s, e->w_o[l], e->i_o[l], xo,
                                                                 st);
 }
@@ -1347,8 +1389,9 @@ template <int C>
 void launch_gu(GDNEngine *e, int l, hipStream_t s) {
     Epi sw{};
     sw.y = e->hbuf;
-    const XSrc xg = xsrc(e, e->resid, e->ybuf_o, nullptr, layer_aux(e, l) + kAuxMlpNorm, e->resid_alt,
-                         nullptr, dump_slot(e, 4 * l + 2));
+    XSrc xg = xsrc(e, e->resid, e->ybuf_o, nullptr, layer_aux(e, l) + kAuxMlpNorm, e->resid_alt, nullptr,
+                   dump_slot(e, 4 * l + 2));
+    xg.stamps = node_stamps(e, 5 * l + 3);
     launch_gemv<C, kH, kCuGu, Depth<C>::gu, PRO_RESNORM, EPI_SWIGLU>(e, dim3(2 * kI / kCuGu), s, e->w_gu[l],
                                                                      e->i_gu[l], xg, sw);
 }
@@ -1357,7 +1400,8 @@ template <int C>
 void launch_down(GDNEngine *e, int l, hipStream_t s) {
     Epi dn{};
     dn.y = e->dbuf;
-    const XSrc xd = xsrc(e, e->hbuf, nullptr, nullptr, nullptr, nullptr, nullptr, dump_slot(e, 4 * l + 3));
+    XSrc xd = xsrc(e, e->hbuf, nullptr, nullptr, nullptr, nullptr, nullptr, dump_slot(e, 4 * l + 3));
+    xd.stamps = node_stamps(e, 5 * l + 4);
     launch_gemv<C, kI, kCuDown, Depth<C>::down, PRO_PLAIN, EPI_STORE>(e, dim3(kH / kCuDown), s, e->w_down[l],
                                                                       e->i_down[l], xd, dn);
 }
@@ -1373,8 +1417,9 @@ void launch_lm(GDNEngine *e, hipStream_t s) {
     lm.y = e->logits;
     lm.part_val = e->lm_val;
     lm.part_idx = e->lm_idx;
-    const XSrc xl = xsrc(e, e->resid_alt, e->dbuf, nullptr, final_norm(e), e->resid, e->fhid,
-                         dump_slot(e, 4 * e->layers));
+    XSrc xl = xsrc(e, e->resid_alt, e->dbuf, nullptr, final_norm(e), e->resid, e->fhid,
+                   dump_slot(e, 4 * e->layers));
+    xl.stamps = node_stamps(e, 5 * e->layers);
     const dim3 grid(lm_blocks(e));
     if ((e->vocab % kCuLm) == 0) {
         launch_gemv<C, kH, kCuLm, Depth<C>::lm, PRO_RESNORM, EPI_LM>(e, grid, s, e->w_lm, e->i_lm, xl, lm);
@@ -1385,7 +1430,12 @@ void launch_lm(GDNEngine *e, hipStream_t s) {
 }
 
 void launch_argmax(GDNEngine *e, hipStream_t s) {
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(kT), 0, s, e->lm_val, e->lm_idx, lm_blocks(e), e->tok_map + 1);
+    if (e->gstamps)
+        hipLaunchKernelGGL(k_argmax<true>, dim3(1), dim3(kT), 0, s, e->lm_val, e->lm_idx, lm_blocks(e),
+                           e->tok_map + 1, node_stamps(e, 5 * e->layers + 1));
+    else
+        hipLaunchKernelGGL(k_argmax<false>, dim3(1), dim3(kT), 0, s, e->lm_val, e->lm_idx, lm_blocks(e),
+                           e->tok_map + 1, nullptr);
 }
 
 template <int C, int PRO0>
@@ -1577,6 +1627,7 @@ void destroy_engine(GDNEngine *e) {
     if (e->tok_host) (void)hipHostFree(e->tok_host);
     persist_xbuf_release(e->xbuf);
     (void)hipFree(e->pp.stamps);
+    (void)hipFree(e->gstamps);
     delete e;
 }
 
@@ -1867,10 +1918,28 @@ int gdn_run_state_init_contract(GDNRunState *state, const GDNModel *model, uint3
         return -1;
     }
     if (e->persist) fill_persist_params(e);
-    if (e->persist && std::getenv("GDN_PERSIST_STAMPS")) {
-        // phase stamps of every step (gdn_test_step_buffers, which = 2)
-        GDN_HIP(hipMalloc(&e->pp.stamps, (size_t)pst::kWG * (kMaxLayers + 1) * pst::kStamps * 8));
-        GDN_HIP(hipMemset(e->pp.stamps, 0, (size_t)pst::kWG * (kMaxLayers + 1) * pst::kStamps * 8));
+    {
+        // phase stamps of every step (gdn_test_step_buffers, which = 2 and 3)
+        const size_t pbytes = (size_t)pst::kWG * (kMaxLayers + 1) * pst::kStamps * 8;
+        const char *gs = std::getenv("GDN_GRAPH_STAMPS");
+        bool sok = true;
+        if (e->persist && std::getenv("GDN_PERSIST_STAMPS"))
+            sok = hipMalloc(&e->pp.stamps, pbytes) == hipSuccess && hipMemset(e->pp.stamps, 0, pbytes) == hipSuccess;
+        if (gs != nullptr && gs[0] == '1' &&
+            (contract != kBf16w || e->persist || (e->vocab % kCuLm) != 0)) {
+            gdn_error("gdn_run_state_init: GDN_GRAPH_STAMPS=1 takes GDN_CONTRACT_BF16W_FP32S, a vocabulary of "
+                      "125-row LM-head blocks, and no GDN_PERSIST");
+            destroy_engine(e);
+            return -1;
+        }
+        if (sok && gs != nullptr && gs[0] == '1')
+            sok = hipMalloc(&e->gstamps, kStampBytes) == hipSuccess &&
+                  hipMemset(e->gstamps, 0, kStampBytes) == hipSuccess;
+        if (!sok) {
+            gdn_error("gdn_run_state_init: phase-stamp buffer allocation failed");
+            destroy_engine(e);
+            return -1;
+        }
     }
     state->engine = e;
     state->workspace = reinterpret_cast<Beat512 *>(hm.workspace);
@@ -2230,7 +2299,7 @@ int gdn_test_recurrence(int contract, uint32_t n_heads, uint32_t n_steps, const 
         const ScalarsFromAB scal{da + os, db + os, dal + os, ddt + os};
 #define GDN_REC(CC)                                                                                       \
     hipLaunchKernelGGL((k_recur<CC, kCB, false>), grid, block, 0, 0, dq + ov, dk + ov, dv + ov, scal, nullptr, \
-                       dS, dout + ov, nullptr)
+                       dS, dout + ov, nullptr, nullptr)
         if (contract == kRef) GDN_REC(kRef);
         else if (contract == kBf16w) GDN_REC(kBf16w);
         else GDN_REC(kFp32);
@@ -2258,8 +2327,6 @@ int gdn_test_recurrence(int contract, uint32_t n_heads, uint32_t n_steps, const 
     return 0;
 }
 
-// Layer `layer` of the run state for n_steps residual inputs x_in[s] (H
-// floats each); x_out[s] receives the layer's residual output.
 int gdn_test_step_buffers(const GDNRunState *state, int which, void *out, size_t bytes) {
     GDNEngine *e = engine_of(state);
     if (!e || out == nullptr) return -1;
@@ -2273,11 +2340,14 @@ int gdn_test_step_buffers(const GDNRunState *state, int which, void *out, size_t
     if (which == 1) return d2h(e, out, e->act, std::min(bytes, e->act_floats * 4));
     if (which == 2 && e->pp.stamps)
         return d2h(e, out, e->pp.stamps, std::min(bytes, (size_t)pst::kWG * (kMaxLayers + 1) * pst::kStamps * 8));
-    gdn_error("gdn_test_step_buffers: which is 0 (exchange area), 1 (activations) or 2 (persistent-step stamps, "
-              "GDN_PERSIST_STAMPS=1 at init)");
+    if (which == 3 && e->gstamps) return d2h(e, out, e->gstamps, std::min(bytes, kStampBytes));
+    gdn_error("gdn_test_step_buffers: which is 0 (exchange area), 1 (activations), 2 (persistent-step stamps, "
+              "GDN_PERSIST_STAMPS=1 at init) or 3 (per-kernel step stamps, GDN_GRAPH_STAMPS=1 at init)");
     return -1;
 }
 
+// Layer `layer` of the run state for n_steps residual inputs x_in[s] (H
+// floats each); x_out[s] receives the layer's residual output.
 int gdn_test_layer(GDNRunState *state, uint32_t layer, uint32_t n_steps, const float *x_in,
                    float *x_out) {
     GDNEngine *e = state->engine;

@@ -195,9 +195,10 @@ class RunState:
 
     def step_buffers(self, which: int, nbytes: int) -> np.ndarray:
         """gdn_test_step_buffers: the last step's exchange area (which = 0,
-        uint32 words), activations (1, float32, ACTIVATION_LAYOUT) or the
-        persistent step's phase stamps (2, uint64)."""
-        dt = {0: np.uint32, 1: np.float32, 2: np.uint64}[which]
+        uint32 words), activations (1, float32, ACTIVATION_LAYOUT), the
+        persistent step's phase stamps (2, uint64) or the per-kernel step's
+        (3, uint64)."""
+        dt = {0: np.uint32, 1: np.float32, 2: np.uint64, 3: np.uint64}[which]
         out = np.empty(nbytes // np.dtype(dt).itemsize, dt)
         _check(L.load().gdn_test_step_buffers(self.ptr, which, out.ctypes.data, out.nbytes), "gdn_test_step_buffers")
         return out

@@ -422,8 +422,13 @@ void gdn_test_libm_array(int which, const float *in, float *out, size_t n);
  * (tag << 16) | payload); which = 1, the per-kernel step's activation
  * buffers (FP32; layout in gateddeltanet_amd/engine.py); which = 2, the
  * persistent step's phase stamps when GDN_PERSIST_STAMPS=1 was set at init
- * (uint64 [256 workgroups][25][16] of the 100 MHz real-time counter).  No
- * reference counterpart. */
+ * (uint64 [256 workgroups][25][16] of the 100 MHz real-time counter);
+ * which = 3, the per-kernel step's phase stamps when GDN_GRAPH_STAMPS=1 was
+ * set at init (uint64 [122 kernels][256 workgroups][4]: start, input ready,
+ * products done, end, from each workgroup's thread 0; kernel 5 l + {0 QKVG,
+ * 1 recurrence, 2 o_proj, 3 gate/up, 4 down} of layer l, then the LM head
+ * and the argmax; the recurrence fills 128 workgroups, the argmax one, with
+ * its slots 0 and 3).  No reference counterpart. */
 int gdn_test_step_buffers(const GDNRunState *state, int which, void *out, size_t bytes);
 /* Layer `layer` of the run state's model for n_steps teacher-forced residual
  * inputs x_in[step][H] (BF16-exact for the BF16 contracts): the same kernels
