@@ -445,19 +445,30 @@ void write_bench_header(FILE *out, const Options &o, size_t stream_len) {
                  contract_name(o.contract));
 }
 
-// One measured interval: its wall-clock bounds and every step's token-in ->
-// token-out time (production_tpot) and graph time between HIP events
-// (kernel).
+// One measured interval: its wall-clock bounds (reported), its duration on
+// the monotonic clock (the rate; a wall-clock step cannot skew it) and every
+// step's token-in -> token-out time (production_tpot) and graph time between
+// HIP events (kernel).
 struct Interval {
     double start_unix = 0, end_unix = 0;
+    std::chrono::steady_clock::time_point t0, t1;
     std::vector<double> outer, inner;
+    void begin() {
+        start_unix = unix_now();
+        t0 = std::chrono::steady_clock::now();
+    }
+    void end() {
+        t1 = std::chrono::steady_clock::now();
+        end_unix = unix_now();
+    }
+    double seconds() const { return std::chrono::duration<double>(t1 - t0).count(); }
 };
 
 void write_interval(FILE *out, size_t index, const Interval &iv, bool first) {
     std::fprintf(out, "%s\n    {\"index\": %zu, \"start_unix\": %.6f, \"end_unix\": %.6f, \"steps\": %zu, "
                  "\"tokens_per_second\": %.3f, \"production_tpot\": ",
                  first ? "" : ",", index, iv.start_unix, iv.end_unix, iv.outer.size(),
-                 (double)iv.outer.size() / (iv.end_unix - iv.start_unix));
+                 (double)iv.outer.size() / iv.seconds());
     write_summary(out, summarize(iv.outer));
     std::fprintf(out, ", \"kernel\": ");
     write_summary(out, summarize(iv.inner));
@@ -482,11 +493,11 @@ int run_benchmark(const Options &o, const GDNModel &model, GDNRunState &rs) {
             die("benchmark warmup failed");
         std::vector<float> inner(steps), outer(steps);
         Interval iv;
-        iv.start_unix = unix_now();
+        iv.begin();
         if (gdn_run_teacher_forced(&rs, tokens.data(), (uint32_t)tokens.size(), steps, nullptr, inner.data(),
                                    outer.data()) != 0)
             die("benchmark failed");
-        iv.end_unix = unix_now();
+        iv.end();
         iv.outer.assign(outer.begin(), outer.end());
         iv.inner.assign(inner.begin(), inner.end());
         FILE *out = open_output(o.output);
@@ -516,14 +527,14 @@ int run_benchmark(const Options &o, const GDNModel &model, GDNRunState &rs) {
     std::vector<Interval> intervals(o.bench_intervals);
     for (uint32_t i = 0; i < o.bench_intervals; ++i) {
         Interval &iv = intervals[i];
-        iv.start_unix = unix_now();
+        iv.begin();
         for (const auto end = clock::now() + std::chrono::seconds(o.bench_interval_s); clock::now() < end;) {
             float inner = 0.0f, outer = 0.0f;
             one(&inner, &outer);
             iv.inner.push_back(inner);
             iv.outer.push_back(outer);
         }
-        iv.end_unix = unix_now();
+        iv.end();
         std::fprintf(stderr, "[benchmark] interval %u/%u steps=%zu\n", i + 1, o.bench_intervals, iv.outer.size());
     }
     FILE *out = open_output(o.output);

@@ -10,6 +10,7 @@ buffers through the HIP runtime the library itself loaded (libamdhip64 of
 the ROCm install); the entry point allocates nothing.
 """
 import ctypes
+import os
 
 import numpy as np
 import pytest
@@ -38,16 +39,21 @@ def _inputs(seed, steps, heads, contract):
 
 
 def _hip():
-    """The libamdhip64 that libgdn_amd.so loaded (one HIP runtime per process)."""
+    """The libamdhip64 that libgdn_amd.so runs on: the process must map
+    exactly one HIP runtime, so the caller-side allocations and copies here
+    and the library's kernels share it."""
     _lib.load()
+    paths = set()
     for line in open("/proc/self/maps"):
-        if "libamdhip64.so" in line:
-            hip = ctypes.CDLL(line.split()[-1])
-            hip.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
-            hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
-            hip.hipFree.argtypes = [ctypes.c_void_p]
-            return hip
-    raise RuntimeError("libamdhip64 is not loaded")
+        fields = line.split()
+        if len(fields) >= 6 and "libamdhip64.so" in fields[-1]:
+            paths.add(os.path.realpath(fields[-1]))
+    assert len(paths) == 1, f"expected one HIP runtime in the process, found {sorted(paths)}"
+    hip = ctypes.CDLL(paths.pop())
+    hip.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    hip.hipFree.argtypes = [ctypes.c_void_p]
+    return hip
 
 
 H2D, D2H = 1, 2
