@@ -89,7 +89,8 @@ MEASURED_TRAFFIC_FP32 = {
 TRAFFIC_SOURCE = ("rocprofv3 FETCH_SIZE + WRITE_SIZE passes, copy-calibrated "
                   "(profiles/k_gemv_cu_gdn13b_bf16w_decode.md); a profile constant, not measured in this run")
 TRAFFIC_SOURCE_FP32 = TRAFFIC_SOURCE.replace("bf16w", "fp32")
-LAUNCHES_PER_TOKEN = {"qkvg": L, "recur": L, "o_proj": L, "gate_up": L, "down": L, "lm_head": 1, "argmax": 1}
+LAUNCHES_PER_TOKEN = {"qkvg": L, "recur": L, "qkvg_recur": L, "o_proj": L, "gate_up": L, "down": L, "lm_head": 1,
+                      "argmax": 1}
 
 
 def cpu_baseline(model, contract_id, state, conv, tokens, threads, single_tokens):
@@ -275,9 +276,9 @@ def run_batch1(contract_name, steps, warmup, profile_rounds, eager, cpu_tokens, 
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": round(achieved_k / PEAK_HBM_GBPS, 4),
-            "traffic": (MEASURED_TRAFFIC[dom] if contract == g.CONTRACT_BF16W_FP32S else
+            "traffic": (MEASURED_TRAFFIC.get(dom) if contract == g.CONTRACT_BF16W_FP32S else
                         MEASURED_TRAFFIC_FP32.get(dom) if contract == g.CONTRACT_FP32 else None),
-            "traffic_source": (TRAFFIC_SOURCE if contract == g.CONTRACT_BF16W_FP32S else
+            "traffic_source": (TRAFFIC_SOURCE if contract == g.CONTRACT_BF16W_FP32S and dom in MEASURED_TRAFFIC else
                                TRAFFIC_SOURCE_FP32 if contract == g.CONTRACT_FP32 else None),
             "algorithmic_bytes_per_launch": kb,
             "avg_launch_us": round(avg_us, 3),

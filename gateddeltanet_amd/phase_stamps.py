@@ -41,6 +41,9 @@ H, I, V = 2048, 5632, 32000
 KERNEL_BYTES = {
     "qkvg": 4 * H * H * 2 + 2 * 8 * H * 2 + 3 * H * 4 * 4 + 3 * 3 * H * 2 * 2 + 2 * H * 2,
     "recur": 8 * 256 * 256 * 4 * 2,
+    # the fused QKVG + recurrence launch: both kernels' bytes
+    "qkvg_recur": (4 * H * H * 2 + 2 * 8 * H * 2 + 3 * H * 4 * 4 + 3 * 3 * H * 2 * 2 + 2 * H * 2
+                   + 8 * 256 * 256 * 4 * 2),
     "o_proj": H * H * 2 + 256 * 2,
     "gate_up": 2 * I * H * 2 + H * 2,
     "down": H * I * 2,
@@ -75,11 +78,20 @@ def collect(rs, tokens: np.ndarray, n_steps: int, layers: int) -> np.ndarray:
     return out
 
 
+def present_nodes(S: np.ndarray, layers: int, lm_wgs: int = 256) -> List[Tuple[int, str, int, int]]:
+    """(index, kind, layer, workgroups) of the nodes the step launched: a
+    node's slots stay zero when the step does not launch it (the recurrence
+    when it runs inside the fused QKVG launch)."""
+    return [(j, k, l, w) for j, (k, l, w) in enumerate(node_table(layers, lm_wgs)) if (S[:, j, :w, 0] != 0).any()]
+
+
 def per_node(S: np.ndarray, layers: int, lm_wgs: int = 256) -> Dict[str, np.ndarray]:
-    """Per step and node (us): start (from the step's first start), duration,
-    input ready (median / last workgroup), products done (last workgroup),
-    gap before the node (0 for the first)."""
-    table = node_table(layers, lm_wgs)
+    """Per step and launched node (us): start (from the step's first start),
+    duration, input ready (median / last workgroup), products done (last
+    workgroup), gap before the node (0 for the first)."""
+    nodes = present_nodes(S, layers, lm_wgs)
+    S = S[:, [j for j, _, _, _ in nodes]]
+    table = [(k, l, w) for _, k, l, w in nodes]
     n = S.shape[0]
     N = len(table)
     start = np.empty((n, N))
@@ -114,10 +126,15 @@ def per_node(S: np.ndarray, layers: int, lm_wgs: int = 256) -> Dict[str, np.ndar
 def summarize(S: np.ndarray, layers: int, lm_wgs: int = 256) -> Dict[str, object]:
     """Means over steps (and layers, for the per-layer kinds)."""
     P = per_node(S, layers, lm_wgs)
-    table = node_table(layers, lm_wgs)
+    table = [(k, l, w) for _, k, l, w in present_nodes(S, layers, lm_wgs)]
+    fused = not any(k == "recur" for k, _, _ in table)
     kinds = {}
     for kind in KINDS + ("lm_head", "argmax"):
         cols = [j for j, (k, _, _) in enumerate(table) if k == kind]
+        if not cols:
+            continue
+        if kind == "qkvg" and fused:
+            kind = "qkvg_recur"  # the QKVG launch that also runs the recurrence
         d = P["dur"][:, cols]
         row = {
             "launches_per_token": len(cols),
@@ -169,7 +186,8 @@ def markdown(summary: Dict[str, object], kernel_bytes: Dict[str, int], peak_gbps
         "```",
         "",
         f"{summary['steps']} teacher-forced steps of the 24-layer model, each one launch of the captured "
-        f"hipGraph of {summary['nodes']} kernels; every workgroup's thread 0 stores the 100 MHz real-time "
+        f"hipGraph of {summary['nodes']} kernels (the recurrence inside the QKVG launch when that has the fused "
+        "form); every workgroup's thread 0 stores the 100 MHz real-time "
         "counter at its start, input ready, products done and end.  Figures are means over the steps "
         "(and the 24 layers for the per-layer kernels); times within a kernel are from its first "
         "workgroup's start; the gap is the previous kernel's last end to this kernel's first start.",
@@ -178,7 +196,9 @@ def markdown(summary: Dict[str, object], kernel_bytes: Dict[str, int], peak_gbps
         "products done, last WG (us) | gap before (us) | algorithmic bytes | GB/s | frac of 8 TB/s |",
         "|---|---:|---:|---:|---:|---:|---:|---:|---:|",
     ]
-    for kind in KINDS + ("lm_head", "argmax"):
+    for kind in ("qkvg", "qkvg_recur") + KINDS[1:] + ("lm_head", "argmax"):
+        if kind not in k:
+            continue
         r = k[kind]
         b = kernel_bytes.get(kind)
         rate = b / (r["dur_us_mean"] * 1e-6) / 1e9 if b and kind != "argmax" else None

@@ -63,6 +63,26 @@ def test_recurrence_and_argmax_use_their_own_workgroup_counts():
     assert ps.summarize(S, 2)["kinds"]["recur"]["dur_us_mean"] == pytest.approx(1.02)
 
 
+def test_unlaunched_nodes_are_dropped():
+    """A step that runs its recurrence inside the QKVG launch leaves the
+    recurrence nodes' slots zero: they drop out, and the gaps join the
+    launched neighbours."""
+    L = 2
+    S = synthetic(L, 3)
+    for l in range(L):
+        S[:, 5 * l + 1] = 0
+    nodes = ps.present_nodes(S, L)
+    assert len(nodes) == 4 * L + 2 and all(k != "recur" for _, k, _, _ in nodes)
+    sm = ps.summarize(S, L)
+    assert "recur" not in sm["kinds"] and sm["nodes"] == 4 * L + 2
+    # the QKVG launch that runs the recurrence is accounted with both kernels' bytes
+    assert "qkvg" not in sm["kinds"] and sm["kinds"]["qkvg_recur"]["launches_per_token"] == L
+    assert ps.KERNEL_BYTES["qkvg_recur"] == ps.KERNEL_BYTES["qkvg"] + ps.KERNEL_BYTES["recur"]
+    # QKVG -> o_proj now spans the recurrence's 1.02 us and two 0.5 us gaps
+    assert sm["kinds"]["o_proj"]["gap_before_us_mean"] == pytest.approx(2.02)
+    assert "| recur |" not in ps.markdown(sm, ps.KERNEL_BYTES, ps.PEAK_HBM_GBPS, "cmd", 0.8, 0.79)
+
+
 @pytest.mark.gpu
 def test_graph_stamps_cover_every_kernel(monkeypatch):
     L = 24
@@ -80,8 +100,9 @@ def test_graph_stamps_cover_every_kernel(monkeypatch):
             assert rs.decode_step(t) == plain.decode_step(t)
             assert (rs.logits().view(np.uint32) == plain.logits().view(np.uint32)).all()
             S[i] = rs.step_buffers(3, S[i].nbytes).reshape(nodes, ps.STAMP_WGS, ps.SLOTS).astype(np.int64)
-        table = ps.node_table(L)
-        for j, (kind, _, w) in enumerate(table):
+        nodes = ps.present_nodes(S, L)
+        assert len(nodes) == 5 * L + 2
+        for j, kind, _, w in nodes:
             blk = S[:, j, :w]
             assert (blk[:, :, 0] > 0).all() and (blk[:, :, 3] > 0).all(), kind
             if kind != "argmax":
