@@ -8,7 +8,8 @@
 //   gdn_eval_amd <weights.gdnw> [fixture.gdnreq] [output.json]
 //       --decode-from-state <state.gdnstate> [--decode-len N]
 //       [--logits-dump F] [--logits-reference F] [--hidden-dump F]
-//       [--dump-state F] [--no-host-check]
+//       [--dump-state F] [--save-gdnstate F] [--interstep-delay-ms N]
+//       [--no-host-check]
 //   gdn_eval_amd <weights.gdnw> [output.json] --decode-from-state <state>
 //       --benchmark-tokens <tokens.txt> [--benchmark-idle-seconds N]
 //       [--benchmark-warmup-seconds N] [--benchmark-interval-seconds N]
@@ -37,8 +38,18 @@
 // Differences from the reference drivers:
 //  - per_step_tpot_ms is the token-in -> token-out time of the step (H2D,
 //    graph, D2H); the independent host checks after it are not included;
-//  - --dump-state writes the post-decode state as a .gdnstate file (the
-//    reference writes its FPGA stripe image, GDNSDMP1);
+//  - --dump-state writes the post-decode state in the reference's GDNSDMP1
+//    layout (gdn_eval.cpp:464-491: magic, {stripe beats, ports, head-buffer
+//    beats, 0}, the four BF16 state stripes, the packed conv tails) from the
+//    host mirrors gdn_sync_host_state refreshes; --save-gdnstate writes the
+//    same state as a .gdnstate another decode can start from (no reference
+//    counterpart; in --prefill mode --dump-state names the .gdnstate);
+//  - --interstep-delay-ms N sleeps N ms after each step, outside the step's
+//    tpot (host.cpp:1772-1775);
+//  - --ftz (gdn_eval.cpp:536-547) is refused: it sets FTZ/DAZ on the CPU
+//    FPU under the reference's native model; this engine computes on the
+//    GPU, where the contract alone fixes what flushes (the BF16 products'
+//    DAZ/FTZ) and the FP32 arithmetic keeps IEEE subnormals;
 //  - --logits-reference also reports the GPU-logit vector gate
 //    (host.cpp:77-110) beside the exact-match count.
 #include <algorithm>
@@ -69,7 +80,8 @@ double now_ms() {
 
 struct Options {
     std::string weights, fixture, output, state, logits_dump, logits_ref, hidden_dump, dump_state,
-        bench_tokens, prefill;
+        save_gdnstate, bench_tokens, prefill;
+    uint32_t interstep_delay_ms = 0;
     uint32_t decode_len = 0, bench_steps = 0, bench_warmup = 64, score_limit = 0, synth_layers = 0;
     // the timed benchmark protocol, with the reference's defaults (host.cpp:208-211)
     uint32_t bench_idle_s = 60, bench_warmup_s = 30, bench_interval_s = 60, bench_intervals = 3;
@@ -101,6 +113,13 @@ Options parse(int argc, char **argv) {
         else if (a == "--logits-reference") o.logits_ref = next("--logits-reference");
         else if (a == "--hidden-dump") o.hidden_dump = next("--hidden-dump");
         else if (a == "--dump-state") o.dump_state = next("--dump-state");
+        else if (a == "--save-gdnstate") o.save_gdnstate = next("--save-gdnstate");
+        else if (a == "--interstep-delay-ms")
+            o.interstep_delay_ms = parse_u32(next("--interstep-delay-ms"), "--interstep-delay-ms");
+        else if (a == "--ftz")
+            die("--ftz is not supported: the reference's flag sets FTZ/DAZ on the CPU FPU that runs its native "
+                "model; this engine computes on the GPU, where the contract alone fixes what flushes (the BF16 "
+                "products) and FP32 arithmetic keeps IEEE subnormals");
         else if (a == "--no-host-check") o.host_check = false;
         else if (a == "--benchmark-tokens") o.bench_tokens = next("--benchmark-tokens");
         else if (a == "--benchmark-steps") o.bench_steps = parse_u32(next("--benchmark-steps"), "--benchmark-steps");
@@ -133,7 +152,7 @@ Options parse(int argc, char **argv) {
                 "usage:\n"
                 "  gdn_eval_amd <weights.gdnw|--synth[=L]> [fixture.gdnreq] [out.json] "
                 "--decode-from-state S [--decode-len N] [--logits-dump F] [--logits-reference F] "
-                "[--hidden-dump F] [--dump-state F] [--no-host-check]\n"
+                "[--hidden-dump F] [--dump-state F] [--save-gdnstate F] [--interstep-delay-ms N] [--no-host-check]\n"
                 "  gdn_eval_amd <weights|--synth[=L]> [out.json] --decode-from-state S --benchmark-tokens T "
                 "[--benchmark-idle-seconds N] [--benchmark-warmup-seconds N] [--benchmark-interval-seconds N] "
                 "[--benchmark-intervals N]   (or a fixed count: [--benchmark-steps N] [--benchmark-warmup N])\n"
@@ -171,6 +190,10 @@ Options parse(int argc, char **argv) {
     if (!o.score && o.state.empty() && o.prefill.empty())
         die("a mode is required: --decode-from-state S, --score or --prefill P; see --help");
     if (!o.bench_tokens.empty() && o.state.empty()) die("--benchmark-tokens requires --decode-from-state");
+    if (!o.bench_tokens.empty() && (!o.dump_state.empty() || !o.save_gdnstate.empty() || o.interstep_delay_ms))
+        die("--dump-state, --save-gdnstate and --interstep-delay-ms apply to the decode run, not --benchmark-tokens");
+    if (!o.prefill.empty() && (!o.save_gdnstate.empty() || o.interstep_delay_ms))
+        die("--save-gdnstate and --interstep-delay-ms apply to the decode run, not --prefill");
     if (!o.bench_tokens.empty() && !o.bench_steps && (o.bench_interval_s == 0 || o.bench_intervals == 0))
         die("--benchmark-interval-seconds and --benchmark-intervals must be positive");
     return o;
@@ -291,6 +314,27 @@ const char *contract_name(int c) {
 
 // ------------------------------------------------------------- decode mode
 
+// The post-decode state in the reference's GDNSDMP1 layout
+// (gdn_eval.cpp:464-491): 8-byte magic, u32 {stripe beats, ports, head-buffer
+// beats, 0}, the BF16 state stripe of each port (the run state's host mirror
+// at weight_shards[28 + p] + gdn_weight_shard_beats), then the head buffer
+// (the packed conv tails).
+void write_state_dump(GDNRunState &rs, const GDNModel &model, const std::string &path) {
+    if (gdn_sync_host_state(&rs) != 0) die("cannot read the state back from the device");
+    FILE *f = std::fopen(path.c_str(), "wb");
+    if (!f) die("cannot create state dump " + path);
+    const uint32_t hb_beats = GDN_WSF_HEADBUF / 16u;
+    const uint32_t hdr[4] = {GDN_RECURRENT_STATE_STRIPE_BF16_BEATS, GDN_RECURRENT_STATE_PORTS, hb_beats, 0};
+    bool ok = std::fwrite("GDNSDMP1", 1, 8, f) == 8 && std::fwrite(hdr, 4, 4, f) == 4;
+    const size_t shard_beats = gdn_weight_shard_beats(&model.config);
+    for (int p = 0; ok && p < GDN_RECURRENT_STATE_PORTS; ++p)
+        ok = std::fwrite(rs.weight_shards[GDN_RECURRENT_STATE_FIRST_PORT + p] + shard_beats, sizeof(Beat512),
+                         GDN_RECURRENT_STATE_STRIPE_BF16_BEATS, f) == GDN_RECURRENT_STATE_STRIPE_BF16_BEATS;
+    ok = ok && std::fwrite(rs.head_buffer, sizeof(Beat512), hb_beats, f) == hb_beats;
+    if (std::fclose(f) != 0 || !ok) die("state dump write failed: " + path);
+    std::fprintf(stderr, "[state_dump] wrote %s\n", path.c_str());
+}
+
 int run_decode(const Options &o, const Fixture *fx, const GDNModel &model, GDNRunState &rs) {
     const uint32_t V = model.config.vocab_size, H = model.config.hidden_size;
     uint32_t prompt_len = 0;
@@ -368,13 +412,15 @@ int run_decode(const Options &o, const Fixture *fx, const GDNModel &model, GDNRu
             gdn_logits_parity_step(&gate, logits.data(), ref_logits.data(), V, (uint32_t)tok, 0);
         }
         if (ldump && std::fwrite(logits.data(), 4, V, ldump) != V) die("logits dump write failed");
+        if (o.interstep_delay_ms) std::this_thread::sleep_for(std::chrono::milliseconds(o.interstep_delay_ms));
     }
     if (ldump) std::fclose(ldump);
     if (hdump) std::fclose(hdump);
     if (lref) std::fclose(lref);
-    if (!o.dump_state.empty() &&
-        gdn_save_gdnstate(&rs, &model, o.dump_state.c_str(), nullptr, 0, traj[n - 1]) != 0)
-        die("cannot write " + o.dump_state);
+    if (!o.save_gdnstate.empty() &&
+        gdn_save_gdnstate(&rs, &model, o.save_gdnstate.c_str(), nullptr, 0, traj[n - 1]) != 0)
+        die("cannot write " + o.save_gdnstate);
+    if (!o.dump_state.empty()) write_state_dump(rs, model, o.dump_state);
     std::fprintf(stderr,
                  "[logits] steps=%u values=%llu max_abs=%.9g max_rel=%.9g cpu_tol_fail=%llu "
                  "exact_ref_mismatch=%llu argmax_mismatch=%u\n",

@@ -2,10 +2,11 @@
 the same model stepped through the library in this process.
 
 * decode-from-state (gdn_eval.cpp:269-529): the trajectory, the GDNLOG1
-  logits and GDNHID1 hidden dumps and the post-decode .gdnstate equal the
-  in-process run bit for bit; the host check passes (exit 0); a second run
-  against the first run's logits dump reports no exact mismatch and passes
-  the vector gate.
+  logits and GDNHID1 hidden dumps, the post-decode GDNSDMP1 state dump
+  (gdn_eval.cpp:464-491) and .gdnstate equal the in-process run bit for bit;
+  the host check passes (exit 0); a second run, with an inter-step delay
+  (host.cpp:1772-1775), against the first run's logits dump reports no exact
+  mismatch and passes the vector gate.  --ftz is refused with a message.
 * the steady teacher-forced benchmark (host.cpp:2150-2256) reports every
   step it was asked for; its timed protocol (idle window, timed warmup,
   timed intervals) reports ordered windows and consistent rates.
@@ -21,12 +22,15 @@ import os
 import shutil
 import struct
 import subprocess
+import time
 
 import numpy as np
 import pytest
 from scipy.special import log_softmax
 
 import gateddeltanet_amd as g
+from gateddeltanet_amd import _lib
+from test_gpu_dropin import decode_stripes
 
 pytestmark = pytest.mark.gpu
 
@@ -87,9 +91,10 @@ def decoded(model, tmp_path_factory):
 
 def test_decode_from_state_matches_library(model, decoded):
     d = decoded["dir"]
-    out, ldump, hdump, sdump = (str(d / n) for n in ("dec.json", "l.gdnlog", "h.gdnhid", "after.gdnstate"))
+    out, ldump, hdump, sdump, sdmp = (str(d / n) for n in ("dec.json", "l.gdnlog", "h.gdnhid", "after.gdnstate",
+                                                           "after.sdmp"))
     r = run_cli("--synth=1", out, "--decode-from-state", decoded["state"], "--decode-len", str(N_DECODE),
-                "--logits-dump", ldump, "--hidden-dump", hdump, "--dump-state", sdump)
+                "--logits-dump", ldump, "--hidden-dump", hdump, "--save-gdnstate", sdump, "--dump-state", sdmp)
     assert r.returncode == 0, r.stderr
     res = json.load(open(out))
     ex = res["examples"][0]
@@ -109,17 +114,40 @@ def test_decode_from_state_matches_library(model, decoded):
         rs.free()
     assert seed == decoded["traj"][-1]
     assert same_bits(rec, decoded["rec"]) and same_bits(conv, decoded["conv"])
+    # GDNSDMP1: header, the four BF16 stripes in the reference's map, then the
+    # head buffer (72 conv-tail stripes of 384 beats; the first 3 hold this
+    # 1-layer model's BF16 tails in their first 192 beats, the rest zero)
+    raw = open(sdmp, "rb").read()
+    assert raw[:8] == b"GDNSDMP1"
+    beats, ports, hb_beats, zero = struct.unpack("<4I", raw[8:24])
+    assert (beats, ports, hb_beats, zero) == (_lib.RECURRENT_STATE_STRIPE_BF16_BEATS, 4, _lib.WSF_HEADBUF // 16, 0)
+    assert len(raw) == 24 + (4 * beats + hb_beats) * 64
+    rows = 8 * 256
+    bits = decode_stripes(raw[24:24 + 4 * beats * 64], rows)
+    assert (bits.astype(np.uint32) << 16 == decoded["rec"].view(np.uint32).reshape(rows, 256)).all()
+    hb = np.frombuffer(raw[24 + 4 * beats * 64:], np.uint16).reshape(72, 384, 32)
+    assert (hb[:3, :192].reshape(-1).astype(np.uint32) << 16 == decoded["conv"].view(np.uint32)).all()
+    assert (hb[3:] == 0).all() and (hb[:, 192:] == 0).all()
 
-    # the same run against its own dump: exact, and inside the vector gate
+    # the same run against its own dump, a step every 20 ms: exact, and
+    # inside the vector gate; the delay sits outside the step's tpot
     out2 = str(d / "dec2.json")
+    t0 = time.monotonic()
     r = run_cli("--synth=1", out2, "--decode-from-state", decoded["state"], "--decode-len", str(N_DECODE),
-                "--logits-reference", ldump, "--no-host-check")
+                "--logits-reference", ldump, "--no-host-check", "--interstep-delay-ms", "20")
     assert r.returncode == 0, r.stderr
+    assert time.monotonic() - t0 >= 0.02 * (N_DECODE - 1)
+    assert max(json.load(open(out2))["examples"][0]["per_step_tpot_ms"]) < 20.0
     res2 = json.load(open(out2))
     assert res2["logits_parity"]["exact_reference_mismatches"] == 0
     vg = res2["vector_gate"]
     assert vg["passes"] is True and vg["global_nrmse"] == 0.0 and vg["min_top5_overlap"] == 5
     assert res2["examples"][0]["gen_traj"] == decoded["traj"]
+
+
+def test_ftz_refused(decoded):
+    r = run_cli("--synth=1", "--decode-from-state", decoded["state"], "--ftz")
+    assert r.returncode != 0 and "--ftz is not supported" in r.stderr
 
 
 def test_decode_length_from_ll_fixture(decoded):
