@@ -130,6 +130,7 @@ __global__ __launch_bounds__(NW * 64) void k_bgemm(const u32x4 *__restrict__ W, 
     __shared__ float lm_v[RT * 4][64];
     __shared__ int lm_i[RT * 4][64];
     __shared__ uint64_t exp2_lds[EPI == EPI_QKVG ? 32 : 1];  // expf's table for the epilogue
+    __shared__ f32x4 conv_lds[EPI == EPI_QKVG ? RT * 16 : 1];  // the conv taps of the workgroup's channels
     if constexpr (EPI == EPI_QKVG) fill_exp2_lds_imm(exp2_lds);
     // QKVG: consecutive row blocks on one XCD (workgroups are dealt to the 8
     // XCDs round-robin), so the two 64-byte halves of a conv-tail line are
@@ -142,22 +143,29 @@ __global__ __launch_bounds__(NW * 64) void k_bgemm(const u32x4 *__restrict__ W, 
     const u32x4 *wp = W + ((size_t)rb * KT + kt0) * (RT * 64) + l;
     const u32x4 *xp = X + (size_t)kt0 * (4 * 64) + l;
 
-    // QKVG epilogue operands (each stream's conv tails and the taps) are
-    // read ahead of the weight stream
-    constexpr int QE = (EPI == EPI_QKVG) ? (RT * 16 * 64) / GT : 1;
-    f32x4 qtl[QE], qcw[QE];
+    // QKVG epilogue tasks: four consecutive channels of one stream per
+    // thread and pass (4-channel group g of the workgroup's RT * 4, stream
+    // q / (RT * 4)), so tails, q/k/v and gate move as 8- and 16-byte
+    // accesses.  Each stream's conv tails (three taps of BF16 bits per
+    // channel) and the workgroup's taps (into LDS) are read ahead of the
+    // weight stream.
+    constexpr int CG = RT * 4;
+    constexpr int QE = (EPI == EPI_QKVG) ? (64 * CG) / GT : 1;
+    static_assert(EPI != EPI_QKVG || (64 * CG) % GT == 0, "whole epilogue tasks per thread");
+    const int which = (rb * 16 * RT) / kH, c0 = rb * 16 * RT - which * kH;  // q, k, v, g section
+    uint2 qtl[QE][3];
     if constexpr (EPI == EPI_QKVG) {
+        if (which < 3 && t < RT * 16)
+            conv_lds[t] = *reinterpret_cast<const f32x4 *>(ep.conv_w + ((size_t)which * kH + c0 + t) * 4);
 #pragma unroll
         for (int j = 0; j < QE; ++j) {
-            const int q = t + GT * j, cl = q & (RT * 16 - 1), m = q / (RT * 16);
-            const int row = rb * 16 * RT + cl, which = row / kH, c = row - which * kH;
-            qtl[j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-            qcw[j] = qtl[j];
+            const int q = t + GT * j, m = q / CG, c = c0 + 4 * (q % CG);
+#pragma unroll
+            for (int k = 0; k < 3; ++k) qtl[j][k] = make_uint2(0u, 0u);
             if (which < 3 && m < ep.n_streams) {
                 const uint16_t *tl = ep.tails + ((size_t)m * 3 + which) * 3 * kH + c;
-                qtl[j] = (f32x4){bf16_bits_to_f32(tl[0]), bf16_bits_to_f32(tl[kH]), bf16_bits_to_f32(tl[2 * kH]),
-                                 0.0f};
-                qcw[j] = *reinterpret_cast<const f32x4 *>(ep.conv_w + ((size_t)which * kH + c) * 4);
+#pragma unroll
+                for (int k = 0; k < 3; ++k) qtl[j][k] = *reinterpret_cast<const uint2 *>(tl + k * kH);
             }
         }
     }
@@ -203,22 +211,14 @@ __global__ __launch_bounds__(NW * 64) void k_bgemm(const u32x4 *__restrict__ W, 
     __syncthreads();
 
     // Task (rt, nq, m): rows rt * 16 + nq * 4 + 0..3 of stream m, held by lane
-    // nq * 16 + m % 16 of stream group m / 16 in every wave's D tile.  Plain
-    // stores take a task per thread; the transcendental epilogues take one
-    // row (component e) of a task per thread.
+    // nq * 16 + m % 16 of stream group m / 16 in every wave's D tile.  Every
+    // epilogue takes whole tasks (the four rows as one f32x4).
     auto red_index = [&](int rt, int nq, int m) { return (rt * 4 + (m >> 4)) * 64 + nq * 16 + (m & 15); };
     auto reduced = [&](int rt, int nq, int m) {
         const int idx = red_index(rt, nq, m);
         f32x4 v = red[idx];
 #pragma unroll
         for (int ww = 1; ww < NW; ++ww) v = v + red[ww * RT * 4 * 64 + idx];
-        return v;
-    };
-    auto reduced1 = [&](int rt, int nq, int m, int e) {
-        const float *rf = reinterpret_cast<const float *>(red) + 4 * red_index(rt, nq, m) + e;
-        float v = rf[0];
-#pragma unroll
-        for (int ww = 1; ww < NW; ++ww) v = v + rf[4 * ww * RT * 4 * 64];
         return v;
     };
     if constexpr (EPI == EPI_RAW || EPI == EPI_STORE || EPI == EPI_LM) {
@@ -251,26 +251,42 @@ __global__ __launch_bounds__(NW * 64) void k_bgemm(const u32x4 *__restrict__ W, 
             }
         }
     } else if constexpr (EPI == EPI_QKVG) {
-        // one element per thread and pass, channels fastest (coalesced tails)
 #pragma unroll
         for (int j = 0; j < QE; ++j) {
-            const int q = t + GT * j, cl = q & (RT * 16 - 1), m = q / (RT * 16);
+            const int q = t + GT * j, g = q % CG, m = q / CG, c = c0 + 4 * g;
             if (m >= ep.n_streams) continue;
-            const int row = rb * 16 * RT + cl;
-            const int which = row / kH, c = row - which * kH;  // q, k, v, g sections
-            const float raw = rne_bf16(reduced1(cl >> 4, (cl >> 2) & 3, m, cl & 3));
+            // channels c..c+3 are rows 4 (g % 4) .. of row tile g / 4
+            const f32x4 v = reduced(g >> 2, g & 3, m);
+            const float raw[4] = {rne_bf16(v.x), rne_bf16(v.y), rne_bf16(v.z), rne_bf16(v.w)};
             if (which < 3) {
                 // gdn_depthwise_conv_silu_head_kind, gdn_model.cpp:1543-1667
                 uint16_t *tl = ep.tails + ((size_t)m * 3 + which) * 3 * kH + c;
-                const f32x4 tv = qtl[j], cw = qcw[j];
-                const float sum = tv.x * cw.x + tv.y * cw.y + tv.z * cw.z + raw * cw.w;
-                tl[0] = bf16_hi(tv.y);
-                tl[kH] = bf16_hi(tv.z);
-                tl[2 * kH] = bf16_hi(raw);
-                ep.qkv[((size_t)m * 3 + which) * kH + c] = rne_bf16(silu_ref(sum, Exp2Lds{exp2_lds}));
+                const uint32_t tw[3][2] = {{qtl[j][0].x, qtl[j][0].y}, {qtl[j][1].x, qtl[j][1].y},
+                                           {qtl[j][2].x, qtl[j][2].y}};
+                float o[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int sh = 16 * (e & 1);
+                    const f32x4 cw = conv_lds[4 * g + e];
+                    const float t0 = bf16_bits_to_f32((uint16_t)(tw[0][e >> 1] >> sh));
+                    const float t1 = bf16_bits_to_f32((uint16_t)(tw[1][e >> 1] >> sh));
+                    const float t2 = bf16_bits_to_f32((uint16_t)(tw[2][e >> 1] >> sh));
+                    const float sum = t0 * cw.x + t1 * cw.y + t2 * cw.z + raw[e] * cw.w;
+                    o[e] = rne_bf16(silu_ref(sum, Exp2Lds{exp2_lds}));
+                }
+                // the tails shift by one tap: (t1, t2, raw)
+                *reinterpret_cast<uint2 *>(tl) = qtl[j][1];
+                *reinterpret_cast<uint2 *>(tl + kH) = qtl[j][2];
+                *reinterpret_cast<uint2 *>(tl + 2 * kH) =
+                    make_uint2((uint32_t)bf16_hi(raw[0]) | ((uint32_t)bf16_hi(raw[1]) << 16),
+                               (uint32_t)bf16_hi(raw[2]) | ((uint32_t)bf16_hi(raw[3]) << 16));
+                *reinterpret_cast<f32x4 *>(ep.qkv + ((size_t)m * 3 + which) * kH + c) =
+                    (f32x4){o[0], o[1], o[2], o[3]};
             } else {
-                ep.gate[(size_t)m * kH + c] = raw;
-                ep.sgate[(size_t)m * kH + c] = sigmoid_ref(raw, Exp2Lds{exp2_lds});
+                *reinterpret_cast<f32x4 *>(ep.gate + (size_t)m * kH + c) = (f32x4){raw[0], raw[1], raw[2], raw[3]};
+                *reinterpret_cast<f32x4 *>(ep.sgate + (size_t)m * kH + c) =
+                    (f32x4){sigmoid_ref(raw[0], Exp2Lds{exp2_lds}), sigmoid_ref(raw[1], Exp2Lds{exp2_lds}),
+                            sigmoid_ref(raw[2], Exp2Lds{exp2_lds}), sigmoid_ref(raw[3], Exp2Lds{exp2_lds})};
             }
         }
     }
