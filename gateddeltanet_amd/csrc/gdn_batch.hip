@@ -1650,6 +1650,119 @@ __global__ __launch_bounds__(kPgW * 64) void k_pgemm(const u32x4 *__restrict__ W
     }
 }
 
+// k_pgemm with the weights streamed straight into registers: one workgroup
+// per 32 kPgW rows (a 32-row block per wave) x 128 tokens, wave w owning
+// rows 32 w .. 32 w + 31 of them for all 128 tokens, so no two waves need the same
+// weight fragment and only the tokens' fragments (8 KB per k tile) pass
+// through LDS.  The k loop runs one class of one split per trip (its KTW
+// tiles unrolled, the next kPaD tiles' operands in flight across trips):
+// a loop of fixed shape, whose waits on memory the compiler keeps exact,
+// where a loop of kPgD tiles with a data-dependent class close waited for
+// every load in flight at its top.  Same fragments, chains, class order and
+// split order as k_pgemm, so the same sums bit for bit.  Measured on the
+// 4096-token segment: q/k/v/g 195 -> 167 us, down 149 -> 121 us; o_proj
+// (16 k tiles per split) stays on k_pgemm, where it measured no faster.
+constexpr int kPaRows = 32 * kPgW;  // rows per workgroup
+constexpr int kPaD = 2;       // k tiles of operands in flight
+template <int KT, int NW, int S>
+__global__ __launch_bounds__(kPgW * 64) void k_pgemm_a(const u32x4 *__restrict__ W, const u32x4 *__restrict__ X,
+                                                       float *__restrict__ y, int n_rows) {
+    constexpr int R = kPaRows / 16 / kPgW;  // 16-row tiles per wave
+    constexpr int T = kPgTok / 16;          // 16-token groups per wave
+    constexpr int GT = kPgW * 64, BU = T * 64, PB = BU / GT;
+    constexpr int NB = R * T, KTS = KT / S, KTW = KTS / NW;
+    static_assert(R == 2 && BU % GT == 0 && KT % S == 0 && KTS % NW == 0, "row and token tiles per workgroup");
+    __shared__ u32x4 stg[2][BU];
+    const int t = threadIdx.x, w = t >> 6, l = t & 63;
+    int rt, tt;
+    pg_place(rt, tt);
+    // wave w's rows: 32-row block kPgW rt + w of the weight layout (its two
+    // tiles at entries 0..63 and 64..127 of each k tile)
+    const u32x4 *ap = W + (size_t)(kPgW * rt + w) * KT * 128 + l;
+    // B entry q of a k tile: token group q / 64 (of 8), lane q % 64
+    const u32x4 *bp[PB];
+#pragma unroll
+    for (int i = 0; i < PB; ++i) {
+        const int q = t + GT * i;
+        bp[i] = X + (size_t)(2 * tt + (q >> 8)) * KT * 256 + (q & 255);
+    }
+    f32x4 chain[NB], part[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        chain[b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        part[b] = chain[b];
+    }
+    u32x4 ra[kPaD][R], rb[kPaD][PB];
+#pragma unroll
+    for (int d = 0; d < kPaD; ++d) {
+        const int kt = pg_tile<KT, NW, S>(d);
+#pragma unroll
+        for (int f = 0; f < R; ++f) ra[d][f] = ap[(size_t)kt * 128 + 64 * f];
+#pragma unroll
+        for (int i = 0; i < PB; ++i) rb[d][i] = bp[i][(size_t)kt * 256];
+    }
+    // row tile f: rows kPaRows rt + 32 w + 16 f + 4 (l / 16) .. +3; token group
+    // g: token 128 tt + 16 g + l % 16
+    const int row = kPaRows * rt + 32 * w + 4 * (l >> 4);
+    const int m = kPgTok * tt + (l & 15);
+    auto out = [&](int f, int g) {
+        return reinterpret_cast<f32x4 *>(y + (size_t)(m + 16 * g) * n_rows + row + 16 * f);
+    };
+    for (int c = 0; c < KT / KTW; ++c) {
+#pragma unroll
+        for (int i = 0; i < KTW; ++i) {
+            const int j = c * KTW + i, sb = j & 1;
+            u32x4 fa[R];
+#pragma unroll
+            for (int f = 0; f < R; ++f) fa[f] = ra[0][f];
+#pragma unroll
+            for (int q = 0; q < PB; ++q) stg[sb][t + GT * q] = rb[0][q];
+#pragma unroll
+            for (int d = 0; d + 1 < kPaD; ++d) {
+#pragma unroll
+                for (int f = 0; f < R; ++f) ra[d][f] = ra[d + 1][f];
+#pragma unroll
+                for (int q = 0; q < PB; ++q) rb[d][q] = rb[d + 1][q];
+            }
+            {
+                // issued on every tile (the last ones re-read the final tile,
+                // unused), so the loop's shape stays fixed
+                const int kt = pg_tile<KT, NW, S>(j + kPaD < KT ? j + kPaD : KT - 1);
+#pragma unroll
+                for (int f = 0; f < R; ++f) ra[kPaD - 1][f] = ap[(size_t)kt * 128 + 64 * f];
+#pragma unroll
+                for (int q = 0; q < PB; ++q) rb[kPaD - 1][q] = bp[q][(size_t)kt * 256];
+            }
+            __syncthreads();
+            u32x4 fb[T];
+#pragma unroll
+            for (int g = 0; g < T; ++g) fb[g] = stg[sb][64 * g + l];
+#pragma unroll
+            for (int g = 0; g < T; ++g)
+#pragma unroll
+                for (int f = 0; f < R; ++f)
+                    chain[T * f + g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(bf16x8, fa[f]), __builtin_bit_cast(bf16x8, fb[g]), chain[T * f + g], 0, 0,
+                        0);
+        }
+        // class c % NW of split c / NW closes: its chain joins the split's
+        // sum, and the last class's sum joins the total in split order
+        const int cls = c % NW;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            part[b] = cls == 0 ? chain[b] : part[b] + chain[b];
+            chain[b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        if (cls == NW - 1) {
+            const bool first = c < NW;
+#pragma unroll
+            for (int f = 0; f < R; ++f)
+#pragma unroll
+                for (int g = 0; g < T; ++g) *out(f, g) = first ? part[T * f + g] : *out(f, g) + part[T * f + g];
+        }
+    }
+}
+
 // Gate/up + SwiGLU for channel groups 2 rt, +1 (k_bgu's layout and sums:
 // four classes of 16 k tiles) and tokens 128 tt .. +127 (pg_place; the
 // first n_tok are written).  Wave w: group w & 1, token block w >> 1.
@@ -2217,8 +2330,8 @@ void enqueue_prefill_segment(GDNBatchEngine *e, int slot, int n, bool last, hipS
     for (int l = 0; l < e->layers; ++l) {
         float *st = b_state(e, l) + (size_t)slot * kLayerState;
         uint16_t *tl = b_tails(e, l) + (size_t)slot * kStreamTails;
-        hipLaunchKernelGGL((k_pgemm<kKtH, 8, 1>), dim3(4 * kH / 128, tiles), dim3(kPgW * 64), 0, s, e->w_qkvg[l], xh,
-                           e->s_y, 4 * kH);
+        hipLaunchKernelGGL((k_pgemm_a<kKtH, 8, 1>), dim3(4 * kH / kPaRows, tiles), dim3(kPgW * 64), 0, s,
+                           e->w_qkvg[l], xh, e->s_y, 4 * kH);
         hipLaunchKernelGGL(k_pconv, dim3(4 * kH / 64, blocks), dim3(kConvT), 0, s, e->s_y, n, tl,
                            b_aux(e, l) + kAuxConv, e->s_qkv, e->s_gate, e->s_sgate);
         hipLaunchKernelGGL(k_pqk, dim3(kNH, n), dim3(kT), 0, s, e->s_qkv, e->s_qn, e->s_kn, e->s_alpha);
@@ -2240,8 +2353,8 @@ void enqueue_prefill_segment(GDNBatchEngine *e, int slot, int n, bool last, hipS
         const BNorm pm = seg_norm(e, e->s_y, b_aux(e, l) + kAuxMlpNorm, e->s_xh, -1, l, l);
         hipLaunchKernelGGL((k_bnorm<1, false, false>), dim3(n), dim3(kT), 0, s, pm);
         hipLaunchKernelGGL(k_pgu, dim3(kGuWgs / 2, tiles), dim3(kPgW * 64), 0, s, e->w_gu[l], xh, e->s_xd, n);
-        hipLaunchKernelGGL((k_pgemm<kKtI, 4, kSplitDown>), dim3(kH / 128, tiles), dim3(kPgW * 64), 0, s, e->w_down[l],
-                           xd, e->s_y, kH);
+        hipLaunchKernelGGL((k_pgemm_a<kKtI, 4, kSplitDown>), dim3(kH / kPaRows, tiles), dim3(kPgW * 64), 0, s,
+                           e->w_down[l], xd, e->s_y, kH);
         if (l + 1 < e->layers) {
             BNorm pa = seg_norm(e, e->s_y, b_aux(e, l + 1) + kAuxAttnNorm, e->s_xh, -1, l, l + 1);
             pa.xn_out = e->s_xn;
@@ -2629,10 +2742,16 @@ int gdn_test_prefill_gemm(int kind, const float *W, const float *X, uint32_t N, 
     GDN_HIP(hipMemcpy(dx, xt.data(), xt.size() * 2, hipMemcpyHostToDevice));
     const u32x4 *w4 = static_cast<const u32x4 *>(dw), *x4 = static_cast<const u32x4 *>(dx);
     const dim3 pg(N / 128, tp / kPgTok);
-    if (kind == 0) hipLaunchKernelGGL((k_pgemm<kKtH, 8, 1>), pg, dim3(kPgW * 64), 0, 0, w4, x4, (float *)dy, (int)N);
+    const dim3 pa(N / kPaRows, tp / kPgTok);
+    if (kind == 0 && N % kPaRows == 0)
+        hipLaunchKernelGGL((k_pgemm_a<kKtH, 8, 1>), pa, dim3(kPgW * 64), 0, 0, w4, x4, (float *)dy, (int)N);
+    if (kind == 0 && N % kPaRows != 0)
+        hipLaunchKernelGGL((k_pgemm<kKtH, 8, 1>), pg, dim3(kPgW * 64), 0, 0, w4, x4, (float *)dy, (int)N);
     if (kind == 1)
         hipLaunchKernelGGL((k_pgemm<kKtH, 4, kSplitO>), pg, dim3(kPgW * 64), 0, 0, w4, x4, (float *)dy, (int)N);
-    if (kind == 2)
+    if (kind == 2 && N % kPaRows == 0)
+        hipLaunchKernelGGL((k_pgemm_a<kKtI, 4, kSplitDown>), pa, dim3(kPgW * 64), 0, 0, w4, x4, (float *)dy, (int)N);
+    if (kind == 2 && N % kPaRows != 0)
         hipLaunchKernelGGL((k_pgemm<kKtI, 4, kSplitDown>), pg, dim3(kPgW * 64), 0, 0, w4, x4, (float *)dy, (int)N);
     if (kind == 3)
         hipLaunchKernelGGL(k_pgu, dim3(kGuWgs / 2, tp / kPgTok), dim3(kPgW * 64), 0, 0, w4, x4,
