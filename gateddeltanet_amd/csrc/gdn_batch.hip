@@ -1659,9 +1659,11 @@ __global__ __launch_bounds__(kPgW * 64) void k_pgemm(const u32x4 *__restrict__ W
 // a loop of fixed shape, whose waits on memory the compiler keeps exact,
 // where a loop of kPgD tiles with a data-dependent class close waited for
 // every load in flight at its top.  Same fragments, chains, class order and
-// split order as k_pgemm, so the same sums bit for bit.  Measured on the
-// 4096-token segment: q/k/v/g 195 -> 167 us, down 149 -> 121 us; o_proj
-// (16 k tiles per split) stays on k_pgemm, where it measured no faster.
+// split order as k_pgemm, so the same sums bit for bit.  Traced in the
+// 4096-token prefill: q/k/v/g 169.5 -> 150.0 us, down 138.9 -> 127.9 us.
+// o_proj (16 k tiles per split) stays on k_pgemm, as it measured no faster
+// in isolation; so does any launch whose grid would not fill the CUs
+// (pa_fills), where k_pgemm's twice as many workgroups do better.
 constexpr int kPaRows = 32 * kPgW;  // rows per workgroup
 constexpr int kPaD = 2;       // k tiles of operands in flight
 template <int KT, int NW, int S>
@@ -2310,6 +2312,11 @@ BNorm seg_norm(GDNBatchEngine *e, const float *y, const float *w, uint16_t *x_ou
 // (k_pconv), and the recurrence chunk by chunk of 64 tokens, in token order
 // (k_pqk, k_pscan) or in the WY form (k_wy_gram and k_wy_inv over every
 // chunk at once, then k_wy_seq over the chunks in order).
+// k_pgemm_a (the faster kernel once its grid fills the CUs) or k_pgemm (twice
+// the workgroups at the same size, so the better one on short segments):
+// the same sums either way.
+bool pa_fills(int rows, int tiles) { return rows % kPaRows == 0 && (rows / kPaRows) * tiles >= 256; }
+
 void enqueue_prefill_segment(GDNBatchEngine *e, int slot, int n, bool last, hipStream_t s) {
     const int blocks = (n + kMaxB - 1) / kMaxB, tiles = (n + kPgTok - 1) / kPgTok;
     const int pab_blocks = (n + kPabTok - 1) / kPabTok;
@@ -2330,8 +2337,12 @@ void enqueue_prefill_segment(GDNBatchEngine *e, int slot, int n, bool last, hipS
     for (int l = 0; l < e->layers; ++l) {
         float *st = b_state(e, l) + (size_t)slot * kLayerState;
         uint16_t *tl = b_tails(e, l) + (size_t)slot * kStreamTails;
-        hipLaunchKernelGGL((k_pgemm_a<kKtH, 8, 1>), dim3(4 * kH / kPaRows, tiles), dim3(kPgW * 64), 0, s,
-                           e->w_qkvg[l], xh, e->s_y, 4 * kH);
+        if (pa_fills(4 * kH, tiles))
+            hipLaunchKernelGGL((k_pgemm_a<kKtH, 8, 1>), dim3(4 * kH / kPaRows, tiles), dim3(kPgW * 64), 0, s,
+                               e->w_qkvg[l], xh, e->s_y, 4 * kH);
+        else
+            hipLaunchKernelGGL((k_pgemm<kKtH, 8, 1>), dim3(4 * kH / 128, tiles), dim3(kPgW * 64), 0, s,
+                               e->w_qkvg[l], xh, e->s_y, 4 * kH);
         hipLaunchKernelGGL(k_pconv, dim3(4 * kH / 64, blocks), dim3(kConvT), 0, s, e->s_y, n, tl,
                            b_aux(e, l) + kAuxConv, e->s_qkv, e->s_gate, e->s_sgate);
         hipLaunchKernelGGL(k_pqk, dim3(kNH, n), dim3(kT), 0, s, e->s_qkv, e->s_qn, e->s_kn, e->s_alpha);
@@ -2353,8 +2364,12 @@ void enqueue_prefill_segment(GDNBatchEngine *e, int slot, int n, bool last, hipS
         const BNorm pm = seg_norm(e, e->s_y, b_aux(e, l) + kAuxMlpNorm, e->s_xh, -1, l, l);
         hipLaunchKernelGGL((k_bnorm<1, false, false>), dim3(n), dim3(kT), 0, s, pm);
         hipLaunchKernelGGL(k_pgu, dim3(kGuWgs / 2, tiles), dim3(kPgW * 64), 0, s, e->w_gu[l], xh, e->s_xd, n);
-        hipLaunchKernelGGL((k_pgemm_a<kKtI, 4, kSplitDown>), dim3(kH / kPaRows, tiles), dim3(kPgW * 64), 0, s,
-                           e->w_down[l], xd, e->s_y, kH);
+        if (pa_fills(kH, tiles))
+            hipLaunchKernelGGL((k_pgemm_a<kKtI, 4, kSplitDown>), dim3(kH / kPaRows, tiles), dim3(kPgW * 64), 0, s,
+                               e->w_down[l], xd, e->s_y, kH);
+        else
+            hipLaunchKernelGGL((k_pgemm<kKtI, 4, kSplitDown>), dim3(kH / 128, tiles), dim3(kPgW * 64), 0, s,
+                               e->w_down[l], xd, e->s_y, kH);
         if (l + 1 < e->layers) {
             BNorm pa = seg_norm(e, e->s_y, b_aux(e, l + 1) + kAuxAttnNorm, e->s_xh, -1, l, l + 1);
             pa.xn_out = e->s_xn;
