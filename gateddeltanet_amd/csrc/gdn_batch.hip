@@ -389,30 +389,50 @@ __global__ __launch_bounds__(NW * 64) void k_bgu(const u32x4 *__restrict__ W, co
         for (int g = 0; g < 4; ++g) red[((w * RT + r) * 4 + g) * 64 + l] = acc[r][g];
     __syncthreads();
 
-    // row rr of tile r, stream m: lane (rr / 4) * 16 + m % 16 of stream
-    // group m / 16, component rr % 4; waves added in order
-    auto val = [&](int r, int rr, int m) {
-        const float *rf =
-            reinterpret_cast<const float *>(red) + 4 * ((r * 4 + (m >> 4)) * 64 + (rr >> 2) * 16 + (m & 15)) + (rr & 3);
-        float v = rf[0];
+    // rows 4 nq .. 4 nq + 3 of tile r for stream m: lane nq * 16 + m % 16 of
+    // stream group m / 16 in every wave's tile, the waves added in order
+    auto val4 = [&](int r, int nq, int m) {
+        const int idx = (r * 4 + (m >> 4)) * 64 + nq * 16 + (m & 15);
+        f32x4 v = red[idx];
 #pragma unroll
-        for (int ww = 1; ww < NW; ++ww) v = v + rf[4 * ww * RT * 4 * 64];
+        for (int ww = 1; ww < NW; ++ww) v = v + red[ww * RT * 4 * 64 + idx];
         return v;
     };
-    // gemv32_store SwiGLU branch, gdn_model.cpp:4751-4767; two channels per
-    // thread and pass, one 4-byte store (22 b is even)
-    for (int q = t; q < 64 * (kGuCh / 2); q += GT) {
-        const int m = q / (kGuCh / 2), cp = q - m * (kGuCh / 2);
-        if (m >= n_streams) continue;
-        uint32_t packed = 0;
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const int cc = 2 * cp + e;
-            const float g = rne_bf16(cc < 16 ? val(0, cc, m) : val(2, cc - 16, m));
-            const float u = rne_bf16(cc < 16 ? val(1, cc, m) : val(2, cc - 16 + (kGuCh - 16), m));
-            packed |= bf16_daz_bits(rne_bf16(silu_ref(g, Exp2Lds{exp2_lds}) * u)) << (16 * e);
+    // gemv32_store SwiGLU branch, gdn_model.cpp:4751-4767, for channel c of
+    // the workgroup (gate g and up u as the GEMM left them)
+    auto swiglu = [&](float g, float u) {
+        return bf16_daz_bits(rne_bf16(silu_ref(rne_bf16(g), Exp2Lds{exp2_lds}) * rne_bf16(u)));
+    };
+    static_assert(kGuCh == 22 && GT == 256, "16 + 6 channels; 256 + 192 tasks over four waves");
+    // channels 4 nq .. 4 nq + 3 (gate rows of tile 0, up rows of tile 1):
+    // task (stream m, nq), thread 4 m + nq
+    {
+        const int m = t >> 2, nq = t & 3;
+        if (m < n_streams) {
+            const f32x4 g = val4(0, nq, m), u = val4(1, nq, m);
+            const uint32_t lo = swiglu(g.x, u.x) | (swiglu(g.y, u.y) << 16);
+            const uint32_t hi = swiglu(g.z, u.z) | (swiglu(g.w, u.w) << 16);
+            const int k0 = rb * kGuCh + 4 * nq;  // even: pairs never straddle an 8-column group
+            if ((k0 & 3) == 0) {
+                *reinterpret_cast<uint2 *>(x_next + xt_index(m, k0, kI)) = make_uint2(lo, hi);
+            } else {
+                *reinterpret_cast<uint32_t *>(x_next + xt_index(m, k0, kI)) = lo;
+                *reinterpret_cast<uint32_t *>(x_next + xt_index(m, k0 + 2, kI)) = hi;
+            }
         }
-        *reinterpret_cast<uint32_t *>(x_next + xt_index(m, rb * kGuCh + 2 * cp, kI)) = packed;
+    }
+    // channels 16 + 2 p, 17 + 2 p (gate rows 2 p, 2 p + 1 and up rows
+    // 2 p + 6, 2 p + 7 of tile 2): task (stream m, p), thread 64 + 3 m + p
+    if (t >= 64) {
+        const int q = t - 64, m = q / 3, p = q - 3 * m;
+        if (m < n_streams) {
+            const int rg = 2 * p, ru = 2 * p + 6;
+            const f32x4 gv = val4(2, rg >> 2, m), uv = val4(2, ru >> 2, m);
+            const float g0 = (rg & 3) ? gv.z : gv.x, g1 = (rg & 3) ? gv.w : gv.y;
+            const float u0 = (ru & 3) ? uv.z : uv.x, u1 = (ru & 3) ? uv.w : uv.y;
+            *reinterpret_cast<uint32_t *>(x_next + xt_index(m, rb * kGuCh + 16 + 2 * p, kI)) =
+                swiglu(g0, u0) | (swiglu(g1, u1) << 16);
+        }
     }
 }
 
