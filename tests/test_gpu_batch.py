@@ -399,6 +399,26 @@ def test_prefill_equals_steps(model, n):
         bs.free()
 
 
+def test_prefill_long_segment_equals_steps():
+    """A 4096-token segment, where the engine runs the q/k/v/g and down
+    projections on k_pgemm_a (its grid fills the CUs only from 1024 and 4096
+    tokens), equals 4096 single-stream steps bit for bit (2 layers)."""
+    m = g.Model.synth(num_layers=2, seed=4, std=0.02, bf16=True)
+    try:
+        prompt = g.synth_tokens(4096, 44, 0)
+        seed_ref, logits_ref, hidden_ref, (rec_ref, conv_ref) = stepped_reference(m, prompt)
+        bs = g.BatchState(m, 1)
+        try:
+            assert bs.prefill(0, prompt) == seed_ref
+            assert same_bits(bs.logits(0), logits_ref) and same_bits(bs.final_hidden(0), hidden_ref)
+            rec, conv = bs.save_stream_state(0)
+            assert same_bits(rec, rec_ref) and same_bits(conv, conv_ref)
+        finally:
+            bs.free()
+    finally:
+        m.free()
+
+
 def test_prefill_continues_a_decoded_stream(model):
     """A prefill on a stream that has already decoded tokens continues from
     its state and conv tails: 5 steps then a 70-token prefill equal 75
