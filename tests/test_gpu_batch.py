@@ -399,13 +399,16 @@ def test_prefill_equals_steps(model, n):
         bs.free()
 
 
-def test_prefill_long_segment_equals_steps():
+@pytest.mark.parametrize("n", [4096, 4200])
+def test_prefill_long_segment_equals_steps(n):
     """A 4096-token segment, where the engine runs the q/k/v/g and down
     projections on k_pgemm_a (its grid fills the CUs only from 1024 and 4096
-    tokens), equals 4096 single-stream steps bit for bit (2 layers)."""
+    tokens), equals n single-stream steps bit for bit (2 layers); at 4200
+    the 104-token second segment runs them on k_pgemm, from the first
+    segment's state."""
     m = g.Model.synth(num_layers=2, seed=4, std=0.02, bf16=True)
     try:
-        prompt = g.synth_tokens(4096, 44, 0)
+        prompt = g.synth_tokens(n, 44, 0)
         seed_ref, logits_ref, hidden_ref, (rec_ref, conv_ref) = stepped_reference(m, prompt)
         bs = g.BatchState(m, 1)
         try:
