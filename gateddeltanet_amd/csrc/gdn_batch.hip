@@ -868,61 +868,78 @@ __global__ __launch_bounds__(2 * CW) void k_brecur(const float *__restrict__ qkv
 // multi-stream step, so a prefill of n tokens equals n steps bit for bit.
 
 // The causal conv of one 64-channel block over 64 tokens of a segment of n:
-// grid (4 kH / 64, ceil(n / 64)).  raw is [n][4 kH] (the unrounded q, k, v,
+// grid (4 kH / 64, ceil(n / 64)), thread 16 m + j on token m and channels
+// 4 j .. 4 j + 3 of the block (16-byte loads and stores).  raw is [n][4 kH] (the unrounded q, k, v,
 // g sums); the tails are the prefilled stream's for this layer,
 // [q,k,v][3 oldest..newest][kH].  Token m's window is (s[m], s[m+1],
 // s[m+2]) and its input s[m+3] in the sequence s = tails ++ R(raw[0..n));
 // the new tails are s[n], s[n+1], s[n+2].  Only the first token block reads
 // the old tails, and it writes the new ones after that read.
-constexpr int kConvT = 1024;  // threads per conv workgroup: 16 token lanes x 64 channels
+constexpr int kConvT = 1024;  // threads per conv workgroup: 64 tokens x 16 lanes of 4 channels
 __global__ __launch_bounds__(kConvT) void k_pconv(const float *__restrict__ raw, int n, uint16_t *__restrict__ tails,
                                                   const float *__restrict__ conv_w, float *__restrict__ qkv,
                                                   float *__restrict__ gate, float *__restrict__ sgate) {
-    constexpr int MG = kConvT / 64;  // tokens in flight per channel
-    __shared__ float xs[kMaxB + 3][64];
+    static_assert(kConvT == 16 * kMaxB, "a thread per token and 4 channels");
+    __shared__ __attribute__((aligned(16))) float xs[kMaxB + 3][64];
     __shared__ uint64_t exp2_lds[32];  // expf's table, read per SiLU / sigmoid
-    const int row0 = blockIdx.x * 64, t = threadIdx.x, cl = t & 63, mg = t >> 6;
+    const int row0 = blockIdx.x * 64, t = threadIdx.x, m = t >> 4, c4 = 4 * (t & 15);
     const int m0 = (int)blockIdx.y * kMaxB, nb = n - m0 < kMaxB ? n - m0 : kMaxB;
     fill_exp2_lds_imm(exp2_lds);
     const Exp2Lds tab{exp2_lds};
-    const int row = row0 + cl, which = row0 / kH, c = row - which * kH;
+    const int which = row0 / kH, cb = row0 - which * kH;  // section and its first channel
+    const bool live = m < nb;
+    // token m0 + m's raw sums of channels cb + c4 .. + 3, one 16-byte load
+    f32x4 r = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (live) r = *reinterpret_cast<const f32x4 *>(raw + (size_t)(m0 + m) * 4 * kH + row0 + c4);
+    const f32x4 rr = {rne_bf16(r.x), rne_bf16(r.y), rne_bf16(r.z), rne_bf16(r.w)};
     if (which < 3) {
-        uint16_t *tl = tails + (size_t)which * 3 * kH + c;
+        uint16_t *tl = tails + (size_t)which * 3 * kH + cb;
+        const f32x4 *cw4 = reinterpret_cast<const f32x4 *>(conv_w + ((size_t)which * kH + cb + c4) * 4);
+        const f32x4 cw[4] = {cw4[0], cw4[1], cw4[2], cw4[3]};
         if (t < 64) {
             if (m0 == 0) {
-                xs[0][cl] = bf16_bits_to_f32(tl[0]);
-                xs[1][cl] = bf16_bits_to_f32(tl[kH]);
-                xs[2][cl] = bf16_bits_to_f32(tl[2 * kH]);
+                xs[0][t] = bf16_bits_to_f32(tl[t]);
+                xs[1][t] = bf16_bits_to_f32(tl[kH + t]);
+                xs[2][t] = bf16_bits_to_f32(tl[2 * kH + t]);
             } else {
 #pragma unroll
-                for (int i = 0; i < 3; ++i) xs[i][cl] = rne_bf16(raw[(size_t)(m0 - 3 + i) * 4 * kH + row]);
+                for (int i = 0; i < 3; ++i) xs[i][t] = rne_bf16(raw[(size_t)(m0 - 3 + i) * 4 * kH + row0 + t]);
             }
         }
-        for (int m = mg; m < nb; m += MG) xs[3 + m][cl] = rne_bf16(raw[(size_t)(m0 + m) * 4 * kH + row]);
+        if (live) *reinterpret_cast<f32x4 *>(&xs[3 + m][c4]) = rr;
         __syncthreads();
-        const f32x4 cw = *reinterpret_cast<const f32x4 *>(conv_w + ((size_t)which * kH + c) * 4);
-        for (int m = mg; m < nb; m += MG) {
+        if (live) {
             // gdn_depthwise_conv_silu_head_kind, gdn_model.cpp:1543-1667
-            const float sum = xs[m][cl] * cw.x + xs[m + 1][cl] * cw.y + xs[m + 2][cl] * cw.z + xs[m + 3][cl] * cw.w;
-            qkv[((size_t)(m0 + m) * 3 + which) * kH + c] = rne_bf16(silu_ref(sum, tab));
+            const f32x4 x0 = *reinterpret_cast<const f32x4 *>(&xs[m][c4]);
+            const f32x4 x1 = *reinterpret_cast<const f32x4 *>(&xs[m + 1][c4]);
+            const f32x4 x2 = *reinterpret_cast<const f32x4 *>(&xs[m + 2][c4]);
+            const f32x4 x3 = *reinterpret_cast<const f32x4 *>(&xs[m + 3][c4]);
+            f32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float sum = x0[e] * cw[e].x + x1[e] * cw[e].y + x2[e] * cw[e].z + x3[e] * cw[e].w;
+                o[e] = rne_bf16(silu_ref(sum, tab));
+            }
+            *reinterpret_cast<f32x4 *>(qkv + ((size_t)(m0 + m) * 3 + which) * kH + cb + c4) = o;
         }
         if (t < 64 && m0 == 0) {
             if (n <= kMaxB) {
-                tl[0] = bf16_hi(xs[n][cl]);
-                tl[kH] = bf16_hi(xs[n + 1][cl]);
-                tl[2 * kH] = bf16_hi(xs[n + 2][cl]);
+                tl[t] = bf16_hi(xs[n][t]);
+                tl[kH + t] = bf16_hi(xs[n + 1][t]);
+                tl[2 * kH + t] = bf16_hi(xs[n + 2][t]);
             } else {
 #pragma unroll
-                for (int i = 0; i < 3; ++i) tl[i * kH] = bf16_hi(rne_bf16(raw[(size_t)(n - 3 + i) * 4 * kH + row]));
+                for (int i = 0; i < 3; ++i)
+                    tl[i * kH + t] = bf16_hi(rne_bf16(raw[(size_t)(n - 3 + i) * 4 * kH + row0 + t]));
             }
         }
     } else {
-        __syncthreads();
-        for (int m = mg; m < nb; m += MG) {
-            const float g = rne_bf16(raw[(size_t)(m0 + m) * 4 * kH + row]);
-            gate[(size_t)(m0 + m) * kH + c] = g;
-            sgate[(size_t)(m0 + m) * kH + c] = sigmoid_ref(g, tab);
-        }
+        __syncthreads();  // expf's table
+        if (!live) return;
+        const size_t o = (size_t)(m0 + m) * kH + cb + c4;
+        *reinterpret_cast<f32x4 *>(gate + o) = rr;
+        *reinterpret_cast<f32x4 *>(sgate + o) = (f32x4){sigmoid_ref(rr.x, tab), sigmoid_ref(rr.y, tab),
+                                                         sigmoid_ref(rr.z, tab), sigmoid_ref(rr.w, tab)};
     }
 }
 
