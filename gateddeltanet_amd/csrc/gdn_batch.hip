@@ -693,16 +693,32 @@ __global__ __launch_bounds__(kT) void k_pab(const float *__restrict__ xn, int n,
         const int q = t + kT * i, grp = q >> 3, sub = q & 7;
         wq[i] = *reinterpret_cast<const f32x4 *>(ab_w + (size_t)ab_row(grp >> 6) * kH + 32 * (grp & 63) + 4 * sub);
     }
-    for (int mt = 0; mt < kPabTok && m0 + mt < n; ++mt) {
-        const float *x = xn + (size_t)(m0 + mt) * kH;
+    // PG tokens' inputs requested together (a token past the segment's end
+    // re-reads its last one, unused), then their products
+    constexpr int PG = 4;
+    static_assert(kPabTok % PG == 0, "whole token groups");
+    for (int mg = 0; mg < kPabTok && m0 + mg < n; mg += PG) {
+        f32x4 xq[PG][ABN];
 #pragma unroll
-        for (int i = 0; i < ABN; ++i) {
-            const int q = t + kT * i, grp = q >> 3, sub = q & 7;
-            const f32x4 xq = *reinterpret_cast<const f32x4 *>(x + 32 * (grp & 63) + 4 * sub);
-            const f32x4 w = wq[i];
-            float s = (xq.x * w.x + xq.y * w.y) + (xq.z * w.z + xq.w * w.w);
-            s = quad_sum(s);
-            if ((sub & 3) == 0) tab[mt][grp >> 6][grp & 63][sub >> 2] = s;
+        for (int g = 0; g < PG; ++g) {
+            const int m = m0 + mg + g < n ? m0 + mg + g : n - 1;
+            const float *x = xn + (size_t)m * kH;
+#pragma unroll
+            for (int i = 0; i < ABN; ++i) {
+                const int q = t + kT * i, grp = q >> 3, sub = q & 7;
+                xq[g][i] = *reinterpret_cast<const f32x4 *>(x + 32 * (grp & 63) + 4 * sub);
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < PG; ++g) {
+#pragma unroll
+            for (int i = 0; i < ABN; ++i) {
+                const int q = t + kT * i, grp = q >> 3, sub = q & 7;
+                const f32x4 w = wq[i], x = xq[g][i];
+                float s = (x.x * w.x + x.y * w.y) + (x.z * w.z + x.w * w.w);
+                s = quad_sum(s);
+                if ((sub & 3) == 0) tab[mg + g][grp >> 6][grp & 63][sub >> 2] = s;
+            }
         }
     }
     __syncthreads();
