@@ -398,8 +398,8 @@ __global__ __launch_bounds__(NW * 64) void k_bgu(const u32x4 *__restrict__ W, co
         for (int ww = 1; ww < NW; ++ww) v = v + red[ww * RT * 4 * 64 + idx];
         return v;
     };
-    // gemv32_store SwiGLU branch, gdn_model.cpp:4751-4767, for channel c of
-    // the workgroup (gate g and up u as the GEMM left them)
+    // gemv32_store SwiGLU branch, gdn_model.cpp:4751-4767, for one channel
+    // (its gate g and up u as the GEMM left them)
     auto swiglu = [&](float g, float u) {
         return bf16_daz_bits(rne_bf16(silu_ref(rne_bf16(g), Exp2Lds{exp2_lds}) * rne_bf16(u)));
     };
@@ -1547,8 +1547,8 @@ __global__ __launch_bounds__(kT) void k_wy_seq(const float *__restrict__ qkv, co
 // ------------------------------------------------ prefill projections
 //
 // A prefill segment runs layer by layer, so each layer's projection weights
-// are read once per segment instead of once per 64 tokens.  k_pgemm and
-// k_pgu form the segment's projections as GEMMs: one workgroup per 128 rows
+// are read once per segment instead of once per 64 tokens.  k_pgemm (and
+// k_pgemm_a, below) and k_pgu form the segment's projections as GEMMs: one workgroup per 128 rows
 // (four 32-row blocks of the weight layout; gate/up: two channel groups) x
 // 128 tokens (two 64-token X tile blocks), eight waves of 64 rows x 32
 // tokens, the k tile's fragments staged once through LDS (double buffer,
