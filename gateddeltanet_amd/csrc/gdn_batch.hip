@@ -884,30 +884,38 @@ __global__ __launch_bounds__(2 * CW) void k_brecur(const float *__restrict__ qkv
 // multi-stream step, so a prefill of n tokens equals n steps bit for bit.
 
 // The causal conv of one 64-channel block over 64 tokens of a segment of n:
-// grid (4 kH / 64, ceil(n / 64)), thread 16 m + j on token m and channels
-// 4 j .. 4 j + 3 of the block (16-byte loads and stores).  raw is [n][4 kH] (the unrounded q, k, v,
-// g sums); the tails are the prefilled stream's for this layer,
-// [q,k,v][3 oldest..newest][kH].  Token m's window is (s[m], s[m+1],
+// grid (4 kH / 64, ceil(n / 64)), thread 16 r + j on channels 4 j .. 4 j + 3
+// of the block and tokens r, r + 16, r + 32, r + 48 (16-byte loads and
+// stores; the four loads in flight together).  raw is [n][4 kH] (the
+// unrounded q, k, v, g sums); the tails are the prefilled stream's for this
+// layer, [q,k,v][3 oldest..newest][kH].  Token m's window is (s[m], s[m+1],
 // s[m+2]) and its input s[m+3] in the sequence s = tails ++ R(raw[0..n));
 // the new tails are s[n], s[n+1], s[n+2].  Only the first token block reads
 // the old tails, and it writes the new ones after that read.
-constexpr int kConvT = 1024;  // threads per conv workgroup: 64 tokens x 16 lanes of 4 channels
+constexpr int kConvT = 256;                  // threads per conv workgroup
+constexpr int kConvR = 16 * kMaxB / kConvT;  // tokens per thread
 __global__ __launch_bounds__(kConvT) void k_pconv(const float *__restrict__ raw, int n, uint16_t *__restrict__ tails,
                                                   const float *__restrict__ conv_w, float *__restrict__ qkv,
                                                   float *__restrict__ gate, float *__restrict__ sgate) {
-    static_assert(kConvT == 16 * kMaxB, "a thread per token and 4 channels");
+    static_assert(kConvR * kConvT == 16 * kMaxB && kConvT >= 64, "16 lanes of 4 channels x kMaxB tokens");
+    constexpr int MS = kConvT / 16;  // token stride between a thread's tokens
     __shared__ __attribute__((aligned(16))) float xs[kMaxB + 3][64];
     __shared__ uint64_t exp2_lds[32];  // expf's table, read per SiLU / sigmoid
-    const int row0 = blockIdx.x * 64, t = threadIdx.x, m = t >> 4, c4 = 4 * (t & 15);
+    const int row0 = blockIdx.x * 64, t = threadIdx.x, mr = t >> 4, c4 = 4 * (t & 15);
     const int m0 = (int)blockIdx.y * kMaxB, nb = n - m0 < kMaxB ? n - m0 : kMaxB;
     fill_exp2_lds_imm(exp2_lds);
     const Exp2Lds tab{exp2_lds};
     const int which = row0 / kH, cb = row0 - which * kH;  // section and its first channel
-    const bool live = m < nb;
-    // token m0 + m's raw sums of channels cb + c4 .. + 3, one 16-byte load
-    f32x4 r = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (live) r = *reinterpret_cast<const f32x4 *>(raw + (size_t)(m0 + m) * 4 * kH + row0 + c4);
-    const f32x4 rr = {rne_bf16(r.x), rne_bf16(r.y), rne_bf16(r.z), rne_bf16(r.w)};
+    // tokens m0 + mr + MS i: raw sums of channels cb + c4 .. + 3.  Tokens
+    // past the segment load its last token (in bounds, unused), so every
+    // load is unconditional and all are in flight at once.
+    f32x4 rr[kConvR];
+#pragma unroll
+    for (int i = 0; i < kConvR; ++i) {
+        const int m = mr + MS * i < nb ? mr + MS * i : nb - 1;
+        const f32x4 r = *reinterpret_cast<const f32x4 *>(raw + (size_t)(m0 + m) * 4 * kH + row0 + c4);
+        rr[i] = (f32x4){rne_bf16(r.x), rne_bf16(r.y), rne_bf16(r.z), rne_bf16(r.w)};
+    }
     if (which < 3) {
         uint16_t *tl = tails + (size_t)which * 3 * kH + cb;
         const f32x4 *cw4 = reinterpret_cast<const f32x4 *>(conv_w + ((size_t)which * kH + cb + c4) * 4);
@@ -922,9 +930,14 @@ __global__ __launch_bounds__(kConvT) void k_pconv(const float *__restrict__ raw,
                 for (int i = 0; i < 3; ++i) xs[i][t] = rne_bf16(raw[(size_t)(m0 - 3 + i) * 4 * kH + row0 + t]);
             }
         }
-        if (live) *reinterpret_cast<f32x4 *>(&xs[3 + m][c4]) = rr;
+#pragma unroll
+        for (int i = 0; i < kConvR; ++i)
+            if (mr + MS * i < nb) *reinterpret_cast<f32x4 *>(&xs[3 + mr + MS * i][c4]) = rr[i];
         __syncthreads();
-        if (live) {
+#pragma unroll
+        for (int i = 0; i < kConvR; ++i) {
+            const int m = mr + MS * i;
+            if (m >= nb) break;
             // gdn_depthwise_conv_silu_head_kind, gdn_model.cpp:1543-1667
             const f32x4 x0 = *reinterpret_cast<const f32x4 *>(&xs[m][c4]);
             const f32x4 x1 = *reinterpret_cast<const f32x4 *>(&xs[m + 1][c4]);
@@ -951,11 +964,16 @@ __global__ __launch_bounds__(kConvT) void k_pconv(const float *__restrict__ raw,
         }
     } else {
         __syncthreads();  // expf's table
-        if (!live) return;
-        const size_t o = (size_t)(m0 + m) * kH + cb + c4;
-        *reinterpret_cast<f32x4 *>(gate + o) = rr;
-        *reinterpret_cast<f32x4 *>(sgate + o) = (f32x4){sigmoid_ref(rr.x, tab), sigmoid_ref(rr.y, tab),
-                                                         sigmoid_ref(rr.z, tab), sigmoid_ref(rr.w, tab)};
+#pragma unroll
+        for (int i = 0; i < kConvR; ++i) {
+            const int m = mr + MS * i;
+            if (m >= nb) break;
+            const size_t o = (size_t)(m0 + m) * kH + cb + c4;
+            *reinterpret_cast<f32x4 *>(gate + o) = rr[i];
+            *reinterpret_cast<f32x4 *>(sgate + o) =
+                (f32x4){sigmoid_ref(rr[i].x, tab), sigmoid_ref(rr[i].y, tab), sigmoid_ref(rr[i].z, tab),
+                        sigmoid_ref(rr[i].w, tab)};
+        }
     }
 }
 
