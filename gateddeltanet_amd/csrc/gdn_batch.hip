@@ -755,42 +755,62 @@ __global__ __launch_bounds__(kT) void k_pab(const float *__restrict__ xn, int n,
 }
 
 // Per (head, stream): the output RMSNorm times the gate and sigmoid(gate)
-// (gdn_output_norm_and_gate, gdn_model.cpp:3226-3349) into X tiles.
+// (gdn_output_norm_and_gate, gdn_model.cpp:3226-3349) into X tiles, for
+// streams (or prefill tokens) PT y .. PT y + PT - 1 of n: every input of
+// the workgroup's PT streams is requested at its start (a stream past n
+// re-reads stream n - 1, unused), so they share one memory latency.
+template <int PT>
 __global__ __launch_bounds__(kT) void k_bonorm(const float *__restrict__ attn, const float *__restrict__ gate,
                                                const float *__restrict__ sgate, const float *__restrict__ w,
-                                               float eps, uint16_t *__restrict__ x_out) {
-    __shared__ float as[kHD];
-    __shared__ float cs[kHD / 16];
-    __shared__ float xs[kHD];
-    __shared__ float scale_s;
-    const int h = blockIdx.x, m = blockIdx.y, t = threadIdx.x, c = h * kHD + t;
-    const float a = attn[(size_t)m * kH + c];
-    as[t] = a;
+                                               float eps, uint16_t *__restrict__ x_out, int n) {
+    static_assert(PT * (kHD / 8) <= kT && kT == kHD, "a thread per channel; one X store task per thread");
+    __shared__ float as[PT][kHD];
+    __shared__ float cs[PT][kHD / 16];
+    __shared__ float xs[PT][kHD];
+    __shared__ float scale_s[PT];
+    const int h = blockIdx.x, m0 = (int)blockIdx.y * PT, t = threadIdx.x, c = h * kHD + t;
+    float a[PT], gt[PT], sg[PT];
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+        const size_t o = (size_t)(m0 + i < n ? m0 + i : n - 1) * kH + c;
+        a[i] = attn[o];
+        gt[i] = gate[o];
+        sg[i] = sgate[o];
+    }
+    const float wt = w[t];
+#pragma unroll
+    for (int i = 0; i < PT; ++i) as[i][t] = a[i];
     __syncthreads();
-    if (t < kHD / 16) {
+    if (t < PT * (kHD / 16)) {
+        const int i = t / (kHD / 16), r = t % (kHD / 16);
         float s = 0.0f;
 #pragma unroll
         for (int kk = 0; kk < 16; ++kk) {
-            const float v = as[16 * t + kk];
+            const float v = as[i][16 * r + kk];
             s += v * v;
         }
-        cs[t] = s;
+        cs[i][r] = s;
     }
     __syncthreads();
-    if (t == 0) {
+    if (t < PT) {
         float v[kHD / 16];
 #pragma unroll
-        for (int i = 0; i < kHD / 16; ++i) v[i] = cs[i];
+        for (int i = 0; i < kHD / 16; ++i) v[i] = cs[t][i];
         float sum = 0.0f;
 #pragma unroll
         for (int i = 0; i < kHD / 16; ++i) sum += v[i];
-        scale_s = 1.0f / __builtin_sqrtf(sum / (float)kHD + eps);
+        scale_s[t] = 1.0f / __builtin_sqrtf(sum / (float)kHD + eps);
     }
     __syncthreads();
-    xs[t] = rne_bf16(a * scale_s * w[t] * gate[(size_t)m * kH + c] * sgate[(size_t)m * kH + c]);
+#pragma unroll
+    for (int i = 0; i < PT; ++i) xs[i][t] = rne_bf16(a[i] * scale_s[i] * wt * gt[i] * sg[i]);
     __syncthreads();
-    if (t < kHD / 8) store_x8(x_out, m, h * kHD + 8 * t, xs + 8 * t);
+    if (t < PT * (kHD / 8)) {
+        const int i = t / (kHD / 8), j = t % (kHD / 8);
+        if (m0 + i < n) store_x8(x_out, m0 + i, h * kHD + 8 * j, xs[i] + 8 * j);
+    }
 }
+constexpr int kOnTok = 4;  // prefill tokens per output-norm workgroup
 
 // The recurrence of one (head, stream, CW-column group) per workgroup of
 // 2 CW threads, with the batch-1 arithmetic (gdn_island_prep / read /
@@ -978,29 +998,47 @@ __global__ __launch_bounds__(kConvT) void k_pconv(const float *__restrict__ raw,
 }
 
 // Per (head, token): the q/k L2 norms and alpha of the recurrence, in the
-// batch-1 tree order (k_brecur's first phase).
-__global__ __launch_bounds__(kT) void k_pqk(const float *__restrict__ qkv, float *__restrict__ qn_out,
+// batch-1 tree order (k_brecur's first phase), for tokens kQkTok y .. +
+// kQkTok - 1 of n, their loads requested together (a token past n re-reads
+// token n - 1, unused).
+constexpr int kQkTok = 4;
+__global__ __launch_bounds__(kT) void k_pqk(const float *__restrict__ qkv, int n, float *__restrict__ qn_out,
                                             float *__restrict__ kn_out, float *__restrict__ alpha_out) {
-    __shared__ float red[8], red2[4];
-    const int h = blockIdx.x, m = blockIdx.y, t = threadIdx.x, w = t >> 6, lane = t & 63;
-    const float *qp = qkv + (size_t)m * 3 * kH + h * kHD;
-    const float q = qp[t], k = qp[kH + t];
-    const float qs = wave_tree64(q * q), ks = wave_tree64(k * k);
-    if (lane == 0) {
-        red[w] = qs;
-        red[4 + w] = ks;
+    static_assert(kT == kHD, "a thread per head channel");
+    __shared__ float red[kQkTok][8], red2[kQkTok][4];
+    const int h = blockIdx.x, m0 = (int)blockIdx.y * kQkTok, t = threadIdx.x, w = t >> 6, lane = t & 63;
+    float q[kQkTok], k[kQkTok];
+#pragma unroll
+    for (int i = 0; i < kQkTok; ++i) {
+        const float *qp = qkv + (size_t)(m0 + i < n ? m0 + i : n - 1) * 3 * kH + h * kHD;
+        q[i] = qp[t];
+        k[i] = qp[kH + t];
+    }
+#pragma unroll
+    for (int i = 0; i < kQkTok; ++i) {
+        const float qs = wave_tree64(q[i] * q[i]), ks = wave_tree64(k[i] * k[i]);
+        if (lane == 0) {
+            red[i][w] = qs;
+            red[i][4 + w] = ks;
+        }
     }
     __syncthreads();
-    const float q_sq = (red[0] + red[1]) + (red[2] + red[3]);
-    const float k_sq = (red[4] + red[5]) + (red[6] + red[7]);
-    const float qv = q * (1.0f / __builtin_sqrtf(q_sq + 1e-6f));
-    const float kv = k * (1.0f / __builtin_sqrtf(k_sq + 1e-6f));
-    qn_out[(size_t)m * kH + h * kHD + t] = qv;
-    kn_out[(size_t)m * kH + h * kHD + t] = kv;
-    const float qk = wave_tree64(qv * kv);
-    if (lane == 0) red2[w] = qk;
+#pragma unroll
+    for (int i = 0; i < kQkTok; ++i) {
+        const int m = m0 + i;
+        const float q_sq = (red[i][0] + red[i][1]) + (red[i][2] + red[i][3]);
+        const float k_sq = (red[i][4] + red[i][5]) + (red[i][6] + red[i][7]);
+        const float qv = q[i] * (1.0f / __builtin_sqrtf(q_sq + 1e-6f));
+        const float kv = k[i] * (1.0f / __builtin_sqrtf(k_sq + 1e-6f));
+        if (m < n) {
+            qn_out[(size_t)m * kH + h * kHD + t] = qv;
+            kn_out[(size_t)m * kH + h * kHD + t] = kv;
+        }
+        const float qk = wave_tree64(qv * kv);
+        if (lane == 0) red2[i][w] = qk;
+    }
     __syncthreads();
-    if (t == 0) alpha_out[m * kNH + h] = (red2[0] + red2[1]) + (red2[2] + red2[3]);
+    if (t < kQkTok && m0 + t < n) alpha_out[(m0 + t) * kNH + h] = (red2[t][0] + red2[t][1]) + (red2[t][2] + red2[t][3]);
 }
 
 // The recurrence over a segment's n_total tokens in order, chunk by chunk of
@@ -2221,8 +2259,8 @@ void launch_recur(GDNBatchEngine *e, int l, hipStream_t s) {
                        e->qkv, e->bd, b_state(e, l), e->attn);
 }
 void launch_onorm(GDNBatchEngine *e, int l, hipStream_t s) {
-    hipLaunchKernelGGL(k_bonorm, dim3(kNH, e->streams), dim3(kT), 0, s, e->attn, e->gate, e->sgate,
-                       b_aux(e, l) + kAuxONorm, e->eps, e->x_o);
+    hipLaunchKernelGGL(k_bonorm<1>, dim3(kNH, e->streams), dim3(kT), 0, s, e->attn, e->gate, e->sgate,
+                       b_aux(e, l) + kAuxONorm, e->eps, e->x_o, e->streams);
 }
 void launch_o(GDNBatchEngine *e, int l, hipStream_t s) {
     BEpi ep{};
@@ -2426,7 +2464,8 @@ void enqueue_prefill_segment(GDNBatchEngine *e, int slot, int n, bool last, hipS
                                e->w_qkvg[l], xh, e->s_y, 4 * kH);
         hipLaunchKernelGGL(k_pconv, dim3(4 * kH / 64, blocks), dim3(kConvT), 0, s, e->s_y, n, tl,
                            b_aux(e, l) + kAuxConv, e->s_qkv, e->s_gate, e->s_sgate);
-        hipLaunchKernelGGL(k_pqk, dim3(kNH, n), dim3(kT), 0, s, e->s_qkv, e->s_qn, e->s_kn, e->s_alpha);
+        hipLaunchKernelGGL(k_pqk, dim3(kNH, (n + kQkTok - 1) / kQkTok), dim3(kT), 0, s, e->s_qkv, n, e->s_qn,
+                           e->s_kn, e->s_alpha);
         if (e->prefill_mode == GDN_PREFILL_CHUNKED)
             hipLaunchKernelGGL(k_wy_gram, dim3(kNH, kMaxB / 16, blocks), dim3(kT), 0, s, e->s_qn, e->s_kn, e->s_bd,
                                n, e->s_wyl, e->s_wym);
@@ -2438,8 +2477,8 @@ void enqueue_prefill_segment(GDNBatchEngine *e, int slot, int n, bool last, hipS
         else
             hipLaunchKernelGGL(k_pscan, dim3(kHD / kScanWgCols, kNH), dim3(kT), 0, s, e->s_qkv, e->s_qn, e->s_kn,
                                e->s_alpha, e->s_bd, n, st, e->s_attn);
-        hipLaunchKernelGGL(k_bonorm, dim3(kNH, n), dim3(kT), 0, s, e->s_attn, e->s_gate, e->s_sgate,
-                           b_aux(e, l) + kAuxONorm, e->eps, e->s_xo);
+        hipLaunchKernelGGL(k_bonorm<kOnTok>, dim3(kNH, (n + kOnTok - 1) / kOnTok), dim3(kT), 0, s, e->s_attn,
+                           e->s_gate, e->s_sgate, b_aux(e, l) + kAuxONorm, e->eps, e->s_xo, n);
         hipLaunchKernelGGL((k_pgemm<kKtH, 4, kSplitO>), dim3(kH / 128, tiles), dim3(kPgW * 64), 0, s, e->w_o[l], xo,
                            e->s_y, kH);
         const BNorm pm = seg_norm(e, e->s_y, b_aux(e, l) + kAuxMlpNorm, e->s_xh, -1, l, l);
