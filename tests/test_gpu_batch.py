@@ -82,13 +82,13 @@ def test_batch_gemm_rounding_bound(K, N):
 
 
 @pytest.mark.parametrize("kind,N,T", [(0, 256, 192), (0, 128, 64), (1, 256, 130), (2, 128, 64), (2, 512, 130),
-                                      (3, 5632, 70)])
+                                      (3, 5632, 70), (3, 5632, 1000)])
 def test_prefill_gemm_equals_step_gemm(kind, N, T):
     """The prefill's projection GEMMs form every sum of the step's GEMMs bit
     for bit: the q/k/v/g configuration (8 classes of k tiles), o_proj's and
     down's (4 classes x 4 splits, split sums in order) and gate/up + SwiGLU
-    (k_bgu's layout); token counts that leave partial 64- and 128-token
-    tiles.  Row counts that are multiples of 256 run k_pgemm_a (weights
+    (k_bgu's layout; 1000 tokens take the XCD super-tile placement); token
+    counts that leave partial 64- and 128-token tiles.  Row counts that are multiples of 256 run k_pgemm_a (weights
     straight into registers, as the engine's q/k/v/g and down launches), the
     others k_pgemm (128 rows x 128 tokens, both operands through LDS)."""
     rng = np.random.default_rng(100 + kind)
